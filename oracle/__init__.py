@@ -1,0 +1,286 @@
+"""ctypes wrapper around the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY.  This is the checker the HIP path is compared
+against.  Only tests/, ``__graft_entry__.smoke()`` and bench.py's
+``cpu_baseline`` leg may import it; the product package ``inferi_amd`` never
+does, and has no CPU fallback built on it.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 8, 12, 13, 14
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+NAMES = {F32: "F32", F16: "F16", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+
+
+def build() -> None:
+    """Compile liboracle.so from oracle.c (gcc only)."""
+    subprocess.run(["make", "-s", "-C", HERE, "-B"], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run `make -C oracle`)")
+        L = C.CDLL(LIB_PATH)
+        vp, i, f, sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+        L.ifo_decode_f16.restype = f
+        L.ifo_decode_f16.argtypes = [C.c_uint16]
+        L.ifo_encode_f16.restype = C.c_uint16
+        L.ifo_encode_f16.argtypes = [f]
+        L.ifo_decode_f16_array.argtypes = [vp, vp, sz]
+        L.ifo_encode_f16_array.argtypes = [vp, vp, sz]
+        L.ifo_get_scale_min_k4.argtypes = [i, vp, vp, vp]
+        L.ifo_dequant.argtypes = [i, vp, sz, vp]
+        L.ifo_dequant.restype = i
+        L.ifo_quantize.argtypes = [i, vp, sz, vp]
+        L.ifo_quantize.restype = i
+        L.ifo_gemv_f64.argtypes = [vp, i, i, vp, vp]
+        L.ifo_gemv_quant.argtypes = [i, vp, i, i, vp, vp, i]
+        L.ifo_gemv_quant.restype = i
+        L.ifo_rms_norm.argtypes = [vp, vp, vp, i, f]
+        L.ifo_rope.argtypes = [i, vp, i, vp, i, i, i, f]
+        L.ifo_silu_mul.argtypes = [vp, vp, i]
+        L.ifo_add.argtypes = [vp, vp, i]
+        L.ifo_attention.argtypes = [vp, vp, vp, vp, i, vp]
+        L.ifo_argmax.argtypes = [vp, i]
+        L.ifo_argmax.restype = i
+        L.ifo_state_new.argtypes = [vp]
+        L.ifo_state_new.restype = vp
+        L.ifo_state_free.argtypes = [vp]
+        L.ifo_forward.argtypes = [vp, vp, i, i, vp, i]
+        L.ifo_forward.restype = i
+        L.ifo_state_buffer.argtypes = [vp, i, i]
+        L.ifo_state_buffer.restype = vp
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def decode_f16(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().ifo_decode_f16_array(_p(h), _p(out), h.size)
+    return out
+
+
+def encode_f16(f) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().ifo_encode_f16_array(_p(f), _p(out), f.size)
+    return out
+
+
+def get_scale_min_k4(j: int, q: bytes) -> tuple[int, int]:
+    qa = np.frombuffer(bytes(q), dtype=np.uint8).copy()
+    d = np.zeros(1, np.uint8)
+    m = np.zeros(1, np.uint8)
+    lib().ifo_get_scale_min_k4(j, _p(qa), _p(d), _p(m))
+    return int(d[0]), int(m[0])
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    return cols // BLOCK_ELEMS[dtype] * BLOCK_BYTES[dtype]
+
+
+def dequant(dtype: int, data, n_elems: int) -> np.ndarray:
+    buf = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8) if isinstance(data, (bytes, bytearray)) else data).view(np.uint8)
+    if buf.size < n_elems // BLOCK_ELEMS[dtype] * BLOCK_BYTES[dtype]:
+        raise ValueError("dequant: buffer too small")
+    out = np.empty(n_elems, np.float32)
+    if lib().ifo_dequant(dtype, _p(buf), n_elems, _p(out)) != 0:
+        raise ValueError("dequant: bad dtype or size")
+    return out
+
+
+def quantize(dtype: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size // BLOCK_ELEMS[dtype] * BLOCK_BYTES[dtype], np.uint8)
+    if lib().ifo_quantize(dtype, _p(x), x.size, _p(out)) != 0:
+        raise ValueError("quantize: bad dtype or size")
+    return out
+
+
+def gemv_f64(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(w.shape[0], np.float32)
+    lib().ifo_gemv_f64(_p(w), w.shape[0], w.shape[1], _p(x), _p(y))
+    return y
+
+
+def gemv_quant(dtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    w = np.ascontiguousarray(w).view(np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    assert w.size >= rows * row_bytes(dtype, cols) and x.size == cols
+    y = np.empty(rows, np.float32)
+    if lib().ifo_gemv_quant(dtype, _p(w), rows, cols, _p(x), _p(y), nthreads) != 0:
+        raise ValueError("gemv_quant: bad shape")
+    return y
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    lib().ifo_rms_norm(_p(out), _p(x), _p(w), x.size, eps)
+    return out
+
+
+def rope(q: np.ndarray, k: np.ndarray | None, head_size: int, pos: int, base: float, neox: bool = False):
+    q = np.array(q, np.float32, copy=True)
+    kk = np.array(k if k is not None else np.zeros(0), np.float32, copy=True)
+    lib().ifo_rope(int(neox), _p(q), q.size, _p(kk) if kk.size else None, kk.size, head_size, pos, base)
+    return q, kk
+
+
+def silu_mul(h1: np.ndarray, h2: np.ndarray) -> np.ndarray:
+    h = np.array(h1, np.float32, copy=True)
+    h2 = np.ascontiguousarray(h2, np.float32)
+    lib().ifo_silu_mul(_p(h), _p(h2), h.size)
+    return h
+
+
+class AttnParams(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("seq_len", "kv_dim", "kv_mul", "n_heads", "head_size", "pos")]
+
+
+def attention(q, k_cache, v_cache, n_heads: int, n_kv_heads: int, head_size: int, pos: int, kv_f16: bool) -> np.ndarray:
+    """k_cache/v_cache: [max_pos, kv_dim] as float32, or uint16 binary16 codes when kv_f16."""
+    q = np.ascontiguousarray(q, np.float32)
+    kt = np.uint16 if kv_f16 else np.float32
+    k_cache = np.ascontiguousarray(k_cache, kt)
+    v_cache = np.ascontiguousarray(v_cache, kt)
+    kv_dim = n_kv_heads * head_size
+    p = AttnParams(k_cache.shape[0], kv_dim, n_heads // n_kv_heads, n_heads, head_size, pos)
+    out = np.empty(n_heads * head_size, np.float32)
+    lib().ifo_attention(C.byref(p), _p(q), _p(k_cache), _p(v_cache), int(kv_f16), _p(out))
+    return out
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return lib().ifo_argmax(_p(v), v.size)
+
+
+# ------------------------------------------------------------------ model --
+
+class _Config(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("ffn", C.c_int), ("n_layers", C.c_int), ("n_heads", C.c_int),
+                ("n_kv_heads", C.c_int), ("vocab", C.c_int), ("max_pos", C.c_int),
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("kv_f16", C.c_int)]
+
+
+class _Tensor(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("data", C.c_void_p), ("rows", C.c_int), ("cols", C.c_int)]
+
+
+class _Layer(C.Structure):
+    _fields_ = [(n, _Tensor) for n in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + [
+        ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p)]
+
+
+class _Model(C.Structure):
+    _fields_ = [("cfg", _Config), ("token_embd", _Tensor), ("output", _Tensor),
+                ("output_norm", C.c_void_p), ("layers", C.c_void_p)]
+
+
+LAYER_MATS = ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+class Model:
+    """Oracle forward over host-resident GGUF blocks.
+
+    ``weights`` maps GGUF tensor names (``blk.N.attn_q.weight`` ...,
+    ``token_embd.weight``, ``output.weight``, ``output_norm.weight``) to
+    ``(dtype, uint8/float32 ndarray, rows, cols)``; norms are float32 arrays.
+    """
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.cfg = dict(cfg)
+        self._keep = []
+        c = cfg
+        self._ccfg = _Config(c["hidden"], c["ffn"], c["n_layers"], c["n_heads"], c["n_kv_heads"], c["vocab"],
+                             c["max_pos"], c["rope_theta"], c["rms_eps"], int(c.get("kv_f16", 1)))
+
+        def tens(name):
+            dt, arr, rows, cols = weights[name]
+            arr = np.ascontiguousarray(arr)
+            self._keep.append(arr)
+            return _Tensor(dt, arr.ctypes.data, rows, cols)
+
+        def vec(name):
+            arr = np.ascontiguousarray(weights[name], np.float32)
+            self._keep.append(arr)
+            return arr.ctypes.data
+
+        layers = (_Layer * c["n_layers"])()
+        for l in range(c["n_layers"]):
+            for m in LAYER_MATS:
+                setattr(layers[l], m, tens(f"blk.{l}.{m}.weight"))
+            layers[l].attn_norm = vec(f"blk.{l}.attn_norm.weight")
+            layers[l].ffn_norm = vec(f"blk.{l}.ffn_norm.weight")
+        self._layers = layers
+        self._m = _Model(self._ccfg, tens("token_embd.weight"), tens("output.weight"), vec("output_norm.weight"),
+                         C.cast(layers, C.c_void_p))
+        self._state = lib().ifo_state_new(C.byref(self._ccfg))
+
+    def __del__(self):
+        try:
+            if self._state:
+                lib().ifo_state_free(self._state)
+                self._state = None
+        except Exception:
+            pass
+
+    def forward(self, token: int, pos: int, nthreads: int = 0) -> np.ndarray:
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        if lib().ifo_forward(C.byref(self._m), self._state, token, pos, _p(logits), nthreads) != 0:
+            raise ValueError("oracle forward: bad token/pos")
+        return logits
+
+    def kv_cache(self, layer: int, which: str) -> np.ndarray:
+        c = self.cfg
+        kv_dim = c["hidden"] * c["n_kv_heads"] // c["n_heads"]
+        ptr = lib().ifo_state_buffer(self._state, 1 if which == "k" else 2, layer)
+        dt = np.uint16 if c.get("kv_f16", 1) else np.float32
+        n = c["max_pos"] * kv_dim
+        buf = (C.c_char * (n * np.dtype(dt).itemsize)).from_address(ptr)
+        return np.frombuffer(buf, dt).reshape(c["max_pos"], kv_dim).copy()
+
+    def generate(self, prompt: list[int], n_new: int, nthreads: int = 0, margins: list | None = None) -> list[int]:
+        """Greedy token loop of chat_llama2.rs:137-160 with forced prompt tokens.
+
+        Returns the ``n_new`` tokens generated after the prompt.
+        """
+        out = []
+        token = prompt[0]
+        for pos in range(len(prompt) + n_new - 1):
+            logits = self.forward(token, pos, nthreads)
+            nxt = argmax(logits)
+            if pos + 1 < len(prompt):
+                token = prompt[pos + 1]
+            else:
+                if margins is not None:
+                    top2 = np.partition(logits, -2)[-2:]
+                    margins.append(float(top2[1] - top2[0]))
+                token = nxt
+                out.append(nxt)
+        return out

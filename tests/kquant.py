@@ -1,0 +1,117 @@
+"""Hand-built GGUF K-quant blocks for known-answer tests.
+
+The builders below write blocks field by field from the GGUF block layouts
+(crates/inferi/src/quantization.rs:42-45, 217-222, 262-268, 335-340 in the
+reference, i.e. ggml's block_q8_0 / block_q6_K / block_q5_K / block_q4_K), so
+that a test can state the expected dequantized values in closed form.  They
+share no code with the oracle.
+"""
+
+import numpy as np
+
+F16_ONE = 0x3C00
+F16_HALF = 0x3800
+F16_QUARTER = 0x3400
+F16_TWO = 0x4000
+
+
+def pack_scales_bits(sc, mn) -> bytes:
+    """Place eight 6-bit scales and mins into the 12-byte K-quant field.
+
+    Bit placement (ggml-common.h, block_q4_K.scales):
+      j < 4 : sc_j -> bits 0..5 of byte j;   m_j -> bits 0..5 of byte j+4
+      j >= 4: sc_j bits 0..3 -> bits 0..3 of byte j+4, bits 4..5 -> bits 6..7 of byte j-4
+              m_j  bits 0..3 -> bits 4..7 of byte j+4, bits 4..5 -> bits 6..7 of byte j
+    """
+    b = [0] * 12
+    for j in range(8):
+        s, m = int(sc[j]) & 63, int(mn[j]) & 63
+        if j < 4:
+            b[j] |= s
+            b[j + 4] |= m
+        else:
+            b[j + 4] |= (s & 15) | ((m & 15) << 4)
+            b[j - 4] |= (s >> 4) << 6
+            b[j] |= (m >> 4) << 6
+    return bytes(b)
+
+
+def q4k_block(d16: int, dmin16: int, sc, mn, q) -> bytes:
+    """q: 256 ints in 0..15 in element order."""
+    q = np.asarray(q, dtype=np.int64)
+    qs = bytearray(128)
+    for g in range(4):
+        for l in range(32):
+            qs[32 * g + l] = int(q[64 * g + l]) | (int(q[64 * g + 32 + l]) << 4)
+    return d16.to_bytes(2, "little") + dmin16.to_bytes(2, "little") + pack_scales_bits(sc, mn) + bytes(qs)
+
+
+def q5k_block(d16: int, dmin16: int, sc, mn, q) -> bytes:
+    """q: 256 ints in 0..31 in element order."""
+    q = np.asarray(q, dtype=np.int64)
+    qh = bytearray(32)
+    qs = bytearray(128)
+    for g in range(4):
+        for l in range(32):
+            a, b = int(q[64 * g + l]), int(q[64 * g + 32 + l])
+            qs[32 * g + l] = (a & 15) | ((b & 15) << 4)
+            qh[l] |= ((a >> 4) & 1) << (2 * g)
+            qh[l] |= ((b >> 4) & 1) << (2 * g + 1)
+    return d16.to_bytes(2, "little") + dmin16.to_bytes(2, "little") + pack_scales_bits(sc, mn) + bytes(qh) + bytes(qs)
+
+
+def q6k_block(d16: int, sc, q) -> bytes:
+    """sc: 16 ints in -128..127 (one per 16 elements); q: 256 ints in -32..31."""
+    u = np.asarray(q, dtype=np.int64) + 32
+    ql = bytearray(128)
+    qh = bytearray(64)
+    for i in range(2):
+        for l in range(32):
+            e = 128 * i + l
+            a, b, c, dd = int(u[e]), int(u[e + 32]), int(u[e + 64]), int(u[e + 96])
+            ql[64 * i + l] = (a & 15) | ((c & 15) << 4)
+            ql[64 * i + l + 32] = (b & 15) | ((dd & 15) << 4)
+            qh[32 * i + l] = (a >> 4) | ((b >> 4) << 2) | ((c >> 4) << 4) | ((dd >> 4) << 6)
+    scb = bytes(int(s) & 0xFF for s in sc)
+    return bytes(ql) + bytes(qh) + scb + d16.to_bytes(2, "little")
+
+
+def q8_0_block(d16: int, q) -> bytes:
+    return d16.to_bytes(2, "little") + bytes(int(v) & 0xFF for v in q)
+
+
+def f16_value(code: int) -> float:
+    return float(np.array([code], np.uint16).view(np.float16)[0])
+
+
+def random_valid_f16_scale(rng: np.random.Generator) -> int:
+    """A finite f16 in [-1, 1], a quarter of them subnormal, as the reference's
+    GEMV tests draw them (crates/inferi/src/ops/gemv_quant.rs:354-365)."""
+    v = rng.random() * 2.0 - 1.0
+    if rng.integers(0, 256) < 64:
+        v *= 1e-5
+    return int(np.array([v], np.float16).view(np.uint16)[0])
+
+
+def random_blocks(dtype: int, n_blocks: int, rng: np.random.Generator) -> np.ndarray:
+    """Raw random bits with valid (finite, often subnormal) f16 scales, the
+    shape of the reference's rand_block_* test generators
+    (gemv_quant.rs:367-430)."""
+    from oracle import BLOCK_BYTES, Q4_K, Q5_K, Q6_K, Q8_0
+
+    bb = BLOCK_BYTES[dtype]
+    raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
+
+    def scales(n):
+        v = rng.random(n) * 2.0 - 1.0
+        v[rng.integers(0, 256, size=n) < 64] *= 1e-5
+        return v.astype(np.float16).view(np.uint8).reshape(n, 2)
+
+    if dtype in (Q4_K, Q5_K):
+        raw[:, 0:2] = scales(n_blocks)
+        raw[:, 2:4] = scales(n_blocks)
+    elif dtype == Q6_K:
+        raw[:, 208:210] = scales(n_blocks)
+    elif dtype == Q8_0:
+        raw[:, 0:2] = scales(n_blocks)
+    return raw.reshape(-1)
