@@ -1,0 +1,295 @@
+"""Benchmark: batch-1 decode tok/s of the 8B-shape Q4_K Llama (BASELINE config
+5) and the Q4_K GEMV's achieved HBM bandwidth against MI355X's 8 TB/s.
+
+One "step" is one decode token through the whole model (embedding, 32
+layers, final norm, Q6_K output head, greedy argmax), replayed from a HIP
+graph with the position on the device.  The timed region starts with the
+weights resident in HBM and the 4096-token prompt already in the KV cache
+(prefilled by sequential decode, untimed).
+
+Prints one JSON line.  Extra modes: --sweep (BASELINE config 2 GEMV sweep,
+GB/s per format and shape), --attn (config 3 attention GB/s).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import inferi_amd as I  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+ROT_BYTES = 640 << 20  # rotate over > 512 MB of distinct buffers: defeats the 256 MB MALL
+
+CFG_8B = dict(n_layers=32, hidden=4096, ffn=14336, n_heads=32, n_kv_heads=8, vocab=128256, rope_theta=500000.0,
+              rms_eps=1e-5)
+CFG_C4 = dict(n_layers=22, hidden=2048, ffn=5632, n_heads=32, n_kv_heads=4, vocab=32000, rope_theta=10000.0,
+              rms_eps=1e-5)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(dtype: int, rows: int, cols: int) -> int:
+    """Algorithmic bytes of one GEMV: the weight blocks, x and y."""
+    return rows * I.row_bytes(dtype, cols) + 4 * cols + 4 * rows
+
+
+def decode_token_bytes(cfg: I.Llama2Config, ctx_len: float, mat=I.Q4_K, head=I.Q6_K) -> float:
+    """Algorithmic HBM bytes of one decode token: every weight once, the f16
+    KV cache up to the position, and the embedding row."""
+    h, kv, f = cfg.hidden, cfg.kv_dim, cfg.ffn
+    per_layer = (I.row_bytes(mat, h) * (h + 2 * kv + h + 2 * f) + I.row_bytes(mat, f) * h + 2 * 4 * h)
+    weights = cfg.n_layers * per_layer + I.row_bytes(head, h) * cfg.vocab + 4 * h + I.row_bytes(mat, h)
+    kv_bytes = cfg.n_layers * 2 * kv * 2 * ctx_len
+    return weights + kv_bytes
+
+
+def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, seed: int = 0) -> dict:
+    """Average launch time of the op-level GEMV over `iters` launches,
+    rotating through enough weight copies to defeat the MALL."""
+    n = rows * cols
+    wbytes = rows * I.row_bytes(dtype, cols)
+    copies = max(2, -(-ROT_BYTES // wbytes))
+    tmp = ctx.alloc(n * 4)
+    ctx.fill_normal(tmp, n, seed, 1, 0.0, 0.02)
+    ws = []
+    for _ in range(copies):
+        b = ctx.alloc(wbytes)
+        ctx.quantize(b, tmp, dtype, n)
+        ws.append(b)
+    tmp.free()
+    x = ctx.upload(np.random.default_rng(seed).standard_normal(cols).astype(np.float32))
+    y = ctx.alloc(rows * 4)
+    for i in range(copies):  # warm-up
+        ctx.matmul_quant_assign(y, ws[i], dtype, rows, cols, x)
+    ctx.sync()
+    ctx.event_record(2)
+    for i in range(iters):
+        ctx.matmul_quant_assign(y, ws[i % copies], dtype, rows, cols, x)
+    ctx.event_record(3)
+    ms = ctx.event_elapsed(2, 3)
+    for b in ws:
+        b.free()
+    x.free()
+    y.free()
+    us = ms * 1000.0 / iters
+    nbytes = gemv_bytes(dtype, rows, cols)
+    return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
+
+
+def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, threads: int) -> dict:
+    """The CPU oracle (a C restatement of the reference's forward) timed on
+    the host cores on a bounded sample: n_tokens decode steps of the same
+    model bytes."""
+    import oracle as O
+
+    if not os.path.exists(O.LIB_PATH):
+        O.build()
+    host = {}
+    for name in cfg.shapes():
+        dt, arr, rows, cols = weights.download(name)
+        host[name] = arr if dt == I.F32 else (dt, arr, rows, cols)
+    c = dict(hidden=cfg.hidden, ffn=cfg.ffn, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+             vocab=cfg.vocab, max_pos=max(16, n_tokens + 1), rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps, kv_f16=1)
+    m = O.Model(c, host)
+    m.forward(1, 0, threads)  # warm the pages
+    t0 = time.perf_counter()
+    for p in range(1, n_tokens + 1):
+        m.forward(p, p, threads)
+    dt = time.perf_counter() - t0
+    return {"value": n_tokens / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n_tokens} decode tokens of the same 8B-shape model bytes (positions 1-{n_tokens}) "
+                      f"through oracle/oracle.c ifo_forward, {threads} threads"}
+
+
+def run_decode(args) -> None:
+    ctx = I.LlmContext(0)
+    dev_name, n_cu = ctx.device_info()
+    base = CFG_8B if args.model == "8b" else CFG_C4
+    prompt_len = args.prompt
+    max_pos = prompt_len + args.warmup + args.steps + 1
+    cfg = I.Llama2Config(max_pos=max_pos, kv_dtype=I.F16, **base)
+    t0 = time.perf_counter()
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=args.seed)
+    log(f"bench: {dev_name}, {n_cu} CUs; synthetic weights in {time.perf_counter() - t0:.1f}s")
+    s = I.Llama2State(ctx, cfg)
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab, prompt_len).astype(np.uint32)
+    s.reset(prompt, 0)
+    t0 = time.perf_counter()
+    chunk = 512
+    done = 0
+    while done < prompt_len - 1:  # prefill: sequential decode of the prompt (untimed)
+        n = min(chunk, prompt_len - 1 - done)
+        I.Llama2.generate(ctx, s, w, n, use_graph=True)
+        ctx.sync()
+        done += n
+        log(f"bench: prefill {done}/{prompt_len - 1} tokens ({time.perf_counter() - t0:.1f}s)")
+    I.Llama2.generate(ctx, s, w, args.warmup, use_graph=True)
+    ctx.sync()
+    pos0 = int(s.read("pos", np.uint32)[0])
+    ctx.event_record(0)
+    I.Llama2.generate(ctx, s, w, args.steps, use_graph=True)
+    ctx.event_record(1)
+    ms = ctx.event_elapsed(0, 1)
+    ctx.sync()
+    ms_per_step = ms / args.steps
+    tok_s = 1000.0 / ms_per_step
+    mean_ctx = pos0 + (args.steps + 1) / 2.0
+    tok_bytes = decode_token_bytes(cfg, mean_ctx)
+    log(f"bench: decode {args.steps} tokens at pos {pos0}..{pos0 + args.steps - 1}: {ms_per_step:.4f} ms/token, "
+        f"{tok_s:.1f} tok/s, {tok_bytes / (ms_per_step * 1e-3) / 1e9:.0f} GB/s of {HBM_PEAK_GBS:.0f}")
+    toks = s.tokens(pos0, args.steps + 1)
+    assert np.all(toks < cfg.vocab)
+
+    # the dominant kernel: Q4_K GEMV, measured on the op-level kernel at the
+    # 14336x4096 shape of the FFN projections
+    g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
+    log(f"bench: gemv_q4_k_plain 14336x4096: {g['us']:.2f} us/launch, {g['gbs']:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(cfg, w, args.cpu_tokens, threads)
+        log(f"bench: cpu baseline {cpu['value']:.3f} tok/s ({time.perf_counter() - t0:.1f}s)")
+
+    out = {
+        "metric": "decode tok/s batch 1 (8B-shape Q4_K); Q4_K GEMV achieved HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init N(0,0.02) weights quantized on device; uniform random prompt ids)",
+        "config": {
+            "workload": ("8B-shape Llama decode: 32 layers, hidden 4096, 32 q / 8 kv heads, FFN 14336, vocab 128256, "
+                         "Q4_K matmuls + Q6_K head, f16 KV cache" if args.model == "8b" else
+                         "22-layer Llama decode: hidden 2048, 32 q / 4 kv heads, FFN 5632, vocab 32000, Q4_K + Q6_K"),
+            "prompt_tokens": prompt_len,
+            "positions": [pos0, pos0 + args.steps - 1],
+            "batch": 1,
+            "decode_bytes_per_token": int(tok_bytes),
+            "decode_hbm_frac": round(tok_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "device": dev_name,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_q4_k_plain 14336x4096 (Q4_K, 33,103,872 algorithmic bytes per launch)",
+            "achieved": round(g["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(g["us"], 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    s.close()
+    w.close()
+    ctx.close()
+
+
+def run_sweep(args) -> None:
+    ctx = I.LlmContext(0)
+    rows_out = []
+    for name, dt in (("Q4_K", I.Q4_K), ("Q5_K", I.Q5_K), ("Q6_K", I.Q6_K), ("Q8_0", I.Q8_0)):
+        for rows, cols in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+            g = time_gemv(ctx, dt, rows, cols, iters=args.gemv_iters)
+            rec = {"format": name, "rows": rows, "cols": cols, "us": round(g["us"], 3), "bytes": g["bytes"],
+                   "gbs": round(g["gbs"], 1), "frac": round(g["gbs"] / HBM_PEAK_GBS, 4)}
+            rows_out.append(rec)
+            log(f"sweep: {name} {rows}x{cols}: {g['us']:.2f} us, {g['gbs']:.0f} GB/s ({rec['frac'] * 100:.1f}%)")
+    print(json.dumps({"sweep": rows_out}), flush=True)
+    ctx.close()
+
+
+def run_attn(args) -> None:
+    ctx = I.LlmContext(0)
+    out = []
+    nh, nkv, hs = 32, 8, 128
+    kv_dim = nkv * hs
+    for L in (512, 2048, 4352, 8192):
+        copies = max(2, -(-ROT_BYTES // (2 * L * kv_dim * 2)))
+        caches = []
+        for i in range(copies):
+            kc = ctx.alloc(2 * L * kv_dim * 4)
+            ctx.fill_normal(kc, 2 * L * kv_dim, 3, i, 0.0, 1.0)
+            k16 = ctx.alloc(L * kv_dim * 2)
+            v16 = ctx.alloc(L * kv_dim * 2)
+            ctx.quantize(k16, kc, I.F16, L * kv_dim)
+            ctx.quantize(v16, kc.at(L * kv_dim * 4), I.F16, L * kv_dim)
+            kc.free()
+            caches.append((k16, v16))
+        q = ctx.upload(np.random.default_rng(5).standard_normal(nh * hs).astype(np.float32))
+        o = ctx.alloc(nh * hs * 4)
+        p = I.AttentionParams(L, kv_dim, nh // nkv, nh, hs, L - 1)
+        dp = ctx.upload(np.frombuffer(bytes(p), np.uint8))
+        for k16, v16 in caches:
+            I.BatchedMultiqueryAttention.launch(ctx, p, dp, q, k16, v16, I.F16, o)
+        ctx.sync()
+        iters = args.gemv_iters
+        ctx.event_record(2)
+        for i in range(iters):
+            k16, v16 = caches[i % copies]
+            I.BatchedMultiqueryAttention.launch(ctx, p, dp, q, k16, v16, I.F16, o)
+        ctx.event_record(3)
+        us = ctx.event_elapsed(2, 3) * 1000.0 / iters
+        nbytes = 2 * L * kv_dim * 2 + 2 * nh * hs * 4
+        rec = {"L": L, "us": round(us, 3), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        out.append(rec)
+        log(f"attn: L={L}: {us:.2f} us, {rec['gbs']:.0f} GB/s")
+        for k16, v16 in caches:
+            k16.free()
+            v16.free()
+        q.free()
+        o.free()
+        dp.free()
+    print(json.dumps({"attention": out}), flush=True)
+    ctx.close()
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=4096)
+    ap.add_argument("--model", choices=["8b", "c4"], default="8b")
+    ap.add_argument("--seed", type=int, default=2000)
+    ap.add_argument("--gemv-iters", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--attn", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU; the multi-GPU sharding of the decode path is designed "
+              "but not built. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if args.sweep:
+        run_sweep(args)
+    elif args.attn:
+        run_attn(args)
+    else:
+        run_decode(args)
+
+
+if __name__ == "__main__":
+    main()

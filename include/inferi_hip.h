@@ -1,0 +1,239 @@
+/*
+ * inferi_hip — C ABI of the MI355X (gfx950) backend for inferi's batch-1
+ * GGUF decode token loop.
+ *
+ * This header is the drop-in boundary.  Every entry point below replaces one
+ * call of the reference's op/model API (dimforge/inferi, Rust); the comment on
+ * each names the reference function (file:line, relative to the reference
+ * root) whose arguments and semantics it keeps.
+ *
+ * Conventions (mirroring crates/inferi/src/context.rs:106-130):
+ *   - Every call returns an ifr_status; on failure ifr_last_error() says why.
+ *     Contract violations that the reference assert!s on (shape, rank,
+ *     contiguity: ops/gemv_quant.rs:197-201, ops/rope.rs:39-44) return
+ *     IFR_EINVAL instead of aborting.
+ *   - Op calls are asynchronous: they enqueue kernels on the context's one
+ *     HIP stream, in call order, and complete at ifr_sync() or at an
+ *     ifr_download(), which waits for everything queued before it.
+ *   - Pointers named dev_* or documented as device pointers are device
+ *     memory owned by the caller (allocate with ifr_alloc or any hipMalloc);
+ *     the library never frees what it did not allocate.
+ *   - One context per thread; a context is not thread-safe.
+ */
+#ifndef INFERI_HIP_H
+#define INFERI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IFR_API __attribute__((visibility("default")))
+
+typedef int32_t ifr_status;
+#define IFR_OK 0
+#define IFR_EINVAL 1       /* bad argument: shape, alignment, dtype, null pointer */
+#define IFR_EUNSUPPORTED 2 /* valid for the reference, not implemented here */
+#define IFR_EHIP 3         /* a HIP runtime call failed */
+#define IFR_ENOMEM 4       /* device allocation failed */
+
+/* GGUF tensor type ids (crates/inferi/src/gguf.rs:74-104). */
+#define IFR_F32 0
+#define IFR_F16 1
+#define IFR_Q8_0 8
+#define IFR_Q4_K 12
+#define IFR_Q5_K 13
+#define IFR_Q6_K 14
+
+/* RoPEVariant (crates/inferi/src/ops/rope.rs:7-13). */
+#define IFR_ROPE_ORIGINAL 0
+#define IFR_ROPE_NEOX 1
+
+/* Device-resident op parameter structs; same field order and types as the
+ * reference's #[repr(C)] structs, so a buffer written for one is valid for
+ * the other. */
+typedef struct { float nudge_factor; } ifr_rms_norm_config; /* RmsNormConfig, inferi-shaders/src/rms_norm.rs:24-26 */
+typedef struct {
+    uint32_t head_size, kv_dim, pos;
+    float base_freq;
+} ifr_rope_config; /* RoPEConfig, inferi-shaders/src/rope.rs:21-26 */
+typedef struct {
+    uint32_t seq_len, kv_dim, kv_mul, n_heads, head_size, pos;
+} ifr_attn_params; /* AttentionParams, inferi-shaders/src/batched_multiquery_attention.rs:18-31 */
+
+typedef struct ifr_ctx ifr_ctx;
+
+/* ---------------------------------------------------------------- context */
+
+/* Opens device `device`, creates the context's stream and loads the gfx950
+ * code object (`code_object_path`, or NULL for inferi_kernels.hsaco beside
+ * this library).  Replaces LlmOps::new (crates/inferi/src/context.rs:58-85),
+ * which loads every compiled kernel of the backend. */
+IFR_API ifr_status ifr_create(int32_t device, const char *code_object_path, ifr_ctx **out);
+IFR_API void ifr_destroy(ifr_ctx *ctx);
+/* Message of the last failed call on this context (or of the last failed
+ * ifr_create on this thread when ctx is NULL). */
+IFR_API const char *ifr_last_error(const ifr_ctx *ctx);
+/* Device name and compute-unit count, for reports. */
+IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, int32_t *n_cu);
+
+/* Tuning knobs (no reference counterpart): "gemv_max_grid" caps the number of
+ * GEMV workgroups (0 = one per 16-row tile, the default). */
+IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
+
+/* ----------------------------------------------------------------- memory */
+
+/* Device buffers (vortx Tensor storage in the reference).  Allocations are
+ * 256-byte aligned. */
+IFR_API ifr_status ifr_alloc(ifr_ctx *ctx, size_t bytes, void **dev_ptr);
+IFR_API ifr_status ifr_free(ifr_ctx *ctx, void *dev_ptr);
+/* Host -> device; returns once the host buffer may be reused
+ * (GpuBackend::write_buffer in crates/inferi-chat/src/chat_llama2.rs:210-216). */
+IFR_API ifr_status ifr_upload(ifr_ctx *ctx, void *dev_dst, const void *host_src, size_t bytes);
+/* Device -> host after all queued work (GpuBackend::read_buffer,
+ * crates/inferi-chat/src/chat_llama2.rs:250-252). */
+IFR_API ifr_status ifr_download(ifr_ctx *ctx, void *host_dst, const void *dev_src, size_t bytes);
+IFR_API ifr_status ifr_memset(ifr_ctx *ctx, void *dev_dst, int32_t byte_value, size_t bytes);
+/* Waits for all queued work (LlmContext::submit + synchronize,
+ * crates/inferi/src/context.rs:117-130). */
+IFR_API ifr_status ifr_sync(ifr_ctx *ctx);
+/* Timing on the context's stream: records event `slot` (0..15) and returns
+ * the milliseconds between two recorded slots (waits for the later one). */
+IFR_API ifr_status ifr_event_record(ifr_ctx *ctx, int32_t slot);
+IFR_API ifr_status ifr_event_elapsed(ifr_ctx *ctx, int32_t start_slot, int32_t end_slot, float *ms);
+
+/* -------------------------------------------------------------------- ops */
+
+/* out[0..n_elems) = dequantize(blocks), bit-exact with the reference's
+ * Block*::dequantize (crates/inferi/src/quantization.rs:47-55, 224-257,
+ * 287-330, 358-392) and decode_f16 (:405-422).  dtype: any IFR_* above;
+ * n_elems a multiple of the block size. */
+IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int32_t dtype, uint64_t n_elems);
+
+/* out[rows] = dequant(W)[rows x cols] . v[cols], fp32 accumulation.
+ * W is `rows` rows of cols/QK consecutive GGUF blocks, exactly as a GGUF file
+ * stores them.  Replaces LlmContext::matmul_quant_assign
+ * (crates/inferi/src/context.rs:441-456) -> GemvQuant::launch
+ * (crates/inferi/src/ops/gemv_quant.rs:183-340).
+ * Requirements: cols % QK == 0, cols <= 16384; W 16-byte aligned for Q4_K
+ * and Q5_K, 4-byte aligned for Q6_K and Q8_0 (GGUF data is 32-aligned). */
+IFR_API ifr_status ifr_matmul_quant(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
+                                    uint32_t cols, const float *v);
+
+/* out = (value * (1/sqrt(sum(value^2)/n + cfg.nudge_factor))) * weight, with
+ * cfg a device pointer.  LlmContext::rms_norm_assign
+ * (crates/inferi/src/context.rs:336-353) -> rms_norm shader
+ * (inferi-shaders/src/rms_norm.rs:81-121). */
+IFR_API ifr_status ifr_rms_norm(ifr_ctx *ctx, const ifr_rms_norm_config *dev_cfg, float *out, const float *value,
+                                const float *weight, uint32_t n);
+
+/* in_out_a += b.  LlmContext::add_assign (crates/inferi/src/context.rs:516-530). */
+IFR_API ifr_status ifr_add(ifr_ctx *ctx, float *in_out_a, const float *b, uint32_t n);
+
+/* Rotary embedding in place on q[0..q_len) and, for pair starts 2i < cfg.kv_dim,
+ * on k.  cfg is a device pointer (pos is device-resident, as in the
+ * reference).  LlmContext::rope (crates/inferi/src/context.rs:687-704) ->
+ * RoPE::launch (crates/inferi/src/ops/rope.rs:25-95). q_len even. */
+IFR_API ifr_status ifr_rope(ifr_ctx *ctx, int32_t variant, const ifr_rope_config *dev_cfg, float *q,
+                            uint32_t q_len, float *k, uint32_t k_len);
+
+/* in_out_h1 <- h2 * (h1 / (1 + exp(-h1))).  LlmContext::silu
+ * (crates/inferi/src/context.rs:706-719) -> silu shader
+ * (inferi-shaders/src/silu.rs:24-53). */
+IFR_API ifr_status ifr_silu(ifr_ctx *ctx, float *in_out_h1, const float *h2, uint32_t n);
+
+/* Decode attention of one token over the KV cache:
+ * xb[h] = softmax_t((q[h] . k_t[h/kv_mul]) / sqrt(head_size)) . v_t, t in [0, pos].
+ * Caches are [seq_len][kv_dim] row-major, kv_dtype IFR_F32 (the reference's
+ * layout) or IFR_F16.  `params` (host) sizes the launch; `dev_params` is the
+ * device copy the kernel reads.  BatchedMultiqueryAttention::launch
+ * (crates/inferi/src/ops/batched_multiquery_attention.rs:87-110) ->
+ * FusedAttention::launch (:27-76).  head_size in {64, 128}, kv_mul <= 8. */
+IFR_API ifr_status ifr_attention(ifr_ctx *ctx, const ifr_attn_params *params, const ifr_attn_params *dev_params,
+                                 const float *q, const void *key_cache, const void *value_cache, int32_t kv_dtype,
+                                 float *xb);
+
+/* dev_index[0] = index of the largest of v[0..n), lowest index on ties.
+ * Replaces the host-side Sampler::sample_argmax
+ * (crates/inferi/src/models/sampler.rs:54-56) so the logits never leave
+ * the device. */
+IFR_API ifr_status ifr_argmax(ifr_ctx *ctx, const float *v, uint32_t n, uint32_t *dev_index);
+
+/* GGUF blocks from f32 values on the device: the deterministic min/max
+ * quantizer used for the synthetic models (the reference only dequantizes;
+ * crates/inferi/src/quantization.rs:1-426).  dtype Q8_0/Q4_K/Q5_K/Q6_K/F16/F32. */
+IFR_API ifr_status ifr_quantize(ifr_ctx *ctx, void *out_blocks, const float *x, int32_t dtype, uint64_t n_elems);
+
+/* Synthetic weights: out[i] = mean + std * z_i, z_i ~ N(0,1) from a
+ * counter-based generator keyed by (seed, stream), so a tensor is reproducible
+ * from its seed alone. */
+IFR_API ifr_status ifr_fill_normal(ifr_ctx *ctx, float *out, uint64_t n, uint64_t seed, uint64_t stream, float mean,
+                                   float std);
+
+/* ------------------------------------------------------------ llama model */
+
+/* Llama2Config (crates/inferi/src/models/llama2/cpu.rs:78-141) plus the two
+ * choices the reference fixes elsewhere: the KV-cache element type (the
+ * reference uses F32, transformer.rs:85-104) and the RoPE variant
+ * (models/llama2/mod.rs:25-30). */
+typedef struct {
+    uint32_t n_layers, hidden, ffn, n_heads, n_kv_heads, vocab, max_pos;
+    float rope_theta, rms_eps;
+    int32_t kv_dtype;     /* IFR_F16 or IFR_F32 */
+    int32_t rope_variant; /* IFR_ROPE_ORIGINAL (llama) */
+} ifr_llama2_config;
+
+typedef struct ifr_llama2_weights ifr_llama2_weights;
+typedef struct ifr_llama2_state ifr_llama2_state;
+
+/* Llama2Weights (crates/inferi/src/models/llama2/transformer.rs:176-196,
+ * 294-393): a table of device tensors keyed by GGUF name.  The tensors stay
+ * owned by the caller. */
+IFR_API ifr_status ifr_llama2_weights_create(ifr_ctx *ctx, const ifr_llama2_config *cfg, ifr_llama2_weights **out);
+/* Binds one GGUF tensor ("token_embd.weight", "output_norm.weight",
+ * "output.weight", "blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_output,
+ * ffn_norm,ffn_gate,ffn_up,ffn_down}.weight") already in device memory.
+ * rows/cols follow gguf.rs:591-593 (dims reversed: rows = ne1, cols = ne0);
+ * norms are F32 vectors with rows = 1. */
+IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *gguf_name, int32_t dtype,
+                                          const void *dev_data, uint32_t rows, uint32_t cols);
+IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w);
+
+/* Llama2State (crates/inferi/src/models/llama2/transformer.rs:46-137):
+ * activations, logits, the KV cache, the device-resident position counter
+ * and the token sequence.  Owned by the library. */
+IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *ctx, const ifr_llama2_config *cfg, ifr_llama2_state **out);
+IFR_API void ifr_llama2_state_destroy(ifr_llama2_state *s);
+/* Sets the token sequence to `prompt` (forced tokens, chat_llama2.rs:137-160)
+ * and the device position counter to `pos`. */
+IFR_API ifr_status ifr_llama2_state_reset(ifr_llama2_state *s, const uint32_t *prompt, uint32_t n_prompt,
+                                          uint32_t pos);
+
+/* One decode step at the state's device position p: embeds token[p], runs
+ * every layer, the final norm and the output head into the logits, stores
+ * argmax(logits) as token[p+1] unless p+1 is a forced prompt position, and
+ * advances the position.  Llama2::launch
+ * (crates/inferi/src/models/llama2/transformer.rs:409-481) plus the
+ * embedding copy and greedy sampling of ChatLlama2::forward_logits
+ * (crates/inferi-chat/src/chat_llama2.rs:191-255).  `fused` selects the fused
+ * kernels (5 launches per layer) instead of the one-kernel-per-reference-op
+ * sequence (14 per layer). */
+IFR_API ifr_status ifr_llama2_launch(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w, int32_t fused);
+/* n_steps decode steps; with use_graph the step is captured once into a HIP
+ * graph and replayed (the position lives on the device, so one graph serves
+ * every step). */
+IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
+                                       uint32_t n_steps, int32_t use_graph);
+/* Copies tokens[start, start+n) of the sequence to the host (waits). */
+IFR_API ifr_status ifr_llama2_read_tokens(ifr_llama2_state *s, uint32_t *host, uint32_t start, uint32_t n);
+/* Device pointer and size of a state buffer: "x", "logits", "pos", "tokens",
+ * "key_cache" / "value_cache" (of `layer`), "q", "att". */
+IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name, int32_t layer, void **dev_ptr,
+                                           size_t *bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

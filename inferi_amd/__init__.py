@@ -1,0 +1,413 @@
+"""Python mirror of inferi's op/model API over the inferi_hip C ABI.
+
+The product is ``libinferi_hip.so`` (C ABI, include/inferi_hip.h) and the
+gfx950 code object it loads.  This module binds it with ctypes and keeps the
+reference's names and argument order, so a test reads like the reference's:
+
+  LlmContext.rms_norm_assign / matmul_quant_assign / add_assign / rope / silu
+      crates/inferi/src/context.rs:336-719
+  BatchedMultiqueryAttention.launch
+      crates/inferi/src/ops/batched_multiquery_attention.rs:87-110
+  Llama2.launch, Llama2State, Llama2Weights
+      crates/inferi/src/models/llama2/transformer.rs:46-481
+
+There is no CPU fallback: if the library is missing the import of a Context
+raises.  Device memory is owned by ``DeviceBuffer`` objects (ifr_alloc).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libinferi_hip.so")
+HSACO_PATH = os.path.join(HERE, "inferi_kernels.hsaco")
+
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 8, 12, 13, 14
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+ROPE_ORIGINAL, ROPE_NEOX = 0, 1
+
+STATUS = {0: "OK", 1: "EINVAL", 2: "EUNSUPPORTED", 3: "EHIP", 4: "ENOMEM"}
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"inferi_hip {STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+class RmsNormConfig(C.Structure):
+    _fields_ = [("nudge_factor", C.c_float)]
+
+
+class RoPEConfig(C.Structure):
+    _fields_ = [("head_size", C.c_uint32), ("kv_dim", C.c_uint32), ("pos", C.c_uint32), ("base_freq", C.c_float)]
+
+
+class AttentionParams(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("seq_len", "kv_dim", "kv_mul", "n_heads", "head_size", "pos")]
+
+
+class Llama2ConfigC(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("n_layers", "hidden", "ffn", "n_heads", "n_kv_heads", "vocab", "max_pos")] + [
+        ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("kv_dtype", C.c_int32), ("rope_variant", C.c_int32)]
+
+
+# Every symbol include/inferi_hip.h declares, with its ctypes signature.
+_vp, _i32, _u32, _u64, _sz, _f, _cp = C.c_void_p, C.c_int32, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float, C.c_char_p
+SIGNATURES = {
+    "ifr_create": (_i32, [_i32, _cp, C.POINTER(_vp)]),
+    "ifr_destroy": (None, [_vp]),
+    "ifr_last_error": (_cp, [_vp]),
+    "ifr_device_info": (_i32, [_vp, _cp, _sz, C.POINTER(_i32)]),
+    "ifr_set_option": (_i32, [_vp, _cp, C.c_int64]),
+    "ifr_alloc": (_i32, [_vp, _sz, C.POINTER(_vp)]),
+    "ifr_free": (_i32, [_vp, _vp]),
+    "ifr_upload": (_i32, [_vp, _vp, _vp, _sz]),
+    "ifr_download": (_i32, [_vp, _vp, _vp, _sz]),
+    "ifr_memset": (_i32, [_vp, _vp, _i32, _sz]),
+    "ifr_sync": (_i32, [_vp]),
+    "ifr_event_record": (_i32, [_vp, _i32]),
+    "ifr_event_elapsed": (_i32, [_vp, _i32, _i32, C.POINTER(_f)]),
+    "ifr_dequant": (_i32, [_vp, _vp, _vp, _i32, _u64]),
+    "ifr_matmul_quant": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
+    "ifr_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32]),
+    "ifr_add": (_i32, [_vp, _vp, _vp, _u32]),
+    "ifr_rope": (_i32, [_vp, _i32, _vp, _vp, _u32, _vp, _u32]),
+    "ifr_silu": (_i32, [_vp, _vp, _vp, _u32]),
+    "ifr_attention": (_i32, [_vp, C.POINTER(AttentionParams), _vp, _vp, _vp, _vp, _i32, _vp]),
+    "ifr_argmax": (_i32, [_vp, _vp, _u32, _vp]),
+    "ifr_quantize": (_i32, [_vp, _vp, _vp, _i32, _u64]),
+    "ifr_fill_normal": (_i32, [_vp, _vp, _u64, _u64, _u64, _f, _f]),
+    "ifr_llama2_weights_create": (_i32, [_vp, C.POINTER(Llama2ConfigC), C.POINTER(_vp)]),
+    "ifr_llama2_weights_set": (_i32, [_vp, _cp, _i32, _vp, _u32, _u32]),
+    "ifr_llama2_weights_destroy": (None, [_vp]),
+    "ifr_llama2_state_create": (_i32, [_vp, C.POINTER(Llama2ConfigC), C.POINTER(_vp)]),
+    "ifr_llama2_state_destroy": (None, [_vp]),
+    "ifr_llama2_state_reset": (_i32, [_vp, _vp, _u32, _u32]),
+    "ifr_llama2_launch": (_i32, [_vp, _vp, _vp, _i32]),
+    "ifr_llama2_generate": (_i32, [_vp, _vp, _vp, _u32, _i32]),
+    "ifr_llama2_read_tokens": (_i32, [_vp, _vp, _u32, _u32]),
+    "ifr_llama2_state_buffer": (_i32, [_vp, _cp, _i32, C.POINTER(_vp), C.POINTER(_sz)]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Loads libinferi_hip.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    return cols // BLOCK_ELEMS[dtype] * BLOCK_BYTES[dtype]
+
+
+class DeviceBuffer:
+    """A device allocation owned by Python (ifr_alloc / ifr_free)."""
+
+    def __init__(self, ctx: "LlmContext", nbytes: int):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        ctx._check(lib().ifr_alloc(ctx.h, max(self.nbytes, 1), C.byref(p)))
+        self.ptr = p.value
+
+    def free(self) -> None:
+        if self.ptr:
+            self.ctx._check(lib().ifr_free(self.ctx.h, self.ptr))
+            self.ptr = None
+
+    def at(self, byte_offset: int) -> int:
+        return self.ptr + int(byte_offset)
+
+    def upload(self, arr: np.ndarray, byte_offset: int = 0) -> "DeviceBuffer":
+        a = np.ascontiguousarray(arr)
+        assert byte_offset + a.nbytes <= self.nbytes, "upload past the end of the buffer"
+        self.ctx._check(lib().ifr_upload(self.ctx.h, self.at(byte_offset), a.ctypes.data, a.nbytes))
+        return self
+
+    def download(self, dtype=np.float32, count: int | None = None, byte_offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = (self.nbytes - byte_offset) // dt.itemsize if count is None else int(count)
+        out = np.empty(n, dt)
+        self.ctx._check(lib().ifr_download(self.ctx.h, out.ctypes.data, self.at(byte_offset), out.nbytes))
+        return out
+
+
+def _ptr(x) -> int | None:
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    return int(x)
+
+
+class LlmContext:
+    """One device, one stream, one loaded code object (LlmOps + LlmContext,
+    crates/inferi/src/context.rs:58-130)."""
+
+    def __init__(self, device: int = 0, code_object: str | None = None):
+        h = C.c_void_p()
+        st = lib().ifr_create(device, (code_object or HSACO_PATH).encode(), C.byref(h))
+        if st != 0:
+            raise HipError(st, lib().ifr_last_error(None).decode())
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().ifr_destroy(self.h)
+            self.h = None
+
+    def _check(self, st: int) -> None:
+        if st != 0:
+            raise HipError(st, lib().ifr_last_error(self.h).decode())
+
+    # ------------------------------------------------------------ plumbing
+    def device_info(self) -> tuple[str, int]:
+        buf = C.create_string_buffer(256)
+        n = C.c_int32()
+        self._check(lib().ifr_device_info(self.h, buf, 256, C.byref(n)))
+        return buf.value.decode(), n.value
+
+    def set_option(self, key: str, value: int) -> None:
+        self._check(lib().ifr_set_option(self.h, key.encode(), int(value)))
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def upload(self, arr: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(arr)
+        return DeviceBuffer(self, a.nbytes).upload(a)
+
+    def zeros(self, nbytes: int) -> DeviceBuffer:
+        b = DeviceBuffer(self, nbytes)
+        self._check(lib().ifr_memset(self.h, b.ptr, 0, b.nbytes))
+        return b
+
+    def sync(self) -> None:
+        self._check(lib().ifr_sync(self.h))
+
+    def event_record(self, slot: int) -> None:
+        self._check(lib().ifr_event_record(self.h, slot))
+
+    def event_elapsed(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        self._check(lib().ifr_event_elapsed(self.h, a, b, C.byref(ms)))
+        return ms.value
+
+    # ----------------------------------------------------------------- ops
+    def dequant(self, out, blocks, dtype: int, n_elems: int) -> None:
+        self._check(lib().ifr_dequant(self.h, _ptr(out), _ptr(blocks), dtype, n_elems))
+
+    def matmul_quant_assign(self, out, a, dtype: int, rows: int, cols: int, b) -> None:
+        """out = deq(a)[rows x cols] . b (context.rs:441-456)."""
+        self._check(lib().ifr_matmul_quant(self.h, _ptr(out), _ptr(a), dtype, rows, cols, _ptr(b)))
+
+    def rms_norm_assign(self, config, out, value, weight, n: int) -> None:
+        """config: device RmsNormConfig (context.rs:336-353)."""
+        self._check(lib().ifr_rms_norm(self.h, _ptr(config), _ptr(out), _ptr(value), _ptr(weight), n))
+
+    def add_assign(self, in_out_a, b, n: int) -> None:
+        self._check(lib().ifr_add(self.h, _ptr(in_out_a), _ptr(b), n))
+
+    def rope(self, variant: int, config, in_out_q, q_len: int, in_out_k, k_len: int) -> None:
+        """config: device RoPEConfig (context.rs:687-704)."""
+        self._check(lib().ifr_rope(self.h, variant, _ptr(config), _ptr(in_out_q), q_len, _ptr(in_out_k), k_len))
+
+    def silu(self, in_out_h1, in_h2, n: int) -> None:
+        self._check(lib().ifr_silu(self.h, _ptr(in_out_h1), _ptr(in_h2), n))
+
+    def argmax(self, v, n: int, out_index) -> None:
+        self._check(lib().ifr_argmax(self.h, _ptr(v), n, _ptr(out_index)))
+
+    def quantize(self, out, x, dtype: int, n_elems: int) -> None:
+        self._check(lib().ifr_quantize(self.h, _ptr(out), _ptr(x), dtype, n_elems))
+
+    def fill_normal(self, out, n: int, seed: int, stream: int, mean: float, std: float) -> None:
+        self._check(lib().ifr_fill_normal(self.h, _ptr(out), n, seed, stream, mean, std))
+
+
+class BatchedMultiqueryAttention:
+    """crates/inferi/src/ops/batched_multiquery_attention.rs:87-110."""
+
+    @staticmethod
+    def launch(ctxt: LlmContext, params: AttentionParams, params_gpu, q, key_cache, value_cache, kv_dtype: int, xb) -> None:
+        ctxt._check(lib().ifr_attention(ctxt.h, C.byref(params), _ptr(params_gpu), _ptr(q), _ptr(key_cache),
+                                        _ptr(value_cache), kv_dtype, _ptr(xb)))
+
+
+# ---------------------------------------------------------------- model --
+
+@dataclass
+class Llama2Config:
+    """Llama2Config (crates/inferi/src/models/llama2/cpu.rs:78-141)."""
+
+    n_layers: int
+    hidden: int
+    ffn: int
+    n_heads: int
+    n_kv_heads: int
+    vocab: int
+    max_pos: int
+    rope_theta: float = 10000.0
+    rms_eps: float = 1e-6
+    kv_dtype: int = F16
+    rope_variant: int = ROPE_ORIGINAL
+
+    @property
+    def head_size(self) -> int:
+        return self.hidden // self.n_heads
+
+    @property
+    def kv_dim(self) -> int:
+        return self.head_size * self.n_kv_heads
+
+    def c(self) -> Llama2ConfigC:
+        return Llama2ConfigC(self.n_layers, self.hidden, self.ffn, self.n_heads, self.n_kv_heads, self.vocab,
+                             self.max_pos, self.rope_theta, self.rms_eps, self.kv_dtype, self.rope_variant)
+
+    def shapes(self) -> dict:
+        """GGUF tensor name -> (rows, cols) (transformer.rs:294-393)."""
+        h, kv, f = self.hidden, self.kv_dim, self.ffn
+        s = {"token_embd.weight": (self.vocab, h), "output.weight": (self.vocab, h), "output_norm.weight": (1, h)}
+        for l in range(self.n_layers):
+            s.update({f"blk.{l}.attn_norm.weight": (1, h), f"blk.{l}.ffn_norm.weight": (1, h),
+                      f"blk.{l}.attn_q.weight": (h, h), f"blk.{l}.attn_k.weight": (kv, h),
+                      f"blk.{l}.attn_v.weight": (kv, h), f"blk.{l}.attn_output.weight": (h, h),
+                      f"blk.{l}.ffn_gate.weight": (f, h), f"blk.{l}.ffn_up.weight": (f, h),
+                      f"blk.{l}.ffn_down.weight": (h, f)})
+        return s
+
+
+class Llama2Weights:
+    """Table of device tensors keyed by GGUF name; the buffers stay owned by
+    this object (transformer.rs:176-196)."""
+
+    def __init__(self, ctxt: LlmContext, config: Llama2Config):
+        self.ctx = ctxt
+        self.config = config
+        self._cfg = config.c()
+        h = C.c_void_p()
+        ctxt._check(lib().ifr_llama2_weights_create(ctxt.h, C.byref(self._cfg), C.byref(h)))
+        self.h = h.value
+        self.buffers: dict[str, tuple[int, DeviceBuffer, int, int]] = {}
+
+    def set(self, name: str, dtype: int, buf: DeviceBuffer, rows: int, cols: int) -> None:
+        self.ctx._check(lib().ifr_llama2_weights_set(self.h, name.encode(), dtype, buf.ptr, rows, cols))
+        self.buffers[name] = (dtype, buf, rows, cols)
+
+    def set_host(self, name: str, dtype: int, data: np.ndarray, rows: int, cols: int) -> None:
+        self.set(name, dtype, self.ctx.upload(np.ascontiguousarray(data)), rows, cols)
+
+    def download(self, name: str) -> tuple[int, np.ndarray, int, int]:
+        dtype, buf, rows, cols = self.buffers[name]
+        if dtype == F32:
+            return dtype, buf.download(np.float32, rows * cols), rows, cols
+        return dtype, buf.download(np.uint8, rows * row_bytes(dtype, cols)), rows, cols
+
+    def close(self) -> None:
+        if self.h:
+            lib().ifr_llama2_weights_destroy(self.h)
+            self.h = None
+        for _, b, _, _ in self.buffers.values():
+            b.free()
+        self.buffers.clear()
+
+    @classmethod
+    def synthetic(cls, ctxt: LlmContext, config: Llama2Config, seed: int, mat_dtype: int = Q4_K,
+                  head_dtype: int = Q6_K, embd_dtype: int = Q4_K, std: float = 0.02, norm_mean: float = 1.0,
+                  norm_std: float = 0.1) -> "Llama2Weights":
+        """Random-init model made on the device: every matrix ~ N(0, std)
+        quantized with the GGUF quantizer, norms ~ N(norm_mean, norm_std) in
+        F32.  Tensor i (in ``config.shapes()`` order) uses generator stream i."""
+        w = cls(ctxt, config)
+        shapes = config.shapes()
+        biggest = max(r * c for r, c in shapes.values())
+        tmp = ctxt.alloc(biggest * 4)
+        try:
+            for i, (name, (rows, cols)) in enumerate(shapes.items()):
+                n = rows * cols
+                if name.endswith("norm.weight"):
+                    buf = ctxt.alloc(n * 4)
+                    ctxt.fill_normal(buf, n, seed, i, norm_mean, norm_std)
+                    w.set(name, F32, buf, rows, cols)
+                    continue
+                dt = head_dtype if name == "output.weight" else embd_dtype if name == "token_embd.weight" else mat_dtype
+                ctxt.fill_normal(tmp, n, seed, i, 0.0, std)
+                buf = ctxt.alloc(rows * row_bytes(dt, cols))
+                ctxt.quantize(buf, tmp, dt, n)
+                w.set(name, dt, buf, rows, cols)
+            ctxt.sync()
+        finally:
+            tmp.free()
+        return w
+
+
+class Llama2State:
+    """Activations, logits, KV cache, device position and token sequence
+    (transformer.rs:46-137)."""
+
+    def __init__(self, ctxt: LlmContext, config: Llama2Config):
+        self.ctx = ctxt
+        self.config = config
+        self._cfg = config.c()
+        h = C.c_void_p()
+        ctxt._check(lib().ifr_llama2_state_create(ctxt.h, C.byref(self._cfg), C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().ifr_llama2_state_destroy(self.h)
+            self.h = None
+
+    def reset(self, prompt, pos: int = 0) -> None:
+        p = np.ascontiguousarray(np.asarray(prompt, np.uint32))
+        self.ctx._check(lib().ifr_llama2_state_reset(self.h, p.ctypes.data if p.size else None, p.size, pos))
+
+    def buffer(self, name: str, layer: int = 0) -> tuple[int, int]:
+        p = C.c_void_p()
+        n = C.c_size_t()
+        self.ctx._check(lib().ifr_llama2_state_buffer(self.h, name.encode(), layer, C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def read(self, name: str, dtype=np.float32, layer: int = 0) -> np.ndarray:
+        p, n = self.buffer(name, layer)
+        dt = np.dtype(dtype)
+        out = np.empty(n // dt.itemsize, dt)
+        self.ctx._check(lib().ifr_download(self.ctx.h, out.ctypes.data, p, out.nbytes))
+        return out
+
+    def tokens(self, start: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.uint32)
+        self.ctx._check(lib().ifr_llama2_read_tokens(self.h, out.ctypes.data, start, n))
+        return out
+
+
+class Llama2:
+    """Llama2::launch (transformer.rs:409-481) with the device-side token loop
+    of ChatLlama2::forward_logits (chat_llama2.rs:191-255)."""
+
+    @staticmethod
+    def launch(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, fused: bool = True) -> None:
+        ctxt._check(lib().ifr_llama2_launch(ctxt.h, state.h, weights.h, int(fused)))
+
+    @staticmethod
+    def generate(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, n_steps: int,
+                 use_graph: bool = True) -> None:
+        ctxt._check(lib().ifr_llama2_generate(ctxt.h, state.h, weights.h, n_steps, int(use_graph)))

@@ -1,0 +1,70 @@
+"""Builds the inferi_hip product library in-tree.
+
+Two artefacts, both written next to this file:
+  inferi_kernels.hsaco  gfx950 code object of csrc/kernels.hip
+                        (hipcc --genco --offload-arch=gfx950), loaded at run
+                        time with hipModuleLoad;
+  libinferi_hip.so      host library with the C ABI of include/inferi_hip.h
+                        (C++17, links libamdhip64).
+
+Every HIP compile carries ``-Xclang -target-feature -Xclang -packed-fp32-ops``
+so the compiler never emits packed FP32 instructions.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HSACO = os.path.join(HERE, "inferi_kernels.hsaco")
+LIB = os.path.join(HERE, "libinferi_hip.so")
+
+HIP_FLAGS = [
+    "--genco",
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout)
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
+
+
+def build_kernels(out: str = HSACO) -> str:
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    tmp = out + ".tmp"
+    _run([hipcc, *HIP_FLAGS, os.path.join(CSRC, "kernels.hip"), "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build_host(out: str = LIB) -> str:
+    cxx = shutil.which("g++") or "g++"
+    tmp = out + ".tmp"
+    _run([cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-result",
+          "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
+          os.path.join(CSRC, "host.cpp"), f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
+    os.replace(tmp, out)
+    return out
+
+
+def build() -> None:
+    build_kernels()
+    build_host()
+
+
+if __name__ == "__main__":
+    build()
+    print(HSACO)
+    print(LIB)

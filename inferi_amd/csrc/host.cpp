@@ -1,0 +1,1048 @@
+// inferi_hip host library: the C ABI of include/inferi_hip.h over the HIP
+// runtime.  Kernels live in a gfx950 code object loaded with hipModuleLoad
+// and are launched with hipModuleLaunchKernel on the context's stream.
+//
+// The model layer mirrors the reference's Llama2 (crates/inferi/src/models/
+// llama2/transformer.rs): Llama2Weights is a table of caller-owned device
+// tensors, Llama2State owns the activations and the KV cache, and one decode
+// step is Llama2::launch (:409-481) plus the embedding copy and greedy
+// sampling of ChatLlama2::forward_logits (crates/inferi-chat/src/
+// chat_llama2.rs:191-255), with the position, the token sequence and the
+// argmax all on the device.
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/inferi_hip.h"
+#include "kargs.h"
+
+using namespace ifr;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+constexpr uint32_t GEMV_ROWS_PER_WG = 16; // 4 waves x 4 rows (device/gemv.h)
+constexpr uint32_t ATTN_CMAX = 256;       // device/attention.h
+constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
+
+int qk_of(int32_t dt) {
+    switch (dt) {
+    case IFR_F32: case IFR_F16: return 1;
+    case IFR_Q8_0: return 32;
+    case IFR_Q4_K: case IFR_Q5_K: case IFR_Q6_K: return 256;
+    default: return 0;
+    }
+}
+int bytes_of(int32_t dt) {
+    switch (dt) {
+    case IFR_F32: return 4;
+    case IFR_F16: return 2;
+    case IFR_Q8_0: return 34;
+    case IFR_Q4_K: return 144;
+    case IFR_Q5_K: return 176;
+    case IFR_Q6_K: return 210;
+    default: return 0;
+    }
+}
+const char *gemv_fmt_name(int32_t dt) {
+    switch (dt) {
+    case IFR_Q8_0: return "q8_0";
+    case IFR_Q4_K: return "q4_k";
+    case IFR_Q5_K: return "q5_k";
+    case IFR_Q6_K: return "q6_k";
+    default: return nullptr;
+    }
+}
+
+} // namespace
+
+struct ifr_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    std::map<std::string, hipFunction_t> fns;
+    std::string err;
+    char dev_name[256] = {0};
+    int n_cu = 0;
+    hipEvent_t events[16] = {};
+    // scratch for the op-level attention and argmax
+    void *scratch = nullptr;
+    size_t scratch_bytes = 0;
+    uint32_t *attn_counters = nullptr;
+    uint32_t attn_counters_n = 0;
+    // tuning: cap on GEMV workgroups (0 = one per row tile)
+    uint32_t gemv_max_grid = 0;
+
+    ifr_status fail(ifr_status st, const char *fmt, ...) {
+        char buf[1024];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        err = buf;
+        return st;
+    }
+    ifr_status hip(hipError_t e, const char *what) {
+        if (e == hipSuccess) return IFR_OK;
+        return fail(e == hipErrorOutOfMemory ? IFR_ENOMEM : IFR_EHIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    hipFunction_t fn(const std::string &name) {
+        auto it = fns.find(name);
+        if (it != fns.end()) return it->second;
+        hipFunction_t f = nullptr;
+        if (hipModuleGetFunction(&f, module, name.c_str()) != hipSuccess) f = nullptr;
+        fns[name] = f;
+        return f;
+    }
+    template <class A>
+    ifr_status launch(const std::string &name, dim3 grid, dim3 block, uint32_t shmem, const A &args) {
+        hipFunction_t f = fn(name);
+        if (!f) return fail(IFR_EUNSUPPORTED, "kernel %s not in the code object", name.c_str());
+        A copy = args;
+        size_t sz = sizeof(A);
+        void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &copy, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz, HIP_LAUNCH_PARAM_END};
+        return hip(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, stream, nullptr,
+                                         cfg),
+                   name.c_str());
+    }
+    ifr_status ensure_scratch(size_t bytes) {
+        if (bytes <= scratch_bytes) return IFR_OK;
+        if (scratch) {
+            hipStreamSynchronize(stream);
+            hipFree(scratch);
+            scratch = nullptr;
+            scratch_bytes = 0;
+        }
+        ifr_status st = hip(hipMalloc(&scratch, bytes), "hipMalloc(scratch)");
+        if (st) return st;
+        scratch_bytes = bytes;
+        return IFR_OK;
+    }
+    ifr_status ensure_counters(uint32_t n) {
+        if (n <= attn_counters_n) return IFR_OK;
+        if (attn_counters) {
+            hipStreamSynchronize(stream);
+            hipFree(attn_counters);
+            attn_counters = nullptr;
+            attn_counters_n = 0;
+        }
+        ifr_status st = hip(hipMalloc(&attn_counters, n * sizeof(uint32_t)), "hipMalloc(counters)");
+        if (st) return st;
+        st = hip(hipMemset(attn_counters, 0, n * sizeof(uint32_t)), "hipMemset(counters)");
+        if (st) return st;
+        attn_counters_n = n;
+        return IFR_OK;
+    }
+};
+
+// ------------------------------------------------------------------ GEMV --
+
+struct GemvPlan {
+    const char *fmt;
+    uint32_t nb, row_bytes;
+};
+
+static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const void *w, GemvPlan &p) {
+    p.fmt = gemv_fmt_name(dtype);
+    if (!p.fmt) return c->fail(IFR_EUNSUPPORTED, "matmul_quant: dtype %d has no GEMV kernel", dtype);
+    const int qk = qk_of(dtype);
+    if (cols == 0 || cols % (uint32_t)qk) return c->fail(IFR_EINVAL, "matmul_quant: cols %u not a multiple of %d", cols, qk);
+    if ((size_t)cols * 4 + 64 > 65536) return c->fail(IFR_EUNSUPPORTED, "matmul_quant: cols %u > 16368", cols);
+    const uintptr_t need = (dtype == IFR_Q4_K || dtype == IFR_Q5_K) ? 16 : 4;
+    if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "matmul_quant: weights not %u-byte aligned", (unsigned)need);
+    p.nb = cols / (uint32_t)qk;
+    p.row_bytes = p.nb * (uint32_t)bytes_of(dtype);
+    return IFR_OK;
+}
+
+static uint32_t gemv_grid(ifr_ctx *c, uint32_t total_rows, uint32_t cap) {
+    uint32_t ntiles = (total_rows + GEMV_ROWS_PER_WG - 1) / GEMV_ROWS_PER_WG;
+    uint32_t g = ntiles;
+    if (c->gemv_max_grid) g = std::min(g, c->gemv_max_grid);
+    if (cap) g = std::min(g, cap);
+    return std::max(g, 1u);
+}
+
+static ifr_status launch_gemv(ifr_ctx *c, const char *fmt, const char *mode, GemvArgs &a, uint32_t cap = 0,
+                              uint32_t *grid_out = nullptr) {
+    const uint32_t g = gemv_grid(c, a.total_rows, cap);
+    if (grid_out) *grid_out = g;
+    std::string name = std::string("gemv_") + fmt + "_" + mode;
+    return c->launch(name, dim3(g), dim3(256), a.cols * 4, a);
+}
+
+// ------------------------------------------------------------- attention --
+
+static uint32_t attn_splits_for(uint32_t T) {
+    uint32_t s = std::max((T + ATTN_CMAX - 1) / ATTN_CMAX, std::min(T, 64u));
+    return std::max(s, 1u);
+}
+
+static ifr_status launch_attn(ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, int32_t kv_dtype, AttnArgs &a,
+                              uint32_t n_kv_heads) {
+    char name[64];
+    snprintf(name, sizeof name, "attn_%s_h%u_g%u", kv_dtype == IFR_F16 ? "f16" : "f32", head_size, kv_mul);
+    return c->launch(name, dim3(n_kv_heads, a.n_splits), dim3(256), 0, a);
+}
+
+// ----------------------------------------------------------------- model --
+
+struct Tens {
+    int32_t dtype = -1;
+    const uint8_t *data = nullptr;
+    uint32_t rows = 0, cols = 0;
+};
+
+struct LayerW {
+    Tens attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down;
+};
+
+struct ifr_llama2_weights {
+    ifr_ctx *ctx;
+    ifr_llama2_config cfg;
+    Tens token_embd, output_norm, output;
+    std::vector<LayerW> layers;
+};
+
+struct ifr_llama2_state {
+    ifr_ctx *ctx;
+    ifr_llama2_config cfg;
+    uint32_t kv_dim, head_size, kv_mul, n_splits;
+    std::vector<void *> allocs;
+    float *x, *xb, *xb2, *q, *ktmp, *vtmp, *hb, *hb2, *att, *logits;
+    uint32_t *tokens;
+    StepCtl *ctl;
+    ifr_rms_norm_config *rms_cfg;
+    ifr_rope_config *rope_cfg;
+    ifr_attn_params *attn_params;
+    uint64_t *part_keys;
+    float *part_o, *part_ml;
+    uint32_t *counters;
+    float *rope_tab;
+    uint8_t *kcache, *vcache;
+    size_t layer_kv_bytes;
+    // captured decode step
+    hipGraphExec_t graph = nullptr;
+    const ifr_llama2_weights *graph_w = nullptr;
+    int graph_fused = -1;
+};
+
+static ifr_status validate_cfg(ifr_ctx *c, const ifr_llama2_config *cfg) {
+    if (!cfg) return c->fail(IFR_EINVAL, "null config");
+    if (!cfg->n_layers || !cfg->hidden || !cfg->n_heads || !cfg->n_kv_heads || !cfg->vocab || !cfg->max_pos || !cfg->ffn)
+        return c->fail(IFR_EINVAL, "config has a zero dimension");
+    if (cfg->hidden % cfg->n_heads || cfg->n_heads % cfg->n_kv_heads)
+        return c->fail(IFR_EINVAL, "hidden %% n_heads or n_heads %% n_kv_heads != 0");
+    const uint32_t hs = cfg->hidden / cfg->n_heads, kv_mul = cfg->n_heads / cfg->n_kv_heads;
+    if (hs != 64 && hs != 128) return c->fail(IFR_EUNSUPPORTED, "head_size %u (64 or 128 supported)", hs);
+    if (kv_mul != 1 && kv_mul != 2 && kv_mul != 4 && kv_mul != 8)
+        return c->fail(IFR_EUNSUPPORTED, "kv_mul %u (1, 2, 4 or 8 supported)", kv_mul);
+    if (cfg->kv_dtype != IFR_F16 && cfg->kv_dtype != IFR_F32) return c->fail(IFR_EINVAL, "kv_dtype must be F16 or F32");
+    if (cfg->rope_variant != IFR_ROPE_ORIGINAL && cfg->rope_variant != IFR_ROPE_NEOX)
+        return c->fail(IFR_EINVAL, "bad rope_variant");
+    if (cfg->max_pos > ATTN_CMAX * 1024u) return c->fail(IFR_EUNSUPPORTED, "max_pos too large");
+    return IFR_OK;
+}
+
+// Enqueues one decode step.
+static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
+    const ifr_llama2_config &cfg = s->cfg;
+    const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn;
+    ifr_status st;
+
+    {   // x <- token_embd[tokens[pos]]
+        EmbedArgs e{};
+        e.x = s->x;
+        e.table = w->token_embd.data;
+        e.tokens = s->tokens;
+        e.ctl = s->ctl;
+        e.hidden = hidden;
+        e.row_bytes = hidden / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
+        e.fmt = w->token_embd.dtype;
+        if ((st = c->launch("embed_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
+    }
+
+    for (uint32_t l = 0; l < cfg.n_layers; l++) {
+        const LayerW &L = w->layers[l];
+        uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
+        uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
+        const bool fuse_qkv = fused && L.attn_q.dtype == L.attn_k.dtype && L.attn_q.dtype == L.attn_v.dtype &&
+                              cfg.rope_variant == IFR_ROPE_ORIGINAL;
+        const bool fuse_ffn = fused && L.ffn_gate.dtype == L.ffn_up.dtype;
+        GemvPlan p;
+
+        // ---- attention block
+        if (fuse_qkv) {
+            if ((st = check_gemv(c, L.attn_q.dtype, hidden, L.attn_q.data, p))) return st;
+            GemvArgs a{};
+            a.w0 = L.attn_q.data;
+            a.w1 = L.attn_k.data;
+            a.w2 = L.attn_v.data;
+            a.rows0 = hidden;
+            a.rows1 = kv_dim;
+            a.rows2 = kv_dim;
+            a.total_rows = hidden + 2 * kv_dim;
+            a.cols = hidden;
+            a.nb = p.nb;
+            a.row_bytes = p.row_bytes;
+            a.x = s->x;
+            a.gamma = (const float *)L.attn_norm.data;
+            a.eps = cfg.rms_eps;
+            a.rope_tab = s->rope_tab;
+            a.y = s->q;
+            a.k_cache = kc;
+            a.v_cache = vc;
+            a.ctl = s->ctl;
+            a.kv_dim = kv_dim;
+            a.head_size = s->head_size;
+            a.kv_f16 = cfg.kv_dtype == IFR_F16;
+            if ((st = launch_gemv(c, p.fmt, "qkv", a))) return st;
+        } else {
+            EltArgs n{};
+            n.a = s->xb;
+            n.b = s->x;
+            n.w = (const float *)L.attn_norm.data;
+            n.cfg = s->rms_cfg;
+            n.n = hidden;
+            if ((st = c->launch("rms_norm_k", dim3(1), dim3(1024), 0, n))) return st;
+            const Tens *mats[3] = {&L.attn_q, &L.attn_k, &L.attn_v};
+            float *outs[3] = {s->q, s->ktmp, s->vtmp};
+            for (int m = 0; m < 3; m++) {
+                if ((st = check_gemv(c, mats[m]->dtype, hidden, mats[m]->data, p))) return st;
+                GemvArgs a{};
+                a.w0 = mats[m]->data;
+                a.total_rows = mats[m]->rows;
+                a.cols = hidden;
+                a.nb = p.nb;
+                a.row_bytes = p.row_bytes;
+                a.x = s->xb;
+                a.y = outs[m];
+                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
+            }
+            EltArgs r{};
+            r.a = s->q;
+            r.k = s->ktmp;
+            r.cfg = s->rope_cfg;
+            r.n = hidden;
+            r.n2 = kv_dim;
+            r.variant = cfg.rope_variant;
+            if ((st = c->launch("rope_k", dim3((hidden / 2 + 255) / 256), dim3(256), 0, r))) return st;
+            KvStoreArgs kv{};
+            kv.k = s->ktmp;
+            kv.v = s->vtmp;
+            kv.k_cache = kc;
+            kv.v_cache = vc;
+            kv.ctl = s->ctl;
+            kv.kv_dim = kv_dim;
+            kv.kv_f16 = cfg.kv_dtype == IFR_F16;
+            if ((st = c->launch("kv_store_k", dim3((kv_dim + 255) / 256), dim3(256), 0, kv))) return st;
+        }
+        {
+            AttnArgs a{};
+            a.q = s->q;
+            a.k_cache = kc;
+            a.v_cache = vc;
+            a.out = s->att;
+            a.part_o = s->part_o;
+            a.part_ml = s->part_ml;
+            a.counters = s->counters;
+            a.pos = &s->ctl->pos;
+            a.kv_dim = kv_dim;
+            a.n_splits = s->n_splits;
+            a.seq_cap = cfg.max_pos;
+            if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, a, cfg.n_kv_heads))) return st;
+        }
+        if ((st = check_gemv(c, L.attn_output.dtype, hidden, L.attn_output.data, p))) return st;
+        {
+            GemvArgs a{};
+            a.w0 = L.attn_output.data;
+            a.total_rows = hidden;
+            a.cols = hidden;
+            a.nb = p.nb;
+            a.row_bytes = p.row_bytes;
+            a.x = s->att;
+            if (fused) {
+                a.y = s->x; // x += Wo att
+                if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
+            } else {
+                a.y = s->xb2;
+                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
+                EltArgs e{};
+                e.a = s->x;
+                e.b = s->xb2;
+                e.n = hidden;
+                if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
+            }
+        }
+
+        // ---- feed-forward block
+        if (fuse_ffn) {
+            if ((st = check_gemv(c, L.ffn_gate.dtype, hidden, L.ffn_gate.data, p))) return st;
+            GemvArgs a{};
+            a.w0 = L.ffn_gate.data;
+            a.w1 = L.ffn_up.data;
+            a.total_rows = 2 * ffn;
+            a.cols = hidden;
+            a.nb = p.nb;
+            a.row_bytes = p.row_bytes;
+            a.x = s->x;
+            a.gamma = (const float *)L.ffn_norm.data;
+            a.eps = cfg.rms_eps;
+            a.y = s->hb;
+            if ((st = launch_gemv(c, p.fmt, "gateup", a))) return st;
+        } else {
+            EltArgs n{};
+            n.a = s->xb;
+            n.b = s->x;
+            n.w = (const float *)L.ffn_norm.data;
+            n.cfg = s->rms_cfg;
+            n.n = hidden;
+            if ((st = c->launch("rms_norm_k", dim3(1), dim3(1024), 0, n))) return st;
+            const Tens *mats[2] = {&L.ffn_gate, &L.ffn_up};
+            float *outs[2] = {s->hb, s->hb2};
+            for (int m = 0; m < 2; m++) {
+                if ((st = check_gemv(c, mats[m]->dtype, hidden, mats[m]->data, p))) return st;
+                GemvArgs a{};
+                a.w0 = mats[m]->data;
+                a.total_rows = ffn;
+                a.cols = hidden;
+                a.nb = p.nb;
+                a.row_bytes = p.row_bytes;
+                a.x = s->xb;
+                a.y = outs[m];
+                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
+            }
+            EltArgs e{};
+            e.a = s->hb;
+            e.b = s->hb2;
+            e.n = ffn;
+            if ((st = c->launch("silu_k", dim3((ffn + 255) / 256), dim3(256), 0, e))) return st;
+        }
+        if ((st = check_gemv(c, L.ffn_down.dtype, ffn, L.ffn_down.data, p))) return st;
+        {
+            GemvArgs a{};
+            a.w0 = L.ffn_down.data;
+            a.total_rows = hidden;
+            a.cols = ffn;
+            a.nb = p.nb;
+            a.row_bytes = p.row_bytes;
+            a.x = s->hb;
+            if (fused) {
+                a.y = s->x;
+                if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
+            } else {
+                a.y = s->xb2;
+                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
+                EltArgs e{};
+                e.a = s->x;
+                e.b = s->xb2;
+                e.n = hidden;
+                if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
+            }
+        }
+    }
+
+    // ---- final norm, output head, argmax, advance
+    const Tens &out = w->output.data ? w->output : w->token_embd; // transformer.rs:376-382
+    GemvPlan p;
+    if ((st = check_gemv(c, out.dtype, hidden, out.data, p))) return st;
+    uint32_t n_parts = 0;
+    if (fused) {
+        GemvArgs a{};
+        a.w0 = out.data;
+        a.total_rows = cfg.vocab;
+        a.cols = hidden;
+        a.nb = p.nb;
+        a.row_bytes = p.row_bytes;
+        a.x = s->x;
+        a.gamma = (const float *)w->output_norm.data;
+        a.eps = cfg.rms_eps;
+        a.y = s->logits;
+        a.part_keys = s->part_keys;
+        if ((st = launch_gemv(c, p.fmt, "head", a, MAX_PARTS, &n_parts))) return st;
+    } else {
+        EltArgs n{};
+        n.a = s->xb;
+        n.b = s->x;
+        n.w = (const float *)w->output_norm.data;
+        n.cfg = s->rms_cfg;
+        n.n = hidden;
+        if ((st = c->launch("rms_norm_k", dim3(1), dim3(1024), 0, n))) return st;
+        GemvArgs a{};
+        a.w0 = out.data;
+        a.total_rows = cfg.vocab;
+        a.cols = hidden;
+        a.nb = p.nb;
+        a.row_bytes = p.row_bytes;
+        a.x = s->xb;
+        a.y = s->logits;
+        if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
+        ArgmaxArgs m{};
+        m.v = s->logits;
+        m.n = cfg.vocab;
+        m.part_keys = s->part_keys;
+        n_parts = std::min((cfg.vocab + 255) / 256, MAX_PARTS);
+        if ((st = c->launch("argmax_part_k", dim3(n_parts), dim3(256), 0, m))) return st;
+    }
+    ArgmaxArgs m{};
+    m.n_parts = n_parts;
+    m.part_keys = s->part_keys;
+    m.ctl = s->ctl;
+    m.tokens = s->tokens;
+    m.rope_pos = &s->rope_cfg->pos;
+    m.attn_pos = &s->attn_params->pos;
+    return c->launch("argmax_final_k", dim3(1), dim3(1024), 0, m);
+}
+
+// =================================================================== C ABI
+
+extern "C" {
+
+IFR_API ifr_status ifr_create(int32_t device, const char *code_object_path, ifr_ctx **out) {
+    if (!out) return IFR_EINVAL;
+    *out = nullptr;
+    auto *c = new ifr_ctx();
+    c->device = device;
+    auto bail = [&](ifr_status st) {
+        g_create_error = c->err;
+        if (c->module) hipModuleUnload(c->module);
+        if (c->stream) hipStreamDestroy(c->stream);
+        delete c;
+        return st;
+    };
+    ifr_status st;
+    if ((st = c->hip(hipSetDevice(device), "hipSetDevice"))) return bail(st);
+    hipDeviceProp_t prop;
+    if ((st = c->hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties"))) return bail(st);
+    snprintf(c->dev_name, sizeof c->dev_name, "%s (%s)", prop.name, prop.gcnArchName);
+    c->n_cu = prop.multiProcessorCount;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return bail(c->fail(IFR_EUNSUPPORTED, "device %d is %s; this build targets gfx950", device, prop.gcnArchName));
+    // default-priority stream (no priority argument anywhere)
+    if ((st = c->hip(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate"))) return bail(st);
+    std::string path;
+    if (code_object_path && *code_object_path) {
+        path = code_object_path;
+    } else {
+        Dl_info info;
+        if (!dladdr((void *)&ifr_create, &info) || !info.dli_fname)
+            return bail(c->fail(IFR_EINVAL, "cannot locate the library to find inferi_kernels.hsaco"));
+        path = info.dli_fname;
+        size_t slash = path.rfind('/');
+        path = (slash == std::string::npos ? std::string(".") : path.substr(0, slash)) + "/inferi_kernels.hsaco";
+    }
+    if ((st = c->hip(hipModuleLoad(&c->module, path.c_str()), ("hipModuleLoad(" + path + ")").c_str())))
+        return bail(st);
+    for (auto &e : c->events)
+        if ((st = c->hip(hipEventCreate(&e), "hipEventCreate"))) return bail(st);
+    *out = c;
+    return IFR_OK;
+}
+
+IFR_API void ifr_destroy(ifr_ctx *c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    if (c->scratch) hipFree(c->scratch);
+    if (c->attn_counters) hipFree(c->attn_counters);
+    for (auto &e : c->events)
+        if (e) hipEventDestroy(e);
+    if (c->module) hipModuleUnload(c->module);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+IFR_API const char *ifr_last_error(const ifr_ctx *c) { return c ? c->err.c_str() : g_create_error.c_str(); }
+
+IFR_API ifr_status ifr_device_info(ifr_ctx *c, char *name, size_t name_len, int32_t *n_cu) {
+    if (!c) return IFR_EINVAL;
+    if (name && name_len) snprintf(name, name_len, "%s", c->dev_name);
+    if (n_cu) *n_cu = c->n_cu;
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
+    if (!c || !key) return IFR_EINVAL;
+    if (!strcmp(key, "gemv_max_grid")) {
+        c->gemv_max_grid = (uint32_t)std::max<int64_t>(0, value);
+        return IFR_OK;
+    }
+    return c->fail(IFR_EINVAL, "unknown option %s", key);
+}
+
+IFR_API ifr_status ifr_alloc(ifr_ctx *c, size_t bytes, void **p) {
+    if (!c || !p) return IFR_EINVAL;
+    *p = nullptr;
+    return c->hip(hipMalloc(p, std::max<size_t>(bytes, 1)), "hipMalloc");
+}
+
+IFR_API ifr_status ifr_free(ifr_ctx *c, void *p) {
+    if (!c) return IFR_EINVAL;
+    if (!p) return IFR_OK;
+    ifr_status st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (st) return st;
+    return c->hip(hipFree(p), "hipFree");
+}
+
+IFR_API ifr_status ifr_upload(ifr_ctx *c, void *dst, const void *src, size_t n) {
+    if (!c || (!dst && n) || (!src && n)) return IFR_EINVAL;
+    if (!n) return IFR_OK;
+    ifr_status st = c->hip(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+    if (st) return st;
+    return c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+IFR_API ifr_status ifr_download(ifr_ctx *c, void *dst, const void *src, size_t n) {
+    if (!c || (!dst && n) || (!src && n)) return IFR_EINVAL;
+    if (!n) return IFR_OK;
+    ifr_status st = c->hip(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+    if (st) return st;
+    return c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+IFR_API ifr_status ifr_memset(ifr_ctx *c, void *dst, int32_t v, size_t n) {
+    if (!c || (!dst && n)) return IFR_EINVAL;
+    return c->hip(hipMemsetAsync(dst, v, n, c->stream), "hipMemsetAsync");
+}
+
+IFR_API ifr_status ifr_sync(ifr_ctx *c) {
+    if (!c) return IFR_EINVAL;
+    return c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+IFR_API ifr_status ifr_event_record(ifr_ctx *c, int32_t slot) {
+    if (!c || slot < 0 || slot >= 16) return IFR_EINVAL;
+    return c->hip(hipEventRecord(c->events[slot], c->stream), "hipEventRecord");
+}
+
+IFR_API ifr_status ifr_event_elapsed(ifr_ctx *c, int32_t a, int32_t b, float *ms) {
+    if (!c || a < 0 || a >= 16 || b < 0 || b >= 16 || !ms) return IFR_EINVAL;
+    ifr_status st = c->hip(hipEventSynchronize(c->events[b]), "hipEventSynchronize");
+    if (st) return st;
+    return c->hip(hipEventElapsedTime(ms, c->events[a], c->events[b]), "hipEventElapsedTime");
+}
+
+// ------------------------------------------------------------------- ops --
+
+IFR_API ifr_status ifr_dequant(ifr_ctx *c, float *out, const void *blocks, int32_t dtype, uint64_t n) {
+    if (!c) return IFR_EINVAL;
+    const int qk = qk_of(dtype);
+    if (!qk) return c->fail(IFR_EINVAL, "dequant: unknown dtype %d", dtype);
+    if (n % (uint64_t)qk) return c->fail(IFR_EINVAL, "dequant: %llu elements not a multiple of %d", (unsigned long long)n, qk);
+    if (!n) return IFR_OK;
+    if (!out || !blocks) return c->fail(IFR_EINVAL, "dequant: null pointer");
+    if ((uintptr_t)blocks % (dtype == IFR_F32 ? 4 : 2)) return c->fail(IFR_EINVAL, "dequant: misaligned blocks");
+    DequantArgs a{out, (const uint8_t *)blocks, n, dtype, 0};
+    const uint64_t g = std::min<uint64_t>((n + 255) / 256, 65536);
+    return c->launch("dequant_k", dim3((uint32_t)g), dim3(256), 0, a);
+}
+
+IFR_API ifr_status ifr_matmul_quant(ifr_ctx *c, float *out, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
+                                    const float *v) {
+    if (!c) return IFR_EINVAL;
+    if (!out || !w || !v) return c->fail(IFR_EINVAL, "matmul_quant: null pointer");
+    if (!rows) return IFR_OK;
+    if ((uintptr_t)v % 16) return c->fail(IFR_EINVAL, "matmul_quant: v not 16-byte aligned");
+    GemvPlan p;
+    ifr_status st = check_gemv(c, dtype, cols, w, p);
+    if (st) return st;
+    GemvArgs a{};
+    a.w0 = (const uint8_t *)w;
+    a.total_rows = rows;
+    a.cols = cols;
+    a.nb = p.nb;
+    a.row_bytes = p.row_bytes;
+    a.x = v;
+    a.y = out;
+    return launch_gemv(c, p.fmt, "plain", a);
+}
+
+IFR_API ifr_status ifr_rms_norm(ifr_ctx *c, const ifr_rms_norm_config *cfg, float *out, const float *value,
+                                const float *weight, uint32_t n) {
+    if (!c) return IFR_EINVAL;
+    if (!cfg || !out || !value || !weight) return c->fail(IFR_EINVAL, "rms_norm: null pointer");
+    if (!n) return IFR_OK;
+    EltArgs a{};
+    a.a = out;
+    a.b = value;
+    a.w = weight;
+    a.cfg = cfg;
+    a.n = n;
+    return c->launch("rms_norm_k", dim3(1), dim3(1024), 0, a);
+}
+
+IFR_API ifr_status ifr_add(ifr_ctx *c, float *x, const float *b, uint32_t n) {
+    if (!c) return IFR_EINVAL;
+    if (!x || !b) return c->fail(IFR_EINVAL, "add: null pointer");
+    if (!n) return IFR_OK;
+    EltArgs a{};
+    a.a = x;
+    a.b = b;
+    a.n = n;
+    return c->launch("add_k", dim3((n + 255) / 256), dim3(256), 0, a);
+}
+
+IFR_API ifr_status ifr_rope(ifr_ctx *c, int32_t variant, const ifr_rope_config *cfg, float *q, uint32_t q_len, float *k,
+                            uint32_t k_len) {
+    if (!c) return IFR_EINVAL;
+    if (!cfg || !q) return c->fail(IFR_EINVAL, "rope: null pointer");
+    if (variant != IFR_ROPE_ORIGINAL && variant != IFR_ROPE_NEOX) return c->fail(IFR_EINVAL, "rope: bad variant");
+    if (q_len % 2) return c->fail(IFR_EINVAL, "rope: q_len must be even (ops/rope.rs:39-44)");
+    if (k_len % 2) return c->fail(IFR_EINVAL, "rope: k_len must be even");
+    if (k_len && !k) return c->fail(IFR_EINVAL, "rope: null k");
+    if (!q_len) return IFR_OK;
+    EltArgs a{};
+    a.a = q;
+    a.k = k;
+    a.cfg = cfg;
+    a.n = q_len;
+    a.n2 = k_len;
+    a.variant = variant;
+    return c->launch("rope_k", dim3((q_len / 2 + 255) / 256), dim3(256), 0, a);
+}
+
+IFR_API ifr_status ifr_silu(ifr_ctx *c, float *h1, const float *h2, uint32_t n) {
+    if (!c) return IFR_EINVAL;
+    if (!h1 || !h2) return c->fail(IFR_EINVAL, "silu: null pointer");
+    if (!n) return IFR_OK;
+    EltArgs a{};
+    a.a = h1;
+    a.b = h2;
+    a.n = n;
+    return c->launch("silu_k", dim3((n + 255) / 256), dim3(256), 0, a);
+}
+
+IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr_attn_params *dev_p, const float *q,
+                                 const void *kc, const void *vc, int32_t kv_dtype, float *xb) {
+    if (!c) return IFR_EINVAL;
+    if (!p || !dev_p || !q || !kc || !vc || !xb) return c->fail(IFR_EINVAL, "attention: null pointer");
+    if (kv_dtype != IFR_F16 && kv_dtype != IFR_F32) return c->fail(IFR_EINVAL, "attention: kv dtype F16 or F32");
+    if (p->head_size != 64 && p->head_size != 128) return c->fail(IFR_EUNSUPPORTED, "attention: head_size %u", p->head_size);
+    if (!p->kv_mul || p->n_heads % p->kv_mul) return c->fail(IFR_EINVAL, "attention: n_heads %% kv_mul");
+    const uint32_t g = p->kv_mul;
+    if (g != 1 && g != 2 && g != 4 && g != 8) return c->fail(IFR_EUNSUPPORTED, "attention: kv_mul %u", g);
+    const uint32_t n_kv = p->n_heads / g;
+    if (p->kv_dim != n_kv * p->head_size) return c->fail(IFR_EINVAL, "attention: kv_dim != n_kv_heads * head_size");
+    if (p->pos >= p->seq_len) return c->fail(IFR_EINVAL, "attention: pos %u >= seq_len %u", p->pos, p->seq_len);
+    if ((uintptr_t)q % 16 || (uintptr_t)kc % 16 || (uintptr_t)vc % 16)
+        return c->fail(IFR_EINVAL, "attention: q and caches must be 16-byte aligned");
+    const uint32_t T = p->pos + 1, S = attn_splits_for(T);
+    const size_t part_o = (size_t)n_kv * S * g * p->head_size, part_ml = (size_t)n_kv * S * g * 2;
+    ifr_status st = c->ensure_scratch((part_o + part_ml) * sizeof(float));
+    if (st) return st;
+    if ((st = c->ensure_counters(n_kv))) return st;
+    AttnArgs a{};
+    a.q = q;
+    a.k_cache = kc;
+    a.v_cache = vc;
+    a.out = xb;
+    a.part_o = (float *)c->scratch;
+    a.part_ml = (float *)c->scratch + part_o;
+    a.counters = c->attn_counters;
+    a.pos = &dev_p->pos;
+    a.kv_dim = p->kv_dim;
+    a.n_splits = S;
+    a.seq_cap = T;
+    return launch_attn(c, p->head_size, g, kv_dtype, a, n_kv);
+}
+
+IFR_API ifr_status ifr_argmax(ifr_ctx *c, const float *v, uint32_t n, uint32_t *dev_index) {
+    if (!c) return IFR_EINVAL;
+    if (!v || !dev_index) return c->fail(IFR_EINVAL, "argmax: null pointer");
+    if (!n) return c->fail(IFR_EINVAL, "argmax: empty input");
+    ifr_status st = c->ensure_scratch(MAX_PARTS * sizeof(uint64_t));
+    if (st) return st;
+    ArgmaxArgs a{};
+    a.v = v;
+    a.n = n;
+    a.part_keys = (uint64_t *)c->scratch;
+    const uint32_t parts = std::min((n + 255) / 256, MAX_PARTS);
+    if ((st = c->launch("argmax_part_k", dim3(parts), dim3(256), 0, a))) return st;
+    ArgmaxArgs b{};
+    b.n_parts = parts;
+    b.part_keys = (uint64_t *)c->scratch;
+    b.out_index = dev_index;
+    return c->launch("argmax_final_k", dim3(1), dim3(1024), 0, b);
+}
+
+IFR_API ifr_status ifr_quantize(ifr_ctx *c, void *out, const float *x, int32_t dtype, uint64_t n) {
+    if (!c) return IFR_EINVAL;
+    const int qk = qk_of(dtype);
+    if (!qk) return c->fail(IFR_EINVAL, "quantize: unknown dtype %d", dtype);
+    if (n % (uint64_t)qk) return c->fail(IFR_EINVAL, "quantize: n not a multiple of %d", qk);
+    if (!n) return IFR_OK;
+    if (!out || !x) return c->fail(IFR_EINVAL, "quantize: null pointer");
+    QuantArgs a{(uint8_t *)out, x, n / (uint64_t)qk, dtype, 0};
+    const uint64_t g = (a.n_blocks + 63) / 64;
+    if (g > 0x7FFFFFFFull) return c->fail(IFR_EINVAL, "quantize: too many blocks for one launch");
+    return c->launch("quantize_k", dim3((uint32_t)g), dim3(64), 0, a);
+}
+
+IFR_API ifr_status ifr_fill_normal(ifr_ctx *c, float *out, uint64_t n, uint64_t seed, uint64_t stream, float mean,
+                                   float std) {
+    if (!c) return IFR_EINVAL;
+    if (!n) return IFR_OK;
+    if (!out) return c->fail(IFR_EINVAL, "fill_normal: null pointer");
+    FillArgs a{};
+    a.out = out;
+    a.n = n;
+    // key = mix of (seed, stream): distinct streams never share pairs
+    uint64_t z = seed * 0x9E3779B97F4A7C15ull + stream * 0xD1B54A32D192ED03ull + 0x2545F4914F6CDD1Dull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    a.key = z ^ (z >> 31);
+    a.mean = mean;
+    a.std = std;
+    const uint64_t pairs = (n + 1) / 2;
+    const uint32_t g = (uint32_t)std::min<uint64_t>((pairs + 255) / 256, 65536);
+    return c->launch("fill_normal_k", dim3(g), dim3(256), 0, a);
+}
+
+// ----------------------------------------------------------------- model --
+
+IFR_API ifr_status ifr_llama2_weights_create(ifr_ctx *c, const ifr_llama2_config *cfg, ifr_llama2_weights **out) {
+    if (!c || !out) return IFR_EINVAL;
+    *out = nullptr;
+    ifr_status st = validate_cfg(c, cfg);
+    if (st) return st;
+    auto *w = new ifr_llama2_weights();
+    w->ctx = c;
+    w->cfg = *cfg;
+    w->layers.resize(cfg->n_layers);
+    *out = w;
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *name, int32_t dtype, const void *data,
+                                          uint32_t rows, uint32_t cols) {
+    if (!w || !name) return IFR_EINVAL;
+    ifr_ctx *c = w->ctx;
+    const ifr_llama2_config &cfg = w->cfg;
+    if (!data) return c->fail(IFR_EINVAL, "%s: null data", name);
+    if (!qk_of(dtype)) return c->fail(IFR_EINVAL, "%s: unknown dtype %d", name, dtype);
+    const uint32_t kv_dim = cfg.hidden / cfg.n_heads * cfg.n_kv_heads;
+    Tens t{dtype, (const uint8_t *)data, rows, cols};
+    auto want = [&](uint32_t r, uint32_t cc, bool vec) -> ifr_status {
+        if (rows != r || cols != cc) return c->fail(IFR_EINVAL, "%s: shape %ux%u, expected %ux%u", name, rows, cols, r, cc);
+        if (vec && dtype != IFR_F32) return c->fail(IFR_EUNSUPPORTED, "%s: norm weights must be F32", name);
+        if (cc % (uint32_t)qk_of(dtype)) return c->fail(IFR_EINVAL, "%s: cols not a multiple of the block", name);
+        if (!vec && !gemv_fmt_name(dtype) && strcmp(name, "token_embd.weight"))
+            return c->fail(IFR_EUNSUPPORTED, "%s: dtype %d has no GEMV kernel", name, dtype);
+        return IFR_OK;
+    };
+    ifr_status st;
+    if (!strcmp(name, "token_embd.weight")) {
+        if ((st = want(cfg.vocab, cfg.hidden, false))) return st;
+        w->token_embd = t;
+        return IFR_OK;
+    }
+    if (!strcmp(name, "output.weight")) {
+        if ((st = want(cfg.vocab, cfg.hidden, false))) return st;
+        w->output = t;
+        return IFR_OK;
+    }
+    if (!strcmp(name, "output_norm.weight")) {
+        if ((st = want(1, cfg.hidden, true))) return st;
+        w->output_norm = t;
+        return IFR_OK;
+    }
+    unsigned layer = 0;
+    char field[64] = {0};
+    if (sscanf(name, "blk.%u.%63[a-z_].weight", &layer, field) != 2 || layer >= cfg.n_layers)
+        return c->fail(IFR_EINVAL, "unknown tensor name %s", name);
+    LayerW &L = w->layers[layer];
+    const std::string f = field;
+    if (f == "attn_norm") { if ((st = want(1, cfg.hidden, true))) return st; L.attn_norm = t; }
+    else if (f == "ffn_norm") { if ((st = want(1, cfg.hidden, true))) return st; L.ffn_norm = t; }
+    else if (f == "attn_q") { if ((st = want(cfg.hidden, cfg.hidden, false))) return st; L.attn_q = t; }
+    else if (f == "attn_k") { if ((st = want(kv_dim, cfg.hidden, false))) return st; L.attn_k = t; }
+    else if (f == "attn_v") { if ((st = want(kv_dim, cfg.hidden, false))) return st; L.attn_v = t; }
+    else if (f == "attn_output") { if ((st = want(cfg.hidden, cfg.hidden, false))) return st; L.attn_output = t; }
+    else if (f == "ffn_gate") { if ((st = want(cfg.ffn, cfg.hidden, false))) return st; L.ffn_gate = t; }
+    else if (f == "ffn_up") { if ((st = want(cfg.ffn, cfg.hidden, false))) return st; L.ffn_up = t; }
+    else if (f == "ffn_down") { if ((st = want(cfg.hidden, cfg.ffn, false))) return st; L.ffn_down = t; }
+    else return c->fail(IFR_EINVAL, "unknown tensor name %s", name);
+    return IFR_OK;
+}
+
+IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w) { delete w; }
+
+static void state_free(ifr_llama2_state *s) {
+    if (!s) return;
+    hipStreamSynchronize(s->ctx->stream);
+    if (s->graph) hipGraphExecDestroy(s->graph);
+    for (void *p : s->allocs) hipFree(p);
+    delete s;
+}
+
+IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *cfg, ifr_llama2_state **out) {
+    if (!c || !out) return IFR_EINVAL;
+    *out = nullptr;
+    ifr_status st = validate_cfg(c, cfg);
+    if (st) return st;
+    auto *s = new ifr_llama2_state();
+    s->ctx = c;
+    s->cfg = *cfg;
+    s->head_size = cfg->hidden / cfg->n_heads;
+    s->kv_dim = s->head_size * cfg->n_kv_heads;
+    s->kv_mul = cfg->n_heads / cfg->n_kv_heads;
+    s->n_splits = std::max(64u, (cfg->max_pos + ATTN_CMAX - 1) / ATTN_CMAX);
+    auto alloc = [&](size_t bytes, void **p) -> ifr_status {
+        ifr_status e = c->hip(hipMalloc(p, std::max<size_t>(bytes, 16)), "hipMalloc(state)");
+        if (e) return e;
+        s->allocs.push_back(*p);
+        return c->hip(hipMemset(*p, 0, std::max<size_t>(bytes, 16)), "hipMemset(state)");
+    };
+    const size_t H = cfg->hidden, F = cfg->ffn, KV = s->kv_dim;
+    const size_t esz = cfg->kv_dtype == IFR_F16 ? 2 : 4;
+    s->layer_kv_bytes = ((size_t)cfg->max_pos * KV * esz + 255) & ~(size_t)255;
+#define A(ptr, bytes) if ((st = alloc((bytes), (void **)&(ptr)))) { state_free(s); return st; }
+    A(s->x, H * 4) A(s->xb, H * 4) A(s->xb2, H * 4) A(s->q, H * 4) A(s->att, H * 4)
+    A(s->ktmp, KV * 4) A(s->vtmp, KV * 4) A(s->hb, F * 4) A(s->hb2, F * 4)
+    A(s->logits, (size_t)cfg->vocab * 4)
+    A(s->tokens, ((size_t)cfg->max_pos + 1) * 4)
+    A(s->ctl, sizeof(StepCtl)) A(s->rms_cfg, sizeof(ifr_rms_norm_config)) A(s->rope_cfg, sizeof(ifr_rope_config))
+    A(s->attn_params, sizeof(ifr_attn_params))
+    A(s->part_keys, MAX_PARTS * 8)
+    A(s->part_o, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * s->head_size * 4)
+    A(s->part_ml, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * 2 * 4)
+    A(s->counters, (size_t)cfg->n_kv_heads * 4)
+    A(s->rope_tab, (size_t)s->head_size / 2 * 4)
+    A(s->kcache, s->layer_kv_bytes * cfg->n_layers)
+    A(s->vcache, s->layer_kv_bytes * cfg->n_layers)
+#undef A
+    ifr_rms_norm_config rc{cfg->rms_eps};
+    if ((st = c->hip(hipMemcpy(s->rms_cfg, &rc, sizeof rc, hipMemcpyHostToDevice), "hipMemcpy"))) { state_free(s); return st; }
+    {   // theta of pair i: base^(-(2i)/hs), f32 exponent, f64 power rounded once
+        std::vector<float> tab(s->head_size / 2);
+        for (uint32_t i = 0; i < s->head_size / 2; i++)
+            tab[i] = (float)std::pow((double)cfg->rope_theta, (double)(-(float)(2 * i) / (float)s->head_size));
+        if ((st = c->hip(hipMemcpy(s->rope_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice), "hipMemcpy"))) {
+            state_free(s);
+            return st;
+        }
+    }
+    *out = s;
+    return ifr_llama2_state_reset(s, nullptr, 0, 0);
+}
+
+IFR_API void ifr_llama2_state_destroy(ifr_llama2_state *s) { state_free(s); }
+
+IFR_API ifr_status ifr_llama2_state_reset(ifr_llama2_state *s, const uint32_t *prompt, uint32_t n, uint32_t pos) {
+    if (!s) return IFR_EINVAL;
+    ifr_ctx *c = s->ctx;
+    const ifr_llama2_config &cfg = s->cfg;
+    if (n > cfg.max_pos) return c->fail(IFR_EINVAL, "prompt longer than max_pos");
+    if (pos >= cfg.max_pos) return c->fail(IFR_EINVAL, "pos %u >= max_pos %u", pos, cfg.max_pos);
+    for (uint32_t i = 0; i < n; i++)
+        if (prompt[i] >= cfg.vocab) return c->fail(IFR_EINVAL, "prompt token %u out of range", prompt[i]);
+    ifr_status st;
+    if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
+    if (n && (st = c->hip(hipMemcpy(s->tokens, prompt, n * 4, hipMemcpyHostToDevice), "hipMemcpy(tokens)"))) return st;
+    StepCtl ctl{pos, n, cfg.max_pos, 0};
+    ifr_rope_config rope{s->head_size, s->kv_dim, pos, cfg.rope_theta};
+    ifr_attn_params ap{cfg.max_pos, s->kv_dim, s->kv_mul, cfg.n_heads, s->head_size, pos};
+    if ((st = c->hip(hipMemcpy(s->ctl, &ctl, sizeof ctl, hipMemcpyHostToDevice), "hipMemcpy(ctl)"))) return st;
+    if ((st = c->hip(hipMemcpy(s->rope_cfg, &rope, sizeof rope, hipMemcpyHostToDevice), "hipMemcpy(rope)"))) return st;
+    return c->hip(hipMemcpy(s->attn_params, &ap, sizeof ap, hipMemcpyHostToDevice), "hipMemcpy(attn)");
+}
+
+static ifr_status check_weights(ifr_ctx *c, const ifr_llama2_state *s, const ifr_llama2_weights *w) {
+    if (!w) return c->fail(IFR_EINVAL, "null weights");
+    const ifr_llama2_config &a = s->cfg, &b = w->cfg;
+    if (a.n_layers != b.n_layers || a.hidden != b.hidden || a.ffn != b.ffn || a.n_heads != b.n_heads ||
+        a.n_kv_heads != b.n_kv_heads || a.vocab != b.vocab)
+        return c->fail(IFR_EINVAL, "state and weights were made for different configs");
+    if (!w->token_embd.data || !w->output_norm.data) return c->fail(IFR_EINVAL, "token_embd/output_norm not set");
+    for (uint32_t l = 0; l < b.n_layers; l++) {
+        const LayerW &L = w->layers[l];
+        const Tens *all[] = {&L.attn_norm, &L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output,
+                             &L.ffn_norm, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
+        for (const Tens *t : all)
+            if (!t->data) return c->fail(IFR_EINVAL, "layer %u has an unset tensor", l);
+    }
+    const Tens &out = w->output.data ? w->output : w->token_embd;
+    if (!gemv_fmt_name(out.dtype)) return c->fail(IFR_EUNSUPPORTED, "output head dtype %d has no GEMV kernel", out.dtype);
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_launch(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int32_t fused) {
+    if (!c || !s) return IFR_EINVAL;
+    ifr_status st = check_weights(c, s, w);
+    if (st) return st;
+    return enqueue_step(c, s, w, fused);
+}
+
+IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, uint32_t n_steps,
+                                       int32_t use_graph) {
+    if (!c || !s) return IFR_EINVAL;
+    ifr_status st = check_weights(c, s, w);
+    if (st) return st;
+    if (!use_graph) {
+        for (uint32_t i = 0; i < n_steps; i++)
+            if ((st = enqueue_step(c, s, w, 1))) return st;
+        return IFR_OK;
+    }
+    if (!s->graph || s->graph_w != w || s->graph_fused != 1) {
+        if (s->graph) {
+            hipStreamSynchronize(c->stream);
+            hipGraphExecDestroy(s->graph);
+            s->graph = nullptr;
+        }
+        if ((st = c->hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture")))
+            return st;
+        ifr_status est = enqueue_step(c, s, w, 1);
+        hipGraph_t g = nullptr;
+        st = c->hip(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+        if (est) {
+            if (g) hipGraphDestroy(g);
+            return est;
+        }
+        if (st) return st;
+        st = c->hip(hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+        hipGraphDestroy(g);
+        if (st) return st;
+        s->graph_w = w;
+        s->graph_fused = 1;
+    }
+    for (uint32_t i = 0; i < n_steps; i++)
+        if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_read_tokens(ifr_llama2_state *s, uint32_t *host, uint32_t start, uint32_t n) {
+    if (!s || (!host && n)) return IFR_EINVAL;
+    if ((uint64_t)start + n > (uint64_t)s->cfg.max_pos + 1) return s->ctx->fail(IFR_EINVAL, "token range out of bounds");
+    return ifr_download(s->ctx, host, s->tokens + start, (size_t)n * 4);
+}
+
+IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name, int32_t layer, void **p, size_t *bytes) {
+    if (!s || !name || !p) return IFR_EINVAL;
+    const ifr_llama2_config &cfg = s->cfg;
+    size_t b = 0;
+    std::string n = name;
+    if (n == "x") { *p = s->x; b = cfg.hidden * 4; }
+    else if (n == "q") { *p = s->q; b = cfg.hidden * 4; }
+    else if (n == "att") { *p = s->att; b = cfg.hidden * 4; }
+    else if (n == "logits") { *p = s->logits; b = (size_t)cfg.vocab * 4; }
+    else if (n == "pos") { *p = &s->ctl->pos; b = 4; }
+    else if (n == "tokens") { *p = s->tokens; b = ((size_t)cfg.max_pos + 1) * 4; }
+    else if (n == "key_cache" || n == "value_cache") {
+        if (layer < 0 || (uint32_t)layer >= cfg.n_layers) return s->ctx->fail(IFR_EINVAL, "layer out of range");
+        *p = (n == "key_cache" ? s->kcache : s->vcache) + (size_t)layer * s->layer_kv_bytes;
+        b = (size_t)cfg.max_pos * s->kv_dim * (cfg.kv_dtype == IFR_F16 ? 2 : 4);
+    } else return s->ctx->fail(IFR_EINVAL, "unknown state buffer %s", name);
+    if (bytes) *bytes = b;
+    return IFR_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,145 @@
+// Kernel argument blocks shared by the host library and the gfx950 kernels.
+// Each kernel takes one of these structs by value; the host passes it through
+// hipModuleLaunchKernel's argument buffer, so the layout must be identical on
+// both sides (plain C types only).
+#pragma once
+#include <stdint.h>
+
+namespace ifr {
+
+enum Fmt : int32_t { F32 = 0, F16 = 1, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14 };
+
+// GEMV epilogue/prologue modes.
+enum GemvMode : int32_t {
+    GEMV_PLAIN = 0,  // y[r] = W x
+    GEMV_RESID = 1,  // y[r] += W x                       (attention-out / down + residual)
+    GEMV_QKV = 2,    // rmsnorm(x) -> [Wq;Wk;Wv] -> RoPE -> q, k/v cache row pos
+    GEMV_GATEUP = 3, // rmsnorm(x) -> [Wgate;Wup] interleaved -> h = silu(g) * u
+    GEMV_HEAD = 4,   // rmsnorm(x) -> logits = W x, per-workgroup argmax keys
+};
+
+// Device copies of the C ABI's op configs (same layout as ifr_rms_norm_config
+// and ifr_rope_config in include/inferi_hip.h).
+struct ifr_rms_cfg_dev {
+    float nudge_factor;
+};
+struct ifr_rope_cfg_dev {
+    uint32_t head_size, kv_dim, pos;
+    float base_freq;
+};
+
+// Device-side control block of a decode state: the position and the number
+// of forced (prompt) tokens.
+struct StepCtl {
+    uint32_t pos;
+    uint32_t n_forced;
+    uint32_t max_pos;
+    uint32_t pad;
+};
+
+struct GemvArgs {
+    const uint8_t *w0, *w1, *w2; // matrices: PLAIN/RESID/HEAD w0; QKV q,k,v; GATEUP gate,up
+    uint32_t rows0, rows1, rows2; // rows of each matrix
+    uint32_t total_rows;          // virtual rows covered by the launch
+    uint32_t cols;                // K
+    uint32_t nb;                  // blocks per row
+    uint32_t row_bytes;           // bytes per row
+    uint32_t pad0;
+    const float *x;      // input vector [cols]
+    const float *gamma;  // RMSNorm weight [cols] (QKV, GATEUP, HEAD)
+    float eps;           // RMSNorm epsilon
+    uint32_t pad2;
+    const float *rope_tab; // QKV: theta of each pair within a head [head_size/2]
+    float *y;            // PLAIN/RESID/HEAD: out[rows]; QKV: q; GATEUP: h
+    void *k_cache;       // QKV: cache base of this layer, [max_pos][kv_dim]
+    void *v_cache;
+    const StepCtl *ctl;  // QKV: position
+    uint32_t kv_dim, head_size;
+    int32_t kv_f16;      // QKV: cache element type
+    uint32_t pad1;
+    uint64_t *part_keys; // HEAD: one argmax key per workgroup (may be null)
+};
+
+struct AttnArgs {
+    const float *q;           // [n_heads * head_size]
+    const void *k_cache;      // [seq_len][kv_dim]
+    const void *v_cache;
+    float *out;               // [n_heads * head_size]
+    float *part_o;            // [n_kv_heads][n_splits][kv_mul][head_size]
+    float *part_ml;           // [n_kv_heads][n_splits][kv_mul][2]
+    uint32_t *counters;       // [n_kv_heads], zero between launches
+    const uint32_t *pos;      // device position
+    uint32_t kv_dim;
+    uint32_t n_splits;        // gridDim.y
+    uint32_t seq_cap;         // positions attended never exceed this (cache rows)
+    uint32_t pad;
+};
+
+struct EltArgs {
+    float *a;
+    const float *b;
+    const float *w;
+    const void *cfg; // op-specific device config
+    float *k;
+    uint32_t n, n2;
+    int32_t variant;
+    uint32_t pad;
+};
+
+struct DequantArgs {
+    float *out;
+    const uint8_t *blocks;
+    uint64_t n_elems;
+    int32_t fmt;
+    uint32_t pad;
+};
+
+struct QuantArgs {
+    uint8_t *out;
+    const float *x;
+    uint64_t n_blocks;
+    int32_t fmt;
+    uint32_t pad;
+};
+
+struct FillArgs {
+    float *out;
+    uint64_t n;
+    uint64_t key;
+    float mean, std;
+};
+
+struct ArgmaxArgs {
+    const float *v;
+    uint32_t n;
+    uint32_t n_parts;
+    uint64_t *part_keys;
+    uint32_t *out_index;
+    StepCtl *ctl;        // step_end: advance the position
+    uint32_t *tokens;    // step_end: token sequence
+    uint32_t *rope_pos;  // step_end: pos field of the state's RoPE config (may be null)
+    uint32_t *attn_pos;  // step_end: pos field of the state's attention params (may be null)
+};
+
+struct EmbedArgs {
+    float *x;
+    const uint8_t *table;
+    const uint32_t *tokens;
+    const StepCtl *ctl;
+    uint32_t hidden;
+    uint32_t row_bytes;
+    int32_t fmt;
+    uint32_t pad;
+};
+
+struct KvStoreArgs {
+    const float *k;
+    const float *v;
+    void *k_cache;
+    void *v_cache;
+    const StepCtl *ctl;
+    uint32_t kv_dim;
+    int32_t kv_f16;
+};
+
+} // namespace ifr

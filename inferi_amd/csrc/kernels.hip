@@ -1,0 +1,53 @@
+// gfx950 kernels of inferi_hip, compiled into one code object
+// (hipcc --genco --offload-arch=gfx950) that the host library loads with
+// hipModuleLoad and launches with hipModuleLaunchKernel.  Every kernel takes
+// one argument struct (csrc/kargs.h) by value.
+#include "device/attention.h"
+#include "device/elementwise.h"
+#include "device/gemv.h"
+
+using namespace ifr;
+
+#define GEMV_KERNEL(NAME, FMT, MODE) \
+    extern "C" __global__ void __launch_bounds__(256) NAME(GemvArgs a) { gemv_body<FMT, MODE>(a); }
+
+#define GEMV_ALL_MODES(FMTNAME, FMT)                            \
+    GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)       \
+    GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID)       \
+    GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)           \
+    GEMV_KERNEL(gemv_##FMTNAME##_gateup, FMT, GEMV_GATEUP)     \
+    GEMV_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD)
+
+GEMV_ALL_MODES(q4_k, Q4_K)
+GEMV_ALL_MODES(q5_k, Q5_K)
+GEMV_ALL_MODES(q6_k, Q6_K)
+GEMV_ALL_MODES(q8_0, Q8_0)
+
+#define ATTN_KERNEL(HS, G)                                                                          \
+    extern "C" __global__ void __launch_bounds__(256) attn_f16_h##HS##_g##G(AttnArgs a) {           \
+        attn_body<HS, G, true>(a);                                                                  \
+    }                                                                                               \
+    extern "C" __global__ void __launch_bounds__(256) attn_f32_h##HS##_g##G(AttnArgs a) {           \
+        attn_body<HS, G, false>(a);                                                                 \
+    }
+
+ATTN_KERNEL(64, 1)
+ATTN_KERNEL(64, 2)
+ATTN_KERNEL(64, 4)
+ATTN_KERNEL(64, 8)
+ATTN_KERNEL(128, 1)
+ATTN_KERNEL(128, 2)
+ATTN_KERNEL(128, 4)
+ATTN_KERNEL(128, 8)
+
+extern "C" __global__ void __launch_bounds__(1024) rms_norm_k(EltArgs a) { rms_norm_body(a); }
+extern "C" __global__ void __launch_bounds__(256) rope_k(EltArgs a) { rope_body(a); }
+extern "C" __global__ void __launch_bounds__(256) silu_k(EltArgs a) { silu_body(a); }
+extern "C" __global__ void __launch_bounds__(256) add_k(EltArgs a) { add_body(a); }
+extern "C" __global__ void __launch_bounds__(256) argmax_part_k(ArgmaxArgs a) { argmax_part_body(a); }
+extern "C" __global__ void __launch_bounds__(1024) argmax_final_k(ArgmaxArgs a) { argmax_final_body(a); }
+extern "C" __global__ void __launch_bounds__(256) embed_k(EmbedArgs a) { embed_body(a); }
+extern "C" __global__ void __launch_bounds__(256) kv_store_k(KvStoreArgs a) { kv_store_body(a); }
+extern "C" __global__ void __launch_bounds__(256) dequant_k(DequantArgs a) { dequant_body(a); }
+extern "C" __global__ void __launch_bounds__(64) quantize_k(QuantArgs a) { quantize_body(a); }
+extern "C" __global__ void __launch_bounds__(256) fill_normal_k(FillArgs a) { fill_normal_body(a); }

@@ -211,7 +211,9 @@ int ifo_dequant(int dtype, const void *data, size_t n_elems, float *y) {
  * is our own deterministic min/max quantizer, written so that a GPU port of it
  * produces the same bytes: every step is a single correctly rounded IEEE
  * operation (division, multiply, add) or exact (min, max, integer), rounding
- * to integers uses round-half-even (rintf), and no FMA contraction.
+ * to integers clamps to the code range in float and then rounds half to even
+ * (rintf), comparisons are explicit (no fminf/fmaxf, so signed zeros resolve
+ * the same everywhere), and there is no FMA contraction.
  *
  *   Q8_0: d = amax/127; q = clamp(rint(x * (1/d)), -127, 127).
  *   Q4_K: per 32-element sub-block j, lo_j = min(0, min x), hi_j = max x,
@@ -225,19 +227,22 @@ int ifo_dequant(int dtype, const void *data, size_t n_elems, float *y) {
  *         sc_j = clamp(rint(s_j/d'), 0, 127);
  *         q = clamp(rint(x/(d'*sc_j)), -32, 31) + 32.
  */
-static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+static inline float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+/* clamp in the float domain first, then round half to even: defined for every
+ * finite input and identical to rounding first and clamping after. */
+static inline int qround(float v, float lo, float hi) { return (int)rintf(clampf(v, lo, hi)); }
 
 static void quant_q8_0(const float *x, uint8_t *blk) {
     float amax = 0.0f;
-    for (int l = 0; l < 32; l++) amax = fmaxf(amax, fabsf(x[l]));
+    for (int l = 0; l < 32; l++) {
+        float a = fabsf(x[l]);
+        amax = a > amax ? a : amax;
+    }
     float d = amax / 127.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;
     uint16_t dh = ifo_encode_f16(d);
     wr16(blk, dh);
-    for (int l = 0; l < 32; l++) {
-        float v = x[l] * id;
-        blk[2 + l] = (uint8_t)(int8_t)clampi((int)rintf(v), -127, 127);
-    }
+    for (int l = 0; l < 32; l++) blk[2 + l] = (uint8_t)(int8_t)qround(x[l] * id, -127.0f, 127.0f);
 }
 
 /* Pack 8 six-bit scales and mins into the 12-byte K-quant layout read by
@@ -258,21 +263,22 @@ static void quant_k_minmax(const float *x, int levels, uint8_t *hdr, uint8_t *q)
     for (int j = 0; j < 8; j++) {
         float lo = 0.0f, hi = -INFINITY;
         for (int l = 0; l < 32; l++) {
-            lo = fminf(lo, x[32 * j + l]);
-            hi = fmaxf(hi, x[32 * j + l]);
+            float v = x[32 * j + l];
+            lo = v < lo ? v : lo;
+            hi = v > hi ? v : hi;
         }
         if (hi < lo) hi = lo;
         s[j] = (hi - lo) / (float)levels;
         n[j] = -lo;
-        smax = fmaxf(smax, s[j]);
-        nmax = fmaxf(nmax, n[j]);
+        smax = s[j] > smax ? s[j] : smax;
+        nmax = n[j] > nmax ? n[j] : nmax;
     }
     uint16_t dh = ifo_encode_f16(smax / 63.0f), mh = ifo_encode_f16(nmax / 63.0f);
     float d = ifo_decode_f16(dh), dmin = ifo_decode_f16(mh);
     uint8_t sc[8], mn[8];
     for (int j = 0; j < 8; j++) {
-        sc[j] = (uint8_t)(d > 0.0f ? clampi((int)rintf(s[j] / d), 0, 63) : 0);
-        mn[j] = (uint8_t)(dmin > 0.0f ? clampi((int)rintf(n[j] / dmin), 0, 63) : 0);
+        sc[j] = (uint8_t)(d > 0.0f ? qround(s[j] / d, 0.0f, 63.0f) : 0);
+        mn[j] = (uint8_t)(dmin > 0.0f ? qround(n[j] / dmin, 0.0f, 63.0f) : 0);
     }
     wr16(hdr, dh);
     wr16(hdr + 2, mh);
@@ -281,7 +287,7 @@ static void quant_k_minmax(const float *x, int levels, uint8_t *hdr, uint8_t *q)
         float es = d * (float)sc[j], em = dmin * (float)mn[j];
         for (int l = 0; l < 32; l++) {
             int v = 0;
-            if (es > 0.0f) v = clampi((int)rintf((x[32 * j + l] + em) / es), 0, levels);
+            if (es > 0.0f) v = qround((x[32 * j + l] + em) / es, 0.0f, (float)levels);
             q[32 * j + l] = (uint8_t)v;
         }
     }
@@ -314,20 +320,23 @@ static void quant_q6_k(const float *x, uint8_t *blk) {
     float s[16], smax = 0.0f;
     for (int j = 0; j < 16; j++) {
         float amax = 0.0f;
-        for (int l = 0; l < 16; l++) amax = fmaxf(amax, fabsf(x[16 * j + l]));
+        for (int l = 0; l < 16; l++) {
+            float a = fabsf(x[16 * j + l]);
+            amax = a > amax ? a : amax;
+        }
         s[j] = amax / 31.0f;
-        smax = fmaxf(smax, s[j]);
+        smax = s[j] > smax ? s[j] : smax;
     }
     uint16_t dh = ifo_encode_f16(smax / 127.0f);
     float d = ifo_decode_f16(dh);
     int8_t sc[16];
     uint8_t u[QK_K];
     for (int j = 0; j < 16; j++) {
-        sc[j] = (int8_t)(d > 0.0f ? clampi((int)rintf(s[j] / d), 0, 127) : 0);
+        sc[j] = (int8_t)(d > 0.0f ? qround(s[j] / d, 0.0f, 127.0f) : 0);
         float es = d * (float)sc[j];
         for (int l = 0; l < 16; l++) {
             int v = 0;
-            if (es > 0.0f) v = clampi((int)rintf(x[16 * j + l] / es), -32, 31);
+            if (es > 0.0f) v = qround(x[16 * j + l] / es, -32.0f, 31.0f);
             u[16 * j + l] = (uint8_t)(v + 32);
         }
     }
@@ -441,14 +450,16 @@ void ifo_rms_norm(float *out, const float *x, const float *w, int n, float eps) 
 }
 
 /* inferi-shaders/src/rope.rs:51-92 (Original) and :97-141 (NeoX).  theta and
- * the angle are f32 values, as the shader computes them
- * (theta = base^(-((2i) mod hs)/hs), angle = (f32)pos * theta); the rotation
+ * the angle are f32 values, as the shader computes them: the exponent
+ * -((2i) mod hs)/hs is an f32 division, theta = base^exponent rounded to f32
+ * (evaluated in f64, so it is the correctly rounded f32 power, where the
+ * shader's powf may be off by an ulp), angle = (f32)pos * theta; the rotation
  * itself is evaluated in f64 and rounded once. */
 void ifo_rope(int neox, float *q, int q_len, float *k, int k_len, int head_size,
               int pos, float base_freq) {
     for (int i = 0; i < q_len / 2; i++) {
         float head_dim = (float)((i * 2) % head_size);
-        float theta = powf(base_freq, -head_dim / (float)head_size);
+        float theta = (float)pow((double)base_freq, (double)(-head_dim / (float)head_size));
         float m_theta = (float)pos * theta;
         double c = cos((double)m_theta), s = sin((double)m_theta);
         int iq, shift;

@@ -27,6 +27,6 @@ def ctx():
     """One HIP context (device 0) shared by every GPU test in the session."""
     import inferi_amd
 
-    c = inferi_amd.Context(0)
+    c = inferi_amd.LlmContext(0)
     yield c
     c.close()
