@@ -55,8 +55,9 @@ def decode_token_bytes(cfg: I.Llama2Config, ctx_len: float, mat=I.Q4_K, head=I.Q
 
 
 def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, seed: int = 0) -> dict:
-    """Average launch time of the op-level GEMV over `iters` launches,
-    rotating through enough weight copies to defeat the MALL."""
+    """Average launch time of the GEMV kernel the decode step uses
+    (ifr_matmul_quant_xq on a pre-quantized x) over `iters` back-to-back
+    launches, rotating through enough weight copies to defeat the MALL."""
     n = rows * cols
     wbytes = rows * I.row_bytes(dtype, cols)
     copies = max(2, -(-ROT_BYTES // wbytes))
@@ -69,18 +70,21 @@ def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, s
         ws.append(b)
     tmp.free()
     x = ctx.upload(np.random.default_rng(seed).standard_normal(cols).astype(np.float32))
+    xq = ctx.alloc(I.LlmContext.activation_bytes(cols))
+    ctx.quantize_activation(xq, x, cols)  # once: the decode step's GEMVs get x quantized by its producer
     y = ctx.alloc(rows * 4)
     for i in range(copies):  # warm-up
-        ctx.matmul_quant_assign(y, ws[i], dtype, rows, cols, x)
+        ctx.matmul_quant_xq(y, ws[i], dtype, rows, cols, xq)
     ctx.sync()
     ctx.event_record(2)
     for i in range(iters):
-        ctx.matmul_quant_assign(y, ws[i % copies], dtype, rows, cols, x)
+        ctx.matmul_quant_xq(y, ws[i % copies], dtype, rows, cols, xq)
     ctx.event_record(3)
     ms = ctx.event_elapsed(2, 3)
     for b in ws:
         b.free()
     x.free()
+    xq.free()
     y.free()
     us = ms * 1000.0 / iters
     nbytes = gemv_bytes(dtype, rows, cols)
@@ -130,15 +134,15 @@ def run_decode(args) -> None:
     done = 0
     while done < prompt_len - 1:  # prefill: sequential decode of the prompt (untimed)
         n = min(chunk, prompt_len - 1 - done)
-        I.Llama2.generate(ctx, s, w, n, use_graph=True)
+        I.Llama2.generate(ctx, s, w, n, use_graph=not args.no_graph)
         ctx.sync()
         done += n
         log(f"bench: prefill {done}/{prompt_len - 1} tokens ({time.perf_counter() - t0:.1f}s)")
-    I.Llama2.generate(ctx, s, w, args.warmup, use_graph=True)
+    I.Llama2.generate(ctx, s, w, args.warmup, use_graph=not args.no_graph)
     ctx.sync()
     pos0 = int(s.read("pos", np.uint32)[0])
     ctx.event_record(0)
-    I.Llama2.generate(ctx, s, w, args.steps, use_graph=True)
+    I.Llama2.generate(ctx, s, w, args.steps, use_graph=not args.no_graph)
     ctx.event_record(1)
     ms = ctx.event_elapsed(0, 1)
     ctx.sync()
@@ -151,7 +155,7 @@ def run_decode(args) -> None:
     toks = s.tokens(pos0, args.steps + 1)
     assert np.all(toks < cfg.vocab)
 
-    # the dominant kernel: Q4_K GEMV, measured on the op-level kernel at the
+    # the dominant kernel: Q4_K GEMV, measured on its plain form at the
     # 14336x4096 shape of the FFN projections
     g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
     log(f"bench: gemv_q4_k_plain 14336x4096: {g['us']:.2f} us/launch, {g['gbs']:.0f} GB/s")
@@ -274,6 +278,7 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=2000)
     ap.add_argument("--gemv-iters", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch the decode step's kernels directly")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")

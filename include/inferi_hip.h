@@ -79,8 +79,11 @@ IFR_API const char *ifr_last_error(const ifr_ctx *ctx);
 /* Device name and compute-unit count, for reports. */
 IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, int32_t *n_cu);
 
-/* Tuning knobs (no reference counterpart): "gemv_max_grid" caps the number of
- * GEMV workgroups (0 = one per 16-row tile, the default). */
+/* Knobs (no reference counterpart): "gemv_max_grid" caps the number of GEMV
+ * workgroups (0 = one per 16-row tile, the default); "gemv_exact" = 1 makes
+ * every GEMV keep x in fp32 and use fp32 FMAs, instead of the default path
+ * that takes x as 22-bit fixed point per 16 elements and multiplies with
+ * int8 dot products (see ifr_quantize_activation). */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */
@@ -117,10 +120,28 @@ IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int
  * stores them.  Replaces LlmContext::matmul_quant_assign
  * (crates/inferi/src/context.rs:441-456) -> GemvQuant::launch
  * (crates/inferi/src/ops/gemv_quant.rs:183-340).
- * Requirements: cols % QK == 0, cols <= 16384; W 16-byte aligned for Q4_K
+ * The product runs on the integer path (see ifr_quantize_activation) unless
+ * the "gemv_exact" option is set.
+ * Requirements: cols % QK == 0, cols <= 16320; W 16-byte aligned for Q4_K
  * and Q5_K, 4-byte aligned for Q6_K and Q8_0 (GGUF data is 32-aligned). */
 IFR_API ifr_status ifr_matmul_quant(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
                                     uint32_t cols, const float *v);
+
+/* Activation pre-quantization (no reference counterpart: the reference
+ * multiplies f32 vectors).  A caller that multiplies several matrices by the
+ * same vector quantizes it once into `xq` (ifr_activation_bytes(n) bytes,
+ * 16-byte aligned): 16-value groups of 22-bit fixed point held as three int8
+ * digit planes, x rounded by at most max|x| of its group * 2.4e-7 (about
+ * the rounding of an f32 significand at the group's largest value); x is multiplied
+ * by gamma first when gamma is not NULL, and ss_out (when not NULL) receives
+ * ceil(n/256) partial sums of x^2.  ifr_matmul_quant_xq is then
+ * ifr_matmul_quant on the quantized vector (the kernel the decode step uses);
+ * ifr_matmul_quant itself quantizes v and calls it.  n, cols: multiples of 32. */
+IFR_API uint64_t ifr_activation_bytes(uint32_t n);
+IFR_API ifr_status ifr_quantize_activation(ifr_ctx *ctx, void *xq, const float *x, const float *gamma, uint32_t n,
+                                           float *ss_out);
+IFR_API ifr_status ifr_matmul_quant_xq(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
+                                       uint32_t cols, const void *xq);
 
 /* out = (value * (1/sqrt(sum(value^2)/n + cfg.nudge_factor))) * weight, with
  * cfg a device pointer.  LlmContext::rms_norm_assign

@@ -76,6 +76,9 @@ SIGNATURES = {
     "ifr_event_elapsed": (_i32, [_vp, _i32, _i32, C.POINTER(_f)]),
     "ifr_dequant": (_i32, [_vp, _vp, _vp, _i32, _u64]),
     "ifr_matmul_quant": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
+    "ifr_activation_bytes": (_u64, [_u32]),
+    "ifr_quantize_activation": (_i32, [_vp, _vp, _vp, _vp, _u32, _vp]),
+    "ifr_matmul_quant_xq": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
     "ifr_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32]),
     "ifr_add": (_i32, [_vp, _vp, _vp, _u32]),
     "ifr_rope": (_i32, [_vp, _i32, _vp, _vp, _u32, _vp, _u32]),
@@ -218,6 +221,17 @@ class LlmContext:
     def matmul_quant_assign(self, out, a, dtype: int, rows: int, cols: int, b) -> None:
         """out = deq(a)[rows x cols] . b (context.rs:441-456)."""
         self._check(lib().ifr_matmul_quant(self.h, _ptr(out), _ptr(a), dtype, rows, cols, _ptr(b)))
+
+    def quantize_activation(self, xq, x, n: int, gamma=None, ss_out=None) -> None:
+        """x (times gamma) -> the GEMV's quantized activation layout."""
+        self._check(lib().ifr_quantize_activation(self.h, _ptr(xq), _ptr(x), _ptr(gamma), n, _ptr(ss_out)))
+
+    def matmul_quant_xq(self, out, a, dtype: int, rows: int, cols: int, xq) -> None:
+        self._check(lib().ifr_matmul_quant_xq(self.h, _ptr(out), _ptr(a), dtype, rows, cols, _ptr(xq)))
+
+    @staticmethod
+    def activation_bytes(n: int) -> int:
+        return int(lib().ifr_activation_bytes(n))
 
     def rms_norm_assign(self, config, out, value, weight, n: int) -> None:
         """config: device RmsNormConfig (context.rs:336-353)."""

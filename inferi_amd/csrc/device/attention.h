@@ -9,17 +9,21 @@
 // position (and a captured graph can be replayed).
 //
 // Per workgroup: scores q.k_t / sqrt(hs) for the chunk into LDS, chunk max m
-// and l = sum exp(s - m), o = sum exp(s - m) v_t.  The partial (m, l, o) goes
-// to global memory; the last workgroup of a KV head to finish (counted with an
-// atomic, fenced) merges the partials: out = sum_s e^(m_s-M) o_s /
-// sum_s e^(m_s-M) l_s, and resets the counter.
+// and l = sum exp(s - m), o = sum exp(s - m) v_t; the partial (m, l, o) goes
+// to global memory.  A second, small kernel (attn_merge_body) combines the
+// partials of each query head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
+// The kernel boundary orders the two: merging inside the first kernel would
+// need device-scope fences, which on this chip write back and invalidate the
+// whole L2 of the XCD for every workgroup.
 #pragma once
-#include "common.h"
+#include "gemv.h"
 
 namespace ifr {
 
 constexpr int ATTN_THREADS = 256;
 constexpr int ATTN_CMAX = 256; // longest chunk a workgroup accepts
+constexpr int ATTN_CMIN = 64;  // shortest chunk a split is given (unless T is shorter)
+constexpr int ATTN_MERGE_MAX = 256;  // most splits one KV head may have
 constexpr int ATTN_UNROLL = 8; // rows per thread loaded before use
 
 template <bool F16>
@@ -54,14 +58,14 @@ __device__ void attn_body(const AttnArgs &a) {
     __shared__ float sc[G][ATTN_CMAX];
     __shared__ float ml[G][2];
     __shared__ float red[4][TPP][8 * G];
-    __shared__ int last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = blockIdx.x, s = blockIdx.y, S = a.n_splits;
     const uint32_t T = min(*a.pos + 1, a.seq_cap);
-    // the host sizes n_splits so that C <= ATTN_CMAX; the min keeps LDS in
-    // bounds whatever the device position holds
-    const uint32_t C = min((T + S - 1) / S, (uint32_t)ATTN_CMAX);
+    // chunk: at least ATTN_CMIN positions (short contexts use few splits, so
+    // the merge reads few partials); the host sizes n_splits so that the
+    // chunk never exceeds ATTN_CMAX, the min keeps LDS in bounds regardless
+    const uint32_t C = min(max((T + S - 1) / S, (uint32_t)ATTN_CMIN), (uint32_t)ATTN_CMAX);
     const uint32_t n_act = (T + C - 1) / C;
     const uint32_t t0 = s * C;
     if (t0 >= T) return;
@@ -209,31 +213,71 @@ __device__ void attn_body(const AttnArgs &a) {
         a.part_ml[(pidx + tid) * 2] = ml[tid][0];
         a.part_ml[(pidx + tid) * 2 + 1] = ml[tid][1];
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.counters[kvh], 1u);
-        last = (prev == n_act - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+}
 
-    // ---- last split of this KV head: merge
-    for (int i = tid; i < G * HS; i += ATTN_THREADS) {
-        const int j = i / HS, d = i % HS;
+// Merge of the split partials: one workgroup of ATTN_MERGE_THREADS per query
+// head; thread (q, d) sums splits q, q + Q, ... for head dim d, all of its
+// loads issued before use, then the Q groups are combined in LDS.
+constexpr int ATTN_MERGE_THREADS = 512;
+
+template <int HS, int G>
+__device__ void attn_merge_body(const AttnArgs &a) {
+    constexpr int Q = ATTN_MERGE_THREADS / HS;             // split groups
+    constexpr int PER = (ATTN_MERGE_MAX + Q - 1) / Q;      // splits per thread at most
+    __shared__ float wgt[ATTN_MERGE_MAX];
+    __shared__ float part[Q][HS];
+    __shared__ float Lsum;
+    const int tid = threadIdx.x;
+    const uint32_t h = blockIdx.x, kvh = h / G, j = h % G, S = a.n_splits;
+    const uint32_t T = min(*a.pos + 1, a.seq_cap);
+    const uint32_t C = min(max((T + S - 1) / S, (uint32_t)ATTN_CMIN), (uint32_t)ATTN_CMAX);
+    const uint32_t n_act = (T + C - 1) / C;
+    for (uint32_t t = tid; t < n_act; t += ATTN_MERGE_THREADS)
+        wgt[t] = a.part_ml[(((size_t)kvh * S + t) * G + j) * 2];
+    __syncthreads();
+    if (tid < 64) {
         float M = -INFINITY;
-        for (uint32_t t = 0; t < n_act; t++) M = fmaxf(M, a.part_ml[(((size_t)kvh * S + t) * G + j) * 2]);
-        float L = 0.0f, O = 0.0f;
-        for (uint32_t t = 0; t < n_act; t++) {
-            const size_t pj = ((size_t)kvh * S + t) * G + j;
-            const float w = expf(a.part_ml[pj * 2] - M);
-            L = fmaf(a.part_ml[pj * 2 + 1], w, L);
-            O = fmaf(a.part_o[pj * HS + d], w, O);
+        for (uint32_t t = tid; t < n_act; t += 64) M = fmaxf(M, wgt[t]);
+        M = wave_max(M);
+        float L = 0.0f;
+        for (uint32_t t = tid; t < n_act; t += 64) {
+            const float w = expf(wgt[t] - M);
+            wgt[t] = w;
+            L = fmaf(a.part_ml[(((size_t)kvh * S + t) * G + j) * 2 + 1], w, L);
         }
-        a.out[(size_t)(kvh * G + j) * HS + d] = O / L;
+        L = wave_sum(L);
+        if (tid == 0) Lsum = L;
     }
-    if (tid == 0) a.counters[kvh] = 0;
+    __syncthreads();
+    const int d = tid % HS, q = tid / HS;
+    const float *po = a.part_o + ((size_t)kvh * S * G + j) * HS + d; // split t at po[t * G * HS]
+    float v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const uint32_t t = (uint32_t)(q + Q * u);
+        v[u] = t < n_act ? po[(size_t)t * G * HS] : 0.0f;
+    }
+    float O = 0.0f;
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const uint32_t t = (uint32_t)(q + Q * u);
+        if (t < n_act) O = fmaf(v[u], wgt[t], O);
+    }
+    part[q][d] = O;
+    __syncthreads();
+    // head dims are written (and quantized for the next GEMV: a head is
+    // HS/16 whole activation groups) by the first HS threads
+    if (tid < ((HS + 63) / 64) * 64) {
+        const bool ok = tid < HS;
+        float r = 0.0f;
+        if (ok) {
+#pragma unroll
+            for (int k = 0; k < Q; k++) r += part[k][tid];
+            r /= Lsum;
+            a.out[(size_t)h * HS + tid] = r;
+        }
+        if (a.xq_out) quant16(r, ok, a.xq_out, a.n_out, (uint32_t)(h * HS + tid), tid & 63);
+    }
 }
 
 } // namespace ifr

@@ -123,16 +123,25 @@ IFR_DEV void scale_min_k4(uint32_t j, uint32_t w0, uint32_t w1, uint32_t w2, uin
     }
 }
 
-// Byte b (0..3) of a word as a float.  Written so the compiler selects
-// v_cvt_f32_ubyte{0..3}.
-IFR_DEV float ub(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
+// Byte B (0..3) of a word as a float: one v_cvt_f32_ubyteB.  Written as
+// inline assembly because after a nibble mask the compiler otherwise splits
+// it into a bit-field extract plus a conversion.
+template <int B>
+IFR_DEV float ub(uint32_t w) {
+    float r;
+    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+    return r;
+}
 
 // Dot of the four bytes of w (as unsigned integers) with x[0..3].
 IFR_DEV float dot4u(uint32_t w, const float *x, float acc) {
-    acc = fmaf(ub(w, 0), x[0], acc);
-    acc = fmaf(ub(w, 1), x[1], acc);
-    acc = fmaf(ub(w, 2), x[2], acc);
-    acc = fmaf(ub(w, 3), x[3], acc);
+    acc = fmaf(ub<0>(w), x[0], acc);
+    acc = fmaf(ub<1>(w), x[1], acc);
+    acc = fmaf(ub<2>(w), x[2], acc);
+    acc = fmaf(ub<3>(w), x[3], acc);
     return acc;
 }
 

@@ -2,7 +2,7 @@
 // token embedding, KV-row store, dequant/quantize of whole tensors and the
 // synthetic-weight generator.
 #pragma once
-#include "dequant.h"
+#include "gemv.h"
 
 namespace ifr {
 
@@ -128,12 +128,41 @@ __device__ void argmax_final_body(const ArgmaxArgs &a) {
 }
 
 // x <- dequant(table)[tokens[pos], :]  (transformer.rs:366-374 dequantizes the
-// table at load; chat_llama2.rs:217-219 copies the row).  Bit-exact.
+// table at load; chat_llama2.rs:217-219 copies the row).  Bit-exact.  Also
+// quantizes x * gamma for the first GEMV and writes per-workgroup partial
+// sums of x^2 (one element per thread: launch ceil(hidden/256) x 256).
 __device__ void embed_body(const EmbedArgs &a) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t tok = a.tokens[a.ctl->pos];
     const uint8_t *row = a.table + (size_t)tok * a.row_bytes;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < a.hidden; i += gridDim.x * blockDim.x)
-        a.x[i] = deq_elem(a.fmt, row, i);
+    const uint32_t i = blockIdx.x * blockDim.x + (uint32_t)tid;
+    const bool ok = i < a.hidden;
+    const float v = ok ? deq_elem(a.fmt, row, i) : 0.0f;
+    if (ok) a.x[i] = v;
+    if (a.xq_out) {
+        quant16(v * (ok ? a.gamma[i] : 0.0f), ok, a.xq_out, a.hidden, i, lane);
+        const float sq = wave_sum(v * v);
+        if (lane == 0) red[wave] = sq;
+        __syncthreads();
+        if (tid == 0) a.ss_out[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+    }
+}
+
+// XQ of x (times gamma when given), one element per thread, 256 threads per
+// workgroup; partial sums of x^2 per workgroup.
+__device__ void quant_act_body(const QActArgs &a) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t i = blockIdx.x * blockDim.x + (uint32_t)tid;
+    const bool ok = i < a.n;
+    const float v = ok ? a.x[i] : 0.0f;
+    const float g = (ok && a.gamma) ? a.gamma[i] : 1.0f;
+    quant16(v * g, ok, a.xq_out, a.n, i, lane);
+    const float sq = wave_sum(v * v);
+    if (lane == 0) red[wave] = sq;
+    __syncthreads();
+    if (tid == 0 && a.ss_out) a.ss_out[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // cache[pos] <- k, v (rounded to binary16 when kv_f16).

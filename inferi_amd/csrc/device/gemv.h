@@ -1,51 +1,62 @@
 // Dequant-fused GEMV for GGUF blocks on gfx950 (HBM-bound; no MFMA).
 //
-// Work mapping.  A workgroup is 4 waves of 64 lanes; each wave owns R = 4
-// consecutive rows and sweeps the whole K range of those rows, so the x
-// values a lane reads from LDS are reused for 4 rows.  Within a wave, a block
-// is split over LPB lanes (8 for the 256-element K-quants, so a lane owns one
-// 16-byte quant chunk = 32 elements; 2 for Q8_0) and a wave covers 64/LPB
-// consecutive blocks per step; every lane issues its R rows' 16-byte loads
-// before it touches them.  Partial dots are combined with a DPP butterfly.
-// The activation vector is staged in LDS once per workgroup (optionally
-// RMS-normalised on the way in), and the workgroups walk row tiles with a
-// grid stride so the launch can be sized to the chip.
+// Work mapping.  A workgroup is W waves of 64 lanes; each wave owns R
+// consecutive rows of a W*R-row tile and walks the K range of those rows in
+// steps: a block is split over LPB lanes (4 for the 256-element K-quants, so a
+// lane owns 64 elements of a block; 2 for Q8_0) and a step covers 64/LPB
+// consecutive blocks.  A wave's work is one flat stream of (tile, step) pairs
+// (tiles with a grid stride), and the next step's weight loads, possibly in
+// the next tile, are always issued before the current step computes; the
+// first step's loads go out before x is staged.  Row results are combined
+// with a DPP butterfly.
 //
-// Arithmetic.  Per 32-element chunk the unsigned quant codes q are
-// dotted with x in fp32 and the block scales are applied afterwards:
-//   sum_e (d1*q_e - m1) x_e = d1 * sum_e q_e x_e - m1 * sum_e x_e,
-// the refactoring the reference kernels use too
-// (inferi-shaders/src/gemv_quant_q4_k.rs:47-93).  Accumulation is fp32.
+// Arithmetic: two paths.
+//  - integer (default): x arrives quantized by the kernel that produced it
+//    (16-element groups of 22-bit fixed point as three int8 digit planes,
+//    see quant16 below); the quant codes are multiplied with v_dot4_i32_i8
+//    and the block and group scales applied in fp32;
+//  - exact fp32: x staged as f32 (times the RMSNorm weight), codes converted
+//    and multiplied with fp32 FMAs.
+// Both use the reference kernels' refactoring of the block affine map
+// (inferi-shaders/src/gemv_quant_q4_k.rs:47-93):
+//   sum_e (d1*q_e - m1) x_e = d1 * sum_e q_e x_e - m1 * sum_e x_e.
 #pragma once
-#include "common.h"
+#include "dequant.h"
 
 namespace ifr {
 
-constexpr int GEMV_R = 4;      // rows per wave
-constexpr int GEMV_WAVES = 4;  // waves per workgroup
+// Geometry of each mode's launch: the quantized-output modes need a tile of
+// exactly 16 output values (one activation group).
+template <int MODE>
+struct GemvGeom {
+    static constexpr int R = gemv_geom(MODE).R, W = gemv_geom(MODE).W;
+    static constexpr bool PIPE = false;
+};
 
-// Scale/min pair for sub-blocks 2g and 2g+1 of a Q4_K/Q5_K block, branch-free
-// (get_scale_min_k4, crates/inferi/src/quantization.rs:394-402).
+// Scale/min pair for sub-blocks 2g and 2g+1 of a Q4_K/Q5_K block
+// (get_scale_min_k4, crates/inferi/src/quantization.rs:394-402), branch-free:
+// both encodings are computed and selected, since g differs between the
+// lanes of a wave.
 IFR_DEV void scale_min_pair(uint32_t g, uint32_t w0, uint32_t w1, uint32_t w2, uint32_t &sc0, uint32_t &m0,
                             uint32_t &sc1, uint32_t &m1) {
-    uint32_t sh = 16u * (g & 1u);
-    if (g < 2) {
-        sc0 = (w0 >> sh) & 63u;
-        m0 = (w1 >> sh) & 63u;
-        sc1 = (w0 >> (sh + 8)) & 63u;
-        m1 = (w1 >> (sh + 8)) & 63u;
-    } else {
-        sc0 = ((w2 >> sh) & 15u) | (((w0 >> (sh + 6)) & 3u) << 4);
-        m0 = ((w2 >> (sh + 4)) & 15u) | (((w1 >> (sh + 6)) & 3u) << 4);
-        sc1 = ((w2 >> (sh + 8)) & 15u) | (((w0 >> (sh + 14)) & 3u) << 4);
-        m1 = ((w2 >> (sh + 12)) & 15u) | (((w1 >> (sh + 14)) & 3u) << 4);
-    }
+    const uint32_t sh = 16u * (g & 1u);
+    const uint32_t a0 = w0 >> sh, a1 = w1 >> sh, a2 = w2 >> sh;
+    const bool lo = g < 2;
+    // j < 4: sc = q[j] & 63, m = q[j+4] & 63
+    // j >= 4: sc = (q[j+4] & 15) | (q[j-4] >> 6) << 4, m = (q[j+4] >> 4) | (q[j] >> 6) << 4
+    const uint32_t hs0 = ((a0 >> 6) & 3u) << 4, hm0 = ((a1 >> 6) & 3u) << 4;
+    const uint32_t hs1 = ((a0 >> 14) & 3u) << 4, hm1 = ((a1 >> 14) & 3u) << 4;
+    sc0 = lo ? (a0 & 63u) : ((a2 & 15u) | hs0);
+    m0 = lo ? (a1 & 63u) : (((a2 >> 4) & 15u) | hm0);
+    sc1 = lo ? ((a0 >> 8) & 63u) : (((a2 >> 8) & 15u) | hs1);
+    m1 = lo ? ((a1 >> 8) & 63u) : (((a2 >> 12) & 15u) | hm1);
 }
 
 IFR_DEV void lds16(const float *p, float *x) {
+    const float4 *p4 = (const float4 *)__builtin_assume_aligned(p, 16);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float4 t = ((const float4 *)p)[i];
+        float4 t = p4[i];
         x[4 * i] = t.x;
         x[4 * i + 1] = t.y;
         x[4 * i + 2] = t.z;
@@ -82,133 +93,468 @@ struct QFmt<Q6_K> { static constexpr int QK = 256, BB = 210, LPB = 8; };
 template <>
 struct QFmt<Q8_0> { static constexpr int QK = 32, BB = 34, LPB = 2; };
 
-// acc[r] += dot(row r, x) over all blocks, for this lane's share.
+// One lane's share of one block step for R rows: the raw bytes (load) and
+// their dot with x (compute), split so the next step's loads can be in
+// flight while this step computes.
 template <int FMT, int R>
-IFR_DEV void gemv_accum(const uint8_t *const *rowp, uint32_t nb, int lane, const float *xs, float *acc) {
-    constexpr int LPB = QFmt<FMT>::LPB, BPI = 64 / LPB, BB = QFmt<FMT>::BB, QK = QFmt<FMT>::QK;
-    const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
-    for (uint32_t kb0 = 0; kb0 < nb; kb0 += BPI) {
-        const uint32_t kb = kb0 + bsub;
-        if (kb >= nb) break;
-        if constexpr (FMT == Q4_K) {
-            // lane chunk c: qs bytes [16c, 16c+16) = elements 64g+16h+t (low
-            // nibbles) and 64g+32+16h+t (high nibbles), g = c/2, h = c%2.
-            const uint32_t g = c >> 1, h = c & 1u;
-            uint4 hv[R], qv[R];
+struct Chunk;
+
+// Q4_K lane chunk c: qs bytes [16c, 16c+16) = elements 64g+16h+t (low
+// nibbles) and 64g+32+16h+t (high nibbles), g = c/2, h = c%2.
+template <int R>
+struct Chunk<Q4_K, R> {
+    uint4 hv[R], qv[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint8_t *b = rowp[r] + (size_t)kb * BB;
-                hv[r] = ld16(b);
-                qv[r] = ld16(b + 16 + 16 * c);
-            }
-            float xl[16], xh[16];
-            const float *xp = xs + kb * QK + 64 * g + 16 * h;
-            lds16(xp, xl);
-            lds16(xp + 32, xh);
-            const float sl = sum16v(xl), sh = sum16v(xh);
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 144;
+            hv[r] = ld16(b);
+            qv[r] = ld16(b + 16 + 16 * c);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        const uint32_t g = c >> 1, h = c & 1u;
+        float xl[16], xh[16];
+        const float *xp = xs + kb * 256 + 64 * g + 16 * h;
+        lds16(xp, xl);
+        lds16(xp + 32, xh);
+        const float sl = sum16v(xl), sh = sum16v(xh);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                uint32_t sc0, m0, sc1, m1;
-                scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
-                const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
-                const uint4 q = qv[r];
-                const float dl = dot16u(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu, xl);
-                const float dh = dot16u((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu,
-                                        (q.w >> 4) & 0x0F0F0F0Fu, xh);
-                acc[r] += (d * (float)sc0) * dl - (dm * (float)m0) * sl + (d * (float)sc1) * dh - (dm * (float)m1) * sh;
-            }
-        } else if constexpr (FMT == Q5_K) {
-            const uint32_t g = c >> 1, h = c & 1u;
-            uint4 hv[R], qv[R], qhv[R];
+        for (int r = 0; r < R; r++) {
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
+            const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
+            const uint4 q = qv[r];
+            const uint32_t M = 0x0F0F0F0Fu;
+            const float dl = dot16u(q.x & M, q.y & M, q.z & M, q.w & M, xl);
+            const float dh = dot16u((q.x >> 4) & M, (q.y >> 4) & M, (q.z >> 4) & M, (q.w >> 4) & M, xh);
+            acc[r] += (d * (float)sc0) * dl - (dm * (float)m0) * sl + (d * (float)sc1) * dh - (dm * (float)m1) * sh;
+        }
+    }
+};
+
+// Q5_K: as Q4_K plus the fifth bit from qh[16h + t], bit 2g (low) / 2g+1 (high).
+template <int R>
+struct Chunk<Q5_K, R> {
+    uint4 hv[R], qv[R], qhv[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+        const uint32_t h = c & 1u;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint8_t *b = rowp[r] + (size_t)kb * BB;
-                hv[r] = ld16(b);
-                qhv[r] = ld16(b + 16 + 16 * h);
-                qv[r] = ld16(b + 48 + 16 * c);
-            }
-            float xl[16], xh[16];
-            const float *xp = xs + kb * QK + 64 * g + 16 * h;
-            lds16(xp, xl);
-            lds16(xp + 32, xh);
-            const float sl = sum16v(xl), sh = sum16v(xh);
-            const uint32_t s0 = 2 * g, s1 = 2 * g + 1;
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 176;
+            hv[r] = ld16(b);
+            qhv[r] = ld16(b + 16 + 16 * h);
+            qv[r] = ld16(b + 48 + 16 * c);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        const uint32_t g = c >> 1, h = c & 1u;
+        float xl[16], xh[16];
+        const float *xp = xs + kb * 256 + 64 * g + 16 * h;
+        lds16(xp, xl);
+        lds16(xp + 32, xh);
+        const float sl = sum16v(xl), sh = sum16v(xh);
+        const uint32_t s0 = 2 * g, s1 = 2 * g + 1;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                uint32_t sc0, m0, sc1, m1;
-                scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
-                const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
-                const uint4 q = qv[r], e = qhv[r];
-                const uint32_t M = 0x0F0F0F0Fu, B = 0x01010101u;
-                const float dl = dot16u((q.x & M) | (((e.x >> s0) & B) << 4), (q.y & M) | (((e.y >> s0) & B) << 4),
-                                        (q.z & M) | (((e.z >> s0) & B) << 4), (q.w & M) | (((e.w >> s0) & B) << 4), xl);
-                const float dh = dot16u(((q.x >> 4) & M) | (((e.x >> s1) & B) << 4),
-                                        ((q.y >> 4) & M) | (((e.y >> s1) & B) << 4),
-                                        ((q.z >> 4) & M) | (((e.z >> s1) & B) << 4),
-                                        ((q.w >> 4) & M) | (((e.w >> s1) & B) << 4), xh);
-                acc[r] += (d * (float)sc0) * dl - (dm * (float)m0) * sl + (d * (float)sc1) * dh - (dm * (float)m1) * sh;
-            }
-        } else if constexpr (FMT == Q6_K) {
-            // lane chunk c: i = c/4 (half), cp = c%4, s = cp%2, u = cp/2.
-            // ql bytes [64i+16cp, +16): low nibbles are elements
-            // 128i+32u+16s+t, high nibbles +64; qh bytes [32i+16s, +16) give
-            // bits 2u..2u+1 (low) and 2u+4..2u+5 (high); scales 8i+s+2u, +4.
-            const uint32_t i = c >> 2, cp = c & 3u, s = cp & 1u, u = cp >> 1;
-            uint4 qlv[R], qhv[R];
-            uint32_t dsc[R], scl[R], sch[R];
+        for (int r = 0; r < R; r++) {
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
+            const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
+            const uint4 q = qv[r], e = qhv[r];
+            const uint32_t M = 0x0F0F0F0Fu, B = 0x01010101u;
+            const float dl = dot16u((q.x & M) | (((e.x >> s0) & B) << 4), (q.y & M) | (((e.y >> s0) & B) << 4),
+                                    (q.z & M) | (((e.z >> s0) & B) << 4), (q.w & M) | (((e.w >> s0) & B) << 4), xl);
+            const float dh = dot16u(((q.x >> 4) & M) | (((e.x >> s1) & B) << 4),
+                                    ((q.y >> 4) & M) | (((e.y >> s1) & B) << 4),
+                                    ((q.z >> 4) & M) | (((e.z >> s1) & B) << 4),
+                                    ((q.w >> 4) & M) | (((e.w >> s1) & B) << 4), xh);
+            acc[r] += (d * (float)sc0) * dl - (dm * (float)m0) * sl + (d * (float)sc1) * dh - (dm * (float)m1) * sh;
+        }
+    }
+};
+
+// Q6_K lane chunk c: i = c/4 (half), cp = c%4, s = cp%2, u = cp/2.  ql bytes
+// [64i+16cp, +16): low nibbles are elements 128i+32u+16s+t, high nibbles +64;
+// qh bytes [32i+16s, +16) give bits 2u..2u+1 (low) and 2u+4..2u+5 (high);
+// scales 8i+s+2u and +4.  Blocks are 210 bytes, so fields are 2-byte aligned.
+template <int R>
+struct Chunk<Q6_K, R> {
+    uint4 qlv[R], qhv[R];
+    uint32_t dsc[R], scl[R], sch[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+        const uint32_t i = c >> 2, cp = c & 3u, s = cp & 1u, u = cp >> 1;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint8_t *b = rowp[r] + (size_t)kb * BB;
-                qlv[r] = ld16_a2(b + 64 * i + 16 * cp);
-                qhv[r] = ld16_a2(b + 128 + 32 * i + 16 * s);
-                scl[r] = b[192 + 8 * i + s + 2 * u];
-                sch[r] = b[192 + 8 * i + s + 2 * u + 4];
-                dsc[r] = ld_u16(b + 208);
-            }
-            float xl[16], xh[16];
-            const float *xp = xs + kb * QK + 128 * i + 32 * u + 16 * s;
-            lds16(xp, xl);
-            lds16(xp + 64, xh);
-            const float sl = sum16v(xl), sh = sum16v(xh);
-            const uint32_t s0 = 2 * u, s1 = 2 * u + 4;
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 210;
+            qlv[r] = ld16_a2(b + 64 * i + 16 * cp);
+            qhv[r] = ld16_a2(b + 128 + 32 * i + 16 * s);
+            scl[r] = b[192 + 8 * i + s + 2 * u];
+            sch[r] = b[192 + 8 * i + s + 2 * u + 4];
+            dsc[r] = ld_u16(b + 208);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        const uint32_t i = c >> 2, cp = c & 3u, s = cp & 1u, u = cp >> 1;
+        float xl[16], xh[16];
+        const float *xp = xs + kb * 256 + 128 * i + 32 * u + 16 * s;
+        lds16(xp, xl);
+        lds16(xp + 64, xh);
+        const float sl = sum16v(xl), sh = sum16v(xh);
+        const uint32_t s0 = 2 * u, s1 = 2 * u + 4;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 q = qlv[r], e = qhv[r];
-                const uint32_t M = 0x0F0F0F0Fu, B = 0x03030303u;
-                const float dl = dot16u((q.x & M) | (((e.x >> s0) & B) << 4), (q.y & M) | (((e.y >> s0) & B) << 4),
-                                        (q.z & M) | (((e.z >> s0) & B) << 4), (q.w & M) | (((e.w >> s0) & B) << 4), xl);
-                const float dh = dot16u(((q.x >> 4) & M) | (((e.x >> s1) & B) << 4),
-                                        ((q.y >> 4) & M) | (((e.y >> s1) & B) << 4),
-                                        ((q.z >> 4) & M) | (((e.z >> s1) & B) << 4),
-                                        ((q.w >> 4) & M) | (((e.w >> s1) & B) << 4), xh);
-                const float d = f16_to_f32(dsc[r]);
-                const float fl = (float)(int)(int8_t)scl[r], fh = (float)(int)(int8_t)sch[r];
-                // codes are stored +32: sum (q-32) x = sum q x - 32 sum x
-                acc[r] += (d * fl) * (dl - 32.0f * sl) + (d * fh) * (dh - 32.0f * sh);
-            }
-        } else { // Q8_0: lane half c of block kb: qs bytes [16c, 16c+16)
-            uint4 qv[R];
-            uint32_t dsc[R];
+        for (int r = 0; r < R; r++) {
+            const uint4 q = qlv[r], e = qhv[r];
+            const uint32_t M = 0x0F0F0F0Fu, B = 0x03030303u;
+            const float dl = dot16u((q.x & M) | (((e.x >> s0) & B) << 4), (q.y & M) | (((e.y >> s0) & B) << 4),
+                                    (q.z & M) | (((e.z >> s0) & B) << 4), (q.w & M) | (((e.w >> s0) & B) << 4), xl);
+            const float dh = dot16u(((q.x >> 4) & M) | (((e.x >> s1) & B) << 4),
+                                    ((q.y >> 4) & M) | (((e.y >> s1) & B) << 4),
+                                    ((q.z >> 4) & M) | (((e.z >> s1) & B) << 4),
+                                    ((q.w >> 4) & M) | (((e.w >> s1) & B) << 4), xh);
+            const float d = f16_to_f32(dsc[r]);
+            const float fl = (float)(int)(int8_t)scl[r], fh = (float)(int)(int8_t)sch[r];
+            // codes are stored +32: sum (q-32) x = sum q x - 32 sum x
+            acc[r] += (d * fl) * (dl - 32.0f * sl) + (d * fh) * (dh - 32.0f * sh);
+        }
+    }
+};
+
+// Q8_0 lane half c of block kb: qs bytes [16c, 16c+16).
+template <int R>
+struct Chunk<Q8_0, R> {
+    uint4 qv[R];
+    uint32_t dsc[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint8_t *b = rowp[r] + (size_t)kb * BB;
-                dsc[r] = ld_u16(b);
-                qv[r] = ld16_a2(b + 2 + 16 * c);
-            }
-            float xv[16];
-            lds16(xs + kb * QK + 16 * c, xv);
-            const float sx = sum16v(xv);
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 34;
+            dsc[r] = ld_u16(b);
+            qv[r] = ld16_a2(b + 2 + 16 * c);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        float xv[16];
+        lds16(xs + kb * 32 + 16 * c, xv);
+        const float sx = sum16v(xv);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                // signed codes: (q ^ 0x80) = q + 128 as an unsigned byte
-                const uint4 q = qv[r];
-                const uint32_t F = 0x80808080u;
-                const float dq = dot16u(q.x ^ F, q.y ^ F, q.z ^ F, q.w ^ F, xv);
-                acc[r] += f16_to_f32(dsc[r]) * (dq - 128.0f * sx);
-            }
+        for (int r = 0; r < R; r++) {
+            // signed codes: (q ^ 0x80) = q + 128 as an unsigned byte
+            const uint4 q = qv[r];
+            const uint32_t F = 0x80808080u;
+            const float dq = dot16u(q.x ^ F, q.y ^ F, q.z ^ F, q.w ^ F, xv);
+            acc[r] += f16_to_f32(dsc[r]) * (dq - 128.0f * sx);
+        }
+    }
+};
+
+// ------------------------------------------------------------------------
+// Integer path.  An activation vector of K values is kept as XQ (K % 16 == 0):
+//   XA, XB, XC int8[K] @0, @K, @2K;  XS f32[K/16] @3K;  XSUM f32[K/16] @3K+K/4.
+// Element i of group J = i/16 is x~_i = XS[J] * v_i, v_i = 65536*XA[i] +
+// 256*XB[i] + XC[i] (balanced base-256 digits of a 22-bit code, |v| <=
+// 2^21 - 1), XS[J] = max|x|_J / (2^21 - 1) and XSUM[J] = sum of x~ over the
+// group: |x~ - x| <= max|x|_J * 2.4e-7.  A group's dot with the unsigned
+// codes q of a K-quant is one exact int32, built by chaining three
+// v_dot4_i32_i8 sums (sum q*XA, shifted left 8, plus sum q*XB, shifted left 8,
+// plus sum q*XC); 16 codes of at most 63 times 2^21 stay below 2^31.  The
+// group scale and the block scales are then applied in fp32.
+
+IFR_DEV uint32_t xq_bytes(uint32_t K) { return 3 * K + K / 2; }
+
+struct XQ {
+    const int8_t *xa, *xb, *xc;
+    const float *xs, *xsum;
+    IFR_DEV XQ(const uint8_t *base, uint32_t K)
+        : xa((const int8_t *)base), xb((const int8_t *)base + K), xc((const int8_t *)base + 2 * K),
+          xs((const float *)(base + 3 * K)), xsum((const float *)(base + 3 * K + K / 4)) {}
+};
+
+constexpr float XQ_MAXCODE = 2097151.0f; // 2^21 - 1
+
+// Quantizes one value per lane into XQ at element i; the 16 lanes of a DPP
+// row form one group (i % 16 == lane % 16).  Every lane of the wave must call
+// it (the reductions read neighbours); `ok` gates the stores.
+IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int lane) {
+    const float am = max16(fabsf(v));
+    const float sc = am / XQ_MAXCODE;
+    const float inv = am > 0.0f ? XQ_MAXCODE / am : 0.0f;
+    const int q = (int)rintf(clampf(v * inv, -XQ_MAXCODE, XQ_MAXCODE));
+    // balanced base-256 digits: dc, db in [-128, 127], da in [-32, 32]
+    const int dc = ((q + 128) & 0xFF) - 128;
+    const int q1 = (q - dc) >> 8;
+    const int db = ((q1 + 128) & 0xFF) - 128;
+    const int da = (q1 - db) >> 8;
+    const float sq = sum16((float)q);
+    if (ok) {
+        xq[i] = (uint8_t)(int8_t)da;
+        xq[K + i] = (uint8_t)(int8_t)db;
+        xq[2 * K + i] = (uint8_t)(int8_t)dc;
+        if ((lane & 15) == 0) {
+            ((float *)(xq + 3 * K))[i / 16] = sc;
+            ((float *)(xq + 3 * K + K / 4))[i / 16] = sc * sq;
         }
     }
 }
+
+IFR_DEV uint4 lds_u4(const int8_t *p) { return *(const uint4 *)__builtin_assume_aligned(p, 16); }
+IFR_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+// c + sum over four words of codes q and x digits
+IFR_DEV int sdot16(uint4 q, uint4 x, int c) {
+    c = sdot4(q.x, x.x, c);
+    c = sdot4(q.y, x.y, c);
+    c = sdot4(q.z, x.z, c);
+    return sdot4(q.w, x.w, c);
+}
+IFR_DEV uint4 and4(uint4 q, uint32_t m) { return make_uint4(q.x & m, q.y & m, q.z & m, q.w & m); }
+IFR_DEV uint4 shr4(uint4 q, uint32_t s) { return make_uint4(q.x >> s, q.y >> s, q.z >> s, q.w >> s); }
+
+// x digits of one 16-element group in LDS
+struct XG {
+    uint4 a, b, c;
+};
+IFR_DEV XG xg_load(const XQ &x, uint32_t e) { return XG{lds_u4(x.xa + e), lds_u4(x.xb + e), lds_u4(x.xc + e)}; }
+// sum_e q_e v_e of one group for codes 0 <= q <= 63: exact in int32
+IFR_DEV int gdot_u(uint4 q, const XG &x) {
+    return sdot16(q, x.c, sdot16(q, x.b, sdot16(q, x.a, 0) << 8) << 8);
+}
+// the same for signed codes |q| <= 127, as a float (two exact int parts)
+IFR_DEV float gdot_s(uint4 q, const XG &x) {
+    const int hi = sdot16(q, x.a, 0);
+    const int lo = sdot16(q, x.c, sdot16(q, x.b, 0) << 8);
+    return fmaf((float)hi, 65536.0f, (float)lo);
+}
+
+template <int FMT, int R>
+struct ChunkI;
+
+// Q4_K, 4 lanes per block: lane g owns sub-blocks 2g (low nibbles, elements
+// 64g+l) and 2g+1 (high nibbles, 64g+32+l), l = 0..31: qs bytes [32g, 32g+32).
+template <int R>
+struct ChunkI<Q4_K, R> {
+    static constexpr int LPB = 4;
+    uint4 hv[R], q0[R], q1[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t g) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 144;
+            hv[r] = ld16(b);
+            q0[r] = ld16(b + 16 + 32 * g);
+            q1[r] = ld16(b + 32 + 32 * g);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t g, const XQ &x, float *acc) const {
+        const uint32_t e = kb * 256 + 64 * g;
+        const float4 s = *(const float4 *)__builtin_assume_aligned(x.xs + e / 16, 16);
+        const float4 S = *(const float4 *)__builtin_assume_aligned(x.xsum + e / 16, 16);
+        const uint32_t M = 0x0F0F0F0Fu;
+        int i0[R], i1[R], i2[R], i3[R];
+        {
+            const XG xg = xg_load(x, e);
+#pragma unroll
+            for (int r = 0; r < R; r++) i0[r] = gdot_u(and4(q0[r], M), xg);
+        }
+        {
+            const XG xg = xg_load(x, e + 16);
+#pragma unroll
+            for (int r = 0; r < R; r++) i1[r] = gdot_u(and4(q1[r], M), xg);
+        }
+        {
+            const XG xg = xg_load(x, e + 32);
+#pragma unroll
+            for (int r = 0; r < R; r++) i2[r] = gdot_u(and4(shr4(q0[r], 4), M), xg);
+        }
+        {
+            const XG xg = xg_load(x, e + 48);
+#pragma unroll
+            for (int r = 0; r < R; r++) i3[r] = gdot_u(and4(shr4(q1[r], 4), M), xg);
+        }
+        const float S_lo = S.x + S.y, S_hi = S.z + S.w;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float t_lo = fmaf((float)i0[r], s.x, (float)i1[r] * s.y);
+            const float t_hi = fmaf((float)i2[r], s.z, (float)i3[r] * s.w);
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
+            const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
+            acc[r] += (d * (float)sc0) * t_lo - (dm * (float)m0) * S_lo + (d * (float)sc1) * t_hi - (dm * (float)m1) * S_hi;
+        }
+    }
+};
+
+// Q5_K: as Q4_K, fifth bit of element l from qh[l], bit 2g (low) / 2g+1 (high).
+template <int R>
+struct ChunkI<Q5_K, R> {
+    static constexpr int LPB = 4;
+    uint4 hv[R], q0[R], q1[R], e0[R], e1[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t g) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 176;
+            hv[r] = ld16(b);
+            e0[r] = ld16(b + 16);
+            e1[r] = ld16(b + 32);
+            q0[r] = ld16(b + 48 + 32 * g);
+            q1[r] = ld16(b + 64 + 32 * g);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t g, const XQ &x, float *acc) const {
+        const uint32_t e = kb * 256 + 64 * g;
+        const float4 s = *(const float4 *)__builtin_assume_aligned(x.xs + e / 16, 16);
+        const float4 S = *(const float4 *)__builtin_assume_aligned(x.xsum + e / 16, 16);
+        const uint32_t M = 0x0F0F0F0Fu, B = 0x10101010u;
+        const uint32_t s0 = 2 * g, s1 = 2 * g + 1;
+        // fifth bit to bit 4 of each byte: ((qh >> s) << 4) & 0x10101010
+        auto lo = [&](uint32_t q, uint32_t h) { return (q & M) | (((h >> s0) << 4) & B); };
+        auto hi = [&](uint32_t q, uint32_t h) { return ((q >> 4) & M) | (((h >> s1) << 4) & B); };
+        int i0[R], i1[R], i2[R], i3[R];
+        {
+            const XG xg = xg_load(x, e);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = q0[r], f = e0[r];
+                i0[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
+            }
+        }
+        {
+            const XG xg = xg_load(x, e + 16);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = q1[r], f = e1[r];
+                i1[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
+            }
+        }
+        {
+            const XG xg = xg_load(x, e + 32);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = q0[r], f = e0[r];
+                i2[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
+            }
+        }
+        {
+            const XG xg = xg_load(x, e + 48);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = q1[r], f = e1[r];
+                i3[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
+            }
+        }
+        const float S_lo = S.x + S.y, S_hi = S.z + S.w;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float t_lo = fmaf((float)i0[r], s.x, (float)i1[r] * s.y);
+            const float t_hi = fmaf((float)i2[r], s.z, (float)i3[r] * s.w);
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
+            const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
+            acc[r] += (d * (float)sc0) * t_lo - (dm * (float)m0) * S_lo + (d * (float)sc1) * t_hi - (dm * (float)m1) * S_hi;
+        }
+    }
+};
+
+// Q6_K, 4 lanes per block: lane c = 2i + u owns ql bytes [64i+32u, +32): low
+// nibbles are elements 128i+32u+l, high nibbles 128i+64+32u+l (l = 0..31),
+// with qh[32i+l] bits 2u..2u+1 / 2u+4..2u+5 and scales sc[8i+2u+l/16] /
+// sc[8i+2u+4+l/16].  Codes are stored +32: sum (q-32) x = sum q x - 32 sum x.
+template <int R>
+struct ChunkI<Q6_K, R> {
+    static constexpr int LPB = 4;
+    uint4 l0[R], l1[R], h0[R], h1[R];
+    uint32_t sc_lo[R], sc_hi[R], dd[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+        const uint32_t i = c >> 1, u = c & 1u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 210;
+            l0[r] = ld16_a2(b + 64 * i + 32 * u);
+            l1[r] = ld16_a2(b + 64 * i + 32 * u + 16);
+            h0[r] = ld16_a2(b + 128 + 32 * i);
+            h1[r] = ld16_a2(b + 144 + 32 * i);
+            sc_lo[r] = ld_u16(b + 192 + 8 * i + 2 * u);
+            sc_hi[r] = ld_u16(b + 196 + 8 * i + 2 * u);
+            dd[r] = ld_u16(b + 208);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const XQ &x, float *acc) const {
+        const uint32_t i = c >> 1, u = c & 1u;
+        const uint32_t e = kb * 256 + 128 * i + 32 * u;
+        const float2 sl = *(const float2 *)(x.xs + e / 16), sh = *(const float2 *)(x.xs + e / 16 + 4);
+        const float2 Sl = *(const float2 *)(x.xsum + e / 16), Sh = *(const float2 *)(x.xsum + e / 16 + 4);
+        const uint32_t M = 0x0F0F0F0Fu, B = 0x30303030u;
+        const uint32_t s_lo = 2 * u, s_hi = 2 * u + 4; // this lane's qh bit pairs
+        // 6-bit codes: ql nibble | (qh pair << 4)
+        auto lo = [&](uint32_t q, uint32_t h) { return (q & M) | (((h >> s_lo) << 4) & B); };
+        auto hi = [&](uint32_t q, uint32_t h) { return ((q >> 4) & M) | (((h >> s_hi) << 4) & B); };
+        int i0[R], i1[R], i2[R], i3[R];
+        {
+            const XG xg = xg_load(x, e);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = l0[r], f = h0[r];
+                i0[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
+            }
+        }
+        {
+            const XG xg = xg_load(x, e + 16);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = l1[r], f = h1[r];
+                i1[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
+            }
+        }
+        {
+            const XG xg = xg_load(x, e + 64);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = l0[r], f = h0[r];
+                i2[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
+            }
+        }
+        {
+            const XG xg = xg_load(x, e + 80);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint4 a = l1[r], f = h1[r];
+                i3[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float t0 = fmaf((float)i0[r], sl.x, -32.0f * Sl.x);
+            const float t1 = fmaf((float)i1[r], sl.y, -32.0f * Sl.y);
+            const float t2 = fmaf((float)i2[r], sh.x, -32.0f * Sh.x);
+            const float t3 = fmaf((float)i3[r], sh.y, -32.0f * Sh.y);
+            const float d = f16_to_f32(dd[r]);
+            const float c0 = (float)(int)(int8_t)(sc_lo[r] & 0xFFu), c1 = (float)(int)(int8_t)(sc_lo[r] >> 8);
+            const float c2 = (float)(int)(int8_t)(sc_hi[r] & 0xFFu), c3 = (float)(int)(int8_t)(sc_hi[r] >> 8);
+            acc[r] += d * (c0 * t0 + c1 * t1 + c2 * t2 + c3 * t3);
+        }
+    }
+};
+
+// Q8_0, 2 lanes per block: lane c owns qs bytes [16c, 16c+16) (signed codes),
+// which is exactly one activation group.
+template <int R>
+struct ChunkI<Q8_0, R> {
+    static constexpr int LPB = 2;
+    uint4 qv[R];
+    uint32_t dd[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 34;
+            dd[r] = ld_u16(b);
+            qv[r] = ld16_a2(b + 2 + 16 * c);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const XQ &x, float *acc) const {
+        const uint32_t e = kb * 32 + 16 * c;
+        const XG xg = xg_load(x, e);
+        const float s = x.xs[e / 16];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] += f16_to_f32(dd[r]) * (gdot_s(qv[r], xg) * s);
+    }
+};
 
 template <int MODE>
 IFR_DEV const uint8_t *gemv_row_ptr(const GemvArgs &a, uint32_t v) {
@@ -238,32 +584,80 @@ IFR_DEV void rope_pair(float &a, float &b, uint32_t idx, uint32_t hs, uint32_t p
     b = sn * x + cs * y;
 }
 
-template <int FMT, int MODE>
-__device__ void gemv_body(const GemvArgs &a) {
-    constexpr int R = GEMV_R;
-    constexpr bool NORM = (MODE == GEMV_QKV || MODE == GEMV_GATEUP || MODE == GEMV_HEAD);
-    extern __shared__ float xs[];
-    __shared__ float red[GEMV_WAVES];
-    __shared__ uint64_t kred[GEMV_WAVES];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <int FMT, bool XI, int R>
+struct ChunkOf { using T = Chunk<FMT, R>; static constexpr int LPB = QFmt<FMT>::LPB; };
+template <int FMT, int R>
+struct ChunkOf<FMT, true, R> { using T = ChunkI<FMT, R>; static constexpr int LPB = ChunkI<FMT, R>::LPB; };
 
-    // Stage x (times gamma when normalising) into LDS.
+// Stages x into LDS.  Integer path: a copy of the producer's XQ, and for the
+// normalising modes the sum of its partial sums of x^2.  Exact path: x (times
+// gamma) as f32 and this thread's share of sum(x^2).
+template <bool XI, bool NORM, int W>
+IFR_DEV float gemv_stage(const GemvArgs &a, uint8_t *lds) {
+    const int tid = threadIdx.x;
     float ss = 0.0f;
-    for (uint32_t i = (uint32_t)tid * 4; i < a.cols; i += 64 * GEMV_WAVES * 4) {
-        float4 v = *(const float4 *)(a.x + i);
-        if constexpr (NORM) {
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
-            const float4 g = *(const float4 *)(a.gamma + i);
-            v.x *= g.x;
-            v.y *= g.y;
-            v.z *= g.z;
-            v.w *= g.w;
+    if constexpr (XI) {
+        const uint4 *src = (const uint4 *)a.xq;
+        uint4 *dst = (uint4 *)lds;
+        const uint32_t n16 = xq_bytes(a.cols) / 16;
+        for (uint32_t i = (uint32_t)tid; i < n16; i += 64 * W) dst[i] = src[i];
+        if constexpr (NORM)
+            for (uint32_t i = (uint32_t)tid; i < a.n_ss; i += 64 * W) ss += a.ss_part[i];
+    } else {
+        float *xs = (float *)lds;
+        for (uint32_t i = (uint32_t)tid * 4; i < a.cols; i += 64 * W * 4) {
+            float4 v = *(const float4 *)(a.x + i);
+            if constexpr (NORM) {
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+                const float4 g = *(const float4 *)(a.gamma + i);
+                v.x *= g.x;
+                v.y *= g.y;
+                v.z *= g.z;
+                v.w *= g.w;
+            }
+            *(float4 *)(xs + i) = v;
         }
-        *(float4 *)(xs + i) = v;
     }
+    return ss;
+}
+
+template <int FMT, int MODE, bool XI, int R = GemvGeom<MODE>::R, int W = GemvGeom<MODE>::W,
+          bool PIPE = GemvGeom<MODE>::PIPE>
+__device__ void gemv_body(const GemvArgs &a) {
+    using CH = typename ChunkOf<FMT, XI, R>::T;
+    constexpr int LPB = ChunkOf<FMT, XI, R>::LPB, BPI = 64 / LPB;
+    constexpr bool NORM = (MODE == GEMV_QKV || MODE == GEMV_GATEUP || MODE == GEMV_HEAD);
+    // RESID and GATEUP also quantize their output for the next GEMV: a tile
+    // must then hold exactly one 16-value activation group
+    constexpr bool QOUT = (MODE == GEMV_RESID || MODE == GEMV_GATEUP);
+    static_assert(!QOUT || (MODE == GEMV_RESID ? W * R == 16 : W * R == 32), "tile must be one activation group");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[W];
+    __shared__ uint64_t kred[W];
+    __shared__ float tvals[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
+    const uint32_t steps = (a.nb + BPI - 1) / BPI;
+    const uint32_t ntiles = (a.total_rows + W * R - 1) / (W * R);
+
+    const uint8_t *rowp[R];
+    auto set_rows = [&](uint32_t t, const uint8_t **rp) {
+        const uint32_t v0 = (t * W + (uint32_t)wave) * R;
+#pragma unroll
+        for (int r = 0; r < R; r++) rp[r] = gemv_row_ptr<MODE>(a, min(v0 + r, a.total_rows - 1));
+    };
+    CH A, B;
+    uint32_t tile = blockIdx.x, step = 0;
+    // the first step's weights do not depend on x: in flight before staging
+    if (tile < ntiles) {
+        set_rows(tile, rowp);
+        if (bsub < a.nb) A.load(rowp, bsub, c);
+    }
+
+    float ss = gemv_stage<XI, NORM, W>(a, lds);
     float rs = 1.0f;
     if constexpr (NORM) {
         ss = wave_sum(ss);
@@ -271,40 +665,31 @@ __device__ void gemv_body(const GemvArgs &a) {
     }
     __syncthreads();
     if constexpr (NORM) {
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
-        // rms_norm.rs:115: 1 / sqrt(sum(x^2)/n + eps)
-        rs = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) t += red[w];
+        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
     }
-
+    const XQ xq(lds, a.cols);
+    const float *xf = (const float *)lds;
     uint32_t pos = 0;
     if constexpr (MODE == GEMV_QKV) pos = a.ctl->pos;
 
-    const uint32_t rows_per_wg = GEMV_WAVES * R;
-    const uint32_t ntiles = (a.total_rows + rows_per_wg - 1) / rows_per_wg;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
     uint64_t best = 0;
-    for (uint32_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-        const uint32_t v0 = (tile * GEMV_WAVES + (uint32_t)wave) * R;
-        if (v0 >= a.total_rows) continue;
-        const uint8_t *rowp[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) rowp[r] = gemv_row_ptr<MODE>(a, min(v0 + r, a.total_rows - 1));
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = 0.0f;
-        gemv_accum<FMT, R>(rowp, a.nb, lane, xs, acc);
+
+    // Row results of tile t: reduce, then the mode's epilogue.  Every wave of
+    // the workgroup calls this for the same tile (barriers inside for QOUT).
+    auto finish = [&](uint32_t t) {
+        const uint32_t v0 = (t * W + (uint32_t)wave) * R;
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]) * rs;
-
-        if constexpr (MODE == GEMV_PLAIN || MODE == GEMV_RESID || MODE == GEMV_HEAD) {
+        if constexpr (MODE == GEMV_PLAIN || MODE == GEMV_HEAD) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                if (lane == r && v0 + r < a.total_rows) {
-                    if constexpr (MODE == GEMV_RESID)
-                        a.y[v0 + r] += acc[r];
-                    else
-                        a.y[v0 + r] = acc[r];
-                }
-            }
+            for (int r = 0; r < R; r++)
+                if (lane == r && v0 + r < a.total_rows) a.y[v0 + r] = acc[r];
             if constexpr (MODE == GEMV_HEAD) {
 #pragma unroll
                 for (int r = 0; r < R; r++)
@@ -313,15 +698,44 @@ __device__ void gemv_body(const GemvArgs &a) {
                         best = k > best ? k : best;
                     }
             }
+        } else if constexpr (MODE == GEMV_RESID) {
+            // x += W v, then x * gamma_next quantized for the next GEMV
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (lane == r && v0 + r < a.total_rows) {
+                    const float xn = a.y[v0 + r] + acc[r];
+                    a.y[v0 + r] = xn;
+                    tvals[wave * R + r] = xn;
+                }
+            __syncthreads();
+            if (wave == 0 && a.xq_out) {
+                const uint32_t i = t * 16 + (uint32_t)(lane & 15);
+                const bool ok = lane < 16 && i < a.total_rows;
+                const float xn = ok ? tvals[lane & 15] : 0.0f;
+                const float g = (ok && a.gamma_next) ? a.gamma_next[i] : 1.0f;
+                quant16(xn * g, ok, a.xq_out, a.total_rows, i, lane);
+                const float sq = sum16(xn * xn);
+                if (lane == 0) a.ss_out[t] = sq;
+            }
+            __syncthreads();
         } else if constexpr (MODE == GEMV_GATEUP) {
             // virtual rows 2j (gate j) and 2j+1 (up j): h[j] = up * silu(gate)
 #pragma unroll
-            for (int p = 0; p < R / 2; p++) {
+            for (int p = 0; p < R / 2; p++)
                 if (lane == p && v0 + 2 * p + 1 < a.total_rows) {
                     const float gt = acc[2 * p], up = acc[2 * p + 1];
-                    a.y[(v0 >> 1) + p] = up * (gt / (1.0f + expf(-gt)));
+                    const float h = up * (gt / (1.0f + expf(-gt)));
+                    a.y[(v0 >> 1) + p] = h;
+                    tvals[wave * (R / 2) + p] = h;
                 }
+            __syncthreads();
+            if (wave == 0 && a.xq_out) {
+                const uint32_t K = a.total_rows / 2;
+                const uint32_t i = t * 16 + (uint32_t)(lane & 15);
+                const bool ok = lane < 16 && i < K;
+                quant16(ok ? tvals[lane & 15] : 0.0f, ok, a.xq_out, K, i, lane);
             }
+            __syncthreads();
         } else if constexpr (MODE == GEMV_QKV) {
 #pragma unroll
             for (int p = 0; p < R / 2; p++) {
@@ -349,14 +763,79 @@ __device__ void gemv_body(const GemvArgs &a) {
                 }
             }
         }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    };
+
+    // One step of the flat (tile, step) stream: issue the next step's loads
+    // into `nxt`, compute `cur`, finish the tile after its last step.
+    auto advance = [&](CH &cur, CH &nxt) -> bool {
+        uint32_t nt = tile, ns = step + 1;
+        if (ns == steps) {
+            nt = tile + gridDim.x;
+            ns = 0;
+        }
+        const uint8_t *rown[R];
+        if (nt < ntiles) {
+            if (nt != tile) set_rows(nt, rown);
+            const uint32_t kn = ns * BPI + bsub;
+            if (kn < a.nb) nxt.load(nt != tile ? rown : rowp, kn, c);
+        }
+        const uint32_t kb = step * BPI + bsub;
+        if (kb < a.nb) {
+            if constexpr (XI)
+                cur.compute(kb, c, xq, acc);
+            else
+                cur.compute(kb, c, xf, acc);
+        }
+        if (ns == 0) {
+            finish(tile);
+            if (nt < ntiles) {
+#pragma unroll
+                for (int r = 0; r < R; r++) rowp[r] = rown[r];
+            }
+        }
+        tile = nt;
+        step = ns;
+        return tile < ntiles;
+    };
+    if (tile < ntiles) {
+        if constexpr (PIPE) {
+            while (true) {
+                if (!advance(A, B)) break;
+                if (!advance(B, A)) break;
+            }
+        } else {
+            // one stage: the step's loads are issued right before its compute
+            // (latency hidden by the other waves of the CU instead)
+            while (true) {
+                const uint32_t kb = step * BPI + bsub;
+                if (step != 0 || tile != blockIdx.x)
+                    if (kb < a.nb) A.load(rowp, kb, c);
+                if (kb < a.nb) {
+                    if constexpr (XI)
+                        A.compute(kb, c, xq, acc);
+                    else
+                        A.compute(kb, c, xf, acc);
+                }
+                if (++step == steps) {
+                    finish(tile);
+                    step = 0;
+                    tile += gridDim.x;
+                    if (tile >= ntiles) break;
+                    set_rows(tile, rowp);
+                }
+            }
+        }
     }
+
     if constexpr (MODE == GEMV_HEAD) {
         if (a.part_keys) {
             if (lane == 0) kred[wave] = best;
             __syncthreads();
             if (tid == 0) {
                 uint64_t b = kred[0];
-                for (int w = 1; w < GEMV_WAVES; w++) b = kred[w] > b ? kred[w] : b;
+                for (int w = 1; w < W; w++) b = kred[w] > b ? kred[w] : b;
                 a.part_keys[blockIdx.x] = b;
             }
         }

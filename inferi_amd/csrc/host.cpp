@@ -30,8 +30,16 @@ namespace {
 
 thread_local std::string g_create_error;
 
-constexpr uint32_t GEMV_ROWS_PER_WG = 16; // 4 waves x 4 rows (device/gemv.h)
+constexpr uint32_t GEMV_MAX_LDS = 65536 - 256;
+
+// Bytes of a quantized activation vector of n values (XQ layout,
+// device/gemv.h): three int8 digit planes plus a scale and a sum per 16 values.
+uint64_t xq_bytes(uint64_t n) { return 3 * n + n / 2; }
+
+// Dynamic LDS of a GEMV launch: x as f32, or its XQ copy.
+uint32_t gemv_lds_bytes(uint32_t cols, bool exact) { return exact ? cols * 4 : (uint32_t)xq_bytes(cols); }
 constexpr uint32_t ATTN_CMAX = 256;       // device/attention.h
+constexpr uint32_t ATTN_MERGE_MAX = 256;  // device/attention.h: most splits per KV head
 constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
 
 int qk_of(int32_t dt) {
@@ -77,10 +85,14 @@ struct ifr_ctx {
     // scratch for the op-level attention and argmax
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
-    uint32_t *attn_counters = nullptr;
-    uint32_t attn_counters_n = 0;
+    // quantized activation of the op-level GEMV
+    void *xq_scratch = nullptr;
+    size_t xq_scratch_bytes = 0;
     // tuning: cap on GEMV workgroups (0 = one per row tile)
     uint32_t gemv_max_grid = 0;
+    // GEMV arithmetic: 0 = x as 16-bit fixed point with int8 dot products,
+    // 1 = exact fp32 x and FMAs
+    int gemv_exact = 0;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -107,12 +119,25 @@ struct ifr_ctx {
     ifr_status launch(const std::string &name, dim3 grid, dim3 block, uint32_t shmem, const A &args) {
         hipFunction_t f = fn(name);
         if (!f) return fail(IFR_EUNSUPPORTED, "kernel %s not in the code object", name.c_str());
+        // every kernel takes one struct argument: kernelParams[0] points at it
         A copy = args;
-        size_t sz = sizeof(A);
-        void *cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &copy, HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz, HIP_LAUNCH_PARAM_END};
-        return hip(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, stream, nullptr,
-                                         cfg),
+        void *params[] = {&copy};
+        return hip(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, stream, params,
+                                         nullptr),
                    name.c_str());
+    }
+    ifr_status ensure_xq_scratch(size_t bytes) {
+        if (bytes <= xq_scratch_bytes) return IFR_OK;
+        if (xq_scratch) {
+            hipStreamSynchronize(stream);
+            hipFree(xq_scratch);
+            xq_scratch = nullptr;
+            xq_scratch_bytes = 0;
+        }
+        ifr_status st = hip(hipMalloc(&xq_scratch, bytes), "hipMalloc(xq scratch)");
+        if (st) return st;
+        xq_scratch_bytes = bytes;
+        return IFR_OK;
     }
     ifr_status ensure_scratch(size_t bytes) {
         if (bytes <= scratch_bytes) return IFR_OK;
@@ -125,21 +150,6 @@ struct ifr_ctx {
         ifr_status st = hip(hipMalloc(&scratch, bytes), "hipMalloc(scratch)");
         if (st) return st;
         scratch_bytes = bytes;
-        return IFR_OK;
-    }
-    ifr_status ensure_counters(uint32_t n) {
-        if (n <= attn_counters_n) return IFR_OK;
-        if (attn_counters) {
-            hipStreamSynchronize(stream);
-            hipFree(attn_counters);
-            attn_counters = nullptr;
-            attn_counters_n = 0;
-        }
-        ifr_status st = hip(hipMalloc(&attn_counters, n * sizeof(uint32_t)), "hipMalloc(counters)");
-        if (st) return st;
-        st = hip(hipMemset(attn_counters, 0, n * sizeof(uint32_t)), "hipMemset(counters)");
-        if (st) return st;
-        attn_counters_n = n;
         return IFR_OK;
     }
 };
@@ -156,7 +166,8 @@ static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const voi
     if (!p.fmt) return c->fail(IFR_EUNSUPPORTED, "matmul_quant: dtype %d has no GEMV kernel", dtype);
     const int qk = qk_of(dtype);
     if (cols == 0 || cols % (uint32_t)qk) return c->fail(IFR_EINVAL, "matmul_quant: cols %u not a multiple of %d", cols, qk);
-    if ((size_t)cols * 4 + 64 > 65536) return c->fail(IFR_EUNSUPPORTED, "matmul_quant: cols %u > 16368", cols);
+    if (gemv_lds_bytes(cols, true) > GEMV_MAX_LDS)
+        return c->fail(IFR_EUNSUPPORTED, "matmul_quant: cols %u too large for one workgroup's LDS", cols);
     const uintptr_t need = (dtype == IFR_Q4_K || dtype == IFR_Q5_K) ? 16 : 4;
     if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "matmul_quant: weights not %u-byte aligned", (unsigned)need);
     p.nb = cols / (uint32_t)qk;
@@ -164,20 +175,57 @@ static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const voi
     return IFR_OK;
 }
 
-static uint32_t gemv_grid(ifr_ctx *c, uint32_t total_rows, uint32_t cap) {
-    uint32_t ntiles = (total_rows + GEMV_ROWS_PER_WG - 1) / GEMV_ROWS_PER_WG;
-    uint32_t g = ntiles;
-    if (c->gemv_max_grid) g = std::min(g, c->gemv_max_grid);
-    if (cap) g = std::min(g, cap);
-    return std::max(g, 1u);
+// Launch geometry per mode (device/gemv.h, GemvGeom): rows per workgroup tile
+// and threads per workgroup.
+static GemvGeomT geom_of(const char *mode) {
+    return gemv_geom(!strcmp(mode, "gateup") ? GEMV_GATEUP : !strcmp(mode, "resid") ? GEMV_RESID : GEMV_PLAIN);
 }
+static uint32_t gemv_tile_rows(const char *mode) { return (uint32_t)(geom_of(mode).R * geom_of(mode).W); }
+static uint32_t gemv_threads(const char *mode) { return (uint32_t)geom_of(mode).W * 64u; }
 
 static ifr_status launch_gemv(ifr_ctx *c, const char *fmt, const char *mode, GemvArgs &a, uint32_t cap = 0,
                               uint32_t *grid_out = nullptr) {
-    const uint32_t g = gemv_grid(c, a.total_rows, cap);
+    const uint32_t tr = gemv_tile_rows(mode);
+    uint32_t g = (a.total_rows + tr - 1) / tr;
+    if (c->gemv_max_grid) g = std::min(g, c->gemv_max_grid);
+    if (cap) g = std::min(g, cap);
+    g = std::max(g, 1u);
     if (grid_out) *grid_out = g;
-    std::string name = std::string("gemv_") + fmt + "_" + mode;
-    return c->launch(name, dim3(g), dim3(256), a.cols * 4, a);
+    const bool exact = c->gemv_exact != 0;
+    if (!exact && (!a.xq || (a.total_rows && a.cols % 16)))
+        return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
+    std::string name = std::string("gemv_") + fmt + "_" + mode + (exact ? "_f32" : "");
+    return c->launch(name, dim3(g), dim3(gemv_threads(mode)), gemv_lds_bytes(a.cols, exact), a);
+}
+
+// x (times gamma) -> XQ with per-256 partial sums of x^2.
+static ifr_status launch_quant_act(ifr_ctx *c, const float *x, const float *gamma, uint32_t n, uint8_t *xq,
+                                   float *ss_out, uint32_t *n_parts = nullptr) {
+    QActArgs q{x, gamma, xq, ss_out, n, 0};
+    const uint32_t g = (n + 255) / 256;
+    if (n_parts) *n_parts = g;
+    return c->launch("quant_act_k", dim3(g), dim3(256), 0, q);
+}
+
+// out = W v for a plain f32 v: quantizes v into `xq` first on the integer path.
+static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
+                             const float *v, uint8_t *xq) {
+    GemvPlan p;
+    ifr_status st = check_gemv(c, dtype, cols, w, p);
+    if (st) return st;
+    GemvArgs a{};
+    a.w0 = (const uint8_t *)w;
+    a.total_rows = rows;
+    a.cols = cols;
+    a.nb = p.nb;
+    a.row_bytes = p.row_bytes;
+    a.x = v;
+    a.y = out;
+    if (!c->gemv_exact) {
+        if ((st = launch_quant_act(c, v, nullptr, cols, xq, nullptr))) return st;
+        a.xq = xq;
+    }
+    return launch_gemv(c, p.fmt, "plain", a);
 }
 
 // ------------------------------------------------------------- attention --
@@ -187,11 +235,15 @@ static uint32_t attn_splits_for(uint32_t T) {
     return std::max(s, 1u);
 }
 
+// Split pass over the KV sequence, then the merge of the partials.
 static ifr_status launch_attn(ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, int32_t kv_dtype, AttnArgs &a,
                               uint32_t n_kv_heads) {
     char name[64];
     snprintf(name, sizeof name, "attn_%s_h%u_g%u", kv_dtype == IFR_F16 ? "f16" : "f32", head_size, kv_mul);
-    return c->launch(name, dim3(n_kv_heads, a.n_splits), dim3(256), 0, a);
+    ifr_status st = c->launch(name, dim3(n_kv_heads, a.n_splits), dim3(256), 0, a);
+    if (st) return st;
+    snprintf(name, sizeof name, "attn_merge_h%u_g%u", head_size, kv_mul);
+    return c->launch(name, dim3(n_kv_heads * kv_mul), dim3(512), 0, a);
 }
 
 // ----------------------------------------------------------------- model --
@@ -226,14 +278,21 @@ struct ifr_llama2_state {
     ifr_attn_params *attn_params;
     uint64_t *part_keys;
     float *part_o, *part_ml;
-    uint32_t *counters;
     float *rope_tab;
+    // quantized activations passed between the fused kernels, and the
+    // partial sums of x^2 the RMSNorm consumers reduce:
+    //   xq_a: x * attn_norm (or output_norm), input of QKV / the head
+    //   xq_f: x * ffn_norm, input of gate/up;  xq_att: attention output;
+    //   xq_h: silu(gate) * up;  xq_u: scratch of the one-op-per-kernel path
+    uint8_t *xq_a, *xq_f, *xq_att, *xq_h, *xq_u;
+    float *ss_a, *ss_f;
     uint8_t *kcache, *vcache;
     size_t layer_kv_bytes;
     // captured decode step
     hipGraphExec_t graph = nullptr;
     const ifr_llama2_weights *graph_w = nullptr;
     int graph_fused = -1;
+    int graph_exact = -1;
 };
 
 static ifr_status validate_cfg(ifr_ctx *c, const ifr_llama2_config *cfg) {
@@ -246,47 +305,58 @@ static ifr_status validate_cfg(ifr_ctx *c, const ifr_llama2_config *cfg) {
     if (hs != 64 && hs != 128) return c->fail(IFR_EUNSUPPORTED, "head_size %u (64 or 128 supported)", hs);
     if (kv_mul != 1 && kv_mul != 2 && kv_mul != 4 && kv_mul != 8)
         return c->fail(IFR_EUNSUPPORTED, "kv_mul %u (1, 2, 4 or 8 supported)", kv_mul);
+    if (cfg->hidden % 32 || cfg->ffn % 32) return c->fail(IFR_EUNSUPPORTED, "hidden and ffn must be multiples of 32");
     if (cfg->kv_dtype != IFR_F16 && cfg->kv_dtype != IFR_F32) return c->fail(IFR_EINVAL, "kv_dtype must be F16 or F32");
     if (cfg->rope_variant != IFR_ROPE_ORIGINAL && cfg->rope_variant != IFR_ROPE_NEOX)
         return c->fail(IFR_EINVAL, "bad rope_variant");
-    if (cfg->max_pos > ATTN_CMAX * 1024u) return c->fail(IFR_EUNSUPPORTED, "max_pos too large");
+    if (cfg->max_pos > ATTN_CMAX * ATTN_MERGE_MAX) return c->fail(IFR_EUNSUPPORTED, "max_pos too large");
     return IFR_OK;
 }
 
-// Enqueues one decode step.
+// Enqueues one decode step.  Fused: per layer QKV+RoPE+KV store, attention
+// (split + merge), O + residual, gate/up + SiLU, down + residual; activations
+// travel between them quantized (integer path) and in f32 (exact path and the
+// residual stream).  Unfused: one kernel per reference op (transformer.rs:418-469).
 static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
     const ifr_llama2_config &cfg = s->cfg;
-    const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn;
+    const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn, L = cfg.n_layers;
+    const uint32_t n_ss_res = hidden / 16; // partial sums written by a RESID GEMV (one per 16-row tile)
     ifr_status st;
 
-    {   // x <- token_embd[tokens[pos]]
+    uint32_t n_ss_a;
+    {   // x <- token_embd[tokens[pos]], and x * attn_norm(0) quantized
         EmbedArgs e{};
         e.x = s->x;
         e.table = w->token_embd.data;
         e.tokens = s->tokens;
         e.ctl = s->ctl;
+        e.xq_out = s->xq_a;
+        e.ss_out = s->ss_a;
+        e.gamma = (const float *)w->layers[0].attn_norm.data;
         e.hidden = hidden;
         e.row_bytes = hidden / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
         e.fmt = w->token_embd.dtype;
-        if ((st = c->launch("embed_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
+        n_ss_a = (hidden + 255) / 256;
+        if ((st = c->launch("embed_k", dim3(n_ss_a), dim3(256), 0, e))) return st;
     }
 
-    for (uint32_t l = 0; l < cfg.n_layers; l++) {
-        const LayerW &L = w->layers[l];
+    for (uint32_t l = 0; l < L; l++) {
+        const LayerW &Lw = w->layers[l];
         uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
         uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
-        const bool fuse_qkv = fused && L.attn_q.dtype == L.attn_k.dtype && L.attn_q.dtype == L.attn_v.dtype &&
+        const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype &&
                               cfg.rope_variant == IFR_ROPE_ORIGINAL;
-        const bool fuse_ffn = fused && L.ffn_gate.dtype == L.ffn_up.dtype;
+        const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
+        const float *next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
         GemvPlan p;
 
         // ---- attention block
         if (fuse_qkv) {
-            if ((st = check_gemv(c, L.attn_q.dtype, hidden, L.attn_q.data, p))) return st;
+            if ((st = check_gemv(c, Lw.attn_q.dtype, hidden, Lw.attn_q.data, p))) return st;
             GemvArgs a{};
-            a.w0 = L.attn_q.data;
-            a.w1 = L.attn_k.data;
-            a.w2 = L.attn_v.data;
+            a.w0 = Lw.attn_q.data;
+            a.w1 = Lw.attn_k.data;
+            a.w2 = Lw.attn_v.data;
             a.rows0 = hidden;
             a.rows1 = kv_dim;
             a.rows2 = kv_dim;
@@ -295,7 +365,10 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.nb = p.nb;
             a.row_bytes = p.row_bytes;
             a.x = s->x;
-            a.gamma = (const float *)L.attn_norm.data;
+            a.gamma = (const float *)Lw.attn_norm.data;
+            a.xq = s->xq_a;
+            a.ss_part = s->ss_a;
+            a.n_ss = n_ss_a;
             a.eps = cfg.rms_eps;
             a.rope_tab = s->rope_tab;
             a.y = s->q;
@@ -310,24 +383,15 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             EltArgs n{};
             n.a = s->xb;
             n.b = s->x;
-            n.w = (const float *)L.attn_norm.data;
+            n.w = (const float *)Lw.attn_norm.data;
             n.cfg = s->rms_cfg;
             n.n = hidden;
             if ((st = c->launch("rms_norm_k", dim3(1), dim3(1024), 0, n))) return st;
-            const Tens *mats[3] = {&L.attn_q, &L.attn_k, &L.attn_v};
+            const Tens *mats[3] = {&Lw.attn_q, &Lw.attn_k, &Lw.attn_v};
             float *outs[3] = {s->q, s->ktmp, s->vtmp};
-            for (int m = 0; m < 3; m++) {
-                if ((st = check_gemv(c, mats[m]->dtype, hidden, mats[m]->data, p))) return st;
-                GemvArgs a{};
-                a.w0 = mats[m]->data;
-                a.total_rows = mats[m]->rows;
-                a.cols = hidden;
-                a.nb = p.nb;
-                a.row_bytes = p.row_bytes;
-                a.x = s->xb;
-                a.y = outs[m];
-                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
-            }
+            for (int m = 0; m < 3; m++)
+                if ((st = gemv_plain(c, outs[m], mats[m]->data, mats[m]->dtype, mats[m]->rows, hidden, s->xb, s->xq_u)))
+                    return st;
             EltArgs r{};
             r.a = s->q;
             r.k = s->ktmp;
@@ -352,102 +416,105 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.k_cache = kc;
             a.v_cache = vc;
             a.out = s->att;
+            a.xq_out = fused ? s->xq_att : nullptr;
             a.part_o = s->part_o;
             a.part_ml = s->part_ml;
-            a.counters = s->counters;
             a.pos = &s->ctl->pos;
             a.kv_dim = kv_dim;
             a.n_splits = s->n_splits;
             a.seq_cap = cfg.max_pos;
+            a.n_out = hidden;
             if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, a, cfg.n_kv_heads))) return st;
         }
-        if ((st = check_gemv(c, L.attn_output.dtype, hidden, L.attn_output.data, p))) return st;
-        {
+        if (fused) {   // x += Wo att; x * ffn_norm quantized for gate/up
+            if ((st = check_gemv(c, Lw.attn_output.dtype, hidden, Lw.attn_output.data, p))) return st;
             GemvArgs a{};
-            a.w0 = L.attn_output.data;
+            a.w0 = Lw.attn_output.data;
             a.total_rows = hidden;
             a.cols = hidden;
             a.nb = p.nb;
             a.row_bytes = p.row_bytes;
             a.x = s->att;
-            if (fused) {
-                a.y = s->x; // x += Wo att
-                if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
-            } else {
-                a.y = s->xb2;
-                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
-                EltArgs e{};
-                e.a = s->x;
-                e.b = s->xb2;
-                e.n = hidden;
-                if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
-            }
+            a.xq = s->xq_att;
+            a.y = s->x;
+            a.xq_out = s->xq_f;
+            a.ss_out = s->ss_f;
+            a.gamma_next = (const float *)Lw.ffn_norm.data;
+            if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
+        } else {
+            if ((st = gemv_plain(c, s->xb2, Lw.attn_output.data, Lw.attn_output.dtype, hidden, hidden, s->att, s->xq_u)))
+                return st;
+            EltArgs e{};
+            e.a = s->x;
+            e.b = s->xb2;
+            e.n = hidden;
+            if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
         }
 
         // ---- feed-forward block
         if (fuse_ffn) {
-            if ((st = check_gemv(c, L.ffn_gate.dtype, hidden, L.ffn_gate.data, p))) return st;
+            if ((st = check_gemv(c, Lw.ffn_gate.dtype, hidden, Lw.ffn_gate.data, p))) return st;
             GemvArgs a{};
-            a.w0 = L.ffn_gate.data;
-            a.w1 = L.ffn_up.data;
+            a.w0 = Lw.ffn_gate.data;
+            a.w1 = Lw.ffn_up.data;
             a.total_rows = 2 * ffn;
             a.cols = hidden;
             a.nb = p.nb;
             a.row_bytes = p.row_bytes;
             a.x = s->x;
-            a.gamma = (const float *)L.ffn_norm.data;
+            a.gamma = (const float *)Lw.ffn_norm.data;
+            a.xq = s->xq_f;
+            a.ss_part = s->ss_f;
+            a.n_ss = n_ss_res;
             a.eps = cfg.rms_eps;
             a.y = s->hb;
+            a.xq_out = s->xq_h;
             if ((st = launch_gemv(c, p.fmt, "gateup", a))) return st;
         } else {
             EltArgs n{};
             n.a = s->xb;
             n.b = s->x;
-            n.w = (const float *)L.ffn_norm.data;
+            n.w = (const float *)Lw.ffn_norm.data;
             n.cfg = s->rms_cfg;
             n.n = hidden;
             if ((st = c->launch("rms_norm_k", dim3(1), dim3(1024), 0, n))) return st;
-            const Tens *mats[2] = {&L.ffn_gate, &L.ffn_up};
+            const Tens *mats[2] = {&Lw.ffn_gate, &Lw.ffn_up};
             float *outs[2] = {s->hb, s->hb2};
-            for (int m = 0; m < 2; m++) {
-                if ((st = check_gemv(c, mats[m]->dtype, hidden, mats[m]->data, p))) return st;
-                GemvArgs a{};
-                a.w0 = mats[m]->data;
-                a.total_rows = ffn;
-                a.cols = hidden;
-                a.nb = p.nb;
-                a.row_bytes = p.row_bytes;
-                a.x = s->xb;
-                a.y = outs[m];
-                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
-            }
+            for (int m = 0; m < 2; m++)
+                if ((st = gemv_plain(c, outs[m], mats[m]->data, mats[m]->dtype, ffn, hidden, s->xb, s->xq_u))) return st;
             EltArgs e{};
             e.a = s->hb;
             e.b = s->hb2;
             e.n = ffn;
             if ((st = c->launch("silu_k", dim3((ffn + 255) / 256), dim3(256), 0, e))) return st;
+            if (fused && (st = launch_quant_act(c, s->hb, nullptr, ffn, s->xq_h, nullptr))) return st;
         }
-        if ((st = check_gemv(c, L.ffn_down.dtype, ffn, L.ffn_down.data, p))) return st;
-        {
+        if (fused) {   // x += Wdown h; x * next norm quantized for the next QKV / the head
+            if ((st = check_gemv(c, Lw.ffn_down.dtype, ffn, Lw.ffn_down.data, p))) return st;
             GemvArgs a{};
-            a.w0 = L.ffn_down.data;
+            a.w0 = Lw.ffn_down.data;
             a.total_rows = hidden;
             a.cols = ffn;
             a.nb = p.nb;
             a.row_bytes = p.row_bytes;
             a.x = s->hb;
-            if (fused) {
-                a.y = s->x;
-                if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
-            } else {
-                a.y = s->xb2;
-                if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
-                EltArgs e{};
-                e.a = s->x;
-                e.b = s->xb2;
-                e.n = hidden;
-                if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
-            }
+            a.xq = s->xq_h;
+            a.y = s->x;
+            a.xq_out = s->xq_a;
+            a.ss_out = s->ss_a;
+            a.gamma_next = next_norm;
+            if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
+            n_ss_a = n_ss_res;
+        } else {
+            if ((st = gemv_plain(c, s->xb2, Lw.ffn_down.data, Lw.ffn_down.dtype, hidden, ffn, s->hb, s->xq_u))) return st;
+            EltArgs e{};
+            e.a = s->x;
+            e.b = s->xb2;
+            e.n = hidden;
+            if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
+        }
+        if (fused && !fuse_qkv && l + 1 < L) {
+            // the next layer's unfused QKV reads f32 xb; nothing to quantize
         }
     }
 
@@ -465,6 +532,9 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         a.row_bytes = p.row_bytes;
         a.x = s->x;
         a.gamma = (const float *)w->output_norm.data;
+        a.xq = s->xq_a;
+        a.ss_part = s->ss_a;
+        a.n_ss = n_ss_a;
         a.eps = cfg.rms_eps;
         a.y = s->logits;
         a.part_keys = s->part_keys;
@@ -477,15 +547,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         n.cfg = s->rms_cfg;
         n.n = hidden;
         if ((st = c->launch("rms_norm_k", dim3(1), dim3(1024), 0, n))) return st;
-        GemvArgs a{};
-        a.w0 = out.data;
-        a.total_rows = cfg.vocab;
-        a.cols = hidden;
-        a.nb = p.nb;
-        a.row_bytes = p.row_bytes;
-        a.x = s->xb;
-        a.y = s->logits;
-        if ((st = launch_gemv(c, p.fmt, "plain", a))) return st;
+        if ((st = gemv_plain(c, s->logits, out.data, out.dtype, cfg.vocab, hidden, s->xb, s->xq_u))) return st;
         ArgmaxArgs m{};
         m.v = s->logits;
         m.n = cfg.vocab;
@@ -553,7 +615,7 @@ IFR_API void ifr_destroy(ifr_ctx *c) {
     hipSetDevice(c->device);
     hipStreamSynchronize(c->stream);
     if (c->scratch) hipFree(c->scratch);
-    if (c->attn_counters) hipFree(c->attn_counters);
+    if (c->xq_scratch) hipFree(c->xq_scratch);
     for (auto &e : c->events)
         if (e) hipEventDestroy(e);
     if (c->module) hipModuleUnload(c->module);
@@ -574,6 +636,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
     if (!c || !key) return IFR_EINVAL;
     if (!strcmp(key, "gemv_max_grid")) {
         c->gemv_max_grid = (uint32_t)std::max<int64_t>(0, value);
+        return IFR_OK;
+    }
+    if (!strcmp(key, "gemv_exact")) {
+        c->gemv_exact = value ? 1 : 0;
         return IFR_OK;
     }
     return c->fail(IFR_EINVAL, "unknown option %s", key);
@@ -652,6 +718,31 @@ IFR_API ifr_status ifr_matmul_quant(ifr_ctx *c, float *out, const void *w, int32
     if (!out || !w || !v) return c->fail(IFR_EINVAL, "matmul_quant: null pointer");
     if (!rows) return IFR_OK;
     if ((uintptr_t)v % 16) return c->fail(IFR_EINVAL, "matmul_quant: v not 16-byte aligned");
+    ifr_status st = c->ensure_xq_scratch(xq_bytes(cols));
+    if (st) return st;
+    return gemv_plain(c, out, w, dtype, rows, cols, v, (uint8_t *)c->xq_scratch);
+}
+
+IFR_API uint64_t ifr_activation_bytes(uint32_t n) { return xq_bytes(n); }
+
+IFR_API ifr_status ifr_quantize_activation(ifr_ctx *c, void *xq, const float *x, const float *gamma, uint32_t n,
+                                           float *ss_out) {
+    if (!c) return IFR_EINVAL;
+    if (!xq || !x) return c->fail(IFR_EINVAL, "quantize_activation: null pointer");
+    if (n % 32) return c->fail(IFR_EINVAL, "quantize_activation: n must be a multiple of 32");
+    if ((uintptr_t)xq % 16) return c->fail(IFR_EINVAL, "quantize_activation: xq not 16-byte aligned");
+    if (!n) return IFR_OK;
+    return launch_quant_act(c, x, gamma, n, (uint8_t *)xq, ss_out);
+}
+
+IFR_API ifr_status ifr_matmul_quant_xq(ifr_ctx *c, float *out, const void *w, int32_t dtype, uint32_t rows,
+                                       uint32_t cols, const void *xq) {
+    if (!c) return IFR_EINVAL;
+    if (!out || !w || !xq) return c->fail(IFR_EINVAL, "matmul_quant_xq: null pointer");
+    if (c->gemv_exact) return c->fail(IFR_EINVAL, "matmul_quant_xq: needs the integer path (gemv_exact = 0)");
+    if ((uintptr_t)xq % 16) return c->fail(IFR_EINVAL, "matmul_quant_xq: xq not 16-byte aligned");
+    if (cols % 32) return c->fail(IFR_EINVAL, "matmul_quant_xq: cols must be a multiple of 32");
+    if (!rows) return IFR_OK;
     GemvPlan p;
     ifr_status st = check_gemv(c, dtype, cols, w, p);
     if (st) return st;
@@ -661,7 +752,7 @@ IFR_API ifr_status ifr_matmul_quant(ifr_ctx *c, float *out, const void *w, int32
     a.cols = cols;
     a.nb = p.nb;
     a.row_bytes = p.row_bytes;
-    a.x = v;
+    a.xq = (const uint8_t *)xq;
     a.y = out;
     return launch_gemv(c, p.fmt, "plain", a);
 }
@@ -733,13 +824,13 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     const uint32_t n_kv = p->n_heads / g;
     if (p->kv_dim != n_kv * p->head_size) return c->fail(IFR_EINVAL, "attention: kv_dim != n_kv_heads * head_size");
     if (p->pos >= p->seq_len) return c->fail(IFR_EINVAL, "attention: pos %u >= seq_len %u", p->pos, p->seq_len);
+    if (p->pos >= ATTN_CMAX * ATTN_MERGE_MAX) return c->fail(IFR_EUNSUPPORTED, "attention: pos %u too large", p->pos);
     if ((uintptr_t)q % 16 || (uintptr_t)kc % 16 || (uintptr_t)vc % 16)
         return c->fail(IFR_EINVAL, "attention: q and caches must be 16-byte aligned");
     const uint32_t T = p->pos + 1, S = attn_splits_for(T);
     const size_t part_o = (size_t)n_kv * S * g * p->head_size, part_ml = (size_t)n_kv * S * g * 2;
     ifr_status st = c->ensure_scratch((part_o + part_ml) * sizeof(float));
     if (st) return st;
-    if ((st = c->ensure_counters(n_kv))) return st;
     AttnArgs a{};
     a.q = q;
     a.k_cache = kc;
@@ -747,7 +838,6 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     a.out = xb;
     a.part_o = (float *)c->scratch;
     a.part_ml = (float *)c->scratch + part_o;
-    a.counters = c->attn_counters;
     a.pos = &dev_p->pos;
     a.kv_dim = p->kv_dim;
     a.n_splits = S;
@@ -915,8 +1005,9 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     A(s->part_keys, MAX_PARTS * 8)
     A(s->part_o, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * s->head_size * 4)
     A(s->part_ml, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * 2 * 4)
-    A(s->counters, (size_t)cfg->n_kv_heads * 4)
     A(s->rope_tab, (size_t)s->head_size / 2 * 4)
+    A(s->xq_a, xq_bytes(H)) A(s->xq_f, xq_bytes(H)) A(s->xq_att, xq_bytes(H)) A(s->xq_h, xq_bytes(F))
+    A(s->xq_u, xq_bytes(std::max(H, F))) A(s->ss_a, H / 16 * 4) A(s->ss_f, H / 16 * 4)
     A(s->kcache, s->layer_kv_bytes * cfg->n_layers)
     A(s->vcache, s->layer_kv_bytes * cfg->n_layers)
 #undef A
@@ -992,7 +1083,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
             if ((st = enqueue_step(c, s, w, 1))) return st;
         return IFR_OK;
     }
-    if (!s->graph || s->graph_w != w || s->graph_fused != 1) {
+    if (!s->graph || s->graph_w != w || s->graph_fused != 1 || s->graph_exact != c->gemv_exact) {
         if (s->graph) {
             hipStreamSynchronize(c->stream);
             hipGraphExecDestroy(s->graph);
@@ -1013,6 +1104,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         if (st) return st;
         s->graph_w = w;
         s->graph_fused = 1;
+        s->graph_exact = c->gemv_exact;
     }
     for (uint32_t i = 0; i < n_steps; i++)
         if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;

@@ -18,6 +18,18 @@ enum GemvMode : int32_t {
     GEMV_HEAD = 4,   // rmsnorm(x) -> logits = W x, per-workgroup argmax keys
 };
 
+// GEMV launch geometry per mode, shared by the kernels and the host: R rows
+// per wave, W waves per workgroup (a workgroup tile is W*R rows).  RESID and
+// GATEUP tiles hold exactly one 16-value output activation group (GATEUP's
+// 32 virtual rows are 16 gate/up pairs).  Measured on MI355X: two rows per
+// wave, no software pipelining and four waves per SIMD stream best.
+struct GemvGeomT {
+    int R, W;
+};
+constexpr GemvGeomT gemv_geom(int mode) {
+    return mode == GEMV_RESID ? GemvGeomT{2, 8} : mode == GEMV_GATEUP ? GemvGeomT{2, 16} : GemvGeomT{2, 4};
+}
+
 // Device copies of the C ABI's op configs (same layout as ifr_rms_norm_config
 // and ifr_rope_config in include/inferi_hip.h).
 struct ifr_rms_cfg_dev {
@@ -44,13 +56,18 @@ struct GemvArgs {
     uint32_t cols;                // K
     uint32_t nb;                  // blocks per row
     uint32_t row_bytes;           // bytes per row
-    uint32_t pad0;
-    const float *x;      // input vector [cols]
-    const float *gamma;  // RMSNorm weight [cols] (QKV, GATEUP, HEAD)
+    uint32_t n_ss;                // integer path + RMSNorm: number of partial sums in ss_part
+    const float *x;      // exact path: input vector [cols]
+    const float *gamma;  // exact path: RMSNorm weight [cols]
+    const uint8_t *xq;   // integer path: the input, quantized (XQ layout, device/gemv.h)
+    const float *ss_part; // integer path + RMSNorm: partial sums of x^2 of the input
     float eps;           // RMSNorm epsilon
-    uint32_t pad2;
+    uint32_t pad0;
+    float *y;            // PLAIN/HEAD: out[rows]; RESID: x (+=); QKV: q; GATEUP: h
+    uint8_t *xq_out;     // RESID/GATEUP: the output quantized for the next GEMV (may be null)
+    float *ss_out;       // RESID: per-tile partial sums of x^2 of the output
+    const float *gamma_next; // RESID: RMSNorm weight of the next GEMV, applied before quantizing
     const float *rope_tab; // QKV: theta of each pair within a head [head_size/2]
-    float *y;            // PLAIN/RESID/HEAD: out[rows]; QKV: q; GATEUP: h
     void *k_cache;       // QKV: cache base of this layer, [max_pos][kv_dim]
     void *v_cache;
     const StepCtl *ctl;  // QKV: position
@@ -65,14 +82,14 @@ struct AttnArgs {
     const void *k_cache;      // [seq_len][kv_dim]
     const void *v_cache;
     float *out;               // [n_heads * head_size]
+    uint8_t *xq_out;          // merge: the output quantized for the next GEMV (may be null)
     float *part_o;            // [n_kv_heads][n_splits][kv_mul][head_size]
     float *part_ml;           // [n_kv_heads][n_splits][kv_mul][2]
-    uint32_t *counters;       // [n_kv_heads], zero between launches
     const uint32_t *pos;      // device position
     uint32_t kv_dim;
     uint32_t n_splits;        // gridDim.y
     uint32_t seq_cap;         // positions attended never exceed this (cache rows)
-    uint32_t pad;
+    uint32_t n_out;           // n_heads * head_size (length of xq_out)
 };
 
 struct EltArgs {
@@ -126,9 +143,23 @@ struct EmbedArgs {
     const uint8_t *table;
     const uint32_t *tokens;
     const StepCtl *ctl;
+    uint8_t *xq_out;          // x * gamma quantized for the first GEMV (may be null)
+    float *ss_out;            // per-workgroup partial sums of x^2
+    const float *gamma;       // RMSNorm weight of the first GEMV
     uint32_t hidden;
     uint32_t row_bytes;
     int32_t fmt;
+    uint32_t pad;
+};
+
+// Quantizes an activation vector (XQ layout), optionally times gamma, with
+// per-workgroup partial sums of x^2.
+struct QActArgs {
+    const float *x;
+    const float *gamma;
+    uint8_t *xq_out;
+    float *ss_out;
+    uint32_t n;
     uint32_t pad;
 };
 

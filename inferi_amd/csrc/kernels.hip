@@ -8,15 +8,26 @@
 
 using namespace ifr;
 
-#define GEMV_KERNEL(NAME, FMT, MODE) \
-    extern "C" __global__ void __launch_bounds__(256) NAME(GemvArgs a) { gemv_body<FMT, MODE>(a); }
+// gemv_<fmt>_<mode>: integer path (x quantized by its producer, v_dot4);
+// gemv_<fmt>_<mode>_f32: exact fp32 path.
+// Four waves per SIMD (at most 128 VGPRs) keeps enough loads in flight.
+#define GEMV_KERNEL(NAME, FMT, MODE, XI)                                                               \
+    extern "C" __global__ void __launch_bounds__(GemvGeom<MODE>::W * 64)                             \
+        __attribute__((amdgpu_waves_per_eu(4, 8))) NAME(GemvArgs a) {                                \
+        gemv_body<FMT, MODE, XI>(a);                                                                 \
+    }
 
-#define GEMV_ALL_MODES(FMTNAME, FMT)                            \
-    GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)       \
-    GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID)       \
-    GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)           \
-    GEMV_KERNEL(gemv_##FMTNAME##_gateup, FMT, GEMV_GATEUP)     \
-    GEMV_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD)
+#define GEMV_ALL_MODES(FMTNAME, FMT)                                  \
+    GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN, true)       \
+    GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID, true)       \
+    GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV, true)           \
+    GEMV_KERNEL(gemv_##FMTNAME##_gateup, FMT, GEMV_GATEUP, true)     \
+    GEMV_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD, true)         \
+    GEMV_KERNEL(gemv_##FMTNAME##_plain_f32, FMT, GEMV_PLAIN, false)  \
+    GEMV_KERNEL(gemv_##FMTNAME##_resid_f32, FMT, GEMV_RESID, false)  \
+    GEMV_KERNEL(gemv_##FMTNAME##_qkv_f32, FMT, GEMV_QKV, false)      \
+    GEMV_KERNEL(gemv_##FMTNAME##_gateup_f32, FMT, GEMV_GATEUP, false)\
+    GEMV_KERNEL(gemv_##FMTNAME##_head_f32, FMT, GEMV_HEAD, false)
 
 GEMV_ALL_MODES(q4_k, Q4_K)
 GEMV_ALL_MODES(q5_k, Q5_K)
@@ -29,6 +40,9 @@ GEMV_ALL_MODES(q8_0, Q8_0)
     }                                                                                               \
     extern "C" __global__ void __launch_bounds__(256) attn_f32_h##HS##_g##G(AttnArgs a) {           \
         attn_body<HS, G, false>(a);                                                                 \
+    }                                                                                               \
+    extern "C" __global__ void __launch_bounds__(512) attn_merge_h##HS##_g##G(AttnArgs a) {         \
+        attn_merge_body<HS, G>(a);                                                                  \
     }
 
 ATTN_KERNEL(64, 1)
@@ -47,6 +61,7 @@ extern "C" __global__ void __launch_bounds__(256) add_k(EltArgs a) { add_body(a)
 extern "C" __global__ void __launch_bounds__(256) argmax_part_k(ArgmaxArgs a) { argmax_part_body(a); }
 extern "C" __global__ void __launch_bounds__(1024) argmax_final_k(ArgmaxArgs a) { argmax_final_body(a); }
 extern "C" __global__ void __launch_bounds__(256) embed_k(EmbedArgs a) { embed_body(a); }
+extern "C" __global__ void __launch_bounds__(256) quant_act_k(QActArgs a) { quant_act_body(a); }
 extern "C" __global__ void __launch_bounds__(256) kv_store_k(KvStoreArgs a) { kv_store_body(a); }
 extern "C" __global__ void __launch_bounds__(256) dequant_k(DequantArgs a) { dequant_body(a); }
 extern "C" __global__ void __launch_bounds__(64) quantize_k(QuantArgs a) { quantize_body(a); }

@@ -62,12 +62,14 @@ def run_steps(ctx, state, weights, prompt, n_total, mode):
     return logits, state.tokens(0, n_total + 1)
 
 
+@pytest.mark.parametrize("exact", [False, True], ids=["int", "exact"])
 @pytest.mark.parametrize("mode", ["fused", "unfused", "graph"])
 @pytest.mark.parametrize("mat,head,kv", [("Q4_K", "Q6_K", "F16"), ("Q8_0", "Q8_0", "F32"), ("Q5_K", "Q4_K", "F16"),
                                          ("Q6_K", "Q5_K", "F32")])
-def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv):
+def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv, exact):
     import inferi_amd as I
 
+    ctx.set_option("gemv_exact", int(exact))
     dt = {"Q4_K": I.Q4_K, "Q5_K": I.Q5_K, "Q6_K": I.Q6_K, "Q8_0": I.Q8_0, "F16": I.F16, "F32": I.F32}
     cfg = tiny_cfg(kv_dtype=dt[kv])
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=11, mat_dtype=dt[mat], head_dtype=dt[head], embd_dtype=dt[mat],
@@ -98,6 +100,7 @@ def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv):
                     got, ref = O.decode_f16(got), O.decode_f16(ref)
                 assert_close(got, ref, tol=2e-3, what=f"{which} cache layer {layer}")
     finally:
+        ctx.set_option("gemv_exact", 0)
         s.close()
         w.close()
 
