@@ -117,7 +117,9 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
 
 
 def run_decode(args) -> None:
-    ctx = I.LlmContext(0)
+    ctx = I.LlmContext(0, args.code_object)
+    ctx.set_option("gemv_max_grid", args.gemv_grid)
+    ctx.set_option("gemv_waves", args.gemv_waves)
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
@@ -210,7 +212,9 @@ def run_decode(args) -> None:
 
 
 def run_sweep(args) -> None:
-    ctx = I.LlmContext(0)
+    ctx = I.LlmContext(0, args.code_object)
+    ctx.set_option("gemv_max_grid", args.gemv_grid)
+    ctx.set_option("gemv_waves", args.gemv_waves)
     rows_out = []
     for name, dt in (("Q4_K", I.Q4_K), ("Q5_K", I.Q5_K), ("Q6_K", I.Q6_K), ("Q8_0", I.Q8_0)):
         for rows, cols in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
@@ -224,7 +228,9 @@ def run_sweep(args) -> None:
 
 
 def run_attn(args) -> None:
-    ctx = I.LlmContext(0)
+    ctx = I.LlmContext(0, args.code_object)
+    ctx.set_option("gemv_max_grid", args.gemv_grid)
+    ctx.set_option("gemv_waves", args.gemv_waves)
     out = []
     nh, nkv, hs = 32, 8, 128
     kv_dim = nkv * hs
@@ -283,6 +289,9 @@ def main() -> None:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")
+    ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
+    ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
+    ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU; the multi-GPU sharding of the decode path is designed "

@@ -79,11 +79,12 @@ IFR_API const char *ifr_last_error(const ifr_ctx *ctx);
 /* Device name and compute-unit count, for reports. */
 IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, int32_t *n_cu);
 
-/* Knobs (no reference counterpart): "gemv_max_grid" caps the number of GEMV
- * workgroups (0 = one per 16-row tile, the default); "gemv_exact" = 1 makes
- * every GEMV keep x in fp32 and use fp32 FMAs, instead of the default path
- * that takes x as 22-bit fixed point per 16 elements and multiplies with
- * int8 dot products (see ifr_quantize_activation). */
+/* Knobs (no reference counterpart): "gemv_max_grid" sets the number of GEMV
+ * workgroups (0 = chosen by shape, the default); "gemv_waves" caps the
+ * waves per GEMV workgroup (1..16, 0 = chosen by shape); "gemv_exact" = 1
+ * makes every GEMV keep x in fp32 and use fp32 FMAs, instead of the default
+ * path that takes x as 22-bit fixed point per 16 elements and multiplies
+ * with int8 dot products (see ifr_quantize_activation). */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */

@@ -78,6 +78,15 @@ IFR_DEV float wave_max(float v) {
     return v;
 }
 
+// Workgroup barrier that orders LDS only: this wave's LDS operations are
+// complete (lgkmcnt 0) before it arrives, and no memory access is moved
+// across it by the compiler.  Unlike __syncthreads it does not wait for the
+// wave's outstanding global loads, so weights prefetched for the next item
+// stay in flight.  Use only where the waves exchange data through LDS.
+IFR_DEV void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // 16 bytes at a 16-byte aligned address.
 IFR_DEV uint4 ld16(const uint8_t *p) {
     u32x4_a16 v = *(const u32x4_a16 *)p;

@@ -41,15 +41,16 @@ IFR_DEV void scale_min_pair(uint32_t g, uint32_t w0, uint32_t w1, uint32_t w2, u
                             uint32_t &sc1, uint32_t &m1) {
     const uint32_t sh = 16u * (g & 1u);
     const uint32_t a0 = w0 >> sh, a1 = w1 >> sh, a2 = w2 >> sh;
-    const bool lo = g < 2;
     // j < 4: sc = q[j] & 63, m = q[j+4] & 63
     // j >= 4: sc = (q[j+4] & 15) | (q[j-4] >> 6) << 4, m = (q[j+4] >> 4) | (q[j] >> 6) << 4
     const uint32_t hs0 = ((a0 >> 6) & 3u) << 4, hm0 = ((a1 >> 6) & 3u) << 4;
     const uint32_t hs1 = ((a0 >> 14) & 3u) << 4, hm1 = ((a1 >> 14) & 3u) << 4;
-    sc0 = lo ? (a0 & 63u) : ((a2 & 15u) | hs0);
-    m0 = lo ? (a1 & 63u) : (((a2 >> 4) & 15u) | hm0);
-    sc1 = lo ? ((a0 >> 8) & 63u) : (((a2 >> 8) & 15u) | hs1);
-    m1 = lo ? ((a1 >> 8) & 63u) : (((a2 >> 12) & 15u) | hm1);
+    // all ones for g >= 2: a bit select, so the compiler emits no branch
+    const uint32_t mk = 0u - (g >> 1);
+    sc0 = ((a0 & 63u) & ~mk) | (((a2 & 15u) | hs0) & mk);
+    m0 = ((a1 & 63u) & ~mk) | ((((a2 >> 4) & 15u) | hm0) & mk);
+    sc1 = (((a0 >> 8) & 63u) & ~mk) | ((((a2 >> 8) & 15u) | hs1) & mk);
+    m1 = (((a1 >> 8) & 63u) & ~mk) | ((((a2 >> 12) & 15u) | hm1) & mk);
 }
 
 IFR_DEV void lds16(const float *p, float *x) {
@@ -296,7 +297,7 @@ IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int 
     }
 }
 
-IFR_DEV uint4 lds_u4(const int8_t *p) { return *(const uint4 *)__builtin_assume_aligned(p, 16); }
+IFR_DEV uint4 ld_u4(const int8_t *p) { return *(const uint4 *)__builtin_assume_aligned(p, 16); }
 IFR_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 // c + sum over four words of codes q and x digits
 IFR_DEV int sdot16(uint4 q, uint4 x, int c) {
@@ -308,11 +309,11 @@ IFR_DEV int sdot16(uint4 q, uint4 x, int c) {
 IFR_DEV uint4 and4(uint4 q, uint32_t m) { return make_uint4(q.x & m, q.y & m, q.z & m, q.w & m); }
 IFR_DEV uint4 shr4(uint4 q, uint32_t s) { return make_uint4(q.x >> s, q.y >> s, q.z >> s, q.w >> s); }
 
-// x digits of one 16-element group in LDS
+// x digits of one 16-element group
 struct XG {
     uint4 a, b, c;
 };
-IFR_DEV XG xg_load(const XQ &x, uint32_t e) { return XG{lds_u4(x.xa + e), lds_u4(x.xb + e), lds_u4(x.xc + e)}; }
+IFR_DEV XG xg_load(const XQ &x, uint32_t e) { return XG{ld_u4(x.xa + e), ld_u4(x.xb + e), ld_u4(x.xc + e)}; }
 // sum_e q_e v_e of one group for codes 0 <= q <= 63: exact in int32
 IFR_DEV int gdot_u(uint4 q, const XG &x) {
     return sdot16(q, x.c, sdot16(q, x.b, sdot16(q, x.a, 0) << 8) << 8);
@@ -324,11 +325,22 @@ IFR_DEV float gdot_s(uint4 q, const XG &x) {
     return fmaf((float)hi, 65536.0f, (float)lo);
 }
 
+// The integer chunks give the GEMV body four operations for the step of one
+// lane: xscales (the scales and sums of the lane's four activation groups),
+// xgroup (the x digits of group q), gdot (the exact int32 dot of row r's
+// codes in group q with those digits) and combine (block and group scales
+// applied in fp32, added to acc[r]).  The body feeds one group at a time so
+// only one group of x digits is live in registers.
+struct XS4 {
+    float4 s, S;
+};
+
 template <int FMT, int R>
 struct ChunkI;
 
 // Q4_K, 4 lanes per block: lane g owns sub-blocks 2g (low nibbles, elements
 // 64g+l) and 2g+1 (high nibbles, 64g+32+l), l = 0..31: qs bytes [32g, 32g+32).
+// Group q = 0..3 holds elements 64g + 16q + (0..15).
 template <int R>
 struct ChunkI<Q4_K, R> {
     static constexpr int LPB = 4;
@@ -342,41 +354,28 @@ struct ChunkI<Q4_K, R> {
             q1[r] = ld16(b + 32 + 32 * g);
         }
     }
-    IFR_DEV void compute(uint32_t kb, uint32_t g, const XQ &x, float *acc) const {
+    static IFR_DEV XS4 xscales(const XQ &x, uint32_t kb, uint32_t g) {
         const uint32_t e = kb * 256 + 64 * g;
-        const float4 s = *(const float4 *)__builtin_assume_aligned(x.xs + e / 16, 16);
-        const float4 S = *(const float4 *)__builtin_assume_aligned(x.xsum + e / 16, 16);
+        return XS4{*(const float4 *)__builtin_assume_aligned(x.xs + e / 16, 16),
+                   *(const float4 *)__builtin_assume_aligned(x.xsum + e / 16, 16)};
+    }
+    static IFR_DEV XG xgroup(const XQ &x, uint32_t kb, uint32_t g, int q) { return xg_load(x, kb * 256 + 64 * g + 16 * q); }
+    IFR_DEV int gdot(uint32_t, int q, int r, const XG &xg) const {
         const uint32_t M = 0x0F0F0F0Fu;
-        int i0[R], i1[R], i2[R], i3[R];
-        {
-            const XG xg = xg_load(x, e);
-#pragma unroll
-            for (int r = 0; r < R; r++) i0[r] = gdot_u(and4(q0[r], M), xg);
-        }
-        {
-            const XG xg = xg_load(x, e + 16);
-#pragma unroll
-            for (int r = 0; r < R; r++) i1[r] = gdot_u(and4(q1[r], M), xg);
-        }
-        {
-            const XG xg = xg_load(x, e + 32);
-#pragma unroll
-            for (int r = 0; r < R; r++) i2[r] = gdot_u(and4(shr4(q0[r], 4), M), xg);
-        }
-        {
-            const XG xg = xg_load(x, e + 48);
-#pragma unroll
-            for (int r = 0; r < R; r++) i3[r] = gdot_u(and4(shr4(q1[r], 4), M), xg);
-        }
-        const float S_lo = S.x + S.y, S_hi = S.z + S.w;
+        const uint4 c = q == 0 ? and4(q0[r], M) : q == 1 ? and4(q1[r], M) : q == 2 ? and4(shr4(q0[r], 4), M) : and4(shr4(q1[r], 4), M);
+        return gdot_u(c, xg);
+    }
+    IFR_DEV void combine(uint32_t g, const int (&iv)[4][R], const XS4 &f, bool valid, float *acc) const {
+        const float S_lo = f.S.x + f.S.y, S_hi = f.S.z + f.S.w;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float t_lo = fmaf((float)i0[r], s.x, (float)i1[r] * s.y);
-            const float t_hi = fmaf((float)i2[r], s.z, (float)i3[r] * s.w);
+            const float t_lo = fmaf((float)iv[0][r], f.s.x, (float)iv[1][r] * f.s.y);
+            const float t_hi = fmaf((float)iv[2][r], f.s.z, (float)iv[3][r] * f.s.w);
             uint32_t sc0, m0, sc1, m1;
             scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
             const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
-            acc[r] += (d * (float)sc0) * t_lo - (dm * (float)m0) * S_lo + (d * (float)sc1) * t_hi - (dm * (float)m1) * S_hi;
+            const float v = (d * (float)sc0) * t_lo - (dm * (float)m0) * S_lo + (d * (float)sc1) * t_hi - (dm * (float)m1) * S_hi;
+            acc[r] += valid ? v : 0.0f;
         }
     }
 };
@@ -397,57 +396,30 @@ struct ChunkI<Q5_K, R> {
             q1[r] = ld16(b + 64 + 32 * g);
         }
     }
-    IFR_DEV void compute(uint32_t kb, uint32_t g, const XQ &x, float *acc) const {
-        const uint32_t e = kb * 256 + 64 * g;
-        const float4 s = *(const float4 *)__builtin_assume_aligned(x.xs + e / 16, 16);
-        const float4 S = *(const float4 *)__builtin_assume_aligned(x.xsum + e / 16, 16);
+    static IFR_DEV XS4 xscales(const XQ &x, uint32_t kb, uint32_t g) { return ChunkI<Q4_K, R>::xscales(x, kb, g); }
+    static IFR_DEV XG xgroup(const XQ &x, uint32_t kb, uint32_t g, int q) { return ChunkI<Q4_K, R>::xgroup(x, kb, g, q); }
+    IFR_DEV int gdot(uint32_t g, int q, int r, const XG &xg) const {
         const uint32_t M = 0x0F0F0F0Fu, B = 0x10101010u;
-        const uint32_t s0 = 2 * g, s1 = 2 * g + 1;
-        // fifth bit to bit 4 of each byte: ((qh >> s) << 4) & 0x10101010
-        auto lo = [&](uint32_t q, uint32_t h) { return (q & M) | (((h >> s0) << 4) & B); };
-        auto hi = [&](uint32_t q, uint32_t h) { return ((q >> 4) & M) | (((h >> s1) << 4) & B); };
-        int i0[R], i1[R], i2[R], i3[R];
-        {
-            const XG xg = xg_load(x, e);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = q0[r], f = e0[r];
-                i0[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
-            }
-        }
-        {
-            const XG xg = xg_load(x, e + 16);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = q1[r], f = e1[r];
-                i1[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
-            }
-        }
-        {
-            const XG xg = xg_load(x, e + 32);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = q0[r], f = e0[r];
-                i2[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
-            }
-        }
-        {
-            const XG xg = xg_load(x, e + 48);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = q1[r], f = e1[r];
-                i3[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
-            }
-        }
-        const float S_lo = S.x + S.y, S_hi = S.z + S.w;
+        const bool hi = q >= 2;
+        const uint32_t sh = 2 * g + (hi ? 1u : 0u); // qh bit of this sub-block
+        const uint4 a = (q & 1) ? q1[r] : q0[r], h = (q & 1) ? e1[r] : e0[r];
+        const uint4 n = hi ? shr4(a, 4) : a;
+        // 4-bit code | fifth bit at bit 4 of each byte
+        const uint4 c = make_uint4((n.x & M) | (((h.x >> sh) << 4) & B), (n.y & M) | (((h.y >> sh) << 4) & B),
+                                   (n.z & M) | (((h.z >> sh) << 4) & B), (n.w & M) | (((h.w >> sh) << 4) & B));
+        return gdot_u(c, xg);
+    }
+    IFR_DEV void combine(uint32_t g, const int (&iv)[4][R], const XS4 &f, bool valid, float *acc) const {
+        const float S_lo = f.S.x + f.S.y, S_hi = f.S.z + f.S.w;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float t_lo = fmaf((float)i0[r], s.x, (float)i1[r] * s.y);
-            const float t_hi = fmaf((float)i2[r], s.z, (float)i3[r] * s.w);
+            const float t_lo = fmaf((float)iv[0][r], f.s.x, (float)iv[1][r] * f.s.y);
+            const float t_hi = fmaf((float)iv[2][r], f.s.z, (float)iv[3][r] * f.s.w);
             uint32_t sc0, m0, sc1, m1;
             scale_min_pair(g, hv[r].y, hv[r].z, hv[r].w, sc0, m0, sc1, m1);
             const float d = f16_to_f32(hv[r].x & 0xFFFFu), dm = f16_to_f32(hv[r].x >> 16);
-            acc[r] += (d * (float)sc0) * t_lo - (dm * (float)m0) * S_lo + (d * (float)sc1) * t_hi - (dm * (float)m1) * S_hi;
+            const float v = (d * (float)sc0) * t_lo - (dm * (float)m0) * S_lo + (d * (float)sc1) * t_hi - (dm * (float)m1) * S_hi;
+            acc[r] += valid ? v : 0.0f;
         }
     }
 };
@@ -456,6 +428,8 @@ struct ChunkI<Q5_K, R> {
 // nibbles are elements 128i+32u+l, high nibbles 128i+64+32u+l (l = 0..31),
 // with qh[32i+l] bits 2u..2u+1 / 2u+4..2u+5 and scales sc[8i+2u+l/16] /
 // sc[8i+2u+4+l/16].  Codes are stored +32: sum (q-32) x = sum q x - 32 sum x.
+// Groups q = 0..3 start at e, e+16 (low nibbles), e+64, e+80 (high), with
+// e = 128i + 32u.
 template <int R>
 struct ChunkI<Q6_K, R> {
     static constexpr int LPB = 4;
@@ -475,59 +449,39 @@ struct ChunkI<Q6_K, R> {
             dd[r] = ld_u16(b + 208);
         }
     }
-    IFR_DEV void compute(uint32_t kb, uint32_t c, const XQ &x, float *acc) const {
-        const uint32_t i = c >> 1, u = c & 1u;
-        const uint32_t e = kb * 256 + 128 * i + 32 * u;
+    static IFR_DEV uint32_t e0(uint32_t kb, uint32_t c) { return kb * 256 + 128 * (c >> 1) + 32 * (c & 1u); }
+    static IFR_DEV XS4 xscales(const XQ &x, uint32_t kb, uint32_t c) {
+        const uint32_t e = e0(kb, c);
         const float2 sl = *(const float2 *)(x.xs + e / 16), sh = *(const float2 *)(x.xs + e / 16 + 4);
         const float2 Sl = *(const float2 *)(x.xsum + e / 16), Sh = *(const float2 *)(x.xsum + e / 16 + 4);
+        return XS4{make_float4(sl.x, sl.y, sh.x, sh.y), make_float4(Sl.x, Sl.y, Sh.x, Sh.y)};
+    }
+    static IFR_DEV XG xgroup(const XQ &x, uint32_t kb, uint32_t c, int q) {
+        return xg_load(x, e0(kb, c) + (q >= 2 ? 64u : 0u) + 16u * (uint32_t)(q & 1));
+    }
+    IFR_DEV int gdot(uint32_t c, int q, int r, const XG &xg) const {
         const uint32_t M = 0x0F0F0F0Fu, B = 0x30303030u;
-        const uint32_t s_lo = 2 * u, s_hi = 2 * u + 4; // this lane's qh bit pairs
+        const bool hi = q >= 2;
+        const uint32_t sh = 2 * (c & 1u) + (hi ? 4u : 0u); // this lane's qh bit pair
+        const uint4 a = (q & 1) ? l1[r] : l0[r], h = (q & 1) ? h1[r] : h0[r];
+        const uint4 n = hi ? shr4(a, 4) : a;
         // 6-bit codes: ql nibble | (qh pair << 4)
-        auto lo = [&](uint32_t q, uint32_t h) { return (q & M) | (((h >> s_lo) << 4) & B); };
-        auto hi = [&](uint32_t q, uint32_t h) { return ((q >> 4) & M) | (((h >> s_hi) << 4) & B); };
-        int i0[R], i1[R], i2[R], i3[R];
-        {
-            const XG xg = xg_load(x, e);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = l0[r], f = h0[r];
-                i0[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
-            }
-        }
-        {
-            const XG xg = xg_load(x, e + 16);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = l1[r], f = h1[r];
-                i1[r] = gdot_u(make_uint4(lo(a.x, f.x), lo(a.y, f.y), lo(a.z, f.z), lo(a.w, f.w)), xg);
-            }
-        }
-        {
-            const XG xg = xg_load(x, e + 64);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = l0[r], f = h0[r];
-                i2[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
-            }
-        }
-        {
-            const XG xg = xg_load(x, e + 80);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint4 a = l1[r], f = h1[r];
-                i3[r] = gdot_u(make_uint4(hi(a.x, f.x), hi(a.y, f.y), hi(a.z, f.z), hi(a.w, f.w)), xg);
-            }
-        }
+        const uint4 cd = make_uint4((n.x & M) | (((h.x >> sh) << 4) & B), (n.y & M) | (((h.y >> sh) << 4) & B),
+                                    (n.z & M) | (((h.z >> sh) << 4) & B), (n.w & M) | (((h.w >> sh) << 4) & B));
+        return gdot_u(cd, xg);
+    }
+    IFR_DEV void combine(uint32_t, const int (&iv)[4][R], const XS4 &f, bool valid, float *acc) const {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float t0 = fmaf((float)i0[r], sl.x, -32.0f * Sl.x);
-            const float t1 = fmaf((float)i1[r], sl.y, -32.0f * Sl.y);
-            const float t2 = fmaf((float)i2[r], sh.x, -32.0f * Sh.x);
-            const float t3 = fmaf((float)i3[r], sh.y, -32.0f * Sh.y);
+            const float t0 = fmaf((float)iv[0][r], f.s.x, -32.0f * f.S.x);
+            const float t1 = fmaf((float)iv[1][r], f.s.y, -32.0f * f.S.y);
+            const float t2 = fmaf((float)iv[2][r], f.s.z, -32.0f * f.S.z);
+            const float t3 = fmaf((float)iv[3][r], f.s.w, -32.0f * f.S.w);
             const float d = f16_to_f32(dd[r]);
             const float c0 = (float)(int)(int8_t)(sc_lo[r] & 0xFFu), c1 = (float)(int)(int8_t)(sc_lo[r] >> 8);
             const float c2 = (float)(int)(int8_t)(sc_hi[r] & 0xFFu), c3 = (float)(int)(int8_t)(sc_hi[r] >> 8);
-            acc[r] += d * (c0 * t0 + c1 * t1 + c2 * t2 + c3 * t3);
+            const float v = d * (c0 * t0 + c1 * t1 + c2 * t2 + c3 * t3);
+            acc[r] += valid ? v : 0.0f;
         }
     }
 };
@@ -547,14 +501,42 @@ struct ChunkI<Q8_0, R> {
             qv[r] = ld16_a2(b + 2 + 16 * c);
         }
     }
-    IFR_DEV void compute(uint32_t kb, uint32_t c, const XQ &x, float *acc) const {
+    IFR_DEV void compute(const XQ &x, uint32_t kb, uint32_t c, bool valid, float *acc) const {
         const uint32_t e = kb * 32 + 16 * c;
         const XG xg = xg_load(x, e);
         const float s = x.xs[e / 16];
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] += f16_to_f32(dd[r]) * (gdot_s(qv[r], xg) * s);
+        for (int r = 0; r < R; r++) {
+            const float v = f16_to_f32(dd[r]) * (gdot_s(qv[r], xg) * s);
+            acc[r] += valid ? v : 0.0f;
+        }
     }
 };
+
+// One step of a lane for R rows (K-quants group by group), added to acc
+// when `valid` (a select, not a branch).
+template <int FMT, int R>
+IFR_DEV void chunk_step(const ChunkI<FMT, R> &w, const XQ &x, uint32_t kb, uint32_t c, bool valid, float *acc) {
+    if constexpr (FMT == Q8_0) {
+        w.compute(x, kb, c, valid, acc);
+    } else {
+        const XS4 sc = ChunkI<FMT, R>::xscales(x, kb, c);
+        int iv[4][R];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const XG xg = ChunkI<FMT, R>::xgroup(x, kb, c, q);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                iv[q][r] = w.gdot(c, q, r, xg);
+                // this group's sums are formed before the next group's x is
+                // read (a compiler-only fence, no instruction is emitted):
+                // one group of x digits is live at a time
+                asm volatile("" : "+v"(iv[q][r])::"memory");
+            }
+        }
+        w.combine(c, iv, sc, valid, acc);
+    }
+}
 
 template <int MODE>
 IFR_DEV const uint8_t *gemv_row_ptr(const GemvArgs &a, uint32_t v) {
@@ -584,51 +566,34 @@ IFR_DEV void rope_pair(float &a, float &b, uint32_t idx, uint32_t hs, uint32_t p
     b = sn * x + cs * y;
 }
 
-template <int FMT, bool XI, int R>
-struct ChunkOf { using T = Chunk<FMT, R>; static constexpr int LPB = QFmt<FMT>::LPB; };
-template <int FMT, int R>
-struct ChunkOf<FMT, true, R> { using T = ChunkI<FMT, R>; static constexpr int LPB = ChunkI<FMT, R>::LPB; };
-
-// Stages x into LDS.  Integer path: a copy of the producer's XQ, and for the
-// normalising modes the sum of its partial sums of x^2.  Exact path: x (times
-// gamma) as f32 and this thread's share of sum(x^2).
-template <bool XI, bool NORM, int W>
-IFR_DEV float gemv_stage(const GemvArgs &a, uint8_t *lds) {
-    const int tid = threadIdx.x;
+// Stages x (times gamma for the normalising modes) into LDS as f32 and
+// returns this thread's share of sum(x^2).
+template <bool NORM, int W>
+IFR_DEV float gemv_stage_f32(const GemvArgs &a, float *xs) {
     float ss = 0.0f;
-    if constexpr (XI) {
-        const uint4 *src = (const uint4 *)a.xq;
-        uint4 *dst = (uint4 *)lds;
-        const uint32_t n16 = xq_bytes(a.cols) / 16;
-        for (uint32_t i = (uint32_t)tid; i < n16; i += 64 * W) dst[i] = src[i];
-        if constexpr (NORM)
-            for (uint32_t i = (uint32_t)tid; i < a.n_ss; i += 64 * W) ss += a.ss_part[i];
-    } else {
-        float *xs = (float *)lds;
-        for (uint32_t i = (uint32_t)tid * 4; i < a.cols; i += 64 * W * 4) {
-            float4 v = *(const float4 *)(a.x + i);
-            if constexpr (NORM) {
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-                const float4 g = *(const float4 *)(a.gamma + i);
-                v.x *= g.x;
-                v.y *= g.y;
-                v.z *= g.z;
-                v.w *= g.w;
-            }
-            *(float4 *)(xs + i) = v;
+    for (uint32_t i = (uint32_t)threadIdx.x * 4; i < a.cols; i += 64 * W * 4) {
+        float4 v = *(const float4 *)(a.x + i);
+        if constexpr (NORM) {
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+            const float4 g = *(const float4 *)(a.gamma + i);
+            v.x *= g.x;
+            v.y *= g.y;
+            v.z *= g.z;
+            v.w *= g.w;
         }
+        *(float4 *)(xs + i) = v;
     }
     return ss;
 }
 
-template <int FMT, int MODE, bool XI, int R = GemvGeom<MODE>::R, int W = GemvGeom<MODE>::W,
-          bool PIPE = GemvGeom<MODE>::PIPE>
-__device__ void gemv_body(const GemvArgs &a) {
-    using CH = typename ChunkOf<FMT, XI, R>::T;
-    constexpr int LPB = ChunkOf<FMT, XI, R>::LPB, BPI = 64 / LPB;
+// Exact fp32 path: W waves of R rows, tiles of W*R rows with a grid stride.
+template <int FMT, int MODE, int R = GemvGeom<MODE>::R, int W = GemvGeom<MODE>::W, bool PIPE = GemvGeom<MODE>::PIPE>
+__device__ void gemv_f32_body(const GemvArgs &a) {
+    using CH = Chunk<FMT, R>;
+    constexpr int LPB = QFmt<FMT>::LPB, BPI = 64 / LPB;
     constexpr bool NORM = (MODE == GEMV_QKV || MODE == GEMV_GATEUP || MODE == GEMV_HEAD);
     // RESID and GATEUP also quantize their output for the next GEMV: a tile
     // must then hold exactly one 16-value activation group
@@ -657,7 +622,7 @@ __device__ void gemv_body(const GemvArgs &a) {
         if (bsub < a.nb) A.load(rowp, bsub, c);
     }
 
-    float ss = gemv_stage<XI, NORM, W>(a, lds);
+    float ss = gemv_stage_f32<NORM, W>(a, (float *)lds);
     float rs = 1.0f;
     if constexpr (NORM) {
         ss = wave_sum(ss);
@@ -670,7 +635,6 @@ __device__ void gemv_body(const GemvArgs &a) {
         for (int w = 0; w < W; w++) t += red[w];
         rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
     }
-    const XQ xq(lds, a.cols);
     const float *xf = (const float *)lds;
     uint32_t pos = 0;
     if constexpr (MODE == GEMV_QKV) pos = a.ctl->pos;
@@ -782,12 +746,7 @@ __device__ void gemv_body(const GemvArgs &a) {
             if (kn < a.nb) nxt.load(nt != tile ? rown : rowp, kn, c);
         }
         const uint32_t kb = step * BPI + bsub;
-        if (kb < a.nb) {
-            if constexpr (XI)
-                cur.compute(kb, c, xq, acc);
-            else
-                cur.compute(kb, c, xf, acc);
-        }
+        if (kb < a.nb) cur.compute(kb, c, xf, acc);
         if (ns == 0) {
             finish(tile);
             if (nt < ntiles) {
@@ -812,12 +771,7 @@ __device__ void gemv_body(const GemvArgs &a) {
                 const uint32_t kb = step * BPI + bsub;
                 if (step != 0 || tile != blockIdx.x)
                     if (kb < a.nb) A.load(rowp, kb, c);
-                if (kb < a.nb) {
-                    if constexpr (XI)
-                        A.compute(kb, c, xq, acc);
-                    else
-                        A.compute(kb, c, xf, acc);
-                }
+                if (kb < a.nb) A.compute(kb, c, xf, acc);
                 if (++step == steps) {
                     finish(tile);
                     step = 0;
@@ -836,6 +790,290 @@ __device__ void gemv_body(const GemvArgs &a) {
             if (tid == 0) {
                 uint64_t b = kred[0];
                 for (int w = 1; w < W; w++) b = kred[w] > b ? kred[w] : b;
+                a.part_keys[blockIdx.x] = b;
+            }
+        }
+    }
+}
+
+
+// ------------------------------------------------------------------------
+// Integer path.  A workgroup of W waves (W = blockDim.x / 64) copies the
+// input XQ into LDS once and then works through output groups of GR virtual
+// rows (16; 32 for GATEUP, whose virtual rows 2j, 2j+1 are gate j and up j),
+// groups with a grid stride.  Its waves form KS K-slices times RW = W / KS
+// row waves: wave (rw, ks) takes R rows of each RW*R-row sub-tile of the
+// group and the steps ks, ks + KS, ... of their K range.  The next item's
+// weights are loaded before the current item computes (PIPE).
+//  - KS = 1 and no quantized output (PLAIN, QKV, HEAD): each wave finishes
+//    its own rows (store, RoPE and KV-cache store, argmax keys);
+//  - otherwise each wave's row sums go to LDS, the workgroup synchronises
+//    once per group and wave 0 adds the K-slices and runs the epilogue on the
+//    group's 16 outputs (residual add and quantization of x * gamma_next for
+//    the next GEMV, or silu(gate) * up and its quantization).
+template <int FMT, int MODE, bool PIPE>
+__device__ void gemv_int_body(const GemvArgs &a) {
+    constexpr int R = 2;
+    using CH = ChunkI<FMT, R>;
+    constexpr int LPB = CH::LPB, BPI = 64 / LPB;
+    constexpr bool NORM = (MODE == GEMV_QKV || MODE == GEMV_GATEUP || MODE == GEMV_HEAD);
+    constexpr bool QOUT = (MODE == GEMV_RESID || MODE == GEMV_GATEUP);
+    constexpr uint32_t GR = MODE == GEMV_GATEUP ? 32 : 16;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float part[2][GEMV_KS_MAX][32];
+
+    // the wave index is uniform across the wave: row addresses stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t W = blockDim.x >> 6, KS = a.ks, RW = W / KS;
+    const uint32_t ks = (uint32_t)wave % KS, rw = (uint32_t)wave / KS;
+    // a geometry that does not tile the group would never advance: the host
+    // never launches one, and the workgroup exits as a whole if it did
+    if (KS == 0 || KS > GEMV_KS_MAX || RW == 0 || RW * KS != W || GR % (RW * R) != 0) return;
+    const uint32_t SUBR = RW * R, SUB = GR / SUBR;
+    const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
+    const uint32_t steps = (a.nb + BPI - 1) / BPI;
+    const uint32_t ngroups = (a.total_rows + GR - 1) / GR;
+    const bool local = !QOUT && KS == 1; // waves finish their own rows
+
+    // one work item: sub-tile j of group g, step st (st >= steps: none)
+    struct Item {
+        uint32_t g, j, st;
+    };
+    auto next = [&](Item it) {
+        it.st += KS;
+        if (it.st >= steps) {
+            it.st = ks;
+            if (++it.j == SUB) {
+                it.j = 0;
+                it.g += gridDim.x;
+            }
+        }
+        return it;
+    };
+    // Loads are unconditional: an item past the end (or a lane past the
+    // row's last block) reads a clamped, valid address and its data is not
+    // used.  A load behind a branch would leave the compiler unsure which
+    // buffer's loads are the newest at the join, and it would then wait for
+    // the prefetched ones too before computing.
+    auto load = [&](CH &w, const Item &it) {
+        const uint32_t kb = min(min(it.st, steps - 1) * BPI + bsub, a.nb - 1);
+        const uint32_t v0 = min(it.g, ngroups - 1) * GR + it.j * SUBR + rw * R;
+        const uint8_t *rowp[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) rowp[r] = gemv_row_ptr<MODE>(a, min(v0 + r, a.total_rows - 1));
+        w.load(rowp, kb, c);
+    };
+
+    Item cur{blockIdx.x, 0, ks};
+    CH A, B;
+    // the first item's weights do not depend on x: in flight before staging
+    if (cur.g >= ngroups) { // no work for this workgroup (the host never launches one)
+        if constexpr (MODE == GEMV_HEAD)
+            if (tid == 0 && a.part_keys) a.part_keys[blockIdx.x] = 0;
+        return;
+    }
+    load(A, cur);
+    {
+        const uint4 *src = (const uint4 *)a.xq;
+        uint4 *dst = (uint4 *)lds;
+        const uint32_t n16 = xq_bytes(a.cols) / 16;
+        for (uint32_t i = (uint32_t)tid; i < n16; i += blockDim.x) dst[i] = src[i];
+    }
+    float rs = 1.0f;
+    if constexpr (NORM) {
+        float t = 0.0f;
+        for (uint32_t i = (uint32_t)lane; i < a.n_ss; i += 64) t += a.ss_part[i];
+        t = wave_sum(t);
+        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+    }
+    uint32_t pos = 0;
+    // QKV: the RoPE theta table (head_size/2 <= 64 values) read once into LDS
+    __shared__ float theta_lds[64];
+    if constexpr (MODE == GEMV_QKV) {
+        pos = a.ctl->pos;
+        if (tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = a.rope_tab[tid];
+    }
+    // RESID: wave 0 reads the group's residual and next RMSNorm weight before
+    // the weights, so the epilogue waits for no load of its own
+    float y_pre = 0.0f, g_pre = 1.0f;
+    auto preload = [&](uint32_t g) {
+        if constexpr (MODE == GEMV_RESID) {
+            const uint32_t v = g * 16 + ((uint32_t)lane & 15u);
+            if (wave == 0 && lane < 16 && v < a.total_rows) {
+                y_pre = a.y[v];
+                if (a.gamma_next) g_pre = a.gamma_next[v];
+            }
+        }
+    };
+    preload(cur.g);
+    __syncthreads();
+    const XQ xq(lds, a.cols);
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    uint64_t best = 0;
+    uint32_t buf = 0;
+
+    // outputs v, v+1 of a QKV launch (an even pair of one head): q, or RoPE'd
+    // k / v into the cache row of this position
+    auto qkv_store = [&](uint32_t v, float x0, float x1) {
+        if (v < a.rows0) {
+            rope_pair(x0, x1, v, a.head_size, pos, theta_lds);
+            a.y[v] = x0;
+            a.y[v + 1] = x1;
+        } else {
+            const bool is_k = v < a.rows0 + a.rows1;
+            const uint32_t idx = is_k ? v - a.rows0 : v - a.rows0 - a.rows1;
+            if (is_k) rope_pair(x0, x1, idx, a.head_size, pos, theta_lds);
+            const size_t off = (size_t)pos * a.kv_dim + idx;
+            void *cache = is_k ? a.k_cache : a.v_cache;
+            if (a.kv_f16) {
+                const uint32_t packed = (uint32_t)f32_to_f16(x0) | ((uint32_t)f32_to_f16(x1) << 16);
+                *(uint32_t *)((uint16_t *)cache + off) = packed;
+            } else {
+                ((float *)cache)[off] = x0;
+                ((float *)cache)[off + 1] = x1;
+            }
+        }
+    };
+
+    // wave 0, after the group's barrier: the group's outputs
+    auto epilogue = [&](uint32_t g) {
+        auto val = [&](uint32_t i) {
+            float t = part[buf][0][i];
+            for (uint32_t k = 1; k < KS; k++) t += part[buf][k][i];
+            return t * rs;
+        };
+        const uint32_t l = (uint32_t)lane & 15u;
+        if constexpr (MODE == GEMV_PLAIN || MODE == GEMV_HEAD) {
+            const uint32_t v = g * 16 + l;
+            if (lane < 16 && v < a.total_rows) {
+                const float y = val(l);
+                a.y[v] = y;
+                if constexpr (MODE == GEMV_HEAD) {
+                    const uint64_t k = argmax_key(y, v);
+                    best = k > best ? k : best;
+                }
+            }
+        } else if constexpr (MODE == GEMV_RESID) {
+            // x += W v, then x * gamma_next quantized for the next GEMV
+            const uint32_t v = g * 16 + l;
+            const bool ok = lane < 16 && v < a.total_rows;
+            float xn = 0.0f;
+            if (ok) {
+                xn = y_pre + val(l);
+                a.y[v] = xn;
+            }
+            if (a.xq_out) {
+                quant16(xn * g_pre, ok, a.xq_out, a.total_rows, v, lane);
+                const float sq = sum16(xn * xn);
+                if (lane == 0) a.ss_out[g] = sq;
+            }
+        } else if constexpr (MODE == GEMV_GATEUP) {
+            // h[j] = up * silu(gate), quantized for the down GEMV
+            const uint32_t K = a.total_rows / 2, v = g * 16 + l;
+            const bool ok = lane < 16 && v < K;
+            float h = 0.0f;
+            if (ok) {
+                const float gt = val(2 * l), up = val(2 * l + 1);
+                h = up * (gt / (1.0f + expf(-gt)));
+                a.y[v] = h;
+            }
+            if (a.xq_out) quant16(h, ok, a.xq_out, K, v, lane);
+        } else if constexpr (MODE == GEMV_QKV) {
+            const uint32_t v = g * 16 + 2 * (uint32_t)lane;
+            if (lane < 8 && v + 1 < a.total_rows) qkv_store(v, val(2 * lane), val(2 * lane + 1));
+        }
+    };
+
+    // every lane computes every item (on the clamped block for a lane past
+    // the row's end or an item past the last step, which is then not added):
+    // the loaded data is consumed on every path
+    auto compute = [&](const CH &w, const Item &it) {
+        const uint32_t kb = it.st * BPI + bsub;
+        const bool valid = it.st < steps && kb < a.nb;
+        chunk_step<FMT, R>(w, xq, min(min(it.st, steps - 1) * BPI + bsub, a.nb - 1), c, valid, acc);
+        if (it.st + KS < steps) return; // more steps of this sub-tile
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+        if constexpr (!QOUT) {
+            if (local) {
+                const uint32_t v0 = it.g * GR + it.j * SUBR + rw * R;
+                if constexpr (MODE == GEMV_QKV) {
+                    if (lane == 0 && v0 + 1 < a.total_rows) qkv_store(v0, acc[0] * rs, acc[1] * rs);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; r++)
+                        if (v0 + r < a.total_rows) {
+                            const float y = acc[r] * rs;
+                            if (lane == r) a.y[v0 + r] = y;
+                            if constexpr (MODE == GEMV_HEAD) {
+                                const uint64_t k = argmax_key(y, v0 + r);
+                                best = k > best ? k : best;
+                            }
+                        }
+                }
+#pragma unroll
+                for (int r = 0; r < R; r++) acc[r] = 0.0f;
+                return;
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; r++) part[buf][ks][it.j * SUBR + rw * R + r] = acc[r];
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+        if (it.j + 1 == SUB) {
+            lds_barrier();
+            if (wave == 0) {
+                epilogue(it.g);
+                preload(it.g + gridDim.x);
+            }
+            buf ^= 1u;
+        }
+    };
+
+    if constexpr (PIPE) {
+        // the scheduling barriers keep each prefetch ahead of the compute
+        while (cur.g < ngroups) {
+            Item nx = next(cur);
+            load(B, nx);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(A, cur);
+            cur = nx;
+            if (cur.g >= ngroups) break;
+            nx = next(cur);
+            load(A, nx);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(B, cur);
+            cur = nx;
+        }
+    } else {
+        bool first = true;
+        while (cur.g < ngroups) {
+            if (!first) load(A, cur);
+            first = false;
+            compute(A, cur);
+            cur = next(cur);
+        }
+    }
+
+    if constexpr (MODE == GEMV_HEAD) {
+        if (a.part_keys) {
+            // every wave holds keys when waves finish their own rows, else wave 0
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint64_t o = __shfl_xor((unsigned long long)best, off, 64);
+                best = o > best ? o : best;
+            }
+            __shared__ uint64_t kred[GEMV_INT_MAX_WAVES];
+            if (lane == 0) kred[wave] = best;
+            __syncthreads();
+            if (tid == 0) {
+                uint64_t b = kred[0];
+                for (uint32_t w = 1; w < W; w++) b = kred[w] > b ? kred[w] : b;
                 a.part_keys[blockIdx.x] = b;
             }
         }

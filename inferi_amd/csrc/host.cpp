@@ -37,7 +37,6 @@ constexpr uint32_t GEMV_MAX_LDS = 65536 - 256;
 uint64_t xq_bytes(uint64_t n) { return 3 * n + n / 2; }
 
 // Dynamic LDS of a GEMV launch: x as f32, or its XQ copy.
-uint32_t gemv_lds_bytes(uint32_t cols, bool exact) { return exact ? cols * 4 : (uint32_t)xq_bytes(cols); }
 constexpr uint32_t ATTN_CMAX = 256;       // device/attention.h
 constexpr uint32_t ATTN_MERGE_MAX = 256;  // device/attention.h: most splits per KV head
 constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
@@ -90,6 +89,7 @@ struct ifr_ctx {
     size_t xq_scratch_bytes = 0;
     // tuning: cap on GEMV workgroups (0 = one per row tile)
     uint32_t gemv_max_grid = 0;
+    uint32_t gemv_waves = 0; // integer-path waves per workgroup (0: by shape)
     // GEMV arithmetic: 0 = x as 16-bit fixed point with int8 dot products,
     // 1 = exact fp32 x and FMAs
     int gemv_exact = 0;
@@ -166,7 +166,7 @@ static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const voi
     if (!p.fmt) return c->fail(IFR_EUNSUPPORTED, "matmul_quant: dtype %d has no GEMV kernel", dtype);
     const int qk = qk_of(dtype);
     if (cols == 0 || cols % (uint32_t)qk) return c->fail(IFR_EINVAL, "matmul_quant: cols %u not a multiple of %d", cols, qk);
-    if (gemv_lds_bytes(cols, true) > GEMV_MAX_LDS)
+    if ((c->gemv_exact ? (uint64_t)cols * 4 : xq_bytes(cols)) > GEMV_MAX_LDS)
         return c->fail(IFR_EUNSUPPORTED, "matmul_quant: cols %u too large for one workgroup's LDS", cols);
     const uintptr_t need = (dtype == IFR_Q4_K || dtype == IFR_Q5_K) ? 16 : 4;
     if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "matmul_quant: weights not %u-byte aligned", (unsigned)need);
@@ -175,27 +175,59 @@ static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const voi
     return IFR_OK;
 }
 
-// Launch geometry per mode (device/gemv.h, GemvGeom): rows per workgroup tile
-// and threads per workgroup.
+// Exact-path launch geometry per mode (kargs.h gemv_geom): rows per
+// workgroup tile and threads per workgroup.
 static GemvGeomT geom_of(const char *mode) {
     return gemv_geom(!strcmp(mode, "gateup") ? GEMV_GATEUP : !strcmp(mode, "resid") ? GEMV_RESID : GEMV_PLAIN);
 }
-static uint32_t gemv_tile_rows(const char *mode) { return (uint32_t)(geom_of(mode).R * geom_of(mode).W); }
-static uint32_t gemv_threads(const char *mode) { return (uint32_t)geom_of(mode).W * 64u; }
+
+// Integer-path geometry (device/gemv.h, gemv_int_body): K-slices KS by the
+// number of 64-lane steps a row takes, as many row waves as the output
+// group allows (16 virtual rows, 32 for gateup, two per wave) up to 16
+// waves, and one resident workgroup set (16 waves per CU) looping over the
+// groups unless a cap is given.
+struct IntGeom {
+    uint32_t ks, waves, grid;
+};
+static IntGeom int_geom(const ifr_ctx *c, const char *fmt, const char *mode, const GemvArgs &a, uint32_t cap) {
+    const uint32_t bpi = !strcmp(fmt, "q8_0") ? 32 : 16;
+    const uint32_t steps = (a.nb + bpi - 1) / bpi;
+    IntGeom g;
+    g.ks = steps <= 1 ? 1 : steps <= 2 ? 2 : 4;
+    const uint32_t gr = !strcmp(mode, "gateup") ? 32 : 16;
+    // gateup: 8 waves (two sub-tiles per group) and three workgroups per CU
+    // measured fastest; the others: as many row waves as a group allows
+    const bool gateup = !strcmp(mode, "gateup");
+    uint32_t rw = gateup ? 8 / g.ks : std::min(GEMV_INT_MAX_WAVES / g.ks, gr / 2);
+    if (c->gemv_waves) rw = std::max(1u, std::min(std::min(GEMV_INT_MAX_WAVES / g.ks, gr / 2), c->gemv_waves / g.ks));
+    g.waves = g.ks * rw;
+    const uint32_t ngroups = (a.total_rows + gr - 1) / gr;
+    uint32_t grid = gateup ? c->n_cu * 3 : c->n_cu * (GEMV_INT_MAX_WAVES / g.waves);
+    if (c->gemv_max_grid) grid = c->gemv_max_grid;
+    if (cap) grid = std::min(grid, cap);
+    g.grid = std::max(std::min(grid, ngroups), 1u);
+    return g;
+}
 
 static ifr_status launch_gemv(ifr_ctx *c, const char *fmt, const char *mode, GemvArgs &a, uint32_t cap = 0,
                               uint32_t *grid_out = nullptr) {
-    const uint32_t tr = gemv_tile_rows(mode);
-    uint32_t g = (a.total_rows + tr - 1) / tr;
-    if (c->gemv_max_grid) g = std::min(g, c->gemv_max_grid);
-    if (cap) g = std::min(g, cap);
-    g = std::max(g, 1u);
-    if (grid_out) *grid_out = g;
     const bool exact = c->gemv_exact != 0;
-    if (!exact && (!a.xq || (a.total_rows && a.cols % 16)))
-        return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
     std::string name = std::string("gemv_") + fmt + "_" + mode + (exact ? "_f32" : "");
-    return c->launch(name, dim3(g), dim3(gemv_threads(mode)), gemv_lds_bytes(a.cols, exact), a);
+    if (exact) {
+        const GemvGeomT ge = geom_of(mode);
+        const uint32_t tr = (uint32_t)(ge.R * ge.W);
+        uint32_t g = (a.total_rows + tr - 1) / tr;
+        if (c->gemv_max_grid) g = std::min(g, c->gemv_max_grid);
+        if (cap) g = std::min(g, cap);
+        g = std::max(g, 1u);
+        if (grid_out) *grid_out = g;
+        return c->launch(name, dim3(g), dim3((uint32_t)ge.W * 64u), a.cols * 4, a);
+    }
+    if (!a.xq || (a.total_rows && a.cols % 16)) return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
+    const IntGeom g = int_geom(c, fmt, mode, a, cap);
+    a.ks = g.ks;
+    if (grid_out) *grid_out = g.grid;
+    return c->launch(name, dim3(g.grid), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
 }
 
 // x (times gamma) -> XQ with per-256 partial sums of x^2.
@@ -640,6 +672,11 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
     }
     if (!strcmp(key, "gemv_exact")) {
         c->gemv_exact = value ? 1 : 0;
+        return IFR_OK;
+    }
+    if (!strcmp(key, "gemv_waves")) {
+        if (value < 0 || value > (int64_t)GEMV_INT_MAX_WAVES) return c->fail(IFR_EINVAL, "gemv_waves must be 0..16");
+        c->gemv_waves = (uint32_t)value;
         return IFR_OK;
     }
     return c->fail(IFR_EINVAL, "unknown option %s", key);

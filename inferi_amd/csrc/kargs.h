@@ -18,11 +18,10 @@ enum GemvMode : int32_t {
     GEMV_HEAD = 4,   // rmsnorm(x) -> logits = W x, per-workgroup argmax keys
 };
 
-// GEMV launch geometry per mode, shared by the kernels and the host: R rows
-// per wave, W waves per workgroup (a workgroup tile is W*R rows).  RESID and
-// GATEUP tiles hold exactly one 16-value output activation group (GATEUP's
-// 32 virtual rows are 16 gate/up pairs).  Measured on MI355X: two rows per
-// wave, no software pipelining and four waves per SIMD stream best.
+// Exact-path GEMV launch geometry per mode, shared by the kernels and the
+// host: R rows per wave, W waves per workgroup (a workgroup tile is W*R
+// rows).  RESID and GATEUP tiles hold exactly one 16-value output activation
+// group (GATEUP's 32 virtual rows are 16 gate/up pairs).
 struct GemvGeomT {
     int R, W;
 };
@@ -49,6 +48,10 @@ struct StepCtl {
     uint32_t pad;
 };
 
+// Integer-path GEMV: at most this many K-slices and 16 waves per workgroup.
+constexpr uint32_t GEMV_KS_MAX = 4;
+constexpr uint32_t GEMV_INT_MAX_WAVES = 16;
+
 struct GemvArgs {
     const uint8_t *w0, *w1, *w2; // matrices: PLAIN/RESID/HEAD w0; QKV q,k,v; GATEUP gate,up
     uint32_t rows0, rows1, rows2; // rows of each matrix
@@ -62,7 +65,7 @@ struct GemvArgs {
     const uint8_t *xq;   // integer path: the input, quantized (XQ layout, device/gemv.h)
     const float *ss_part; // integer path + RMSNorm: partial sums of x^2 of the input
     float eps;           // RMSNorm epsilon
-    uint32_t pad0;
+    uint32_t ks;         // integer path: K-slices per workgroup (1, 2 or 4)
     float *y;            // PLAIN/HEAD: out[rows]; RESID: x (+=); QKV: q; GATEUP: h
     uint8_t *xq_out;     // RESID/GATEUP: the output quantized for the next GEMV (may be null)
     float *ss_out;       // RESID: per-tile partial sums of x^2 of the output

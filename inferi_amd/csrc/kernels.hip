@@ -8,26 +8,29 @@
 
 using namespace ifr;
 
-// gemv_<fmt>_<mode>: integer path (x quantized by its producer, v_dot4);
-// gemv_<fmt>_<mode>_f32: exact fp32 path.
+// gemv_<fmt>_<mode>: integer path (x quantized by its producer, v_dot4),
+// up to 16 waves per workgroup; gemv_<fmt>_<mode>_f32: exact fp32 path.
 // Four waves per SIMD (at most 128 VGPRs) keeps enough loads in flight.
-#define GEMV_KERNEL(NAME, FMT, MODE, XI)                                                               \
-    extern "C" __global__ void __launch_bounds__(GemvGeom<MODE>::W * 64)                             \
+#define GEMV_KERNEL(NAME, FMT, MODE)                                                                   \
+    extern "C" __global__ void __launch_bounds__(GEMV_INT_MAX_WAVES * 64)                            \
         __attribute__((amdgpu_waves_per_eu(4, 8))) NAME(GemvArgs a) {                                \
-        gemv_body<FMT, MODE, XI>(a);                                                                 \
+        gemv_int_body<FMT, MODE, GEMV_INT_PIPE>(a);                                                  \
+    }                                                                                                \
+    extern "C" __global__ void __launch_bounds__(GemvGeom<MODE>::W * 64)                             \
+        __attribute__((amdgpu_waves_per_eu(4, 8))) NAME##_f32(GemvArgs a) {                          \
+        gemv_f32_body<FMT, MODE>(a);                                                                 \
     }
 
-#define GEMV_ALL_MODES(FMTNAME, FMT)                                  \
-    GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN, true)       \
-    GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID, true)       \
-    GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV, true)           \
-    GEMV_KERNEL(gemv_##FMTNAME##_gateup, FMT, GEMV_GATEUP, true)     \
-    GEMV_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD, true)         \
-    GEMV_KERNEL(gemv_##FMTNAME##_plain_f32, FMT, GEMV_PLAIN, false)  \
-    GEMV_KERNEL(gemv_##FMTNAME##_resid_f32, FMT, GEMV_RESID, false)  \
-    GEMV_KERNEL(gemv_##FMTNAME##_qkv_f32, FMT, GEMV_QKV, false)      \
-    GEMV_KERNEL(gemv_##FMTNAME##_gateup_f32, FMT, GEMV_GATEUP, false)\
-    GEMV_KERNEL(gemv_##FMTNAME##_head_f32, FMT, GEMV_HEAD, false)
+#ifndef GEMV_INT_PIPE
+#define GEMV_INT_PIPE false
+#endif
+
+#define GEMV_ALL_MODES(FMTNAME, FMT)                  \
+    GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)   \
+    GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID)   \
+    GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)       \
+    GEMV_KERNEL(gemv_##FMTNAME##_gateup, FMT, GEMV_GATEUP) \
+    GEMV_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD)
 
 GEMV_ALL_MODES(q4_k, Q4_K)
 GEMV_ALL_MODES(q5_k, Q5_K)
