@@ -180,7 +180,7 @@ def run_decode(args) -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "q4_k x int8 (v_dot4) + f32",
         "data": "synthetic (random-init N(0,0.02) weights quantized on device; uniform random prompt ids)",
         "config": {
             "workload": ("8B-shape Llama decode: 32 layers, hidden 4096, 32 q / 8 kv heads, FFN 14336, vocab 128256, "
@@ -277,7 +277,7 @@ def run_attn(args) -> None:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--model", choices=["8b", "c4"], default="8b")
@@ -285,7 +285,7 @@ def main() -> None:
     ap.add_argument("--gemv-iters", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch the decode step's kernels directly")
-    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=32)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")

@@ -81,7 +81,7 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
 
 /* Knobs (no reference counterpart): "gemv_max_grid" sets the number of GEMV
  * workgroups (0 = chosen by shape, the default); "gemv_waves" caps the
- * waves per GEMV workgroup (1..16, 0 = chosen by shape); "gemv_exact" = 1
+ * waves per GEMV workgroup (1, 2, 4, 8 or 16; 0 = chosen by shape); "gemv_exact" = 1
  * makes every GEMV keep x in fp32 and use fp32 FMAs, instead of the default
  * path that takes x as 22-bit fixed point per 16 elements and multiplies
  * with int8 dot products (see ifr_quantize_activation). */
@@ -123,8 +123,10 @@ IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int
  * (crates/inferi/src/ops/gemv_quant.rs:183-340).
  * The product runs on the integer path (see ifr_quantize_activation) unless
  * the "gemv_exact" option is set.
- * Requirements: cols % QK == 0, cols <= 16320; W 16-byte aligned for Q4_K
- * and Q5_K, 4-byte aligned for Q6_K and Q8_0 (GGUF data is 32-aligned). */
+ * Requirements: cols % QK == 0; cols <= 18432 (integer path; 16320 with
+ * "gemv_exact"), as x is staged in one workgroup's LDS; W 16-byte aligned
+ * for Q4_K and Q5_K, 4-byte aligned for Q6_K and Q8_0 (GGUF data is
+ * 32-aligned). */
 IFR_API ifr_status ifr_matmul_quant(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
                                     uint32_t cols, const float *v);
 
@@ -240,7 +242,7 @@ IFR_API ifr_status ifr_llama2_state_reset(ifr_llama2_state *s, const uint32_t *p
  * (crates/inferi/src/models/llama2/transformer.rs:409-481) plus the
  * embedding copy and greedy sampling of ChatLlama2::forward_logits
  * (crates/inferi-chat/src/chat_llama2.rs:191-255).  `fused` selects the fused
- * kernels (5 launches per layer) instead of the one-kernel-per-reference-op
+ * kernels (6 launches per layer) instead of the one-kernel-per-reference-op
  * sequence (14 per layer). */
 IFR_API ifr_status ifr_llama2_launch(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w, int32_t fused);
 /* n_steps decode steps; with use_graph the step is captured once into a HIP

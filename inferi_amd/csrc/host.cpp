@@ -675,7 +675,9 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         return IFR_OK;
     }
     if (!strcmp(key, "gemv_waves")) {
-        if (value < 0 || value > (int64_t)GEMV_INT_MAX_WAVES) return c->fail(IFR_EINVAL, "gemv_waves must be 0..16");
+        // a power of two, so that the row waves always tile a 16-row group
+        if (value < 0 || value > (int64_t)GEMV_INT_MAX_WAVES || (value & (value - 1)))
+            return c->fail(IFR_EINVAL, "gemv_waves must be 0, 1, 2, 4, 8 or 16");
         c->gemv_waves = (uint32_t)value;
         return IFR_OK;
     }
