@@ -4,17 +4,16 @@
 // heads that share KV head h (grouped-query attention reads each K/V row once
 // for all of them, where the reference's fused_attention reads it once per
 // query head: fused_attention.rs:66-241) over the s-th chunk of the positions
-// [0, pos].  The chunk length is ceil((pos+1)/n_splits), at least ATTN_CMIN,
-// computed on the device from the device-resident position, so one launch
-// shape serves every position (and a captured graph can be replayed).
+// [0, pos].  The chunk length is ceil((pos+1)/n_splits) rounded up to whole
+// batches, computed on the device from the device-resident position, so one
+// launch shape serves every position (and a captured graph can be replayed).
 //
 // A position's K (and V) row of one head is read by TPP = HS/8 lanes, 8 dims
 // each.  Per batch a thread issues the K and the V rows of its ATTN_BATCH
 // positions together, then forms the scores q.k / sqrt(hs) (a DPP sum over
 // the TPP lanes) and folds them into a running softmax (m, l, o) per query
-// head.  The per-thread states are combined over the wave with shuffles and
-// over the workgroup through LDS; the chunk's partial (m, l, o) goes to
-// global memory.  A second, small kernel (attn_merge_body) combines the
+// head.  The per-thread states are combined through LDS; the chunk's partial
+// (m, l, o) goes to global memory.  A second, small kernel (attn_merge_body) combines the
 // partials of each query head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
 // The kernel boundary orders the two: merging inside the first kernel would
 // need device-scope fences, which on this chip write back and invalidate the
@@ -26,7 +25,6 @@ namespace ifr {
 
 constexpr int ATTN_THREADS = 256;
 constexpr int ATTN_CMAX = 256; // longest chunk a workgroup accepts
-constexpr int ATTN_CMIN = 64;  // shortest chunk a split is given (unless T is shorter)
 constexpr int ATTN_MERGE_MAX = 256;  // most splits one KV head may have
 constexpr int ATTN_BATCH = 4;  // positions per thread whose K and V are loaded together
 
@@ -54,36 +52,40 @@ IFR_DEV float group_sum(float v) {
     else return sum8(v);
 }
 
-// Running-softmax update: fold a state (m2, l2, o2) into (m, l, o).  An
-// empty state has m = -inf, l = 0, o = 0.
-template <int N>
-IFR_DEV void softmax_fold(float &m, float &l, float *o, float m2, float l2, const float *o2) {
-    const float mn = fmaxf(m, m2);
-    const float a1 = m == -INFINITY ? 0.0f : expf(m - mn);
-    const float a2 = m2 == -INFINITY ? 0.0f : expf(m2 - mn);
-    l = l * a1 + l2 * a2;
-#pragma unroll
-    for (int e = 0; e < N; e++) o[e] = o[e] * a1 + o2[e] * a2;
-    m = mn;
+// Positions per batch of one workgroup (every thread loads ATTN_BATCH
+// positions): the chunk of a split is a multiple of it.
+template <int HS>
+constexpr uint32_t attn_quantum() { return (uint32_t)(ATTN_THREADS / (HS / 8)) * ATTN_BATCH; }
+
+// Chunk length of every split for T positions over S splits: at least one
+// batch, a whole number of batches, at most ATTN_CMAX (the host sizes S so
+// that T <= S * ATTN_CMAX).
+template <int HS>
+IFR_DEV uint32_t attn_chunk(uint32_t T, uint32_t S) {
+    constexpr uint32_t Q = attn_quantum<HS>();
+    const uint32_t c = max((T + S - 1) / S, Q);
+    return min((c + Q - 1) / Q * Q, (uint32_t)ATTN_CMAX);
 }
 
+// Scores are kept in base-2 units: q is pre-scaled by log2(e)/sqrt(hs), so
+// e^(s - m) of the reference's softmax is 2^(s2 - m2) here, and the partial
+// maxima handed to the merge are in the same units.
 template <int HS, int G, bool F16>
 __device__ void attn_body(const AttnArgs &a) {
     constexpr int TPP = HS / 8;             // lanes per position (8 dims each)
     constexpr int PPW = 64 / TPP;           // positions per wave and pass
     constexpr int NW = ATTN_THREADS / 64;   // waves
     constexpr int PPP = NW * PPW;           // positions per workgroup and pass
+    constexpr int NPG = PPP;                // position groups (threads sharing a dim slice)
     constexpr int U = ATTN_BATCH;
-    __shared__ float wo[NW][G][HS];
-    __shared__ float wml[NW][G][2];
+    __shared__ float og[NPG][G][HS];        // per position group: unnormalised o
+    __shared__ float mg[NPG][G], lg[NPG][G];
+    __shared__ float wg[NPG][G], Mh[G];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = blockIdx.x, s = blockIdx.y, S = a.n_splits;
     const uint32_t T = min(*a.pos + 1, a.seq_cap);
-    // chunk: at least ATTN_CMIN positions (short contexts use few splits, so
-    // the merge reads few partials); the host sizes n_splits so that the
-    // chunk never exceeds ATTN_CMAX
-    const uint32_t C = min(max((T + S - 1) / S, (uint32_t)ATTN_CMIN), (uint32_t)ATTN_CMAX);
+    const uint32_t C = attn_chunk<HS>(T, S);
     const uint32_t t0 = s * C;
     if (t0 >= T) return;
     const uint32_t n = min(C, T - t0);
@@ -92,16 +94,16 @@ __device__ void attn_body(const AttnArgs &a) {
     const uint32_t pg = (uint32_t)(wave * PPW + lane / TPP);
     const size_t head_off = (size_t)kvh * HS + (size_t)dc * 8;
 
-    // this thread's 8 query dims of every head of the group
+    // this thread's 8 query dims of every head of the group, pre-scaled
+    const float qs = 1.44269504088896341f / sqrtf((float)HS);
     float q[G][8];
 #pragma unroll
     for (int j = 0; j < G; j++) {
         const float4 u = *(const float4 *)(a.q + (size_t)(kvh * G + j) * HS + dc * 8);
         const float4 w = *(const float4 *)(a.q + (size_t)(kvh * G + j) * HS + dc * 8 + 4);
-        q[j][0] = u.x; q[j][1] = u.y; q[j][2] = u.z; q[j][3] = u.w;
-        q[j][4] = w.x; q[j][5] = w.y; q[j][6] = w.z; q[j][7] = w.w;
+        q[j][0] = u.x * qs; q[j][1] = u.y * qs; q[j][2] = u.z * qs; q[j][3] = u.w * qs;
+        q[j][4] = w.x * qs; q[j][5] = w.y * qs; q[j][6] = w.z * qs; q[j][7] = w.w * qs;
     }
-    const float inv_div = sqrtf((float)HS);
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -131,19 +133,19 @@ __device__ void attn_body(const AttnArgs &a) {
                 float d = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; e++) d = fmaf(q[j][e], kr[u][e], d);
-                d = group_sum<TPP>(d) / inv_div;
+                d = group_sum<TPP>(d);
                 sc[u] = (base + pg + PPP * u < n) ? d : -INFINITY;
                 mb = fmaxf(mb, sc[u]);
             }
             if (mb == -INFINITY) continue; // no position of this batch for this thread
             const float mn = fmaxf(m[j], mb);
-            const float al = m[j] == -INFINITY ? 0.0f : expf(m[j] - mn);
+            const float al = exp2f(m[j] - mn); // 0 while m[j] is still -inf
             float lsum = l[j] * al, ov[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) ov[e] = o[j][e] * al;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const float p = expf(sc[u] - mn); // 0 for a masked position
+                const float p = exp2f(sc[u] - mn); // 0 for a masked position
                 lsum += p;
 #pragma unroll
                 for (int e = 0; e < 8; e++) ov[e] = fmaf(p, vr[u][e], ov[e]);
@@ -155,49 +157,42 @@ __device__ void attn_body(const AttnArgs &a) {
         }
     }
 
-    // combine the PPW position groups of the wave (lanes dc + TPP*k)
+    // combine the NPG position groups through LDS: states, then per-head
+    // maxima and weights 2^(m_g - M), then the weighted sums of o
 #pragma unroll
-    for (int sh = TPP; sh < 64; sh <<= 1) {
+    for (int j = 0; j < G; j++) {
 #pragma unroll
-        for (int j = 0; j < G; j++) {
-            const float m2 = __shfl_xor(m[j], sh, 64), l2 = __shfl_xor(l[j], sh, 64);
-            float o2[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) o2[e] = __shfl_xor(o[j][e], sh, 64);
-            softmax_fold<8>(m[j], l[j], o[j], m2, l2, o2);
-        }
-    }
-    if (lane < TPP) {
-#pragma unroll
-        for (int j = 0; j < G; j++) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) wo[wave][j][dc * 8 + e] = o[j][e];
-            if (dc == 0) {
-                wml[wave][j][0] = m[j];
-                wml[wave][j][1] = l[j];
-            }
+        for (int e = 0; e < 8; e++) og[pg][j][dc * 8 + e] = o[j][e];
+        if (dc == 0) {
+            mg[pg][j] = m[j];
+            lg[pg][j] = l[j];
         }
     }
     __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int g = 0; g < NPG; g++) M = fmaxf(M, mg[g][tid]);
+        Mh[tid] = M;
+    }
+    __syncthreads();
+    for (int i = tid; i < NPG * G; i += ATTN_THREADS) {
+        const int g = i / G, j = i % G;
+        wg[g][j] = exp2f(mg[g][j] - Mh[j]); // 0 for a group that saw no position
+    }
+    __syncthreads();
 
-    // ... then over the waves, and write this split's partial
     const size_t pidx = ((size_t)kvh * S + s) * G;
     for (int i = tid; i < G * HS; i += ATTN_THREADS) {
         const int j = i / HS, d = i % HS;
-        float M = wml[0][j][0];
-#pragma unroll
-        for (int w = 1; w < NW; w++) M = fmaxf(M, wml[w][j][0]);
         float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; w++)
-            if (wml[w][j][0] != -INFINITY) v = fmaf(expf(wml[w][j][0] - M), wo[w][j][d], v);
+        for (int g = 0; g < NPG; g++) v = fmaf(wg[g][j], og[g][j][d], v);
         a.part_o[(pidx + j) * HS + d] = v;
         if (d == 0) {
             float L = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NW; w++)
-                if (wml[w][j][0] != -INFINITY) L = fmaf(expf(wml[w][j][0] - M), wml[w][j][1], L);
-            a.part_ml[(pidx + j) * 2] = M;
+            for (int g = 0; g < NPG; g++) L = fmaf(wg[g][j], lg[g][j], L);
+            a.part_ml[(pidx + j) * 2] = Mh[j];
             a.part_ml[(pidx + j) * 2 + 1] = L;
         }
     }
@@ -219,7 +214,7 @@ __device__ void attn_merge_body(const AttnArgs &a) {
     const int tid = threadIdx.x;
     const uint32_t h = blockIdx.x, kvh = h / G, j = h % G, S = a.n_splits;
     const uint32_t T = min(*a.pos + 1, a.seq_cap);
-    const uint32_t C = min(max((T + S - 1) / S, (uint32_t)ATTN_CMIN), (uint32_t)ATTN_CMAX);
+    const uint32_t C = attn_chunk<HS>(T, S);
     const uint32_t n_act = (T + C - 1) / C;
     const int d = tid % HS, qg = tid / HS;
     const float *po = a.part_o + ((size_t)kvh * S * G + j) * HS + d; // split t at po[t * G * HS]
@@ -241,7 +236,7 @@ __device__ void attn_merge_body(const AttnArgs &a) {
         M = wave_max(M);
         float L = 0.0f;
         for (uint32_t t = tid; t < n_act; t += 64) {
-            const float w = expf(wm[t] - M);
+            const float w = exp2f(wm[t] - M); // maxima are in base-2 units
             wm[t] = w;
             L = fmaf(wl[t], w, L);
         }

@@ -262,9 +262,13 @@ static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtyp
 
 // ------------------------------------------------------------- attention --
 
-static uint32_t attn_splits_for(uint32_t T) {
-    uint32_t s = std::max((T + ATTN_CMAX - 1) / ATTN_CMAX, std::min(T, 64u));
-    return std::max(s, 1u);
+// Splits of the attention over the sequence for T positions: one batch of
+// the split kernel each (8192/head_size positions, device/attention.h
+// attn_quantum), at most ATTN_MERGE_MAX; longer chunks beyond that.
+static uint32_t attn_quantum(uint32_t head_size) { return 8192u / head_size; }
+static uint32_t attn_splits_for(uint32_t T, uint32_t head_size) {
+    const uint32_t q = attn_quantum(head_size);
+    return std::max(1u, std::min(ATTN_MERGE_MAX, (T + q - 1) / q));
 }
 
 // Split pass over the KV sequence, then the merge of the partials.
@@ -866,7 +870,7 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     if (p->pos >= ATTN_CMAX * ATTN_MERGE_MAX) return c->fail(IFR_EUNSUPPORTED, "attention: pos %u too large", p->pos);
     if ((uintptr_t)q % 16 || (uintptr_t)kc % 16 || (uintptr_t)vc % 16)
         return c->fail(IFR_EINVAL, "attention: q and caches must be 16-byte aligned");
-    const uint32_t T = p->pos + 1, S = attn_splits_for(T);
+    const uint32_t T = p->pos + 1, S = attn_splits_for(T, p->head_size);
     const size_t part_o = (size_t)n_kv * S * g * p->head_size, part_ml = (size_t)n_kv * S * g * 2;
     ifr_status st = c->ensure_scratch((part_o + part_ml) * sizeof(float));
     if (st) return st;
@@ -1024,7 +1028,7 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     s->head_size = cfg->hidden / cfg->n_heads;
     s->kv_dim = s->head_size * cfg->n_kv_heads;
     s->kv_mul = cfg->n_heads / cfg->n_kv_heads;
-    s->n_splits = std::max(64u, (cfg->max_pos + ATTN_CMAX - 1) / ATTN_CMAX);
+    s->n_splits = attn_splits_for(cfg->max_pos, s->head_size);
     auto alloc = [&](size_t bytes, void **p) -> ifr_status {
         ifr_status e = c->hip(hipMalloc(p, std::max<size_t>(bytes, 16)), "hipMalloc(state)");
         if (e) return e;
