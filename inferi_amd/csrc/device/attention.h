@@ -84,15 +84,11 @@ __device__ void attn_body(const AttnArgs &a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = blockIdx.x, s = blockIdx.y, S = a.n_splits;
-    const uint32_t T = min(*a.pos + 1, a.seq_cap);
-    const uint32_t C = attn_chunk<HS>(T, S);
-    const uint32_t t0 = s * C;
-    if (t0 >= T) return;
-    const uint32_t n = min(C, T - t0);
-
+    constexpr uint32_t Qb = attn_quantum<HS>();
     const int dc = lane % TPP;
     const uint32_t pg = (uint32_t)(wave * PPW + lane / TPP);
     const size_t head_off = (size_t)kvh * HS + (size_t)dc * 8;
+    const size_t pidx = ((size_t)kvh * S + s) * G;
 
     // this thread's 8 query dims of every head of the group, pre-scaled
     const float qs = 1.44269504088896341f / sqrtf((float)HS);
@@ -105,6 +101,36 @@ __device__ void attn_body(const AttnArgs &a) {
         q[j][4] = w.x * qs; q[j][5] = w.y * qs; q[j][6] = w.z * qs; q[j][7] = w.w * qs;
     }
 
+    // When S batches cover the whole cache (S * Qb >= seq_cap) every chunk is
+    // one batch of Qb positions at s * Qb, known before the device position
+    // arrives: the first batch's K and V loads go out together with the
+    // position load (rows clamped into the cache, masked below).
+    const bool fixed = S * Qb >= a.seq_cap;
+    float kr[ATTN_BATCH][8], vr[ATTN_BATCH][8];
+    auto load_batch = [&](uint32_t t0, uint32_t base, uint32_t n) {
+#pragma unroll
+        for (int u = 0; u < ATTN_BATCH; u++) {
+            const uint32_t tt = base + pg + PPP * u;
+            const uint32_t row = n ? t0 + (tt < n ? tt : 0) : min(t0 + tt, a.seq_cap - 1);
+            const size_t off = (size_t)row * a.kv_dim + head_off;
+            load_kv8<F16>(a.k_cache, off, kr[u]);
+            load_kv8<F16>(a.v_cache, off, vr[u]);
+        }
+    };
+    if (fixed) load_batch(s * Qb, 0, 0);
+    const uint32_t T = min(*a.pos + 1, a.seq_cap);
+    const uint32_t C = fixed ? Qb : attn_chunk<HS>(T, S);
+    const uint32_t t0 = s * C;
+    if (t0 >= T) {
+        // an empty split: a partial the merge gives weight 0
+        if (tid < G) {
+            a.part_ml[(pidx + tid) * 2] = -INFINITY;
+            a.part_ml[(pidx + tid) * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+    const uint32_t n = min(C, T - t0);
+
     float m[G], l[G], o[G][8];
 #pragma unroll
     for (int j = 0; j < G; j++) {
@@ -115,15 +141,14 @@ __device__ void attn_body(const AttnArgs &a) {
     }
 
     for (uint32_t base = 0; base < n; base += PPP * U) {
-        float kr[U][8], vr[U][8];
+        if (!fixed || base) load_batch(t0, base, n);
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t tt = base + pg + PPP * u;
-            // a position past the chunk reads the chunk's first row (in bounds) and is masked below
-            const size_t off = (size_t)(t0 + (tt < n ? tt : 0)) * a.kv_dim + head_off;
-            load_kv8<F16>(a.k_cache, off, kr[u]);
-            load_kv8<F16>(a.v_cache, off, vr[u]);
-        }
+        for (int u = 0; u < U; u++)
+            if (base + pg + PPP * u >= n) {
+                // a masked row (possibly never written): its values must not reach the sums
+#pragma unroll
+                for (int e = 0; e < 8; e++) vr[u][e] = 0.0f;
+            }
 #pragma unroll
         for (int j = 0; j < G; j++) {
             float sc[U];
@@ -181,7 +206,6 @@ __device__ void attn_body(const AttnArgs &a) {
     }
     __syncthreads();
 
-    const size_t pidx = ((size_t)kvh * S + s) * G;
     for (int i = tid; i < G * HS; i += ATTN_THREADS) {
         const int j = i / HS, d = i % HS;
         float v = 0.0f;
@@ -199,56 +223,52 @@ __device__ void attn_body(const AttnArgs &a) {
 }
 
 // Merge of the split partials: one workgroup of ATTN_MERGE_THREADS per query
-// head; thread (q, d) sums splits q, q + Q, ... for head dim d.  Every
-// partial load is issued at the start, then the split weights e^(m_s - M)
-// are formed in LDS and the Q groups combined there.
+// head; thread (q, d) sums splits q, q + Q, ... for head dim d.  Every split
+// of the launch is read (an empty one carries m = -inf and weight 0), so the
+// merge does not wait for the device position: all loads go out at the
+// start.  Split weights are 2^(m_s - M) (base-2 units).
 constexpr int ATTN_MERGE_THREADS = 512;
 
 template <int HS, int G>
 __device__ void attn_merge_body(const AttnArgs &a) {
     constexpr int Q = ATTN_MERGE_THREADS / HS;             // split groups
     constexpr int PER = (ATTN_MERGE_MAX + Q - 1) / Q;      // splits per thread at most
-    __shared__ float wm[ATTN_MERGE_MAX], wl[ATTN_MERGE_MAX];
+    __shared__ float wm[ATTN_MERGE_MAX], wl[ATTN_MERGE_MAX], wt[ATTN_MERGE_MAX];
     __shared__ float part[Q][HS];
-    __shared__ float Lsum;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const uint32_t h = blockIdx.x, kvh = h / G, j = h % G, S = a.n_splits;
-    const uint32_t T = min(*a.pos + 1, a.seq_cap);
-    const uint32_t C = attn_chunk<HS>(T, S);
-    const uint32_t n_act = (T + C - 1) / C;
     const int d = tid % HS, qg = tid / HS;
     const float *po = a.part_o + ((size_t)kvh * S * G + j) * HS + d; // split t at po[t * G * HS]
     float v[PER];
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const uint32_t t = (uint32_t)(qg + Q * u);
-        v[u] = t < n_act ? po[(size_t)t * G * HS] : 0.0f;
+        v[u] = t < S ? po[(size_t)t * G * HS] : 0.0f;
     }
-    for (uint32_t t = tid; t < n_act; t += ATTN_MERGE_THREADS) {
-        const float *ml = a.part_ml + (((size_t)kvh * S + t) * G + j) * 2;
-        wm[t] = ml[0];
-        wl[t] = ml[1];
-    }
-    __syncthreads();
-    if (tid < 64) {
-        float M = -INFINITY;
-        for (uint32_t t = tid; t < n_act; t += 64) M = fmaxf(M, wm[t]);
-        M = wave_max(M);
-        float L = 0.0f;
-        for (uint32_t t = tid; t < n_act; t += 64) {
-            const float w = exp2f(wm[t] - M); // maxima are in base-2 units
-            wm[t] = w;
-            L = fmaf(wl[t], w, L);
-        }
-        L = wave_sum(L);
-        if (tid == 0) Lsum = L;
+    if ((uint32_t)tid < S) {
+        const float *ml = a.part_ml + (((size_t)kvh * S + tid) * G + j) * 2;
+        wm[tid] = ml[0];
+        wl[tid] = ml[1];
     }
     __syncthreads();
+    // every wave forms M itself; split weights 2^(m_s - M) once, in LDS
+    float M = -INFINITY;
+    for (uint32_t t = lane; t < S; t += 64) M = fmaxf(M, wm[t]);
+    M = wave_max(M);
+    if ((uint32_t)tid < S) wt[tid] = wm[tid] == -INFINITY ? 0.0f : exp2f(wm[tid] - M);
+    __syncthreads();
+    float L = 0.0f;
+    for (uint32_t t = lane; t < S; t += 64) L = fmaf(wl[t], wt[t], L);
+    L = wave_sum(L);
     float O = 0.0f;
 #pragma unroll
     for (int u = 0; u < PER; u++) {
         const uint32_t t = (uint32_t)(qg + Q * u);
-        if (t < n_act) O = fmaf(v[u], wm[t], O);
+        if (t < S) {
+            const float w = wt[t];
+            // an empty split's o was never written: skipped, not multiplied by 0
+            if (w != 0.0f) O = fmaf(v[u], w, O);
+        }
     }
     part[qg][d] = O;
     __syncthreads();
@@ -260,7 +280,7 @@ __device__ void attn_merge_body(const AttnArgs &a) {
         if (ok) {
 #pragma unroll
             for (int k = 0; k < Q; k++) r += part[k][tid];
-            r /= Lsum;
+            r /= L;
             a.out[(size_t)h * HS + tid] = r;
         }
         if (a.xq_out) quant16(r, ok, a.xq_out, a.n_out, (uint32_t)(h * HS + tid), tid & 63);
