@@ -91,6 +91,17 @@ def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, s
     return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (calibrated on add_k), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_q4_k_14336x4096_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, threads: int) -> dict:
     """The CPU oracle (a C restatement of the reference's forward) timed on
     the host cores on a bounded sample: n_tokens decode steps of the same
@@ -200,7 +211,7 @@ def run_decode(args) -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_launch_us": round(g["us"], 3),
         },
         "cpu_baseline": cpu,
@@ -224,6 +235,27 @@ def run_sweep(args) -> None:
             rows_out.append(rec)
             log(f"sweep: {name} {rows}x{cols}: {g['us']:.2f} us, {g['gbs']:.0f} GB/s ({rec['frac'] * 100:.1f}%)")
     print(json.dumps({"sweep": rows_out}), flush=True)
+    ctx.close()
+
+
+def run_pmc_sample(args) -> None:
+    """Workload for the rocprofv3 --pmc passes behind roofline.traffic: the
+    element-wise add kernel (add_k) over 64 Mi floats, whose HBM traffic is
+    known (reads 2 x 256 MiB, writes 256 MiB), calibrates FETCH_SIZE and
+    WRITE_SIZE; then the roofline kernel (gemv_q4_k_plain 14336x4096) on
+    weight copies rotated past the Infinity Cache."""
+    ctx = I.LlmContext(0, args.code_object)
+    n = 64 << 20
+    a, b = ctx.alloc(n * 4), ctx.alloc(n * 4)
+    ctx.fill_normal(a, n, 1, 0, 0.0, 1.0)
+    ctx.fill_normal(b, n, 2, 0, 0.0, 1.0)
+    for _ in range(3):
+        ctx.add_assign(a, b, n)
+    ctx.sync()
+    a.free()
+    b.free()
+    g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
+    log(f"pmc sample: add_k {3} x {n} floats; gemv_q4_k_plain 14336x4096 {g['us']:.2f} us")
     ctx.close()
 
 
@@ -289,6 +321,7 @@ def main() -> None:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")
+    ap.add_argument("--pmc-sample", action="store_true", help="workload for the rocprofv3 --pmc traffic passes")
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
@@ -297,7 +330,9 @@ def main() -> None:
         print("bench.py: this build runs on one GPU; the multi-GPU sharding of the decode path is designed "
               "but not built. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    if args.sweep:
+    if args.pmc_sample:
+        run_pmc_sample(args)
+    elif args.sweep:
         run_sweep(args)
     elif args.attn:
         run_attn(args)
