@@ -91,6 +91,20 @@ def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, s
     return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
 
 
+MFMA_F16_PEAK = 2.5e15  # MI355X dense f16 matrix-core FLOP/s
+
+
+def prefill_flops(cfg: I.Llama2Config, n: int) -> float:
+    """Algorithmic FLOPs of a prompt of n tokens: 2 per weight per token for
+    the layer matrices, plus causal attention (q.k and p.v: 2 x 2 x hs per
+    key per head, sum over t of t+1 keys)."""
+    hs = cfg.hidden // cfg.n_heads
+    kv = cfg.n_kv_heads * hs
+    mats = cfg.hidden * (cfg.hidden + 2 * kv) + cfg.hidden * cfg.hidden + 3 * cfg.hidden * cfg.ffn
+    attn = 4.0 * hs * cfg.n_heads * (n * (n + 1) / 2)
+    return cfg.n_layers * (2.0 * n * mats + attn)
+
+
 def measured_traffic():
     """HBM bytes per launch of the roofline kernel from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (calibrated on add_k), or None."""
@@ -142,15 +156,24 @@ def run_decode(args) -> None:
     s = I.Llama2State(ctx, cfg)
     prompt = np.random.default_rng(8).integers(0, cfg.vocab, prompt_len).astype(np.uint32)
     s.reset(prompt, 0)
-    t0 = time.perf_counter()
-    chunk = 512
-    done = 0
-    while done < prompt_len - 1:  # prefill: sequential decode of the prompt (untimed)
-        n = min(chunk, prompt_len - 1 - done)
-        I.Llama2.generate(ctx, s, w, n, use_graph=not args.no_graph)
+    # prompt: the first prompt_len - 1 tokens through the matrix-core prefill
+    # (the last one goes through the first decode step); timed on its own
+    n_pf = prompt_len - 1
+    pf = None
+    if n_pf > 0:
+        I.Llama2.prefill(ctx, s, w, n_pf)  # warm-up: kernels loaded, scratch allocated
+        s.reset(prompt, 0)
         ctx.sync()
-        done += n
-        log(f"bench: prefill {done}/{prompt_len - 1} tokens ({time.perf_counter() - t0:.1f}s)")
+        ctx.event_record(4)
+        I.Llama2.prefill(ctx, s, w, n_pf)
+        ctx.event_record(5)
+        pf_ms = ctx.event_elapsed(4, 5)
+        flops = prefill_flops(cfg, n_pf)
+        pf = {"tokens": n_pf, "ms": round(pf_ms, 3), "tok_s": round(n_pf / pf_ms * 1000.0, 1),
+              "tflops": round(flops / (pf_ms * 1e-3) / 1e12, 2), "flops": int(flops),
+              "mfma_frac": round(flops / (pf_ms * 1e-3) / MFMA_F16_PEAK, 4)}
+        log(f"bench: prefill {n_pf} tokens in {pf_ms:.2f} ms ({pf['tok_s']:.0f} tok/s, {pf['tflops']:.1f} TFLOP/s, "
+            f"{pf['mfma_frac'] * 100:.1f}% of the f16 dense peak)")
     I.Llama2.generate(ctx, s, w, args.warmup, use_graph=not args.no_graph)
     ctx.sync()
     pos0 = int(s.read("pos", np.uint32)[0])
@@ -203,6 +226,7 @@ def run_decode(args) -> None:
             "decode_bytes_per_token": int(tok_bytes),
             "decode_hbm_frac": round(tok_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "device": dev_name,
+            "prefill": pf,
         },
         "roofline": {
             "bound": "hbm",

@@ -185,6 +185,17 @@ IFR_API ifr_status ifr_attention(ifr_ctx *ctx, const ifr_attn_params *params, co
  * the device. */
 IFR_API ifr_status ifr_argmax(ifr_ctx *ctx, const float *v, uint32_t n, uint32_t *dev_index);
 
+/* Prompt-path GEMM (no reference counterpart; the reference multiplies
+ * the prompt one token at a time through GemvQuant,
+ * crates/inferi/src/ops/gemv_quant.rs:183-340):
+ * y[m][rows] (+)= x[m][cols] . dequant(W)[rows x cols]^T, x f16 (IEEE
+ * binary16, row-major, 16-byte aligned), W Q4_K rows as a GGUF file stores
+ * them, y f32 row-major with leading dimension `rows`.  The weights are
+ * dequantized into f16 tiles and multiplied on the matrix cores
+ * (v_mfma_f32_32x32x16_f16, f32 accumulation); accumulate != 0 adds to y. */
+IFR_API ifr_status ifr_gemm_quant(ifr_ctx *ctx, float *y, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
+                                  const void *x_f16, uint32_t m, int32_t accumulate);
+
 /* GGUF blocks from f32 values on the device: the deterministic min/max
  * quantizer used for the synthetic models (the reference only dequantizes;
  * crates/inferi/src/quantization.rs:1-426).  dtype Q8_0/Q4_K/Q5_K/Q6_K/F16/F32. */
@@ -250,6 +261,17 @@ IFR_API ifr_status ifr_llama2_launch(ifr_ctx *ctx, ifr_llama2_state *s, const if
  * every step). */
 IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
                                        uint32_t n_steps, int32_t use_graph);
+/* Prompt prefill (the reference runs a prompt through Llama2::launch one
+ * token at a time, crates/inferi-chat/src/chat_llama2.rs:137-160): the
+ * n_tokens forced prompt tokens at device positions [pos, pos + n_tokens)
+ * go through every layer in chunks, with their matrix products as GEMMs on
+ * the matrix cores (ifr_gemm_quant) and causal attention over the cache;
+ * their KV-cache rows are written and the position advances by n_tokens.
+ * No logits are formed: the next decode step, at the prompt's last token,
+ * produces them.  Waits for queued work (it reads the position).  Requires
+ * Q4_K attention and FFN matrices and the original RoPE variant. */
+IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
+                                      uint32_t n_tokens);
 /* Copies tokens[start, start+n) of the sequence to the host (waits). */
 IFR_API ifr_status ifr_llama2_read_tokens(ifr_llama2_state *s, uint32_t *host, uint32_t start, uint32_t n);
 /* Device pointer and size of a state buffer: "x", "logits", "pos", "tokens",

@@ -79,6 +79,7 @@ SIGNATURES = {
     "ifr_activation_bytes": (_u64, [_u32]),
     "ifr_quantize_activation": (_i32, [_vp, _vp, _vp, _vp, _u32, _vp]),
     "ifr_matmul_quant_xq": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
+    "ifr_gemm_quant": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp, _u32, _i32]),
     "ifr_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32]),
     "ifr_add": (_i32, [_vp, _vp, _vp, _u32]),
     "ifr_rope": (_i32, [_vp, _i32, _vp, _vp, _u32, _vp, _u32]),
@@ -95,6 +96,7 @@ SIGNATURES = {
     "ifr_llama2_state_reset": (_i32, [_vp, _vp, _u32, _u32]),
     "ifr_llama2_launch": (_i32, [_vp, _vp, _vp, _i32]),
     "ifr_llama2_generate": (_i32, [_vp, _vp, _vp, _u32, _i32]),
+    "ifr_llama2_prefill": (_i32, [_vp, _vp, _vp, _u32]),
     "ifr_llama2_read_tokens": (_i32, [_vp, _vp, _u32, _u32]),
     "ifr_llama2_state_buffer": (_i32, [_vp, _cp, _i32, C.POINTER(_vp), C.POINTER(_sz)]),
 }
@@ -228,6 +230,10 @@ class LlmContext:
 
     def matmul_quant_xq(self, out, a, dtype: int, rows: int, cols: int, xq) -> None:
         self._check(lib().ifr_matmul_quant_xq(self.h, _ptr(out), _ptr(a), dtype, rows, cols, _ptr(xq)))
+
+    def gemm_quant(self, y, w, dtype: int, rows: int, cols: int, x_f16, m: int, accumulate: bool = False) -> None:
+        """y[m][rows] (+)= x_f16[m][cols] . dequant(W)^T on the matrix cores."""
+        self._check(lib().ifr_gemm_quant(self.h, _ptr(y), _ptr(w), dtype, rows, cols, _ptr(x_f16), m, int(accumulate)))
 
     @staticmethod
     def activation_bytes(n: int) -> int:
@@ -420,6 +426,11 @@ class Llama2:
     @staticmethod
     def launch(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, fused: bool = True) -> None:
         ctxt._check(lib().ifr_llama2_launch(ctxt.h, state.h, weights.h, int(fused)))
+
+    @staticmethod
+    def prefill(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, n_tokens: int) -> None:
+        """The next n_tokens forced prompt tokens through the batched (matrix-core) path."""
+        ctxt._check(lib().ifr_llama2_prefill(ctxt.h, state.h, weights.h, n_tokens))
 
     @staticmethod
     def generate(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, n_steps: int,

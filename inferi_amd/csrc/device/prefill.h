@@ -1,0 +1,322 @@
+// Prompt (prefill) kernels: a chunk of M tokens through one decoder layer.
+//
+// The reference feeds a prompt through its decode step one token at a time
+// (crates/inferi-chat/src/chat_llama2.rs:137-160).  Here the prompt's
+// matrix products are GEMMs on the matrix cores: Q4_K weight tiles are
+// dequantized (the reference's arithmetic, quantization.rs:358-392) into
+// LDS as f16, the activations arrive as f16, and v_mfma_f32_32x32x16_f16
+// accumulates in f32.  Around them: embedding, RMSNorm to f16, RoPE plus
+// the KV-cache store, causal attention over the cache, and silu(g) * u.
+// The prompt's last token then goes through the ordinary decode step,
+// which produces the logits and the next token.
+#pragma once
+#include "attention.h"
+
+namespace ifr {
+
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------------ GEMM --
+// Y[m][n] = sum_k X[m][k] * deq(W)[n][k]   (EPI 0: Y =, EPI 1: Y +=)
+// X: f16, row m at x + m * ldx; W: Q4_K rows of K/256 blocks; Y: f32, row m
+// at y + m * ldy.  Tile 128 (m) x 128 (n), K steps of 64; four waves, each a
+// 64 x 64 quadrant as 2 x 2 MFMA 32x32x16 tiles.  The next K step's global
+// loads are issued before the current step's MFMAs.
+constexpr int PF_BM = 128, PF_BN = 128, PF_BK = 64;
+constexpr int PF_LDS = PF_BK + 8; // halves per LDS row: 144 B, so the 32 rows an MFMA operand read touches spread over the banks
+
+template <int EPI>
+__device__ void gemm_q4k_f16_body(const PfGemmArgs &a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[PF_BM][PF_LDS];
+    __shared__ __attribute__((aligned(16))) _Float16 ws[PF_BN][PF_LDS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t m0 = blockIdx.y * PF_BM, n0 = blockIdx.x * PF_BN;
+
+    // global -> register staging: thread t owns tile row t/2, halves [32*(t%2), +32)
+    const uint32_t r = (uint32_t)tid >> 1, hseg = (uint32_t)tid & 1u;
+    const bool xrow_ok = m0 + r < a.M, wrow_ok = n0 + r < a.N;
+    const _Float16 *xrow = (const _Float16 *)a.x + (size_t)min(m0 + r, a.M - 1) * a.ldx;
+    const uint8_t *wrow = a.w + (size_t)min(n0 + r, a.N - 1) * a.row_bytes;
+    uint4 xv[4], hv, qv[2];
+    auto gload = [&](uint32_t k0) {
+        const uint4 *xp = (const uint4 *)(xrow + k0 + 32 * hseg);
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[i] = xrow_ok ? xp[i] : make_uint4(0, 0, 0, 0);
+        const uint32_t kb = k0 / 256, g = (k0 % 256) / 64; // block, 64-element chunk within it
+        const uint8_t *b = wrow + (size_t)kb * 144;
+        hv = ld16(b);
+        qv[0] = ld16(b + 16 + 32 * g);
+        qv[1] = ld16(b + 32 + 32 * g);
+    };
+    // dequantize this thread's 32 weights (sub-block 2g + hseg) into LDS:
+    // y = (d * sc) * q - (dmin * m), quantization.rs:371-389
+    auto lstore = [&](uint32_t k0) {
+        const uint32_t g = (k0 % 256) / 64;
+        uint32_t sc0, m0s, sc1, m1s;
+        scale_min_pair(g, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
+        const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
+        const float d1 = d * (float)(hseg ? sc1 : sc0), mm = dm * (float)(hseg ? m1s : m0s);
+        const uint32_t w8[8] = {qv[0].x, qv[0].y, qv[0].z, qv[0].w, qv[1].x, qv[1].y, qv[1].z, qv[1].w};
+        _Float16 h[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t word = hseg ? (w8[i] >> 4) : w8[i];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float q = (float)((word >> (8 * e)) & 0xFu);
+                const float y = __fsub_rn(__fmul_rn(d1, q), mm); // no contraction: the reference's roundings
+                h[4 * i + e] = wrow_ok ? (_Float16)y : (_Float16)0.0f;
+            }
+        }
+        uint4 *wd = (uint4 *)&ws[r][32 * hseg];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint4 u;
+            __builtin_memcpy(&u, &h[8 * i], 16);
+            wd[i] = u;
+        }
+        uint4 *xd = (uint4 *)&xs[r][32 * hseg];
+#pragma unroll
+        for (int i = 0; i < 4; i++) xd[i] = xv[i];
+    };
+
+    float16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    const uint32_t wm = 64 * (uint32_t)(wave >> 1), wn = 64 * (uint32_t)(wave & 1);
+    const uint32_t li = (uint32_t)lane & 31u, lk = 8 * ((uint32_t)lane >> 5);
+    gload(0);
+    for (uint32_t k0 = 0; k0 < a.K; k0 += PF_BK) {
+        __syncthreads(); // the previous step's operand reads are done
+        lstore(k0);
+        if (k0 + PF_BK < a.K) gload(k0 + PF_BK);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < PF_BK; kk += 16) {
+            half8v av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) av[i] = *(const half8v *)&xs[wm + 32 * i + li][kk + lk];
+#pragma unroll
+            for (int j = 0; j < 2; j++) bv[j] = *(const half8v *)&ws[wn + 32 * j + li][kk + lk];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    // D[row][col]: col = lane % 32, row = 8*(e/4) + 4*(lane/32) + e%4
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t n = n0 + wn + 32 * j + li;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+                if (m < a.M && n < a.N) {
+                    float *yp = a.y + (size_t)m * a.ldy + n;
+                    if constexpr (EPI == 1)
+                        *yp += acc[i][j][e];
+                    else
+                        *yp = acc[i][j][e];
+                }
+            }
+        }
+}
+
+// ------------------------------------------------------------ pointwise --
+
+// X[m] = dequant(table)[tok[p0 + m]]
+IFR_DEV void pf_embed_body(const PfArgs &a) {
+    float *xo = (float *)a.x;
+    const uint32_t m = blockIdx.x;
+    const uint32_t tok = a.tokens[a.p0 + m];
+    const uint8_t *row = a.table + (size_t)tok * a.row_bytes;
+    for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x)
+        xo[(size_t)m * a.hidden + i] = deq_elem(a.fmt, row, i);
+}
+
+// xh[m] = f16((x[m] * (1/sqrt(mean(x[m]^2) + eps))) * gamma), rms_norm.rs:81-121
+IFR_DEV void pf_rmsnorm_f16_body(const PfArgs &a) {
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, n = a.hidden;
+    const float *x = (const float *)a.x + (size_t)m * n;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t w = 0; w < blockDim.x / 64; w++) t += red[w];
+    const float rs = 1.0f / sqrtf(t / (float)n + a.eps);
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+        ((_Float16 *)a.xh)[(size_t)m * a.ldh + i] = (_Float16)((x[i] * rs) * a.gamma[i]);
+}
+
+// Token m (position p0 + m) of qkv [M][q_dim + 2 kv_dim]: RoPE on q (in
+// place) and k, then k and v to the cache rows (rope.rs:51-92 with the
+// state's theta table).
+IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
+    const uint32_t m = blockIdx.x, pos = a.p0 + m, hs = a.head_size;
+    float *row = (float *)a.qkv + (size_t)m * a.ld_qkv;
+    const uint32_t qd = a.q_dim, kd = a.kv_dim;
+    for (uint32_t i = threadIdx.x; i < (qd + kd) / 2; i += blockDim.x) {
+        const uint32_t v = 2 * i;
+        float x0 = row[v], x1 = row[v + 1];
+        const uint32_t idx = v < qd ? v : v - qd;
+        rope_pair(x0, x1, idx, hs, pos, a.rope_tab);
+        if (v < qd) {
+            row[v] = x0;
+            row[v + 1] = x1;
+        } else {
+            const size_t off = (size_t)pos * kd + idx;
+            if (a.kv_f16) {
+                ((uint16_t *)a.k_cache)[off] = f32_to_f16(x0);
+                ((uint16_t *)a.k_cache)[off + 1] = f32_to_f16(x1);
+            } else {
+                ((float *)a.k_cache)[off] = x0;
+                ((float *)a.k_cache)[off + 1] = x1;
+            }
+        }
+    }
+    for (uint32_t i = threadIdx.x; i < kd; i += blockDim.x) {
+        const float v = row[qd + kd + i];
+        const size_t off = (size_t)pos * kd + i;
+        if (a.kv_f16)
+            ((uint16_t *)a.v_cache)[off] = f32_to_f16(v);
+        else
+            ((float *)a.v_cache)[off] = v;
+    }
+}
+
+// h[m][j] = f16(u * (g / (1 + exp(-g)))), g = gu[m][j], u = gu[m][F + j] (silu.rs:24-53)
+IFR_DEV void pf_silu_body(const PfArgs &a) {
+    const uint32_t m = blockIdx.y, F = a.ffn;
+    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= F) return;
+    const float *gu = (const float *)a.gu;
+    const float g = gu[(size_t)m * 2 * F + j], u = gu[(size_t)m * 2 * F + F + j];
+    ((_Float16 *)a.xh)[(size_t)m * a.ldh + j] = (_Float16)(u * (g / (1.0f + expf(-g))));
+}
+
+// ------------------------------------------------------------ attention --
+// Causal attention of the chunk's queries (positions p0 .. p0+M-1) over the
+// cache rows [0, position].  Workgroup (h, qt): KV head h, its G query heads
+// and 64/G queries, i.e. 64 rows r = qi * G + j.  Key tiles of 64 rows go
+// through LDS; each thread forms a 4 x 4 block of scores (rows x keys) from
+// register fragments, scores are in base-2 units (q pre-scaled by
+// log2(e)/sqrt(hs)), and each row keeps a running softmax; out = o / l is
+// written as f16 for the O GEMM.
+constexpr int PF_ROWS = 64, PF_KT = 64;
+
+template <int G>
+constexpr uint32_t pf_attn_queries() { return (uint32_t)(PF_ROWS / G); }
+
+template <int HS, int G, bool F16>
+__device__ void pf_attn_body(const PfArgs &a) {
+    constexpr int R = PF_ROWS, NT = 256, QT = PF_ROWS / G;
+    constexpr int TPR = NT / R;              // threads per row in the PV phase (4)
+    constexpr int DPT = HS / TPR;            // dims per thread in the PV phase
+    __shared__ float qsh[R][HS + 1];
+    __shared__ float ksh[PF_KT][HS + 1];
+    __shared__ float vsh[PF_KT][HS];
+    __shared__ float psh[R][PF_KT + 1];
+    const int tid = threadIdx.x;
+    const uint32_t kvh = blockIdx.x, qt0 = blockIdx.y * QT;
+    const uint32_t nq = min((uint32_t)QT, a.M - qt0);
+    const float qscale = 1.44269504088896341f / sqrtf((float)HS);
+    const float *qbase = (const float *)a.qkv;
+    for (uint32_t i = tid; i < (uint32_t)R * HS; i += NT) {
+        const uint32_t rr = i / HS, d = i % HS, qi = rr / G, j = rr % G;
+        const float v = qi < nq ? qbase[(size_t)(qt0 + qi) * a.ld_qkv + (kvh * G + j) * HS + d] : 0.0f;
+        qsh[rr][d] = v * qscale;
+    }
+    // score block: rows [sr0, sr0 + 4), keys [sk0, sk0 + 4)
+    const uint32_t sr0 = ((uint32_t)tid % 16) * 4, sk0 = ((uint32_t)tid / 16) * 4;
+    // PV: row pr, dims part + TPR * e
+    const uint32_t pr = (uint32_t)tid / TPR, part = (uint32_t)tid % TPR;
+    float o[DPT];
+#pragma unroll
+    for (int e = 0; e < DPT; e++) o[e] = 0.0f;
+    float mrow = -INFINITY, lrow = 0.0f;
+    const uint32_t last = a.p0 + qt0 + nq - 1; // largest query position of the tile
+    for (uint32_t k0 = 0; k0 <= last; k0 += PF_KT) {
+        __syncthreads();
+        for (uint32_t i = tid; i < (uint32_t)PF_KT * HS; i += NT) {
+            const uint32_t kr = i / HS, d = i % HS, kp = k0 + kr;
+            float kvk = 0.0f, kvv = 0.0f;
+            if (kp <= last) {
+                const size_t off = (size_t)kp * a.kv_dim + (size_t)kvh * HS + d;
+                if constexpr (F16) {
+                    kvk = f16_to_f32(((const uint16_t *)a.k_cache)[off]);
+                    kvv = f16_to_f32(((const uint16_t *)a.v_cache)[off]);
+                } else {
+                    kvk = ((const float *)a.k_cache)[off];
+                    kvv = ((const float *)a.v_cache)[off];
+                }
+            }
+            ksh[kr][d] = kvk;
+            vsh[kr][d] = kvv;
+        }
+        __syncthreads();
+        {
+            float sc[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) sc[i][j] = 0.0f;
+#pragma unroll 4
+            for (int d = 0; d < HS; d++) {
+                float qv[4], kv[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) qv[i] = qsh[sr0 + i][d];
+#pragma unroll
+                for (int j = 0; j < 4; j++) kv[j] = ksh[sk0 + j][d];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) sc[i][j] = fmaf(qv[i], kv[j], sc[i][j]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t qi = (sr0 + i) / G, qpos = a.p0 + qt0 + qi;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    psh[sr0 + i][sk0 + j] = (k0 + sk0 + j <= qpos && qi < nq) ? sc[i][j] : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // running softmax of row pr over this tile, then o += p v
+        float mt = -INFINITY;
+        for (int k = 0; k < PF_KT; k++) mt = fmaxf(mt, psh[pr][k]);
+        if (mt != -INFINITY) {
+            const float mn = fmaxf(mrow, mt);
+            const float al = exp2f(mrow - mn); // 0 while mrow is -inf
+            lrow *= al;
+#pragma unroll
+            for (int e = 0; e < DPT; e++) o[e] *= al;
+            for (int k = 0; k < PF_KT; k++) {
+                const float p = exp2f(psh[pr][k] - mn); // 0 for a masked key
+                lrow += p;
+#pragma unroll
+                for (int e = 0; e < DPT; e++) o[e] = fmaf(p, vsh[k][part + TPR * e], o[e]);
+            }
+            mrow = mn;
+        }
+    }
+    const uint32_t pqi = pr / G;
+    if (pqi < nq) {
+        _Float16 *out = (_Float16 *)a.xh + (size_t)(qt0 + pqi) * a.ldh + (kvh * G + pr % G) * HS;
+#pragma unroll
+        for (int e = 0; e < DPT; e++) out[part + TPR * e] = (_Float16)(o[e] / lrow);
+    }
+}
+
+} // namespace ifr

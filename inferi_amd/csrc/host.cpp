@@ -40,6 +40,8 @@ uint64_t xq_bytes(uint64_t n) { return 3 * n + n / 2; }
 constexpr uint32_t ATTN_CMAX = 256;       // device/attention.h
 constexpr uint32_t ATTN_MERGE_MAX = 256;  // device/attention.h: most splits per KV head
 constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
+constexpr uint32_t PF_GEMM_TILE = 128;    // device/prefill.h: PF_BM = PF_BN
+constexpr uint32_t PF_CHUNK = 512;        // prompt tokens per prefill pass
 
 int qk_of(int32_t dt) {
     switch (dt) {
@@ -324,6 +326,10 @@ struct ifr_llama2_state {
     float *ss_a, *ss_f;
     uint8_t *kcache, *vcache;
     size_t layer_kv_bytes;
+    // prefill scratch (allocated at the first prefill): a chunk of pf_chunk tokens
+    uint32_t pf_chunk = 0, pf_ldh = 0;
+    float *pf_x = nullptr, *pf_qkv = nullptr, *pf_gu = nullptr;
+    uint16_t *pf_xh = nullptr;
     // captured decode step
     hipGraphExec_t graph = nullptr;
     const ifr_llama2_weights *graph_w = nullptr;
@@ -1107,6 +1113,140 @@ static ifr_status check_weights(ifr_ctx *c, const ifr_llama2_state *s, const ifr
     const Tens &out = w->output.data ? w->output : w->token_embd;
     if (!gemv_fmt_name(out.dtype)) return c->fail(IFR_EUNSUPPORTED, "output head dtype %d has no GEMV kernel", out.dtype);
     return IFR_OK;
+}
+
+// ---------------------------------------------------------------- prefill --
+
+// Y[m][n] (+)= sum_k Xh[m][k] * deq(W)[n][k] on the matrix cores.
+static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const Tens &w, float *y, uint32_t ldy,
+                                 uint32_t M, bool accumulate) {
+    PfGemmArgs g{};
+    g.x = xh;
+    g.w = w.data;
+    g.y = y;
+    g.M = M;
+    g.N = w.rows;
+    g.K = w.cols;
+    g.ldx = ldx;
+    g.ldy = ldy;
+    g.row_bytes = (w.cols / 256) * 144;
+    const dim3 grid((w.rows + PF_GEMM_TILE - 1) / PF_GEMM_TILE, (M + PF_GEMM_TILE - 1) / PF_GEMM_TILE);
+    return c->launch(accumulate ? "gemm_q4_k_f16_add" : "gemm_q4_k_f16_store", grid, dim3(256), 0, g);
+}
+
+IFR_API ifr_status ifr_gemm_quant(ifr_ctx *c, float *y, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
+                                  const void *x_f16, uint32_t m, int32_t accumulate) {
+    if (!c) return IFR_EINVAL;
+    if (!y || !w || !x_f16) return c->fail(IFR_EINVAL, "gemm_quant: null pointer");
+    if (dtype != IFR_Q4_K) return c->fail(IFR_EUNSUPPORTED, "gemm_quant: dtype %d (Q4_K only)", dtype);
+    if (!rows || !m || !cols || cols % 256) return c->fail(IFR_EINVAL, "gemm_quant: rows, m > 0 and cols %% 256 == 0");
+    if ((uintptr_t)w % 16 || (uintptr_t)x_f16 % 16) return c->fail(IFR_EINVAL, "gemm_quant: w and x must be 16-byte aligned");
+    Tens t;
+    t.dtype = dtype;
+    t.data = (const uint8_t *)w;
+    t.rows = rows;
+    t.cols = cols;
+    return launch_pf_gemm(c, x_f16, cols, t, y, rows, m, accumulate != 0);
+}
+
+static ifr_status pf_ensure_scratch(ifr_llama2_state *s) {
+    if (s->pf_x) return IFR_OK;
+    ifr_ctx *c = s->ctx;
+    const ifr_llama2_config &cfg = s->cfg;
+    const uint32_t C = PF_CHUNK, H = cfg.hidden, F = cfg.ffn, qd = cfg.n_heads * s->head_size;
+    s->pf_chunk = C;
+    s->pf_ldh = std::max(std::max(H, F), qd);
+    auto A = [&](size_t bytes, void **p) -> ifr_status {
+        ifr_status e = c->hip(hipMalloc(p, bytes), "hipMalloc(prefill)");
+        if (!e) s->allocs.push_back(*p);
+        return e;
+    };
+    ifr_status st;
+    if ((st = A((size_t)C * H * 4, (void **)&s->pf_x))) return st;
+    if ((st = A((size_t)C * s->pf_ldh * 2, (void **)&s->pf_xh))) return st;
+    if ((st = A((size_t)C * (qd + 2 * s->kv_dim) * 4, (void **)&s->pf_qkv))) return st;
+    return A((size_t)C * 2 * F * 4, (void **)&s->pf_gu);
+}
+
+IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, uint32_t n) {
+    if (!c || !s) return IFR_EINVAL;
+    ifr_status st = check_weights(c, s, w);
+    if (st) return st;
+    const ifr_llama2_config &cfg = s->cfg;
+    if (cfg.rope_variant != IFR_ROPE_ORIGINAL) return c->fail(IFR_EUNSUPPORTED, "prefill: NeoX RoPE");
+    for (const LayerW &L : w->layers) {
+        const Tens *mats[] = {&L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
+        for (const Tens *t : mats)
+            if (t->dtype != IFR_Q4_K) return c->fail(IFR_EUNSUPPORTED, "prefill: matrices must be Q4_K (found dtype %d)", t->dtype);
+    }
+    if (!n) return IFR_OK;
+    if ((st = pf_ensure_scratch(s))) return st;
+    // the position lives on the device: read it once
+    StepCtl ctl;
+    if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
+    if ((st = c->hip(hipMemcpy(&ctl, s->ctl, sizeof ctl, hipMemcpyDeviceToHost), "hipMemcpy(ctl)"))) return st;
+    const uint32_t pos0 = ctl.pos;
+    if ((uint64_t)pos0 + n > cfg.max_pos) return c->fail(IFR_EINVAL, "prefill: %u tokens from position %u exceed max_pos", n, pos0);
+    if (pos0 + n > ctl.n_forced) return c->fail(IFR_EINVAL, "prefill: positions up to %u hold no prompt token", pos0 + n);
+
+    const uint32_t H = cfg.hidden, F = cfg.ffn, hs = s->head_size, kvd = s->kv_dim, qd = cfg.n_heads * hs;
+    const uint32_t G = s->kv_mul, ldq = qd + 2 * kvd, ldh = s->pf_ldh;
+    char attn_name[64];
+    snprintf(attn_name, sizeof attn_name, "pf_attn_%s_h%u_g%u", cfg.kv_dtype == IFR_F16 ? "f16" : "f32", hs, G);
+    const uint32_t attn_qt = 64 / G;
+    for (uint32_t c0 = 0; c0 < n; c0 += s->pf_chunk) {
+        const uint32_t M = std::min(s->pf_chunk, n - c0), p0 = pos0 + c0;
+        PfArgs a{};
+        a.x = s->pf_x;
+        a.xh = s->pf_xh;
+        a.ldh = ldh;
+        a.hidden = H;
+        a.eps = cfg.rms_eps;
+        a.M = M;
+        a.p0 = p0;
+        a.tokens = s->tokens;
+        a.table = w->token_embd.data;
+        a.row_bytes = H / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
+        a.fmt = w->token_embd.dtype;
+        a.qkv = s->pf_qkv;
+        a.ld_qkv = ldq;
+        a.q_dim = qd;
+        a.kv_dim = kvd;
+        a.head_size = hs;
+        a.rope_tab = s->rope_tab;
+        a.kv_f16 = cfg.kv_dtype == IFR_F16;
+        a.ffn = F;
+        a.gu = s->pf_gu;
+        if ((st = c->launch("pf_embed_k", dim3(M), dim3(256), 0, a))) return st;
+        for (uint32_t l = 0; l < cfg.n_layers; l++) {
+            const LayerW &L = w->layers[l];
+            a.k_cache = s->kcache + (size_t)l * s->layer_kv_bytes;
+            a.v_cache = s->vcache + (size_t)l * s->layer_kv_bytes;
+            a.gamma = (const float *)L.attn_norm.data;
+            if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, M, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, M, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, M, false))) return st;
+            if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
+            if ((st = c->launch(attn_name, dim3(cfg.n_kv_heads, (M + attn_qt - 1) / attn_qt), dim3(256), 0, a))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, M, true))) return st;
+            a.gamma = (const float *)L.ffn_norm.data;
+            if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, M, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, M, false))) return st;
+            if ((st = c->launch("pf_silu_k", dim3((F + 255) / 256, M), dim3(256), 0, a))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, M, true))) return st;
+        }
+    }
+    // advance the device position (and the unfused path's op parameters)
+    const uint32_t pos = pos0 + n;
+    if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
+    ctl.pos = pos;
+    ifr_rope_config rope{hs, kvd, pos, cfg.rope_theta};
+    ifr_attn_params ap{cfg.max_pos, kvd, G, cfg.n_heads, hs, pos};
+    if ((st = c->hip(hipMemcpy(s->ctl, &ctl, sizeof ctl, hipMemcpyHostToDevice), "hipMemcpy(ctl)"))) return st;
+    if ((st = c->hip(hipMemcpy(s->rope_cfg, &rope, sizeof rope, hipMemcpyHostToDevice), "hipMemcpy(rope)"))) return st;
+    return c->hip(hipMemcpy(s->attn_params, &ap, sizeof ap, hipMemcpyHostToDevice), "hipMemcpy(attn)");
 }
 
 IFR_API ifr_status ifr_llama2_launch(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int32_t fused) {

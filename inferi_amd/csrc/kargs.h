@@ -176,4 +176,35 @@ struct KvStoreArgs {
     int32_t kv_f16;
 };
 
+// Prefill GEMM: Y[m][n] (+)= sum_k X[m][k] * deq(W)[n][k]; X f16 (as raw
+// halves), W Q4_K rows, Y f32.
+struct PfGemmArgs {
+    const void *x;       // f16 [M][ldx]
+    const uint8_t *w;    // Q4_K rows
+    float *y;            // f32 [M][ldy]
+    uint32_t M, N, K, ldx, ldy, row_bytes;
+};
+
+// Prefill pointwise and attention kernels (one chunk of M prompt tokens at
+// positions p0 .. p0+M-1).
+struct PfArgs {
+    void *x;             // f32 [M][hidden] residual stream
+    void *xh;            // f16 [M][ldh] GEMM input / attention output / h
+    uint32_t ldh, hidden;
+    const float *gamma;  // RMSNorm weight
+    float eps;
+    uint32_t M, p0;
+    const uint32_t *tokens; // token sequence (embedding)
+    const uint8_t *table;   // token_embd rows
+    uint32_t row_bytes;
+    int32_t fmt;
+    void *qkv;           // f32 [M][ld_qkv]: q | k | v
+    uint32_t ld_qkv, q_dim, kv_dim, head_size;
+    const float *rope_tab;
+    void *k_cache, *v_cache; // this layer's cache base
+    int32_t kv_f16;
+    uint32_t ffn;
+    void *gu;            // f32 [M][2*ffn]: gate | up
+};
+
 } // namespace ifr

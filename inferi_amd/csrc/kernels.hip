@@ -5,6 +5,7 @@
 #include "device/attention.h"
 #include "device/elementwise.h"
 #include "device/gemv.h"
+#include "device/prefill.h"
 
 using namespace ifr;
 
@@ -69,3 +70,28 @@ extern "C" __global__ void __launch_bounds__(256) kv_store_k(KvStoreArgs a) { kv
 extern "C" __global__ void __launch_bounds__(256) dequant_k(DequantArgs a) { dequant_body(a); }
 extern "C" __global__ void __launch_bounds__(64) quantize_k(QuantArgs a) { quantize_body(a); }
 extern "C" __global__ void __launch_bounds__(256) fill_normal_k(FillArgs a) { fill_normal_body(a); }
+
+// prompt (prefill) path
+extern "C" __global__ void __launch_bounds__(256) gemm_q4_k_f16_store(PfGemmArgs a) { gemm_q4k_f16_body<0>(a); }
+extern "C" __global__ void __launch_bounds__(256) gemm_q4_k_f16_add(PfGemmArgs a) { gemm_q4k_f16_body<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) pf_embed_k(PfArgs a) { pf_embed_body(a); }
+extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { pf_rmsnorm_f16_body(a); }
+extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }
+extern "C" __global__ void __launch_bounds__(256) pf_silu_k(PfArgs a) { pf_silu_body(a); }
+
+#define PF_ATTN_KERNEL(HS, G)                                                                    \
+    extern "C" __global__ void __launch_bounds__(256) pf_attn_f16_h##HS##_g##G(PfArgs a) {       \
+        pf_attn_body<HS, G, true>(a);                                                            \
+    }                                                                                            \
+    extern "C" __global__ void __launch_bounds__(256) pf_attn_f32_h##HS##_g##G(PfArgs a) {       \
+        pf_attn_body<HS, G, false>(a);                                                           \
+    }
+
+PF_ATTN_KERNEL(64, 1)
+PF_ATTN_KERNEL(64, 2)
+PF_ATTN_KERNEL(64, 4)
+PF_ATTN_KERNEL(64, 8)
+PF_ATTN_KERNEL(128, 1)
+PF_ATTN_KERNEL(128, 2)
+PF_ATTN_KERNEL(128, 4)
+PF_ATTN_KERNEL(128, 8)

@@ -1,0 +1,167 @@
+"""GPU parity of the prompt (prefill) path.
+
+ifr_gemm_quant multiplies f16 activations by Q4_K weights dequantized to f16
+tiles on the matrix cores: it is checked against an f64 product of the same
+f16-rounded operands (only the f32 accumulation order may differ).
+
+ifr_llama2_prefill runs a prompt through every layer in chunks; the state it
+leaves (KV-cache rows, position) must continue exactly like a state that
+decoded the prompt token by token.  Its products take f16 inputs where the
+decode path keeps 22-bit activations, so KV rows and logits are compared
+within 2e-2 of max(|e|, 1) (the tolerance is a property of the f16 path),
+and the continuation's greedy ids are compared where the sequential path's
+top-2 logit margin exceeds that tolerance.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def synthetic_q4k(ctx, rows, cols, seed):
+    import inferi_amd as I
+
+    n = rows * cols
+    tmp = ctx.alloc(n * 4)
+    ctx.fill_normal(tmp, n, seed, 0, 0.0, 0.02)
+    w = ctx.alloc(rows * I.row_bytes(I.Q4_K, cols))
+    ctx.quantize(w, tmp, I.Q4_K, n)
+    tmp.free()
+    return w
+
+
+@pytest.mark.parametrize("rows,cols,m", [(128, 256, 128), (300, 512, 70), (1000, 1024, 257), (4096, 4096, 128),
+                                         (64, 14336, 33)])
+def test_gemm_quant_matches_f64(ctx, oracle_lib, rows, cols, m):
+    import inferi_amd as I
+
+    rng = np.random.default_rng(rows * 7 + cols + m)
+    w = synthetic_q4k(ctx, rows, cols, seed=rows + m)
+    rb = I.row_bytes(I.Q4_K, cols)
+    deq = O.dequant(I.Q4_K, w.download(np.uint8, rows * rb), rows * cols).reshape(rows, cols)
+    wh = deq.astype(np.float16).astype(np.float64)
+    x = rng.standard_normal((m, cols)).astype(np.float16)
+    dx = ctx.upload(x)
+    y = ctx.alloc(m * rows * 4)
+    ctx.gemm_quant(y, w, I.Q4_K, rows, cols, dx, m)
+    got = y.download(np.float32, m * rows).reshape(m, rows).astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd @ wh.T
+    bound = 2e-5 * (np.abs(xd) @ np.abs(wh).T) + 1e-30
+    assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) - bound):.3e}"
+    ctx.gemm_quant(y, w, I.Q4_K, rows, cols, dx, m, accumulate=True)
+    got2 = y.download(np.float32, m * rows).reshape(m, rows).astype(np.float64)
+    assert np.all(np.abs(got2 - 2 * ref) <= 2 * bound)
+    for b in (w, dx, y):
+        b.free()
+
+
+def test_gemm_quant_rejects_bad_input(ctx):
+    import inferi_amd as I
+
+    buf = ctx.alloc(1 << 16)
+    with pytest.raises(I.HipError):
+        ctx.gemm_quant(buf, buf, I.Q6_K, 16, 256, buf, 4)  # Q4_K only
+    with pytest.raises(I.HipError):
+        ctx.gemm_quant(buf, buf, I.Q4_K, 16, 100, buf, 4)  # cols % 256
+    buf.free()
+
+
+def _prefill_vs_decode(ctx, cfg, w, prompt, n_gen, tol=2e-2):
+    import inferi_amd as I
+
+    P = len(prompt)
+    sa, sb = I.Llama2State(ctx, cfg), I.Llama2State(ctx, cfg)
+    try:
+        # A: the prompt token by token, then n_gen greedy steps, logits kept
+        sa.reset(prompt, 0)
+        I.Llama2.generate(ctx, sa, w, P - 1, use_graph=True)
+        logits_a = []
+        for _ in range(n_gen):
+            I.Llama2.generate(ctx, sa, w, 1, use_graph=True)
+            logits_a.append(sa.read("logits"))
+        # B: prefill of the first P-1 tokens, then the same decode steps
+        sb.reset(prompt, 0)
+        I.Llama2.prefill(ctx, sb, w, P - 1)
+        assert int(sb.read("pos", np.uint32)[0]) == P - 1
+        logits_b = []
+        for _ in range(n_gen):
+            I.Llama2.generate(ctx, sb, w, 1, use_graph=True)
+            logits_b.append(sb.read("logits"))
+        f16 = cfg.kv_dtype == I.F16
+        for layer in range(cfg.n_layers):
+            for which in ("key_cache", "value_cache"):
+                ga = sa.read(which, np.uint16 if f16 else np.float32, layer).reshape(cfg.max_pos, cfg.kv_dim)[: P - 1]
+                gb = sb.read(which, np.uint16 if f16 else np.float32, layer).reshape(cfg.max_pos, cfg.kv_dim)[: P - 1]
+                if f16:
+                    ga, gb = O.decode_f16(ga), O.decode_f16(gb)
+                err = np.abs(gb.astype(np.float64) - ga) / np.maximum(np.abs(ga), 1.0)
+                assert err.max() <= tol, f"{which} layer {layer}: {err.max():.3e} at row {int(err.argmax()) // cfg.kv_dim}"
+        toks_a, toks_b = sa.tokens(0, P + n_gen), sb.tokens(0, P + n_gen)
+        compared = 0
+        for i in range(n_gen):
+            la, lb = logits_a[i].astype(np.float64), logits_b[i].astype(np.float64)
+            if not np.array_equal(toks_a[: P + i], toks_b[: P + i]):
+                break  # the sequences diverged earlier: later steps see different inputs
+            err = np.abs(lb - la) / np.maximum(np.abs(la), 1.0)
+            assert err.max() <= tol, f"logits of step {i}: {err.max():.3e}"
+            top2 = np.partition(la, -2)[-2:]
+            if top2[1] - top2[0] > 2 * tol * max(abs(top2[1]), 1.0):
+                assert toks_b[P + i] == toks_a[P + i], f"token {P + i}"
+                compared += 1
+        return compared
+    finally:
+        sa.close()
+        sb.close()
+
+
+def test_prefill_matches_sequential_decode_hs64(ctx, oracle_lib):
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=3, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=1000, max_pos=200,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=31, std=0.05)
+    try:
+        prompt = np.random.default_rng(3).integers(0, cfg.vocab, 150).tolist()
+        assert _prefill_vs_decode(ctx, cfg, w, prompt, 12) > 0
+    finally:
+        w.close()
+
+
+def test_prefill_chunks_and_gqa4_hs128(ctx, oracle_lib):
+    """Two prefill chunks (512 + rest), head size 128, 4 query heads per KV head, f32 cache."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=512, ffn=1024, n_heads=4, n_kv_heads=1, vocab=512, max_pos=700,
+                         rope_theta=500000.0, rms_eps=1e-5, kv_dtype=I.F32)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=41, std=0.05)
+    try:
+        prompt = np.random.default_rng(4).integers(0, cfg.vocab, 600).tolist()
+        assert _prefill_vs_decode(ctx, cfg, w, prompt, 8) > 0
+    finally:
+        w.close()
+
+
+def test_prefill_rejects_unsupported(ctx):
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=1, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=300, max_pos=64,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=5, mat_dtype=I.Q8_0, head_dtype=I.Q8_0, embd_dtype=I.Q8_0)
+    s = I.Llama2State(ctx, cfg)
+    try:
+        s.reset([1, 2, 3], 0)
+        with pytest.raises(I.HipError):
+            I.Llama2.prefill(ctx, s, w, 2)  # Q8_0 matrices
+        w2 = I.Llama2Weights.synthetic(ctx, cfg, seed=5)
+        try:
+            with pytest.raises(I.HipError):
+                I.Llama2.prefill(ctx, s, w2, 5)  # only 3 prompt tokens
+        finally:
+            w2.close()
+    finally:
+        s.close()
+        w.close()
