@@ -208,12 +208,14 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
 
 // ------------------------------------------------------------ attention --
 // Causal attention of the chunk's queries (positions p0 .. p0+M-1) over the
-// cache rows [0, position].  Workgroup (h, qt): KV head h, its G query heads
-// and 64/G queries, i.e. 64 rows r = qi * G + j.  Key tiles of 64 rows go
-// through LDS; each thread forms a 4 x 4 block of scores (rows x keys) from
-// register fragments, scores are in base-2 units (q pre-scaled by
-// log2(e)/sqrt(hs)), and each row keeps a running softmax; out = o / l is
-// written as f16 for the O GEMM.
+// cache rows [0, position], on the matrix cores (flash attention).
+// Workgroup (h, qt): KV head h, its G query heads and 64/G queries, i.e. 64
+// rows r = qi * G + j.  Per key tile of 64 cache rows:
+//   S = Q K^T     (f16 operands from LDS, 4 waves x one 32x32 MFMA tile)
+//   running softmax per row in base-2 units (q pre-scaled by
+//   log2(e)/sqrt(hs)); P = 2^(S - m) as f16
+//   O = alpha O + P V   (4 waves x 32 rows x 64 dims)
+// and out = O / l is written as f16 for the O GEMM.
 constexpr int PF_ROWS = 64, PF_KT = 64;
 
 template <int G>
@@ -222,13 +224,15 @@ constexpr uint32_t pf_attn_queries() { return (uint32_t)(PF_ROWS / G); }
 template <int HS, int G, bool F16>
 __device__ void pf_attn_body(const PfArgs &a) {
     constexpr int R = PF_ROWS, NT = 256, QT = PF_ROWS / G;
-    constexpr int TPR = NT / R;              // threads per row in the PV phase (4)
-    constexpr int DPT = HS / TPR;            // dims per thread in the PV phase
-    __shared__ float qsh[R][HS + 1];
-    __shared__ float ksh[PF_KT][HS + 1];
-    __shared__ float vsh[PF_KT][HS];
-    __shared__ float psh[R][PF_KT + 1];
-    const int tid = threadIdx.x;
+    constexpr int HSP = HS + 8, KTP = PF_KT + 8; // padded LDS rows (halves)
+    constexpr int DT = HS / 64;                  // 32x32 O tiles per wave along the dims
+    __shared__ __attribute__((aligned(16))) _Float16 qh[R][HSP];
+    __shared__ __attribute__((aligned(16))) _Float16 kh[PF_KT][HSP];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[HS][KTP];
+    __shared__ __attribute__((aligned(16))) _Float16 ph[R][KTP];
+    __shared__ float sf[R][PF_KT + 1];
+    __shared__ float alpha_s[R], l_s[R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = blockIdx.x, qt0 = blockIdx.y * QT;
     const uint32_t nq = min((uint32_t)QT, a.M - qt0);
     const float qscale = 1.44269504088896341f / sqrtf((float)HS);
@@ -236,87 +240,116 @@ __device__ void pf_attn_body(const PfArgs &a) {
     for (uint32_t i = tid; i < (uint32_t)R * HS; i += NT) {
         const uint32_t rr = i / HS, d = i % HS, qi = rr / G, j = rr % G;
         const float v = qi < nq ? qbase[(size_t)(qt0 + qi) * a.ld_qkv + (kvh * G + j) * HS + d] : 0.0f;
-        qsh[rr][d] = v * qscale;
+        qh[rr][d] = (_Float16)(v * qscale);
     }
-    // score block: rows [sr0, sr0 + 4), keys [sk0, sk0 + 4)
-    const uint32_t sr0 = ((uint32_t)tid % 16) * 4, sk0 = ((uint32_t)tid / 16) * 4;
-    // PV: row pr, dims part + TPR * e
-    const uint32_t pr = (uint32_t)tid / TPR, part = (uint32_t)tid % TPR;
-    float o[DPT];
+    // softmax ownership: row sr, keys [16 * sq, 16 * sq + 16)
+    const uint32_t sr = (uint32_t)tid >> 2, sq = (uint32_t)tid & 3u;
+    float m_run = -INFINITY, l_run = 0.0f;
+    // MFMA roles
+    const uint32_t li = (uint32_t)lane & 31u, lk = 8 * ((uint32_t)lane >> 5);
+    const uint32_t srow = 32 * (uint32_t)(wave >> 1), skey = 32 * (uint32_t)(wave & 1); // S tile of this wave
+    const uint32_t orow = 32 * (uint32_t)(wave >> 1), odim = (HS / 2) * (uint32_t)(wave & 1); // O block
+    float16v oacc[DT];
 #pragma unroll
-    for (int e = 0; e < DPT; e++) o[e] = 0.0f;
-    float mrow = -INFINITY, lrow = 0.0f;
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) oacc[t][e] = 0.0f;
+
     const uint32_t last = a.p0 + qt0 + nq - 1; // largest query position of the tile
     for (uint32_t k0 = 0; k0 <= last; k0 += PF_KT) {
-        __syncthreads();
+        __syncthreads(); // previous tile's operands are consumed
         for (uint32_t i = tid; i < (uint32_t)PF_KT * HS; i += NT) {
             const uint32_t kr = i / HS, d = i % HS, kp = k0 + kr;
-            float kvk = 0.0f, kvv = 0.0f;
+            _Float16 kk = (_Float16)0.0f, vv = (_Float16)0.0f;
             if (kp <= last) {
                 const size_t off = (size_t)kp * a.kv_dim + (size_t)kvh * HS + d;
                 if constexpr (F16) {
-                    kvk = f16_to_f32(((const uint16_t *)a.k_cache)[off]);
-                    kvv = f16_to_f32(((const uint16_t *)a.v_cache)[off]);
+                    const uint16_t kb = ((const uint16_t *)a.k_cache)[off], vb = ((const uint16_t *)a.v_cache)[off];
+                    __builtin_memcpy(&kk, &kb, 2);
+                    __builtin_memcpy(&vv, &vb, 2);
                 } else {
-                    kvk = ((const float *)a.k_cache)[off];
-                    kvv = ((const float *)a.v_cache)[off];
+                    kk = (_Float16)((const float *)a.k_cache)[off];
+                    vv = (_Float16)((const float *)a.v_cache)[off];
                 }
             }
-            ksh[kr][d] = kvk;
-            vsh[kr][d] = kvv;
+            kh[kr][d] = kk;
+            vt[d][kr] = vv;
         }
         __syncthreads();
+        // S tile: rows srow.., keys skey..
         {
-            float sc[4][4];
+            float16v sacc;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int e = 0; e < 16; e++) sacc[e] = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 4; j++) sc[i][j] = 0.0f;
-#pragma unroll 4
-            for (int d = 0; d < HS; d++) {
-                float qv[4], kv[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) qv[i] = qsh[sr0 + i][d];
-#pragma unroll
-                for (int j = 0; j < 4; j++) kv[j] = ksh[sk0 + j][d];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) sc[i][j] = fmaf(qv[i], kv[j], sc[i][j]);
+            for (int kk = 0; kk < HS; kk += 16) {
+                const half8v av = *(const half8v *)&qh[srow + li][kk + lk];
+                const half8v bv = *(const half8v *)&kh[skey + li][kk + lk];
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, sacc, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t qi = (sr0 + i) / G, qpos = a.p0 + qt0 + qi;
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    psh[sr0 + i][sk0 + j] = (k0 + sk0 + j <= qpos && qi < nq) ? sc[i][j] : -INFINITY;
+            for (int e = 0; e < 16; e++) {
+                const uint32_t row = srow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+                const uint32_t key = skey + li;
+                const uint32_t qi = row / G, qpos = a.p0 + qt0 + qi;
+                sf[row][key] = (k0 + key <= qpos && qi < nq) ? sacc[e] : -INFINITY;
             }
         }
         __syncthreads();
-        // running softmax of row pr over this tile, then o += p v
-        float mt = -INFINITY;
-        for (int k = 0; k < PF_KT; k++) mt = fmaxf(mt, psh[pr][k]);
-        if (mt != -INFINITY) {
-            const float mn = fmaxf(mrow, mt);
-            const float al = exp2f(mrow - mn); // 0 while mrow is -inf
-            lrow *= al;
+        // running softmax: 4 threads per row, 16 keys each
+        {
+            float mt = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < DPT; e++) o[e] *= al;
-            for (int k = 0; k < PF_KT; k++) {
-                const float p = exp2f(psh[pr][k] - mn); // 0 for a masked key
-                lrow += p;
+            for (int k = 0; k < 16; k++) mt = fmaxf(mt, sf[sr][16 * sq + k]);
+            mt = fmaxf(mt, __shfl_xor(mt, 1, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 2, 64));
+            const float mn = fmaxf(m_run, mt);
+            // a row with no key yet (mn = -inf) keeps alpha 1 and p 0
+            const float al = (mn == -INFINITY) ? 1.0f : exp2f(m_run - mn);
+            float ls = 0.0f;
 #pragma unroll
-                for (int e = 0; e < DPT; e++) o[e] = fmaf(p, vsh[k][part + TPR * e], o[e]);
+            for (int k = 0; k < 16; k++) {
+                const float p = (mn == -INFINITY) ? 0.0f : exp2f(sf[sr][16 * sq + k] - mn);
+                ls += p;
+                ph[sr][16 * sq + k] = (_Float16)p;
             }
-            mrow = mn;
+            ls += __shfl_xor(ls, 1, 64);
+            ls += __shfl_xor(ls, 2, 64);
+            l_run = l_run * al + ls;
+            m_run = mn;
+            if (sq == 0) alpha_s[sr] = al;
+        }
+        __syncthreads();
+        // O = alpha O + P V
+#pragma unroll
+        for (int t = 0; t < DT; t++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t row = orow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+                oacc[t][e] *= alpha_s[row];
+            }
+#pragma unroll
+        for (int kk = 0; kk < PF_KT; kk += 16) {
+            const half8v av = *(const half8v *)&ph[orow + li][kk + lk];
+#pragma unroll
+            for (int t = 0; t < DT; t++) {
+                const half8v bv = *(const half8v *)&vt[odim + 32 * t + li][kk + lk];
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, oacc[t], 0, 0, 0);
+            }
         }
     }
-    const uint32_t pqi = pr / G;
-    if (pqi < nq) {
-        _Float16 *out = (_Float16 *)a.xh + (size_t)(qt0 + pqi) * a.ldh + (kvh * G + pr % G) * HS;
+    if (sq == 0) l_s[sr] = l_run;
+    __syncthreads();
 #pragma unroll
-        for (int e = 0; e < DPT; e++) out[part + TPR * e] = (_Float16)(o[e] / lrow);
-    }
+    for (int t = 0; t < DT; t++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t row = orow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+            const uint32_t qi = row / G, dim = odim + 32 * t + li;
+            if (qi < nq)
+                ((_Float16 *)a.xh)[(size_t)(qt0 + qi) * a.ldh + (kvh * G + row % G) * HS + dim] =
+                    (_Float16)(oacc[t][e] / l_s[row]);
+        }
 }
 
 } // namespace ifr
