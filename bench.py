@@ -94,6 +94,27 @@ def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, s
 MFMA_F16_PEAK = 2.5e15  # MI355X dense f16 matrix-core FLOP/s
 
 
+SAMPLE_WARMUP = 4
+
+
+def time_sampler(ctx: I.LlmContext, n: int, iters: int = 50) -> float:
+    """Microseconds per ifr_sample call (T 0.7, top-p 0.95) on n logits of
+    an N(0, 4^2) draw."""
+    x = (np.random.default_rng(3).standard_normal(n) * 4).astype(np.float32)
+    dl, dp = ctx.upload(x), ctx.alloc(n * 4)
+    dc, di = ctx.upload(np.array([0.37], np.float32)), ctx.alloc(4)
+    ctx.sample(dl, dp, n, 0.7, 0.95, dc, di)
+    ctx.sync()
+    ctx.event_record(6)
+    for _ in range(iters):
+        ctx.sample(dl, dp, n, 0.7, 0.95, dc, di)
+    ctx.event_record(7)
+    us = ctx.event_elapsed(6, 7) * 1000.0 / iters
+    for b in (dl, dp, dc, di):
+        b.free()
+    return us
+
+
 def prefill_flops(cfg: I.Llama2Config, n: int) -> float:
     """Algorithmic FLOPs of a prompt of n tokens: 2 per weight per token for
     the layer matrices, plus causal attention (q.k and p.v: 2 x 2 x hs per
@@ -148,7 +169,7 @@ def run_decode(args) -> None:
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
-    max_pos = prompt_len + args.warmup + args.steps + 1
+    max_pos = prompt_len + args.warmup + args.steps + SAMPLE_WARMUP + args.sample_steps + 1
     cfg = I.Llama2Config(max_pos=max_pos, kv_dtype=I.F16, **base)
     t0 = time.perf_counter()
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=args.seed)
@@ -191,6 +212,23 @@ def run_decode(args) -> None:
     toks = s.tokens(pos0, args.steps + 1)
     assert np.all(toks < cfg.vocab)
 
+    # the same loop sampling as the reference's chat loop does
+    # (Sampler::new(vocab, 0.7, 0.95), crates/inferi-chat/src/sampler.rs:109)
+    sampled = None
+    if args.sample_steps > 0:
+        s.set_sampler(0.7, 0.95, args.seed)
+        I.Llama2.generate(ctx, s, w, SAMPLE_WARMUP, use_graph=not args.no_graph)
+        ctx.sync()
+        ctx.event_record(2)
+        I.Llama2.generate(ctx, s, w, args.sample_steps, use_graph=not args.no_graph)
+        ctx.event_record(3)
+        sms = ctx.event_elapsed(2, 3) / args.sample_steps
+        s.set_sampler(0.0)
+        sampled = {"temperature": 0.7, "topp": 0.95, "steps": args.sample_steps, "ms_per_step": round(sms, 5),
+                   "tok_s": round(1000.0 / sms, 2), "sampler_us": round(time_sampler(ctx, cfg.vocab), 2)}
+        log(f"bench: sampled decode (T 0.7, top-p 0.95): {sms:.4f} ms/token, {1000.0 / sms:.1f} tok/s; "
+            f"sampler alone {sampled['sampler_us']:.1f} us")
+
     # the dominant kernel: Q4_K GEMV, measured on its plain form at the
     # 14336x4096 shape of the FFN projections
     g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
@@ -227,6 +265,7 @@ def run_decode(args) -> None:
             "decode_hbm_frac": round(tok_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "device": dev_name,
             "prefill": pf,
+            "sampled_decode": sampled,
         },
         "roofline": {
             "bound": "hbm",
@@ -342,6 +381,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch the decode step's kernels directly")
     ap.add_argument("--cpu-tokens", type=int, default=32)
+    ap.add_argument("--sample-steps", type=int, default=64,
+                    help="decode steps timed with the reference chat loop's sampler (T 0.7, top-p 0.95)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")

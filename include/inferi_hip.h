@@ -185,6 +185,24 @@ IFR_API ifr_status ifr_attention(ifr_ctx *ctx, const ifr_attn_params *params, co
  * the device. */
 IFR_API ifr_status ifr_argmax(ifr_ctx *ctx, const float *v, uint32_t n, uint32_t *dev_index);
 
+/* Sampler::sample (crates/inferi/src/models/sampler.rs:32-52) on the device,
+ * with the coin passed in instead of drawn by rand::random() (:41):
+ *   temperature == 0: dev_index[0] = argmax(logits) (sample_argmax, :54-56);
+ *   otherwise probs = softmax(logits / temperature) (:38-39 and
+ *   SoftMax::run_cpu, crates/inferi/src/ops/softmax.rs:130-143; probs may
+ *   alias logits, which is what the reference does to its logits), then
+ *   dev_index[0] = sample_mult(probs, coin) (:60-76) when topp <= 0 or
+ *   topp >= 1, else sample_topp(probs, coin) (:83-131).
+ * dev_coin points to one float in [0, 1) in device memory.  The running sums
+ * the choice compares are exact (probabilities truncated to multiples of
+ * 2^-40), so the result is deterministic; it can differ from the reference's
+ * f32 running sums only for a coin within their rounding of a boundary.
+ * When no probability reaches the top-p cutoff (1 - topp) / (n - 1), where
+ * the reference fails, the most probable token is returned.
+ * n <= 262144; logits and probs 16-byte aligned. */
+IFR_API ifr_status ifr_sample(ifr_ctx *ctx, const float *logits, float *probs, uint32_t n, float temperature,
+                              float topp, const float *dev_coin, uint32_t *dev_index);
+
 /* Prompt-path GEMM (no reference counterpart; the reference multiplies
  * the prompt one token at a time through GemvQuant,
  * crates/inferi/src/ops/gemv_quant.rs:183-340):
@@ -272,9 +290,17 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const 
  * Q4_K attention and FFN matrices and the original RoPE variant. */
 IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
                                       uint32_t n_tokens);
+/* Sampling at the end of each decode step, as sample_next_token does
+ * (crates/inferi-chat/src/sampler.rs:91-111, with Sampler::new(vocab, 0.7,
+ * 0.95)): with temperature != 0 the step chooses token[p+1] by ifr_sample's
+ * algorithm instead of the argmax, its probabilities going to the state's
+ * "probs" buffer and its coin drawn on the device from (seed, p + 1); forced
+ * prompt positions are not sampled.  temperature 0 (the default) restores
+ * the argmax.  A captured decode step is captured again. */
+IFR_API ifr_status ifr_llama2_set_sampler(ifr_llama2_state *s, float temperature, float topp, uint64_t seed);
 /* Copies tokens[start, start+n) of the sequence to the host (waits). */
 IFR_API ifr_status ifr_llama2_read_tokens(ifr_llama2_state *s, uint32_t *host, uint32_t start, uint32_t n);
-/* Device pointer and size of a state buffer: "x", "logits", "pos", "tokens",
+/* Device pointer and size of a state buffer: "x", "logits", "probs", "pos", "tokens",
  * "key_cache" / "value_cache" (of `layer`), "q", "att". */
 IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name, int32_t layer, void **dev_ptr,
                                            size_t *bytes);

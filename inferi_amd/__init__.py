@@ -86,6 +86,7 @@ SIGNATURES = {
     "ifr_silu": (_i32, [_vp, _vp, _vp, _u32]),
     "ifr_attention": (_i32, [_vp, C.POINTER(AttentionParams), _vp, _vp, _vp, _vp, _i32, _vp]),
     "ifr_argmax": (_i32, [_vp, _vp, _u32, _vp]),
+    "ifr_sample": (_i32, [_vp, _vp, _vp, _u32, _f, _f, _vp, _vp]),
     "ifr_quantize": (_i32, [_vp, _vp, _vp, _i32, _u64]),
     "ifr_fill_normal": (_i32, [_vp, _vp, _u64, _u64, _u64, _f, _f]),
     "ifr_llama2_weights_create": (_i32, [_vp, C.POINTER(Llama2ConfigC), C.POINTER(_vp)]),
@@ -97,6 +98,7 @@ SIGNATURES = {
     "ifr_llama2_launch": (_i32, [_vp, _vp, _vp, _i32]),
     "ifr_llama2_generate": (_i32, [_vp, _vp, _vp, _u32, _i32]),
     "ifr_llama2_prefill": (_i32, [_vp, _vp, _vp, _u32]),
+    "ifr_llama2_set_sampler": (_i32, [_vp, _f, _f, _u64]),
     "ifr_llama2_read_tokens": (_i32, [_vp, _vp, _u32, _u32]),
     "ifr_llama2_state_buffer": (_i32, [_vp, _cp, _i32, C.POINTER(_vp), C.POINTER(_sz)]),
 }
@@ -256,6 +258,12 @@ class LlmContext:
     def argmax(self, v, n: int, out_index) -> None:
         self._check(lib().ifr_argmax(self.h, _ptr(v), n, _ptr(out_index)))
 
+    def sample(self, logits, probs, n: int, temperature: float, topp: float, coin, out_index) -> None:
+        """Sampler::sample (models/sampler.rs:32-52) with a device coin;
+        probs may be logits itself."""
+        self._check(lib().ifr_sample(self.h, _ptr(logits), _ptr(probs), n, temperature, topp, _ptr(coin),
+                                     _ptr(out_index)))
+
     def quantize(self, out, x, dtype: int, n_elems: int) -> None:
         self._check(lib().ifr_quantize(self.h, _ptr(out), _ptr(x), dtype, n_elems))
 
@@ -412,6 +420,11 @@ class Llama2State:
         out = np.empty(n // dt.itemsize, dt)
         self.ctx._check(lib().ifr_download(self.ctx.h, out.ctypes.data, p, out.nbytes))
         return out
+
+    def set_sampler(self, temperature: float, topp: float = 0.0, seed: int = 0) -> None:
+        """Decode steps sample instead of taking the argmax (temperature 0
+        restores it); sample_next_token uses temperature 0.7, topp 0.95."""
+        self.ctx._check(lib().ifr_llama2_set_sampler(self.h, temperature, topp, seed))
 
     def tokens(self, start: int, n: int) -> np.ndarray:
         out = np.empty(n, np.uint32)

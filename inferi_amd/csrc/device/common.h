@@ -162,6 +162,13 @@ IFR_DEV float rope_theta_f32(float base, float head_dim, float hs) {
     return (float)pow((double)base, (double)(-head_dim / hs));
 }
 
+// splitmix64 finaliser: a bijective 64-bit mix.
+IFR_DEV uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
 // Orderable key of a float (larger float -> larger key).
 IFR_DEV uint32_t f32_order_key(float f) {
     uint32_t u = __float_as_uint(f);

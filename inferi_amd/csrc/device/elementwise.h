@@ -78,7 +78,7 @@ __device__ void argmax_part_body(const ArgmaxArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t best = 0;
     for (uint32_t i = blockIdx.x * blockDim.x + tid; i < a.n; i += gridDim.x * blockDim.x) {
-        const uint64_t k = argmax_key(a.v[i], i);
+        const uint64_t k = argmax_key(a.div != 0.0f ? a.v[i] / a.div : a.v[i], i);
         best = k > best ? k : best;
     }
     for (int sh = 1; sh < 64; sh <<= 1) {
@@ -91,6 +91,21 @@ __device__ void argmax_part_body(const ArgmaxArgs &a) {
         uint64_t b = red[0];
         for (uint32_t w = 1; w < (blockDim.x >> 6); w++) b = red[w] > b ? red[w] : b;
         a.part_keys[blockIdx.x] = b;
+    }
+}
+
+// End of a decode step at position p with next token idx (one thread): store
+// the token unless position p+1 is forced, advance the device position and
+// the position fields of the op configs.  The position saturates at
+// max_pos - 1, so a step run past the end of the cache rewrites the last row
+// instead of leaving it.
+IFR_DEV void step_advance(StepCtl *ctl, uint32_t *tokens, uint32_t *rope_pos, uint32_t *attn_pos, uint32_t p,
+                          uint32_t idx) {
+    if (p + 1 < ctl->max_pos) {
+        if (p + 1 >= ctl->n_forced) tokens[p + 1] = idx;
+        ctl->pos = p + 1;
+        if (rope_pos) *rope_pos = p + 1;
+        if (attn_pos) *attn_pos = p + 1;
     }
 }
 
@@ -113,17 +128,7 @@ __device__ void argmax_final_body(const ArgmaxArgs &a) {
         for (uint32_t w = 1; w < (blockDim.x >> 6); w++) b = red[w] > b ? red[w] : b;
         const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu);
         if (a.out_index) *a.out_index = idx;
-        if (a.ctl) {
-            // the position saturates at max_pos - 1, so a step run past the
-            // end of the cache rewrites the last row instead of leaving it
-            const uint32_t p = a.ctl->pos;
-            if (p + 1 < a.ctl->max_pos) {
-                if (p + 1 >= a.ctl->n_forced) a.tokens[p + 1] = idx;
-                a.ctl->pos = p + 1;
-                if (a.rope_pos) *a.rope_pos = p + 1;
-                if (a.attn_pos) *a.attn_pos = p + 1;
-            }
-        }
+        if (a.ctl) step_advance(a.ctl, a.tokens, a.rope_pos, a.attn_pos, a.ctl->pos, idx);
     }
 }
 
@@ -200,13 +205,6 @@ __device__ void quantize_body(const QuantArgs &a) {
     case Q5_K: quant_q5_k(x, out); break;
     default: quant_q6_k(x, out); break;
     }
-}
-
-// splitmix64 finaliser: a bijective 64-bit mix.
-IFR_DEV uint64_t mix64(uint64_t z) {
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
 }
 
 // out[i] = mean + std * z_i; z from Box-Muller on two 24-bit uniforms drawn

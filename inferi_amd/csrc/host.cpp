@@ -308,7 +308,8 @@ struct ifr_llama2_state {
     ifr_llama2_config cfg;
     uint32_t kv_dim, head_size, kv_mul, n_splits;
     std::vector<void *> allocs;
-    float *x, *xb, *xb2, *q, *ktmp, *vtmp, *hb, *hb2, *att, *logits;
+    float *x, *xb, *xb2, *q, *ktmp, *vtmp, *hb, *hb2, *att, *logits, *probs;
+    uint8_t *smp_work;
     uint32_t *tokens;
     StepCtl *ctl;
     ifr_rms_norm_config *rms_cfg;
@@ -330,8 +331,13 @@ struct ifr_llama2_state {
     uint32_t pf_chunk = 0, pf_ldh = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_gu = nullptr;
     uint16_t *pf_xh = nullptr;
+    // sampler of the step end: temperature 0 takes the argmax
+    float temperature = 0.0f, topp = 0.0f;
+    uint64_t seed = 0;
+    uint32_t sampler_gen = 0;
     // captured decode step
     hipGraphExec_t graph = nullptr;
+    uint32_t graph_sampler = 0;
     const ifr_llama2_weights *graph_w = nullptr;
     int graph_fused = -1;
     int graph_exact = -1;
@@ -359,6 +365,32 @@ static ifr_status validate_cfg(ifr_ctx *c, const ifr_llama2_config *cfg) {
 // (split + merge), O + residual, gate/up + SiLU, down + residual; activations
 // travel between them quantized (integer path) and in f32 (exact path and the
 // residual stream).  Unfused: one kernel per reference op (transformer.rs:418-469).
+// Sampler::sample with T != 0: exp sums, probabilities and (top-p) the
+// candidates grouped by bucket over many workgroups, the choice in one.  The
+// maximum of y = logits / T comes from argmax keys: `parts` keys of the
+// logits when keys_of_y is 0 (T > 0 only), of y when 1.
+static ifr_status launch_sample(ifr_ctx *c, SampleArgs a) {
+    const uint32_t groups = (a.n + SAMPLE_GROUP_ELEMS - 1) / SAMPLE_GROUP_ELEMS;
+    ifr_status st;
+    if ((st = c->launch("sample_exp_k", dim3(groups), dim3(256), 0, a))) return st;
+    if ((st = c->launch("sample_prob_k", dim3(groups), dim3(256), 0, a))) return st;
+    const bool nucleus = !(a.topp <= 0.0f || a.topp >= 1.0f); // sampler.rs:44
+    if (nucleus && (st = c->launch("sample_group_k", dim3(groups), dim3(256), 0, a))) return st;
+    return c->launch("sample_select_k", dim3(1), dim3(1024), 0, a);
+}
+
+// Argmax keys of logits / T into keys (the maximum the sampler subtracts).
+static ifr_status launch_keys_of_y(ifr_ctx *c, const float *logits, uint32_t n, float T, uint64_t *keys,
+                                   uint32_t &parts) {
+    ArgmaxArgs k{};
+    k.v = logits;
+    k.n = n;
+    k.part_keys = keys;
+    k.div = T;
+    parts = std::min((n + 255) / 256, MAX_PARTS);
+    return c->launch("argmax_part_k", dim3(parts), dim3(256), 0, k);
+}
+
 static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
     const ifr_llama2_config &cfg = s->cfg;
     const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn, L = cfg.n_layers;
@@ -596,6 +628,28 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         m.part_keys = s->part_keys;
         n_parts = std::min((cfg.vocab + 255) / 256, MAX_PARTS);
         if ((st = c->launch("argmax_part_k", dim3(n_parts), dim3(256), 0, m))) return st;
+    }
+    if (s->temperature != 0.0f) {
+        // sample_next_token -> Sampler::sample (crates/inferi-chat/src/sampler.rs:91-111)
+        SampleArgs a{};
+        a.logits = s->logits;
+        a.probs = s->probs;
+        a.n = cfg.vocab;
+        a.temperature = s->temperature;
+        a.topp = s->topp;
+        a.n_parts = n_parts; // the head's keys of the logits
+        a.part_keys = s->part_keys;
+        if (s->temperature < 0.0f) { // the order reverses: keys of y itself
+            if ((st = launch_keys_of_y(c, s->logits, cfg.vocab, s->temperature, s->part_keys, a.n_parts))) return st;
+            a.keys_of_y = 1;
+        }
+        a.seed = s->seed;
+        a.work = s->smp_work;
+        a.ctl = s->ctl;
+        a.tokens = s->tokens;
+        a.rope_pos = &s->rope_cfg->pos;
+        a.attn_pos = &s->attn_params->pos;
+        return launch_sample(c, a);
     }
     ArgmaxArgs m{};
     m.n_parts = n_parts;
@@ -913,6 +967,34 @@ IFR_API ifr_status ifr_argmax(ifr_ctx *c, const float *v, uint32_t n, uint32_t *
     return c->launch("argmax_final_k", dim3(1), dim3(1024), 0, b);
 }
 
+IFR_API ifr_status ifr_sample(ifr_ctx *c, const float *logits, float *probs, uint32_t n, float temperature, float topp,
+                              const float *dev_coin, uint32_t *dev_index) {
+    if (!c) return IFR_EINVAL;
+    if (!logits || !dev_index) return c->fail(IFR_EINVAL, "sample: null pointer");
+    if (!n) return c->fail(IFR_EINVAL, "sample: empty input");
+    if (!std::isfinite(temperature) || std::isnan(topp))
+        return c->fail(IFR_EINVAL, "sample: temperature must be finite and topp a number");
+    if (temperature == 0.0f) return ifr_argmax(c, logits, n, dev_index); // sampler.rs:33-35
+    if (!probs || !dev_coin) return c->fail(IFR_EINVAL, "sample: null pointer");
+    if (n > SAMPLE_MAX_N) return c->fail(IFR_EUNSUPPORTED, "sample: n %u above %u", n, SAMPLE_MAX_N);
+    if (((uintptr_t)logits | (uintptr_t)probs) & 15) return c->fail(IFR_EINVAL, "sample: logits/probs not 16-byte aligned");
+    ifr_status st = c->ensure_scratch(MAX_PARTS * sizeof(uint64_t) + SAMPLE_WORK_BYTES);
+    if (st) return st;
+    SampleArgs a{};
+    a.logits = logits;
+    a.probs = probs;
+    a.n = n;
+    a.temperature = temperature;
+    a.topp = topp;
+    a.part_keys = (uint64_t *)c->scratch;
+    a.keys_of_y = 1;
+    if ((st = launch_keys_of_y(c, logits, n, temperature, (uint64_t *)c->scratch, a.n_parts))) return st;
+    a.coin = dev_coin;
+    a.work = (uint8_t *)c->scratch + MAX_PARTS * sizeof(uint64_t);
+    a.out_index = dev_index;
+    return launch_sample(c, a);
+}
+
 IFR_API ifr_status ifr_quantize(ifr_ctx *c, void *out, const float *x, int32_t dtype, uint64_t n) {
     if (!c) return IFR_EINVAL;
     const int qk = qk_of(dtype);
@@ -1047,7 +1129,7 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
 #define A(ptr, bytes) if ((st = alloc((bytes), (void **)&(ptr)))) { state_free(s); return st; }
     A(s->x, H * 4) A(s->xb, H * 4) A(s->xb2, H * 4) A(s->q, H * 4) A(s->att, H * 4)
     A(s->ktmp, KV * 4) A(s->vtmp, KV * 4) A(s->hb, F * 4) A(s->hb2, F * 4)
-    A(s->logits, (size_t)cfg->vocab * 4)
+    A(s->logits, (size_t)cfg->vocab * 4) A(s->probs, (size_t)cfg->vocab * 4) A(s->smp_work, SAMPLE_WORK_BYTES)
     A(s->tokens, ((size_t)cfg->max_pos + 1) * 4)
     A(s->ctl, sizeof(StepCtl)) A(s->rms_cfg, sizeof(ifr_rms_norm_config)) A(s->rope_cfg, sizeof(ifr_rope_config))
     A(s->attn_params, sizeof(ifr_attn_params))
@@ -1266,7 +1348,8 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
             if ((st = enqueue_step(c, s, w, 1))) return st;
         return IFR_OK;
     }
-    if (!s->graph || s->graph_w != w || s->graph_fused != 1 || s->graph_exact != c->gemv_exact) {
+    if (!s->graph || s->graph_w != w || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
+        s->graph_sampler != s->sampler_gen) {
         if (s->graph) {
             hipStreamSynchronize(c->stream);
             hipGraphExecDestroy(s->graph);
@@ -1288,9 +1371,23 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         s->graph_w = w;
         s->graph_fused = 1;
         s->graph_exact = c->gemv_exact;
+        s->graph_sampler = s->sampler_gen;
     }
     for (uint32_t i = 0; i < n_steps; i++)
         if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_set_sampler(ifr_llama2_state *s, float temperature, float topp, uint64_t seed) {
+    if (!s) return IFR_EINVAL;
+    if (!std::isfinite(temperature) || std::isnan(topp))
+        return s->ctx->fail(IFR_EINVAL, "sampler: temperature must be finite and topp a number");
+    if (temperature != 0.0f && s->cfg.vocab > SAMPLE_MAX_N)
+        return s->ctx->fail(IFR_EUNSUPPORTED, "sampler: vocab %u above %u", s->cfg.vocab, SAMPLE_MAX_N);
+    s->temperature = temperature;
+    s->topp = topp;
+    s->seed = seed;
+    s->sampler_gen++;
     return IFR_OK;
 }
 
@@ -1309,6 +1406,7 @@ IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name
     else if (n == "q") { *p = s->q; b = cfg.hidden * 4; }
     else if (n == "att") { *p = s->att; b = cfg.hidden * 4; }
     else if (n == "logits") { *p = s->logits; b = (size_t)cfg.vocab * 4; }
+    else if (n == "probs") { *p = s->probs; b = (size_t)cfg.vocab * 4; }
     else if (n == "pos") { *p = &s->ctl->pos; b = 4; }
     else if (n == "tokens") { *p = s->tokens; b = ((size_t)cfg.max_pos + 1) * 4; }
     else if (n == "key_cache" || n == "value_cache") {

@@ -139,6 +139,42 @@ struct ArgmaxArgs {
     uint32_t *tokens;    // step_end: token sequence
     uint32_t *rope_pos;  // step_end: pos field of the state's RoPE config (may be null)
     uint32_t *attn_pos;  // step_end: pos field of the state's attention params (may be null)
+    float div;           // part keys of v / div when non-zero
+};
+
+// Token sampling: temperature, softmax, multinomial or top-p selection in
+// up to four kernels (exp sums, probabilities and the grouping of the top-p
+// candidates over many workgroups, the selection in one), optionally ending
+// a decode step as ArgmaxArgs does.
+constexpr uint32_t SAMPLE_MAX_N = 262144;     // vocabulary limit (1024 chunks of 256)
+constexpr uint32_t SAMPLE_GROUP_ELEMS = 2048; // elements per workgroup of the exp / prob kernels
+// Scratch the three kernels share (byte offsets from SampleArgs::work).
+constexpr uint32_t SMPW_PART = 0;                       // float[128]: per-workgroup sums of exp(y - max)
+constexpr uint32_t SMPW_MASS = 512;                     // uint64[2048]: candidate mass per level-0 bucket
+constexpr uint32_t SMPW_CNT = SMPW_MASS + 2048 * 8;     // uint32[2048]: candidates per level-0 bucket
+constexpr uint32_t SMPW_CHUNK = SMPW_CNT + 2048 * 4;    // uint64[1024]: mass per chunk of 256 (multinomial)
+constexpr uint32_t SMPW_N0 = SMPW_CHUNK + 1024 * 8;     // uint32: candidates
+constexpr uint32_t SMPW_KMIN = SMPW_N0 + 8;             // uint64: smallest candidate key
+constexpr uint32_t SMPW_CUR = SMPW_KMIN + 8;            // uint32[2048]: fill cursor per bucket
+constexpr uint32_t SMPW_KEYS = SMPW_CUR + 2048 * 4;     // uint64[SAMPLE_MAX_N]: candidate keys grouped by bucket
+constexpr uint32_t SAMPLE_WORK_BYTES = SMPW_KEYS + SAMPLE_MAX_N * 8;
+struct SampleArgs {
+    const float *logits;        // n logits
+    float *probs;               // n probabilities out (may alias logits)
+    uint32_t n;
+    float temperature;          // != 0
+    float topp;                 // top-p mass; <= 0 or >= 1 samples from the whole distribution
+    uint32_t n_parts;           // argmax keys giving the maximum (> 0)
+    const uint64_t *part_keys;
+    int32_t keys_of_y;          // 1: keys of logits / T; 0: keys of the logits (T > 0)
+    const float *coin;          // device coin in [0, 1); null: drawn from (seed, position)
+    uint64_t seed;
+    uint8_t *work;              // SAMPLE_WORK_BYTES of scratch
+    uint32_t *out_index;        // may be null
+    StepCtl *ctl;               // step end (may be null), as ArgmaxArgs
+    uint32_t *tokens;
+    uint32_t *rope_pos;
+    uint32_t *attn_pos;
 };
 
 struct EmbedArgs {

@@ -6,6 +6,7 @@
 #include "device/elementwise.h"
 #include "device/gemv.h"
 #include "device/prefill.h"
+#include "device/sample.h"
 
 using namespace ifr;
 
@@ -64,6 +65,10 @@ extern "C" __global__ void __launch_bounds__(256) silu_k(EltArgs a) { silu_body(
 extern "C" __global__ void __launch_bounds__(256) add_k(EltArgs a) { add_body(a); }
 extern "C" __global__ void __launch_bounds__(256) argmax_part_k(ArgmaxArgs a) { argmax_part_body(a); }
 extern "C" __global__ void __launch_bounds__(1024) argmax_final_k(ArgmaxArgs a) { argmax_final_body(a); }
+extern "C" __global__ void __launch_bounds__(256) sample_exp_k(SampleArgs a) { sample_exp_body(a); }
+extern "C" __global__ void __launch_bounds__(256) sample_prob_k(SampleArgs a) { sample_prob_body(a); }
+extern "C" __global__ void __launch_bounds__(256) sample_group_k(SampleArgs a) { sample_group_body(a); }
+extern "C" __global__ void __launch_bounds__(1024) sample_select_k(SampleArgs a) { sample_select_body(a); }
 extern "C" __global__ void __launch_bounds__(256) embed_k(EmbedArgs a) { embed_body(a); }
 extern "C" __global__ void __launch_bounds__(256) quant_act_k(QActArgs a) { quant_act_body(a); }
 extern "C" __global__ void __launch_bounds__(256) kv_store_k(KvStoreArgs a) { kv_store_body(a); }

@@ -59,6 +59,13 @@ def lib() -> C.CDLL:
         L.ifo_attention.argtypes = [vp, vp, vp, vp, i, vp]
         L.ifo_argmax.argtypes = [vp, i]
         L.ifo_argmax.restype = i
+        L.ifo_softmax.argtypes = [vp, i]
+        L.ifo_sample_mult.argtypes = [vp, i, f]
+        L.ifo_sample_mult.restype = i
+        L.ifo_sample_topp.argtypes = [vp, i, f, f, vp, vp]
+        L.ifo_sample_topp.restype = i
+        L.ifo_sample.argtypes = [vp, i, f, f, f]
+        L.ifo_sample.restype = i
         L.ifo_state_new.argtypes = [vp]
         L.ifo_state_new.restype = vp
         L.ifo_state_free.argtypes = [vp]
@@ -178,6 +185,101 @@ def attention(q, k_cache, v_cache, n_heads: int, n_kv_heads: int, head_size: int
 def argmax(v: np.ndarray) -> int:
     v = np.ascontiguousarray(v, np.float32)
     return lib().ifo_argmax(_p(v), v.size)
+
+
+# --------------------------------------------------------------- sampler --
+# Reference restatement in C (f32 running sums, models/sampler.rs:32-131) and
+# the same algorithm with exact running sums over probabilities truncated to
+# multiples of 2^-40, which is what the device sampler computes.
+
+def softmax(v: np.ndarray) -> np.ndarray:
+    """SoftMax::run_cpu (ops/softmax.rs:130-143) on a copy."""
+    out = np.array(v, np.float32, copy=True)
+    lib().ifo_softmax(_p(out), out.size)
+    return out
+
+
+def sample_mult(p: np.ndarray, coin: float) -> int:
+    p = np.ascontiguousarray(p, np.float32)
+    return lib().ifo_sample_mult(_p(p), p.size, float(coin))
+
+
+def sample_topp(p: np.ndarray, topp: float, coin: float) -> tuple[int, int, float]:
+    """(index, truncation position, cumulative probability); index -1 where
+    the reference has no candidate."""
+    p = np.ascontiguousarray(p, np.float32)
+    last, cum = C.c_int(-1), C.c_float(0.0)
+    idx = lib().ifo_sample_topp(_p(p), p.size, float(topp), float(coin), C.byref(last), C.byref(cum))
+    return idx, last.value, cum.value
+
+
+def sample(logits: np.ndarray, temperature: float, topp: float, coin: float) -> tuple[int, np.ndarray]:
+    """Sampler::sample (models/sampler.rs:32-52) with the coin given: (index,
+    the logits as the reference leaves them, i.e. the probabilities)."""
+    v = np.array(logits, np.float32, copy=True)
+    idx = lib().ifo_sample(_p(v), v.size, float(temperature), float(topp), float(coin))
+    return idx, v
+
+
+FX_ONE = 2 ** 40
+
+
+def prob_fx(p) -> np.ndarray:
+    """floor(p * 2^40) of non-negative f32 values, as uint64 (exact)."""
+    p = np.asarray(p, np.float32).astype(np.float64)
+    return np.floor(np.maximum(p, 0.0) * FX_ONE).astype(np.uint64)
+
+
+def clamp_coin(coin: float) -> np.float32:
+    c = np.float32(coin)
+    if not c >= 0:
+        return np.float32(0.0)
+    return min(c, np.float32(np.nextafter(np.float32(1.0), np.float32(0.0))))
+
+
+def sample_mult_exact(p: np.ndarray, coin: float) -> int:
+    """sample_mult with exact running sums: the first index whose summed
+    2^-40 units exceed floor(coin * 2^40), n - 1 if none does."""
+    c = prob_fx(clamp_coin(coin))
+    cdf = np.cumsum(prob_fx(p), dtype=np.uint64)
+    i = int(np.searchsorted(cdf, c, side="right"))
+    return min(i, p.size - 1)
+
+
+def sample_topp_exact(p: np.ndarray, topp: float, coin: float, fallback: int) -> int:
+    """sample_topp with exact running sums.  The candidates (p >= cutoff,
+    f32 as the reference computes it) in order of probability descending,
+    index ascending; truncated at the first whose running sum exceeds
+    floor(topp * 2^40) (else all); then the first whose running sum exceeds
+    floor(coin * cum) with the product in f64.  `fallback` is returned when
+    there is no candidate."""
+    p = np.asarray(p, np.float32)
+    n = p.size
+    with np.errstate(divide="ignore", invalid="ignore"):  # n == 1: cutoff inf, no candidate
+        cutoff = np.float32(np.float32(np.float32(1.0) - np.float32(topp)) / np.float32(np.float32(n) - np.float32(1.0)))
+        cand = np.nonzero(p >= cutoff)[0]
+    if cand.size == 0:
+        return int(fallback)
+    order = cand[np.lexsort((cand, -p[cand]))]
+    cum = np.cumsum(prob_fx(p[order]), dtype=np.uint64)
+    t = prob_fx(np.float32(topp))
+    hit = np.nonzero(cum > t)[0]
+    last = int(hit[0]) if hit.size else order.size - 1
+    cum_last = cum[last]
+    r = np.uint64(np.floor(np.float64(clamp_coin(coin)) * np.float64(cum_last)))
+    j = int(np.searchsorted(cum[: last + 1], r, side="right"))
+    return int(order[min(j, last)])
+
+
+def seeded_coin(seed: int, pos: int) -> np.float32:
+    """The decode step's coin for position `pos`: 24 bits of the splitmix64
+    finaliser of seed + pos * 0x9E3779B97F4A7C15 (mod 2^64)."""
+    m = (1 << 64) - 1
+    z = (seed + pos * 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    z ^= z >> 31
+    return np.float32((z >> 40) / 16777216.0)
 
 
 # ------------------------------------------------------------------ model --

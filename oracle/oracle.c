@@ -546,6 +546,95 @@ int ifo_argmax(const float *v, int n) {
     return best;
 }
 
+/* ops/softmax.rs:130-143: max, then exp(x - max) accumulated left to right
+ * into an f32 sum, then every element divided by the sum. */
+void ifo_softmax(float *v, int n) {
+    float mx = v[0];
+    for (int i = 1; i < n; i++)
+        if (v[i] > mx) mx = v[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        v[i] = expf(v[i] - mx);
+        sum += v[i];
+    }
+    for (int i = 0; i < n; i++) v[i] /= sum;
+}
+
+/* models/sampler.rs:60-76: f32 running CDF, first index with coin < cdf. */
+int ifo_sample_mult(const float *p, int n, float coin) {
+    float cdf = 0.0f;
+    for (int i = 0; i < n; i++) {
+        cdf += p[i];
+        if (coin < cdf) return i;
+    }
+    return n - 1;
+}
+
+typedef struct {
+    float prob;
+    int index;
+} ifo_prob_index;
+
+/* The reference sorts with a stable sort keyed on -prob (sampler.rs:101);
+ * the candidates are gathered in index order, so "probability descending,
+ * then index ascending" is the same order. */
+static int cmp_prob_desc(const void *a, const void *b) {
+    const ifo_prob_index *x = (const ifo_prob_index *)a, *y = (const ifo_prob_index *)b;
+    if (x->prob > y->prob) return -1;
+    if (x->prob < y->prob) return 1;
+    return (x->index > y->index) - (x->index < y->index);
+}
+
+/* models/sampler.rs:83-131. */
+int ifo_sample_topp(const float *p, int n, float topp, float coin, int *last, float *cum) {
+    const float cutoff = (1.0f - topp) / ((float)n - 1.0f);
+    ifo_prob_index *pi = (ifo_prob_index *)malloc((size_t)n * sizeof *pi);
+    int n0 = 0;
+    for (int i = 0; i < n; i++)
+        if (p[i] >= cutoff) {
+            pi[n0].index = i;
+            pi[n0].prob = p[i];
+            n0++;
+        }
+    if (n0 == 0) {
+        free(pi);
+        return -1;
+    }
+    qsort(pi, (size_t)n0, sizeof *pi, cmp_prob_desc);
+    float cumulative = 0.0f;
+    int last_idx = n0 - 1;
+    for (int i = 0; i < n0; i++) {
+        cumulative += pi[i].prob;
+        if (cumulative > topp) {
+            last_idx = i;
+            break;
+        }
+    }
+    if (last) *last = last_idx;
+    if (cum) *cum = cumulative;
+    const float r = coin * cumulative;
+    float cdf = 0.0f;
+    int out = pi[last_idx].index;
+    for (int i = 0; i <= last_idx; i++) {
+        cdf += pi[i].prob;
+        if (r < cdf) {
+            out = pi[i].index;
+            break;
+        }
+    }
+    free(pi);
+    return out;
+}
+
+/* models/sampler.rs:32-52. */
+int ifo_sample(float *logits, int n, float temperature, float topp, float coin) {
+    if (temperature == 0.0f) return ifo_argmax(logits, n);
+    for (int i = 0; i < n; i++) logits[i] /= temperature;
+    ifo_softmax(logits, n);
+    if (topp <= 0.0f || topp >= 1.0f) return ifo_sample_mult(logits, n, coin);
+    return ifo_sample_topp(logits, n, topp, coin, NULL, NULL);
+}
+
 /* --------------------------------------------------------------- model -- */
 
 struct ifo_state {

@@ -103,6 +103,19 @@ void ifo_attention(const ifo_attn_params *p, const float *q, const void *k_cache
 /* models/sampler.rs:54-56: index of the maximum, lowest index on ties. */
 int ifo_argmax(const float *v, int n);
 
+/* SoftMax::run_cpu (ops/softmax.rs:130-143), in place, f32 left-to-right. */
+void ifo_softmax(float *v, int n);
+/* Sampler::sample_mult (models/sampler.rs:60-76). */
+int ifo_sample_mult(const float *p, int n, float coin);
+/* Sampler::sample_topp (models/sampler.rs:83-131) with vocab_size = n.
+ * Returns -1 where the reference has no candidate to sort (it panics);
+ * *last and *cum (when not NULL) receive the truncation position in the
+ * sorted list and the cumulative probability the coin is scaled by. */
+int ifo_sample_topp(const float *p, int n, float topp, float coin, int *last, float *cum);
+/* Sampler::sample (models/sampler.rs:32-52) with the coin given instead of
+ * drawn; logits are overwritten as the reference overwrites them. */
+int ifo_sample(float *logits, int n, float temperature, float topp, float coin);
+
 /* ---- Llama-style model forward (models/llama2/transformer.rs:409-481) ---- */
 typedef struct {
     int hidden, ffn, n_layers, n_heads, n_kv_heads, vocab, max_pos;
