@@ -59,6 +59,7 @@ def lib() -> C.CDLL:
         L.ifo_attention.argtypes = [vp, vp, vp, vp, i, vp]
         L.ifo_argmax.argtypes = [vp, i]
         L.ifo_argmax.restype = i
+        L.ifo_set_f32_accum.argtypes = [i]
         L.ifo_softmax.argtypes = [vp, i]
         L.ifo_sample_mult.argtypes = [vp, i, f]
         L.ifo_sample_mult.restype = i
@@ -180,6 +181,20 @@ def attention(q, k_cache, v_cache, n_heads: int, n_kv_heads: int, head_size: int
     out = np.empty(n_heads * head_size, np.float32)
     lib().ifo_attention(C.byref(p), _p(q), _p(k_cache), _p(v_cache), int(kv_f16), _p(out))
     return out
+
+
+class f32_accumulation:
+    """Within the block the quantized GEMVs (and so Model.forward) accumulate
+    in f32 left to right, as the reference's CPU path does, instead of f64:
+    the spread between the two is the noise floor of f32 arithmetic."""
+
+    def __enter__(self):
+        lib().ifo_set_f32_accum(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().ifo_set_f32_accum(0)
+        return False
 
 
 def argmax(v: np.ndarray) -> int:

@@ -390,6 +390,12 @@ typedef struct {
     float *y;
 } gemv_job;
 
+/* Accumulation of the quantized GEMVs: 0 (default) in f64, rounded once;
+ * 1 in f32, left to right, each product and sum rounded (nalgebra's gemv,
+ * cpu.rs:375-381), to measure what plain f32 arithmetic costs a model. */
+static int g_f32_accum = 0;
+void ifo_set_f32_accum(int on) { g_f32_accum = on; }
+
 static void *gemv_worker(void *arg) {
     gemv_job *j = (gemv_job *)arg;
     int qk = ifo_block_elems(j->dtype), bb = ifo_block_bytes(j->dtype);
@@ -398,12 +404,16 @@ static void *gemv_worker(void *arg) {
     for (int r = j->r0; r < j->r1; r++) {
         const uint8_t *row = j->w + (size_t)r * nb * bb;
         double sum = 0.0;
+        float sum32 = 0.0f;
         for (int b = 0; b < nb; b++) {
             ifo_dequant(j->dtype, row + (size_t)b * bb, (size_t)qk, buf);
             const float *xb = j->x + (size_t)b * qk;
-            for (int l = 0; l < qk; l++) sum += (double)buf[l] * (double)xb[l];
+            if (g_f32_accum)
+                for (int l = 0; l < qk; l++) sum32 += buf[l] * xb[l];
+            else
+                for (int l = 0; l < qk; l++) sum += (double)buf[l] * (double)xb[l];
         }
-        j->y[r] = (float)sum;
+        j->y[r] = g_f32_accum ? sum32 : (float)sum;
     }
     return NULL;
 }

@@ -100,6 +100,10 @@ typedef struct {
 void ifo_attention(const ifo_attn_params *p, const float *q, const void *k_cache,
                    const void *v_cache, int kv_f16, float *out);
 
+/* GEMV accumulation of ifo_gemv_quant and the model forward: 0 (default)
+ * f64 rounded once; 1 f32 left to right (the reference CPU path's order). */
+void ifo_set_f32_accum(int on);
+
 /* models/sampler.rs:54-56: index of the maximum, lowest index on ties. */
 int ifo_argmax(const float *v, int n);
 

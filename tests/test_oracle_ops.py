@@ -44,6 +44,26 @@ def test_gemv_quant_vs_numpy(oracle_lib, dtype):
     assert np.allclose(O.gemv_f64(deq, x), ref, rtol=1e-6, atol=1e-30)
 
 
+@pytest.mark.parametrize("dtype", [O.Q8_0, O.Q4_K], ids=["Q8_0", "Q4_K"])
+def test_gemv_f32_accumulation_mode(oracle_lib, dtype):
+    """The f32-accumulation mode is the left-to-right f32 dot (each product
+    and sum rounded) bit for bit, the f64 mode is restored after the block,
+    and the two differ by no more than the f32 rounding bound."""
+    rng = np.random.default_rng(11)
+    rows, cols = 6, 512
+    blocks = K.random_blocks(dtype, rows * cols // O.BLOCK_ELEMS[dtype], rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    wd = O.dequant(dtype, blocks, rows * cols).reshape(rows, cols)
+    with O.f32_accumulation():
+        y32 = O.gemv_quant(dtype, blocks, rows, cols, x)
+    y64 = O.gemv_quant(dtype, blocks, rows, cols, x)
+    seq = np.array([np.add.accumulate((wd[r] * x).astype(np.float32), dtype=np.float32)[-1] for r in range(rows)])
+    assert np.array_equal(y32.view(np.uint32), seq.view(np.uint32))
+    assert np.array_equal(y64, (wd.astype(np.float64) @ x.astype(np.float64)).astype(np.float32))
+    bound = cols * np.finfo(np.float32).eps * (np.abs(wd).astype(np.float64) @ np.abs(x).astype(np.float64))
+    assert np.all(np.abs(y32.astype(np.float64) - y64) <= bound + np.abs(y64) * 1e-7)
+
+
 def test_rms_norm_closed_forms(oracle_lib):
     n = 4096
     w = np.linspace(0.5, 1.5, n).astype(np.float32)
