@@ -73,8 +73,9 @@ typedef struct ifr_ctx ifr_ctx;
  * which loads every compiled kernel of the backend. */
 IFR_API ifr_status ifr_create(int32_t device, const char *code_object_path, ifr_ctx **out);
 IFR_API void ifr_destroy(ifr_ctx *ctx);
-/* Message of the last failed call on this context (or of the last failed
- * ifr_create on this thread when ctx is NULL). */
+/* Message of the last failed call on this context (or, when ctx is NULL, of
+ * the last failed call made without a context on this thread: ifr_create,
+ * ifr_gguf_*). */
 IFR_API const char *ifr_last_error(const ifr_ctx *ctx);
 /* Device name and compute-unit count, for reports. */
 IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, int32_t *n_cu);
@@ -304,6 +305,102 @@ IFR_API ifr_status ifr_llama2_read_tokens(ifr_llama2_state *s, uint32_t *host, u
  * "key_cache" / "value_cache" (of `layer`), "q", "att". */
 IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name, int32_t layer, void **dev_ptr,
                                            size_t *bytes);
+
+/* ------------------------------------------------------------------ GGUF */
+
+/* Gguf::from_bytes (crates/inferi/src/gguf.rs:516-692).  The file is
+ * memory-mapped; metadata and tensor infos are parsed as the reference does:
+ * the magic in either byte order, typed metadata (MetadataValueType,
+ * gguf.rs:388-511), tensor dimensions reversed from GGUF's order into
+ * [rows, cols, ...] with unused dimensions 1 (gguf.rs:620-626), tensor data
+ * at the aligned end of the infos plus the tensor's offset, the alignment
+ * being general.alignment when it is a U32, else 32.  Where the reference
+ * panics (a read past the end, rank > 4) or errs (bad magic, unknown value
+ * or tensor type) the call returns IFR_EINVAL (ifr_last_error(NULL)).
+ * Tensor data pointers point into the mapping and live until ifr_gguf_close. */
+typedef struct ifr_gguf ifr_gguf;
+/* Metadata value types (gguf.rs MetadataValueType). */
+#define IFR_GGUF_U8 0
+#define IFR_GGUF_I8 1
+#define IFR_GGUF_U16 2
+#define IFR_GGUF_I16 3
+#define IFR_GGUF_U32 4
+#define IFR_GGUF_I32 5
+#define IFR_GGUF_F32 6
+#define IFR_GGUF_BOOL 7
+#define IFR_GGUF_STRING 8
+#define IFR_GGUF_ARRAY 9
+#define IFR_GGUF_U64 10
+#define IFR_GGUF_I64 11
+#define IFR_GGUF_F64 12
+
+IFR_API ifr_status ifr_gguf_open(const char *path, ifr_gguf **out);
+/* Parses a copy of bytes[0..len) (Gguf::from_bytes on an in-memory file). */
+IFR_API ifr_status ifr_gguf_from_bytes(const void *bytes, size_t len, ifr_gguf **out);
+IFR_API void ifr_gguf_close(ifr_gguf *g);
+IFR_API uint32_t ifr_gguf_version(const ifr_gguf *g);
+IFR_API uint32_t ifr_gguf_alignment(const ifr_gguf *g);
+/* Metadata keys in file order (a repeated key keeps its first position and
+ * its last value, as the reference's map insert does). */
+IFR_API uint64_t ifr_gguf_metadata_count(const ifr_gguf *g);
+IFR_API const char *ifr_gguf_metadata_key(const ifr_gguf *g, uint64_t i);
+/* The value type of key (-1 when absent); for an array, its element type
+ * and length; for a string, its byte length. */
+IFR_API int32_t ifr_gguf_metadata_type(const ifr_gguf *g, const char *key, int32_t *elem_type, uint64_t *len);
+/* A scalar of exactly `type` (the reference's unwrap_u32 / as_f32 are
+ * strict): its 1, 2, 4 or 8 little-endian bytes to *out (BOOL: one byte). */
+IFR_API ifr_status ifr_gguf_get_scalar(const ifr_gguf *g, const char *key, int32_t type, void *out);
+/* A STRING value (not NUL-terminated in the file; the pointer here is). */
+IFR_API ifr_status ifr_gguf_get_string(const ifr_gguf *g, const char *key, const char **s, uint64_t *len);
+/* An ARRAY: element type and length; for scalar elements, *data points at
+ * the packed little-endian elements in the file (unaligned). */
+IFR_API ifr_status ifr_gguf_get_array(const ifr_gguf *g, const char *key, int32_t *elem_type, uint64_t *len,
+                                      const void **data);
+IFR_API ifr_status ifr_gguf_get_array_string(const ifr_gguf *g, const char *key, uint64_t i, const char **s,
+                                             uint64_t *len);
+/* Tensors in file order; info by name: type id (gguf.rs:74-104), dims in
+ * the reference's order, rank, the data in the file and its byte size (NULL
+ * and 0 for the types whose data the reference does not read). */
+IFR_API uint64_t ifr_gguf_tensor_count(const ifr_gguf *g);
+IFR_API const char *ifr_gguf_tensor_name(const ifr_gguf *g, uint64_t i);
+IFR_API ifr_status ifr_gguf_tensor_info(const ifr_gguf *g, const char *name, int32_t *dtype, uint64_t dims[4],
+                                        uint32_t *rank, const void **data, uint64_t *bytes);
+
+/* GGUF writer (no reference counterpart: the reference only reads).  Writes
+ * version 3 with metadata and tensor infos in insertion order and each
+ * tensor's data at the next multiple of general.alignment (32 unless set),
+ * zero-padded, so the files read back through ifr_gguf_open and the
+ * reference's Gguf::from_bytes alike.  Tensor dims are given in the
+ * reference's order ([rows, cols, ...]); data is copied. */
+typedef struct ifr_gguf_writer ifr_gguf_writer;
+IFR_API ifr_status ifr_gguf_writer_create(ifr_gguf_writer **out);
+IFR_API void ifr_gguf_writer_destroy(ifr_gguf_writer *w);
+/* A scalar (value points at its bytes) or a STRING (value is a C string);
+ * setting a key again replaces its value in place. */
+IFR_API ifr_status ifr_gguf_writer_set(ifr_gguf_writer *w, const char *key, int32_t type, const void *value);
+/* An array of scalars (packed elements) or of STRINGs (const char *const *). */
+IFR_API ifr_status ifr_gguf_writer_set_array(ifr_gguf_writer *w, const char *key, int32_t elem_type,
+                                             const void *data, uint64_t len);
+IFR_API ifr_status ifr_gguf_writer_add_tensor(ifr_gguf_writer *w, const char *name, int32_t dtype, uint32_t rank,
+                                              const uint64_t *dims, const void *data, uint64_t bytes);
+IFR_API ifr_status ifr_gguf_writer_save(ifr_gguf_writer *w, const char *path);
+
+/* Llama2Config::from_gguf (crates/inferi/src/models/llama2/cpu.rs:74-107):
+ * llama.{embedding_length, feed_forward_length, block_count,
+ * attention.head_count, attention.head_count_kv, context_length} as U32,
+ * vocab = the length of tokenizer.ggml.tokens, rope.freq_base (F32, default
+ * 10000) and attention.layer_norm_rms_epsilon (F32, default 1e-6); max_pos =
+ * context_length.  kv_dtype is set to IFR_F32 (the reference's cache) and
+ * rope_variant to the original; a caller may change kv_dtype before creating
+ * a state.  A general.architecture naming qwen2 returns IFR_EUNSUPPORTED
+ * (its QKV biases are not built). */
+IFR_API ifr_status ifr_llama2_config_from_gguf(const ifr_gguf *g, ifr_llama2_config *cfg);
+/* Llama2Weights::from_gguf (crates/inferi/src/models/llama2/transformer.rs:
+ * 294-393): every tensor the model uses is copied verbatim (GGUF blocks) to
+ * device memory that the weights own and free at ifr_llama2_weights_destroy;
+ * output.weight falls back to token_embd.weight when absent (:376-382). */
+IFR_API ifr_status ifr_llama2_weights_from_gguf(ifr_ctx *ctx, const ifr_gguf *g, const ifr_llama2_config *cfg,
+                                                ifr_llama2_weights **out);
 
 #ifdef __cplusplus
 }

@@ -101,6 +101,30 @@ SIGNATURES = {
     "ifr_llama2_set_sampler": (_i32, [_vp, _f, _f, _u64]),
     "ifr_llama2_read_tokens": (_i32, [_vp, _vp, _u32, _u32]),
     "ifr_llama2_state_buffer": (_i32, [_vp, _cp, _i32, C.POINTER(_vp), C.POINTER(_sz)]),
+    "ifr_gguf_open": (_i32, [_cp, C.POINTER(_vp)]),
+    "ifr_gguf_from_bytes": (_i32, [_vp, _sz, C.POINTER(_vp)]),
+    "ifr_gguf_close": (None, [_vp]),
+    "ifr_gguf_version": (_u32, [_vp]),
+    "ifr_gguf_alignment": (_u32, [_vp]),
+    "ifr_gguf_metadata_count": (_u64, [_vp]),
+    "ifr_gguf_metadata_key": (_cp, [_vp, _u64]),
+    "ifr_gguf_metadata_type": (_i32, [_vp, _cp, C.POINTER(_i32), C.POINTER(_u64)]),
+    "ifr_gguf_get_scalar": (_i32, [_vp, _cp, _i32, _vp]),
+    "ifr_gguf_get_string": (_i32, [_vp, _cp, C.POINTER(_vp), C.POINTER(_u64)]),
+    "ifr_gguf_get_array": (_i32, [_vp, _cp, C.POINTER(_i32), C.POINTER(_u64), C.POINTER(_vp)]),
+    "ifr_gguf_get_array_string": (_i32, [_vp, _cp, _u64, C.POINTER(_vp), C.POINTER(_u64)]),
+    "ifr_gguf_tensor_count": (_u64, [_vp]),
+    "ifr_gguf_tensor_name": (_cp, [_vp, _u64]),
+    "ifr_gguf_tensor_info": (_i32, [_vp, _cp, C.POINTER(_i32), C.POINTER(_u64), C.POINTER(_u32), C.POINTER(_vp),
+                                    C.POINTER(_u64)]),
+    "ifr_gguf_writer_create": (_i32, [C.POINTER(_vp)]),
+    "ifr_gguf_writer_destroy": (None, [_vp]),
+    "ifr_gguf_writer_set": (_i32, [_vp, _cp, _i32, _vp]),
+    "ifr_gguf_writer_set_array": (_i32, [_vp, _cp, _i32, _vp, _u64]),
+    "ifr_gguf_writer_add_tensor": (_i32, [_vp, _cp, _i32, _u32, C.POINTER(_u64), _vp, _u64]),
+    "ifr_gguf_writer_save": (_i32, [_vp, _cp]),
+    "ifr_llama2_config_from_gguf": (_i32, [_vp, C.POINTER(Llama2ConfigC)]),
+    "ifr_llama2_weights_from_gguf": (_i32, [_vp, _vp, C.POINTER(Llama2ConfigC), C.POINTER(_vp)]),
 }
 
 _lib = None
@@ -310,6 +334,24 @@ class Llama2Config:
         return Llama2ConfigC(self.n_layers, self.hidden, self.ffn, self.n_heads, self.n_kv_heads, self.vocab,
                              self.max_pos, self.rope_theta, self.rms_eps, self.kv_dtype, self.rope_variant)
 
+    @classmethod
+    def from_gguf(cls, gguf: "Gguf") -> "Llama2Config":
+        """Llama2Config::from_gguf (cpu.rs:74-107); kv_dtype F32 as the reference."""
+        c = Llama2ConfigC()
+        _free_check(lib().ifr_llama2_config_from_gguf(gguf.h, C.byref(c)))
+        return cls(n_layers=c.n_layers, hidden=c.hidden, ffn=c.ffn, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads,
+                   vocab=c.vocab, max_pos=c.max_pos, rope_theta=c.rope_theta, rms_eps=c.rms_eps, kv_dtype=c.kv_dtype,
+                   rope_variant=c.rope_variant)
+
+    def gguf_metadata(self) -> list:
+        """(key, type, value) of the llama.* keys from_gguf reads."""
+        m = "llama"
+        return [(f"{m}.embedding_length", GGUF_U32, self.hidden), (f"{m}.feed_forward_length", GGUF_U32, self.ffn),
+                (f"{m}.block_count", GGUF_U32, self.n_layers), (f"{m}.attention.head_count", GGUF_U32, self.n_heads),
+                (f"{m}.attention.head_count_kv", GGUF_U32, self.n_kv_heads),
+                (f"{m}.context_length", GGUF_U32, self.max_pos), (f"{m}.rope.freq_base", GGUF_F32, self.rope_theta),
+                (f"{m}.attention.layer_norm_rms_epsilon", GGUF_F32, self.rms_eps)]
+
     def shapes(self) -> dict:
         """GGUF tensor name -> (rows, cols) (transformer.rs:294-393)."""
         h, kv, f = self.hidden, self.kv_dim, self.ffn
@@ -356,6 +398,37 @@ class Llama2Weights:
         for _, b, _, _ in self.buffers.values():
             b.free()
         self.buffers.clear()
+
+    @classmethod
+    def from_gguf(cls, ctxt: LlmContext, gguf: "Gguf", config: Llama2Config) -> "Llama2Weights":
+        """Llama2Weights::from_gguf (transformer.rs:294-393): the tensors are
+        copied to device memory owned by the weights."""
+        w = cls.__new__(cls)
+        w.ctx, w.config, w._cfg, w.buffers = ctxt, config, config.c(), {}
+        h = C.c_void_p()
+        ctxt._check(lib().ifr_llama2_weights_from_gguf(ctxt.h, gguf.h, C.byref(w._cfg), C.byref(h)))
+        w.h = h.value
+        return w
+
+    def to_gguf(self, path: str, tokens: list | None = None, architecture: str = "llama") -> None:
+        """Writes the model as a GGUF file that from_gguf (here and in the
+        reference) reads: general.architecture, the llama.* keys, a
+        tokenizer.ggml.tokens list of vocab length, and every tensor's blocks."""
+        wr = GgufWriter()
+        try:
+            wr.set("general.architecture", GGUF_STRING, architecture)
+            wr.set("tokenizer.ggml.model", GGUF_STRING, "llama")
+            for key, ty, val in self.config.gguf_metadata():
+                wr.set(key, ty, val)
+            toks = tokens if tokens is not None else [f"<t{i}>" for i in range(self.config.vocab)]
+            wr.set_array("tokenizer.ggml.tokens", GGUF_STRING, toks)
+            for name in self.buffers:
+                dtype, arr, rows, cols = self.download(name)
+                dims = [cols] if rows == 1 and name.endswith("norm.weight") else [rows, cols]
+                wr.add_tensor(name, dtype, dims, arr)
+            wr.save(path)
+        finally:
+            wr.close()
 
     @classmethod
     def synthetic(cls, ctxt: LlmContext, config: Llama2Config, seed: int, mat_dtype: int = Q4_K,
@@ -449,3 +522,160 @@ class Llama2:
     def generate(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, n_steps: int,
                  use_graph: bool = True) -> None:
         ctxt._check(lib().ifr_llama2_generate(ctxt.h, state.h, weights.h, n_steps, int(use_graph)))
+
+
+# ------------------------------------------------------------------- GGUF
+# Metadata value types (gguf.rs MetadataValueType).
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL, GGUF_STRING, GGUF_ARRAY, \
+    GGUF_U64, GGUF_I64, GGUF_F64 = range(13)
+_GGUF_NP = {GGUF_U8: np.uint8, GGUF_I8: np.int8, GGUF_U16: np.uint16, GGUF_I16: np.int16, GGUF_U32: np.uint32,
+            GGUF_I32: np.int32, GGUF_F32: np.float32, GGUF_BOOL: np.uint8, GGUF_U64: np.uint64, GGUF_I64: np.int64,
+            GGUF_F64: np.float64}
+
+
+def _free_check(st: int) -> None:
+    if st != 0:
+        raise HipError(st, (lib().ifr_last_error(None) or b"").decode())
+
+
+class GgufTensor:
+    """GgufTensor (gguf.rs:336-349): dims in [rows, cols, ...] order."""
+
+    def __init__(self, dtype: int, dims: tuple, rank: int, data: np.ndarray | None):
+        self.dtype, self.dims, self.rank, self.data = dtype, dims, rank, data
+
+
+class Gguf:
+    """Gguf::from_bytes (gguf.rs:516-692) through ifr_gguf_open /
+    ifr_gguf_from_bytes: version, metadata and tensors."""
+
+    def __init__(self, path: str | None = None, data: bytes | None = None):
+        self.h = None
+        h = C.c_void_p()
+        if path is not None:
+            _free_check(lib().ifr_gguf_open(os.fsencode(path), C.byref(h)))
+        else:
+            buf = C.create_string_buffer(bytes(data), len(data))
+            _free_check(lib().ifr_gguf_from_bytes(buf, len(data), C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().ifr_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return lib().ifr_gguf_version(self.h)
+
+    @property
+    def alignment(self) -> int:
+        return lib().ifr_gguf_alignment(self.h)
+
+    def keys(self) -> list:
+        return [lib().ifr_gguf_metadata_key(self.h, i).decode() for i in range(lib().ifr_gguf_metadata_count(self.h))]
+
+    def type_of(self, key: str) -> tuple[int, int, int]:
+        et, n = C.c_int32(), C.c_uint64()
+        t = lib().ifr_gguf_metadata_type(self.h, key.encode(), C.byref(et), C.byref(n))
+        return t, et.value, n.value
+
+    def get(self, key: str):
+        """The value as Python data: int / float / bool / str, a numpy array
+        or list of str for arrays (None for an array of arrays)."""
+        t, et, n = self.type_of(key)
+        k = key.encode()
+        if t < 0:
+            raise KeyError(key)
+        if t == GGUF_STRING:
+            p, ln = C.c_void_p(), C.c_uint64()
+            _free_check(lib().ifr_gguf_get_string(self.h, k, C.byref(p), C.byref(ln)))
+            return C.string_at(p.value, ln.value).decode("utf-8", "replace")
+        if t == GGUF_ARRAY:
+            if et == GGUF_STRING:
+                out = []
+                for i in range(n):
+                    p, ln = C.c_void_p(), C.c_uint64()
+                    _free_check(lib().ifr_gguf_get_array_string(self.h, k, i, C.byref(p), C.byref(ln)))
+                    out.append(C.string_at(p.value, ln.value).decode("utf-8", "replace"))
+                return out
+            if et not in _GGUF_NP:
+                return None
+            p = C.c_void_p()
+            _free_check(lib().ifr_gguf_get_array(self.h, k, None, None, C.byref(p)))
+            dt = np.dtype(_GGUF_NP[et]).newbyteorder("<")
+            a = np.frombuffer(C.string_at(p.value, n * dt.itemsize), dt).copy() if n else np.zeros(0, dt)
+            return a.astype(bool) if et == GGUF_BOOL else a
+        raw = (C.c_uint8 * 8)()
+        _free_check(lib().ifr_gguf_get_scalar(self.h, k, t, raw))
+        v = np.frombuffer(bytes(raw), np.dtype(_GGUF_NP[t]).newbyteorder("<"), 1)[0]
+        if t == GGUF_BOOL:
+            return bool(v)
+        return float(v) if t in (GGUF_F32, GGUF_F64) else int(v)
+
+    @property
+    def metadata(self) -> dict:
+        return {k: self.get(k) for k in self.keys()}
+
+    def tensor_names(self) -> list:
+        return [lib().ifr_gguf_tensor_name(self.h, i).decode() for i in range(lib().ifr_gguf_tensor_count(self.h))]
+
+    def tensor(self, name: str) -> GgufTensor:
+        dt, rank, p, nb = C.c_int32(), C.c_uint32(), C.c_void_p(), C.c_uint64()
+        dims = (C.c_uint64 * 4)()
+        _free_check(lib().ifr_gguf_tensor_info(self.h, name.encode(), C.byref(dt), dims, C.byref(rank), C.byref(p),
+                                               C.byref(nb)))
+        data = np.frombuffer(C.string_at(p.value, nb.value), np.uint8).copy() if p.value else None
+        return GgufTensor(dt.value, tuple(int(d) for d in dims), rank.value, data)
+
+    @property
+    def tensors(self) -> dict:
+        return {n: self.tensor(n) for n in self.tensor_names()}
+
+
+class GgufWriter:
+    """ifr_gguf_writer: metadata and tensors written in insertion order."""
+
+    def __init__(self):
+        self.h = None
+        h = C.c_void_p()
+        _free_check(lib().ifr_gguf_writer_create(C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().ifr_gguf_writer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def set(self, key: str, type_: int, value) -> None:
+        if type_ == GGUF_STRING:
+            v = C.create_string_buffer(value.encode())
+        else:
+            v = C.create_string_buffer(np.array([value], _GGUF_NP[type_]).astype(np.dtype(_GGUF_NP[type_]).newbyteorder("<")).tobytes(), 8)
+        _free_check(lib().ifr_gguf_writer_set(self.h, key.encode(), type_, v))
+
+    def set_array(self, key: str, elem_type: int, values) -> None:
+        if elem_type == GGUF_STRING:
+            enc = [str(x).encode() for x in values]
+            arr = (C.c_char_p * max(len(enc), 1))(*enc)
+            _free_check(lib().ifr_gguf_writer_set_array(self.h, key.encode(), elem_type, arr, len(enc)))
+        else:
+            a = np.ascontiguousarray(np.asarray(values, _GGUF_NP[elem_type]).astype(
+                np.dtype(_GGUF_NP[elem_type]).newbyteorder("<")))
+            _free_check(lib().ifr_gguf_writer_set_array(self.h, key.encode(), elem_type,
+                                                        a.ctypes.data if a.size else None, a.size))
+
+    def add_tensor(self, name: str, dtype: int, dims, data) -> None:
+        b = np.ascontiguousarray(np.asarray(data)).view(np.uint8).reshape(-1)
+        d = (C.c_uint64 * max(4, len(dims)))(*[int(x) for x in dims], *([1] * (4 - len(dims))))
+        _free_check(lib().ifr_gguf_writer_add_tensor(self.h, name.encode(), dtype, len(dims), d,
+                                                     b.ctypes.data if b.size else None, b.size))
+
+    def save(self, path: str) -> None:
+        _free_check(lib().ifr_gguf_writer_save(self.h, os.fsencode(path)))

@@ -5,7 +5,8 @@ Two artefacts, both written next to this file:
                         (hipcc --genco --offload-arch=gfx950), loaded at run
                         time with hipModuleLoad;
   libinferi_hip.so      host library with the C ABI of include/inferi_hip.h
-                        (C++17, links libamdhip64).
+                        (csrc/host.cpp and csrc/gguf.cpp, C++17, links
+                        libamdhip64).
 
 Every HIP compile carries ``-Xclang -target-feature -Xclang -packed-fp32-ops``
 so the compiler never emits packed FP32 instructions.
@@ -54,7 +55,7 @@ def build_host(out: str = LIB) -> str:
     tmp = out + ".tmp"
     _run([cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-result",
           "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
-          os.path.join(CSRC, "host.cpp"), f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
+          os.path.join(CSRC, "host.cpp"), os.path.join(CSRC, "gguf.cpp"), f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
     os.replace(tmp, out)
     return out
 

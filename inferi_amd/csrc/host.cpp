@@ -26,9 +26,12 @@
 
 using namespace ifr;
 
-namespace {
+// Message of the last failed call made without a context on this thread
+// (ifr_create, the GGUF reader and writer of gguf.cpp).
+static thread_local std::string g_create_error;
+std::string &ifr_free_error() { return g_create_error; }
 
-thread_local std::string g_create_error;
+namespace {
 
 constexpr uint32_t GEMV_MAX_LDS = 65536 - 256;
 
@@ -301,6 +304,7 @@ struct ifr_llama2_weights {
     ifr_llama2_config cfg;
     Tens token_embd, output_norm, output;
     std::vector<LayerW> layers;
+    std::vector<void *> owned; // device copies made by ifr_llama2_weights_from_gguf
 };
 
 struct ifr_llama2_state {
@@ -1095,7 +1099,106 @@ IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *nam
     return IFR_OK;
 }
 
-IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w) { delete w; }
+IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w) {
+    if (!w) return;
+    if (!w->owned.empty()) {
+        hipStreamSynchronize(w->ctx->stream);
+        for (void *p : w->owned) hipFree(p);
+    }
+    delete w;
+}
+
+static ifr_status gguf_u32(const ifr_gguf *g, const std::string &key, uint32_t &v) {
+    if (ifr_gguf_get_scalar(g, key.c_str(), IFR_GGUF_U32, &v))
+        return ifr_free_error() = "gguf: " + key + " missing or not a U32", IFR_EINVAL;
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_config_from_gguf(const ifr_gguf *g, ifr_llama2_config *cfg) {
+    if (!g || !cfg) return ifr_free_error() = "null argument", IFR_EINVAL;
+    const char *arch = nullptr;
+    uint64_t alen = 0;
+    if (!ifr_gguf_get_string(g, "general.architecture", &arch, &alen)) {
+        std::string a(arch, alen);
+        for (char &ch : a) ch = (char)tolower((unsigned char)ch);
+        if (a.find("qwen2") != std::string::npos)
+            return ifr_free_error() = "gguf: qwen2 models (QKV biases) are not supported", IFR_EUNSUPPORTED;
+    }
+    ifr_llama2_config c{};
+    const std::string m = "llama"; // LlamaModelType::Llama.gguf_model_name()
+    ifr_status st;
+    if ((st = gguf_u32(g, m + ".embedding_length", c.hidden)) || (st = gguf_u32(g, m + ".feed_forward_length", c.ffn)) ||
+        (st = gguf_u32(g, m + ".block_count", c.n_layers)) || (st = gguf_u32(g, m + ".attention.head_count", c.n_heads)) ||
+        (st = gguf_u32(g, m + ".attention.head_count_kv", c.n_kv_heads)) ||
+        (st = gguf_u32(g, m + ".context_length", c.max_pos)))
+        return st;
+    uint64_t vocab = 0;
+    int32_t et;
+    if (ifr_gguf_get_array(g, "tokenizer.ggml.tokens", &et, &vocab, nullptr))
+        return ifr_free_error() = "gguf: tokenizer.ggml.tokens missing or not an array", IFR_EINVAL;
+    if (vocab == 0 || vocab > 0xFFFFFFFFull) return ifr_free_error() = "gguf: vocabulary size out of range", IFR_EINVAL;
+    c.vocab = (uint32_t)vocab;
+    c.rope_theta = 10000.0f;
+    c.rms_eps = 1.0e-6f;
+    // optional keys: absent -> default; present with another type -> error (as_f32 panics)
+    for (auto [key, dst] : {std::pair<std::string, float *>{m + ".rope.freq_base", &c.rope_theta},
+                            {m + ".attention.layer_norm_rms_epsilon", &c.rms_eps}}) {
+        if (ifr_gguf_metadata_type(g, key.c_str(), nullptr, nullptr) < 0) continue;
+        if (ifr_gguf_get_scalar(g, key.c_str(), IFR_GGUF_F32, dst))
+            return ifr_free_error() = "gguf: " + key + " is not an F32", IFR_EINVAL;
+    }
+    c.kv_dtype = IFR_F32;
+    c.rope_variant = IFR_ROPE_ORIGINAL;
+    *cfg = c;
+    return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_weights_from_gguf(ifr_ctx *c, const ifr_gguf *g, const ifr_llama2_config *cfg,
+                                                ifr_llama2_weights **out) {
+    if (!c || !g || !cfg || !out) return IFR_EINVAL;
+    *out = nullptr;
+    ifr_llama2_weights *w = nullptr;
+    ifr_status st = ifr_llama2_weights_create(c, cfg, &w);
+    if (st) return st;
+    std::vector<std::string> names = {"token_embd.weight", "output_norm.weight"};
+    if (ifr_gguf_tensor_info(g, "output.weight", nullptr, nullptr, nullptr, nullptr, nullptr) == IFR_OK)
+        names.push_back("output.weight");
+    for (uint32_t l = 0; l < cfg->n_layers; l++)
+        for (const char *f : {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm", "ffn_gate", "ffn_up",
+                              "ffn_down"})
+            names.push_back("blk." + std::to_string(l) + "." + f + ".weight");
+    for (const std::string &name : names) {
+        int32_t dtype;
+        uint64_t dims[4];
+        uint32_t rank;
+        const void *data;
+        uint64_t bytes;
+        if (ifr_gguf_tensor_info(g, name.c_str(), &dtype, dims, &rank, &data, &bytes)) {
+            ifr_llama2_weights_destroy(w);
+            return c->fail(IFR_EINVAL, "gguf: %s", ifr_free_error().c_str());
+        }
+        if (!data || rank < 1 || rank > 2 || dims[2] != 1 || dims[3] != 1 || dims[0] > 0xFFFFFFFFull ||
+            dims[1] > 0xFFFFFFFFull) {
+            ifr_llama2_weights_destroy(w);
+            return c->fail(IFR_EINVAL, "gguf: %s has rank %u or a type without data", name.c_str(), rank);
+        }
+        // rank 1: a vector of dims[0] (rows 1); rank 2: [rows, cols] (gguf.rs:591-593)
+        const uint32_t rows = rank == 1 ? 1u : (uint32_t)dims[0], cols = rank == 1 ? (uint32_t)dims[0] : (uint32_t)dims[1];
+        void *dev = nullptr;
+        if ((st = ifr_alloc(c, std::max<size_t>(bytes, 16), &dev))) {
+            ifr_llama2_weights_destroy(w);
+            return st;
+        }
+        w->owned.push_back(dev);
+        if ((st = c->hip(hipMemcpy(dev, data, bytes, hipMemcpyHostToDevice), "hipMemcpy(gguf tensor)")) ||
+            (st = ifr_llama2_weights_set(w, name.c_str(), dtype, dev, rows, cols))) {
+            ifr_llama2_weights_destroy(w);
+            return st;
+        }
+    }
+    *out = w;
+    return IFR_OK;
+}
 
 static void state_free(ifr_llama2_state *s) {
     if (!s) return;
