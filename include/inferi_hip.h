@@ -248,9 +248,11 @@ typedef struct ifr_llama2_state ifr_llama2_state;
 IFR_API ifr_status ifr_llama2_weights_create(ifr_ctx *ctx, const ifr_llama2_config *cfg, ifr_llama2_weights **out);
 /* Binds one GGUF tensor ("token_embd.weight", "output_norm.weight",
  * "output.weight", "blk.N.{attn_norm,attn_q,attn_k,attn_v,attn_output,
- * ffn_norm,ffn_gate,ffn_up,ffn_down}.weight") already in device memory.
+ * ffn_norm,ffn_gate,ffn_up,ffn_down}.weight", and Qwen2's
+ * "blk.N.attn_{q,k,v}.bias") already in device memory.
  * rows/cols follow gguf.rs:591-593 (dims reversed: rows = ne1, cols = ne0);
- * norms are F32 vectors with rows = 1. */
+ * norms and biases are F32 vectors with rows = 1.  A layer with biases adds
+ * them to q, k and v before RoPE (transformer.rs:434-442). */
 IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *gguf_name, int32_t dtype,
                                           const void *dev_data, uint32_t rows, uint32_t cols);
 IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w);
@@ -288,7 +290,8 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const 
  * their KV-cache rows are written and the position advances by n_tokens.
  * No logits are formed: the next decode step, at the prompt's last token,
  * produces them.  Waits for queued work (it reads the position).  Requires
- * Q4_K attention and FFN matrices and the original RoPE variant. */
+ * Q4_K attention and FFN matrices; both RoPE variants and QKV biases are
+ * handled. */
 IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
                                       uint32_t n_tokens);
 /* Sampling at the end of each decode step, as sample_next_token does
@@ -385,20 +388,23 @@ IFR_API ifr_status ifr_gguf_writer_add_tensor(ifr_gguf_writer *w, const char *na
                                               const uint64_t *dims, const void *data, uint64_t bytes);
 IFR_API ifr_status ifr_gguf_writer_save(ifr_gguf_writer *w, const char *path);
 
-/* Llama2Config::from_gguf (crates/inferi/src/models/llama2/cpu.rs:74-107):
- * llama.{embedding_length, feed_forward_length, block_count,
+/* Llama2Config::from_gguf_with_model_type (crates/inferi/src/models/llama2/
+ * cpu.rs:74-107): with M = "qwen2" when general.architecture names qwen2
+ * (ChatLlm::from_gguf, inferi-chat/src/llm.rs:71-92), else "llama":
+ * M.{embedding_length, feed_forward_length, block_count,
  * attention.head_count, attention.head_count_kv, context_length} as U32,
- * vocab = the length of tokenizer.ggml.tokens, rope.freq_base (F32, default
- * 10000) and attention.layer_norm_rms_epsilon (F32, default 1e-6); max_pos =
- * context_length.  kv_dtype is set to IFR_F32 (the reference's cache) and
- * rope_variant to the original; a caller may change kv_dtype before creating
- * a state.  A general.architecture naming qwen2 returns IFR_EUNSUPPORTED
- * (its QKV biases are not built). */
+ * vocab = the length of tokenizer.ggml.tokens, M.rope.freq_base (F32,
+ * default 10000) and M.attention.layer_norm_rms_epsilon (F32, default 1e-6);
+ * max_pos = context_length.  kv_dtype is set to IFR_F32 (the reference's
+ * cache), rope_variant to NeoX for qwen2 and the original otherwise
+ * (models/llama2/mod.rs:25-30); a caller may change kv_dtype before creating
+ * a state. */
 IFR_API ifr_status ifr_llama2_config_from_gguf(const ifr_gguf *g, ifr_llama2_config *cfg);
 /* Llama2Weights::from_gguf (crates/inferi/src/models/llama2/transformer.rs:
  * 294-393): every tensor the model uses is copied verbatim (GGUF blocks) to
- * device memory that the weights own and free at ifr_llama2_weights_destroy;
- * output.weight falls back to token_embd.weight when absent (:376-382). */
+ * device memory that the weights own and free at ifr_llama2_weights_destroy,
+ * including blk.N.attn_{q,k,v}.bias when present (Qwen2); output.weight
+ * falls back to token_embd.weight when absent (:376-382). */
 IFR_API ifr_status ifr_llama2_weights_from_gguf(ifr_ctx *ctx, const ifr_gguf *g, const ifr_llama2_config *cfg,
                                                 ifr_llama2_weights **out);
 

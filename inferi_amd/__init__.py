@@ -343,17 +343,18 @@ class Llama2Config:
                    vocab=c.vocab, max_pos=c.max_pos, rope_theta=c.rope_theta, rms_eps=c.rms_eps, kv_dtype=c.kv_dtype,
                    rope_variant=c.rope_variant)
 
-    def gguf_metadata(self) -> list:
-        """(key, type, value) of the llama.* keys from_gguf reads."""
-        m = "llama"
+    def gguf_metadata(self, arch: str = "llama") -> list:
+        """(key, type, value) of the <arch>.* keys from_gguf reads."""
+        m = arch
         return [(f"{m}.embedding_length", GGUF_U32, self.hidden), (f"{m}.feed_forward_length", GGUF_U32, self.ffn),
                 (f"{m}.block_count", GGUF_U32, self.n_layers), (f"{m}.attention.head_count", GGUF_U32, self.n_heads),
                 (f"{m}.attention.head_count_kv", GGUF_U32, self.n_kv_heads),
                 (f"{m}.context_length", GGUF_U32, self.max_pos), (f"{m}.rope.freq_base", GGUF_F32, self.rope_theta),
                 (f"{m}.attention.layer_norm_rms_epsilon", GGUF_F32, self.rms_eps)]
 
-    def shapes(self) -> dict:
-        """GGUF tensor name -> (rows, cols) (transformer.rs:294-393)."""
+    def shapes(self, bias: bool = False) -> dict:
+        """GGUF tensor name -> (rows, cols) (transformer.rs:294-393); bias adds
+        Qwen2's blk.N.attn_{q,k,v}.bias vectors."""
         h, kv, f = self.hidden, self.kv_dim, self.ffn
         s = {"token_embd.weight": (self.vocab, h), "output.weight": (self.vocab, h), "output_norm.weight": (1, h)}
         for l in range(self.n_layers):
@@ -362,6 +363,9 @@ class Llama2Config:
                       f"blk.{l}.attn_v.weight": (kv, h), f"blk.{l}.attn_output.weight": (h, h),
                       f"blk.{l}.ffn_gate.weight": (f, h), f"blk.{l}.ffn_up.weight": (f, h),
                       f"blk.{l}.ffn_down.weight": (h, f)})
+            if bias:
+                s.update({f"blk.{l}.attn_q.bias": (1, h), f"blk.{l}.attn_k.bias": (1, kv),
+                          f"blk.{l}.attn_v.bias": (1, kv)})
         return s
 
 
@@ -410,21 +414,23 @@ class Llama2Weights:
         w.h = h.value
         return w
 
-    def to_gguf(self, path: str, tokens: list | None = None, architecture: str = "llama") -> None:
+    def to_gguf(self, path: str, tokens: list | None = None, architecture: str | None = None) -> None:
         """Writes the model as a GGUF file that from_gguf (here and in the
         reference) reads: general.architecture, the llama.* keys, a
         tokenizer.ggml.tokens list of vocab length, and every tensor's blocks."""
+        if architecture is None:
+            architecture = "qwen2" if self.config.rope_variant == ROPE_NEOX else "llama"
         wr = GgufWriter()
         try:
             wr.set("general.architecture", GGUF_STRING, architecture)
             wr.set("tokenizer.ggml.model", GGUF_STRING, "llama")
-            for key, ty, val in self.config.gguf_metadata():
+            for key, ty, val in self.config.gguf_metadata(architecture):
                 wr.set(key, ty, val)
             toks = tokens if tokens is not None else [f"<t{i}>" for i in range(self.config.vocab)]
             wr.set_array("tokenizer.ggml.tokens", GGUF_STRING, toks)
             for name in self.buffers:
                 dtype, arr, rows, cols = self.download(name)
-                dims = [cols] if rows == 1 and name.endswith("norm.weight") else [rows, cols]
+                dims = [cols] if rows == 1 and name.endswith(("norm.weight", ".bias")) else [rows, cols]
                 wr.add_tensor(name, dtype, dims, arr)
             wr.save(path)
         finally:
@@ -433,20 +439,22 @@ class Llama2Weights:
     @classmethod
     def synthetic(cls, ctxt: LlmContext, config: Llama2Config, seed: int, mat_dtype: int = Q4_K,
                   head_dtype: int = Q6_K, embd_dtype: int = Q4_K, std: float = 0.02, norm_mean: float = 1.0,
-                  norm_std: float = 0.1) -> "Llama2Weights":
+                  norm_std: float = 0.1, qkv_bias: bool = False, bias_std: float = 0.5) -> "Llama2Weights":
         """Random-init model made on the device: every matrix ~ N(0, std)
         quantized with the GGUF quantizer, norms ~ N(norm_mean, norm_std) in
-        F32.  Tensor i (in ``config.shapes()`` order) uses generator stream i."""
+        F32, and with qkv_bias Qwen2's QKV biases ~ N(0, bias_std) in F32.
+        Tensor i (in ``config.shapes(qkv_bias)`` order) uses generator stream i."""
         w = cls(ctxt, config)
-        shapes = config.shapes()
+        shapes = config.shapes(qkv_bias)
         biggest = max(r * c for r, c in shapes.values())
         tmp = ctxt.alloc(biggest * 4)
         try:
             for i, (name, (rows, cols)) in enumerate(shapes.items()):
                 n = rows * cols
-                if name.endswith("norm.weight"):
+                if name.endswith(("norm.weight", ".bias")):
                     buf = ctxt.alloc(n * 4)
-                    ctxt.fill_normal(buf, n, seed, i, norm_mean, norm_std)
+                    bias = name.endswith(".bias")
+                    ctxt.fill_normal(buf, n, seed, i, 0.0 if bias else norm_mean, bias_std if bias else norm_std)
                     w.set(name, F32, buf, rows, cols)
                     continue
                 dt = head_dtype if name == "output.weight" else embd_dtype if name == "token_embd.weight" else mat_dtype

@@ -167,27 +167,49 @@ IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
     const uint32_t m = blockIdx.x, pos = a.p0 + m, hs = a.head_size;
     float *row = (float *)a.qkv + (size_t)m * a.ld_qkv;
     const uint32_t qd = a.q_dim, kd = a.kv_dim;
+    // each thread owns whole rotation pairs of q | k: pair i of a vector
+    // rotates (e0, e1) = (2i, 2i+1), or NeoX (rope.rs:97-141): within head
+    // h = 2i / hs, (h hs + j, h hs + j + hs/2) with j = i mod hs/2; the
+    // biases (Qwen2) are added first, as transformer.rs:434-445 orders it
     for (uint32_t i = threadIdx.x; i < (qd + kd) / 2; i += blockDim.x) {
-        const uint32_t v = 2 * i;
-        float x0 = row[v], x1 = row[v + 1];
-        const uint32_t idx = v < qd ? v : v - qd;
-        rope_pair(x0, x1, idx, hs, pos, a.rope_tab);
-        if (v < qd) {
-            row[v] = x0;
-            row[v + 1] = x1;
+        const bool is_q = 2 * i < qd;
+        const uint32_t pi = is_q ? i : i - qd / 2; // pair index within its vector
+        uint32_t e0, e1;
+        if (a.neox) {
+            const uint32_t h = (2 * pi) / hs, j = pi % (hs / 2);
+            e0 = h * hs + j;
+            e1 = e0 + hs / 2;
         } else {
-            const size_t off = (size_t)pos * kd + idx;
+            e0 = 2 * pi;
+            e1 = e0 + 1;
+        }
+        const uint32_t base = is_q ? 0 : qd;
+        float x0 = row[base + e0], x1 = row[base + e1];
+        const float *bias = is_q ? a.q_bias : a.k_bias;
+        if (bias) {
+            x0 = x0 + bias[e0];
+            x1 = x1 + bias[e1];
+        }
+        // theta index j (the table holds base^(-2j/hs)); rope_pair takes 2j
+        const uint32_t tj = a.neox ? 2 * (pi % (hs / 2)) : e0;
+        rope_pair(x0, x1, tj, hs, pos, a.rope_tab);
+        if (is_q) {
+            row[e0] = x0;
+            row[e1] = x1;
+        } else {
+            const size_t off = (size_t)pos * kd;
             if (a.kv_f16) {
-                ((uint16_t *)a.k_cache)[off] = f32_to_f16(x0);
-                ((uint16_t *)a.k_cache)[off + 1] = f32_to_f16(x1);
+                ((uint16_t *)a.k_cache)[off + e0] = f32_to_f16(x0);
+                ((uint16_t *)a.k_cache)[off + e1] = f32_to_f16(x1);
             } else {
-                ((float *)a.k_cache)[off] = x0;
-                ((float *)a.k_cache)[off + 1] = x1;
+                ((float *)a.k_cache)[off + e0] = x0;
+                ((float *)a.k_cache)[off + e1] = x1;
             }
         }
     }
     for (uint32_t i = threadIdx.x; i < kd; i += blockDim.x) {
-        const float v = row[qd + kd + i];
+        float v = row[qd + kd + i];
+        if (a.v_bias) v = v + a.v_bias[i];
         const size_t off = (size_t)pos * kd + i;
         if (a.kv_f16)
             ((uint16_t *)a.v_cache)[off] = f32_to_f16(v);

@@ -297,6 +297,7 @@ struct Tens {
 
 struct LayerW {
     Tens attn_norm, attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down;
+    Tens q_bias, k_bias, v_bias; // Qwen2 (transformer.rs:434-442); data null when absent
 };
 
 struct ifr_llama2_weights {
@@ -422,8 +423,9 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         const LayerW &Lw = w->layers[l];
         uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
         uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
+        const bool has_bias = Lw.q_bias.data || Lw.k_bias.data || Lw.v_bias.data;
         const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype &&
-                              cfg.rope_variant == IFR_ROPE_ORIGINAL;
+                              cfg.rope_variant == IFR_ROPE_ORIGINAL && !has_bias;
         const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
         const float *next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
         GemvPlan p;
@@ -470,6 +472,16 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             for (int m = 0; m < 3; m++)
                 if ((st = gemv_plain(c, outs[m], mats[m]->data, mats[m]->dtype, mats[m]->rows, hidden, s->xb, s->xq_u)))
                     return st;
+            // Qwen2: q += q_bias, k += k_bias, v += v_bias before RoPE (transformer.rs:434-442)
+            const Tens *bias[3] = {&Lw.q_bias, &Lw.k_bias, &Lw.v_bias};
+            for (int m = 0; m < 3; m++) {
+                if (!bias[m]->data) continue;
+                EltArgs e{};
+                e.a = outs[m];
+                e.b = (const float *)bias[m]->data;
+                e.n = mats[m]->rows;
+                if ((st = c->launch("add_k", dim3((e.n + 255) / 256), dim3(256), 0, e))) return st;
+            }
             EltArgs r{};
             r.a = s->q;
             r.k = s->ktmp;
@@ -1081,11 +1093,19 @@ IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *nam
         return IFR_OK;
     }
     unsigned layer = 0;
-    char field[64] = {0};
-    if (sscanf(name, "blk.%u.%63[a-z_].weight", &layer, field) != 2 || layer >= cfg.n_layers)
+    char field[64] = {0}, kind[8] = {0};
+    if (sscanf(name, "blk.%u.%63[a-z_].%7[a-z]", &layer, field, kind) != 3 || layer >= cfg.n_layers)
         return c->fail(IFR_EINVAL, "unknown tensor name %s", name);
     LayerW &L = w->layers[layer];
     const std::string f = field;
+    if (!strcmp(kind, "bias")) { // Qwen2's QKV biases: F32 vectors
+        if (f == "attn_q") { if ((st = want(1, cfg.hidden, true))) return st; L.q_bias = t; }
+        else if (f == "attn_k") { if ((st = want(1, kv_dim, true))) return st; L.k_bias = t; }
+        else if (f == "attn_v") { if ((st = want(1, kv_dim, true))) return st; L.v_bias = t; }
+        else return c->fail(IFR_EINVAL, "unknown tensor name %s", name);
+        return IFR_OK;
+    }
+    if (strcmp(kind, "weight")) return c->fail(IFR_EINVAL, "unknown tensor name %s", name);
     if (f == "attn_norm") { if ((st = want(1, cfg.hidden, true))) return st; L.attn_norm = t; }
     else if (f == "ffn_norm") { if ((st = want(1, cfg.hidden, true))) return st; L.ffn_norm = t; }
     else if (f == "attn_q") { if ((st = want(cfg.hidden, cfg.hidden, false))) return st; L.attn_q = t; }
@@ -1116,16 +1136,19 @@ static ifr_status gguf_u32(const ifr_gguf *g, const std::string &key, uint32_t &
 
 IFR_API ifr_status ifr_llama2_config_from_gguf(const ifr_gguf *g, ifr_llama2_config *cfg) {
     if (!g || !cfg) return ifr_free_error() = "null argument", IFR_EINVAL;
+    // the architecture picks the key prefix and the RoPE pairing, as
+    // ChatLlm::from_gguf (inferi-chat/src/llm.rs:71-92) picks LlamaModelType
+    // (models/llama2/mod.rs:18-30)
     const char *arch = nullptr;
     uint64_t alen = 0;
+    bool qwen2 = false;
     if (!ifr_gguf_get_string(g, "general.architecture", &arch, &alen)) {
         std::string a(arch, alen);
         for (char &ch : a) ch = (char)tolower((unsigned char)ch);
-        if (a.find("qwen2") != std::string::npos)
-            return ifr_free_error() = "gguf: qwen2 models (QKV biases) are not supported", IFR_EUNSUPPORTED;
+        qwen2 = a.find("qwen2") != std::string::npos;
     }
     ifr_llama2_config c{};
-    const std::string m = "llama"; // LlamaModelType::Llama.gguf_model_name()
+    const std::string m = qwen2 ? "qwen2" : "llama";
     ifr_status st;
     if ((st = gguf_u32(g, m + ".embedding_length", c.hidden)) || (st = gguf_u32(g, m + ".feed_forward_length", c.ffn)) ||
         (st = gguf_u32(g, m + ".block_count", c.n_layers)) || (st = gguf_u32(g, m + ".attention.head_count", c.n_heads)) ||
@@ -1148,7 +1171,7 @@ IFR_API ifr_status ifr_llama2_config_from_gguf(const ifr_gguf *g, ifr_llama2_con
             return ifr_free_error() = "gguf: " + key + " is not an F32", IFR_EINVAL;
     }
     c.kv_dtype = IFR_F32;
-    c.rope_variant = IFR_ROPE_ORIGINAL;
+    c.rope_variant = qwen2 ? IFR_ROPE_NEOX : IFR_ROPE_ORIGINAL;
     *cfg = c;
     return IFR_OK;
 }
@@ -1163,10 +1186,16 @@ IFR_API ifr_status ifr_llama2_weights_from_gguf(ifr_ctx *c, const ifr_gguf *g, c
     std::vector<std::string> names = {"token_embd.weight", "output_norm.weight"};
     if (ifr_gguf_tensor_info(g, "output.weight", nullptr, nullptr, nullptr, nullptr, nullptr) == IFR_OK)
         names.push_back("output.weight");
-    for (uint32_t l = 0; l < cfg->n_layers; l++)
+    for (uint32_t l = 0; l < cfg->n_layers; l++) {
         for (const char *f : {"attn_norm", "attn_q", "attn_k", "attn_v", "attn_output", "ffn_norm", "ffn_gate", "ffn_up",
                               "ffn_down"})
             names.push_back("blk." + std::to_string(l) + "." + f + ".weight");
+        for (const char *f : {"attn_q", "attn_k", "attn_v"}) { // Qwen2's biases, when the file has them
+            const std::string b = "blk." + std::to_string(l) + "." + f + ".bias";
+            if (ifr_gguf_tensor_info(g, b.c_str(), nullptr, nullptr, nullptr, nullptr, nullptr) == IFR_OK)
+                names.push_back(b);
+        }
+    }
     for (const std::string &name : names) {
         int32_t dtype;
         uint64_t dims[4];
@@ -1358,7 +1387,6 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     ifr_status st = check_weights(c, s, w);
     if (st) return st;
     const ifr_llama2_config &cfg = s->cfg;
-    if (cfg.rope_variant != IFR_ROPE_ORIGINAL) return c->fail(IFR_EUNSUPPORTED, "prefill: NeoX RoPE");
     for (const LayerW &L : w->layers) {
         const Tens *mats[] = {&L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
         for (const Tens *t : mats)
@@ -1402,12 +1430,16 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
         a.kv_f16 = cfg.kv_dtype == IFR_F16;
         a.ffn = F;
         a.gu = s->pf_gu;
+        a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
         if ((st = c->launch("pf_embed_k", dim3(M), dim3(256), 0, a))) return st;
         for (uint32_t l = 0; l < cfg.n_layers; l++) {
             const LayerW &L = w->layers[l];
             a.k_cache = s->kcache + (size_t)l * s->layer_kv_bytes;
             a.v_cache = s->vcache + (size_t)l * s->layer_kv_bytes;
             a.gamma = (const float *)L.attn_norm.data;
+            a.q_bias = (const float *)L.q_bias.data;
+            a.k_bias = (const float *)L.k_bias.data;
+            a.v_bias = (const float *)L.v_bias.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
             if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, M, false))) return st;
             if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, M, false))) return st;

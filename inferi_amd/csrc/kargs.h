@@ -241,6 +241,8 @@ struct PfArgs {
     int32_t kv_f16;
     uint32_t ffn;
     void *gu;            // f32 [M][2*ffn]: gate | up
+    const float *q_bias, *k_bias, *v_bias; // QKV biases (may be null)
+    int32_t neox;        // RoPE pairs (j, j + hs/2) instead of (2j, 2j+1)
 };
 
 } // namespace ifr

@@ -302,7 +302,7 @@ def seeded_coin(seed: int, pos: int) -> np.float32:
 class _Config(C.Structure):
     _fields_ = [("hidden", C.c_int), ("ffn", C.c_int), ("n_layers", C.c_int), ("n_heads", C.c_int),
                 ("n_kv_heads", C.c_int), ("vocab", C.c_int), ("max_pos", C.c_int),
-                ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("kv_f16", C.c_int)]
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("kv_f16", C.c_int), ("rope_neox", C.c_int)]
 
 
 class _Tensor(C.Structure):
@@ -311,7 +311,8 @@ class _Tensor(C.Structure):
 
 class _Layer(C.Structure):
     _fields_ = [(n, _Tensor) for n in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")] + [
-        ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p)]
+        ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p), ("q_bias", C.c_void_p), ("k_bias", C.c_void_p),
+        ("v_bias", C.c_void_p)]
 
 
 class _Model(C.Structure):
@@ -328,6 +329,8 @@ class Model:
     ``weights`` maps GGUF tensor names (``blk.N.attn_q.weight`` ...,
     ``token_embd.weight``, ``output.weight``, ``output_norm.weight``) to
     ``(dtype, uint8/float32 ndarray, rows, cols)``; norms are float32 arrays.
+    Qwen2-style models add ``blk.N.attn_{q,k,v}.bias`` (float32 arrays) and
+    ``cfg["rope_neox"] = 1``.
     """
 
     def __init__(self, cfg: dict, weights: dict):
@@ -335,7 +338,8 @@ class Model:
         self._keep = []
         c = cfg
         self._ccfg = _Config(c["hidden"], c["ffn"], c["n_layers"], c["n_heads"], c["n_kv_heads"], c["vocab"],
-                             c["max_pos"], c["rope_theta"], c["rms_eps"], int(c.get("kv_f16", 1)))
+                             c["max_pos"], c["rope_theta"], c["rms_eps"], int(c.get("kv_f16", 1)),
+                             int(c.get("rope_neox", 0)))
 
         def tens(name):
             dt, arr, rows, cols = weights[name]
@@ -354,6 +358,9 @@ class Model:
                 setattr(layers[l], m, tens(f"blk.{l}.{m}.weight"))
             layers[l].attn_norm = vec(f"blk.{l}.attn_norm.weight")
             layers[l].ffn_norm = vec(f"blk.{l}.ffn_norm.weight")
+            for b in ("q", "k", "v"):
+                if f"blk.{l}.attn_{b}.bias" in weights:
+                    setattr(layers[l], f"{b}_bias", vec(f"blk.{l}.attn_{b}.bias"))
         self._layers = layers
         self._m = _Model(self._ccfg, tens("token_embd.weight"), tens("output.weight"), vec("output_norm.weight"),
                          C.cast(layers, C.c_void_p))

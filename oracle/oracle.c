@@ -726,7 +726,11 @@ int ifo_forward(const ifo_model *m, ifo_state *s, int token, int pos, float *log
         tensor_gemv(&wl->attn_q, s->xb, s->q, nthreads);
         tensor_gemv(&wl->attn_k, s->xb, k, nthreads);
         tensor_gemv(&wl->attn_v, s->xb, v, nthreads);
-        ifo_rope(0, s->q, dim, k, kv_dim, hs, pos, c->rope_theta);
+        /* transformer.rs:434-442: the biases are added before RoPE */
+        if (wl->q_bias) ifo_add(s->q, wl->q_bias, dim);
+        if (wl->k_bias) ifo_add(k, wl->k_bias, kv_dim);
+        if (wl->v_bias) ifo_add(v, wl->v_bias, kv_dim);
+        ifo_rope(c->rope_neox, s->q, dim, k, kv_dim, hs, pos, c->rope_theta);
         size_t off = (size_t)pos * kv_dim;
         if (c->kv_f16) {
             ifo_encode_f16_array(k, (uint16_t *)s->k_cache[l] + off, (size_t)kv_dim);

@@ -125,6 +125,7 @@ typedef struct {
     int hidden, ffn, n_layers, n_heads, n_kv_heads, vocab, max_pos;
     float rope_theta, rms_eps;
     int kv_f16; /* 1: K/V rounded to binary16 at store time */
+    int rope_neox; /* 1: NeoX pairs (LlamaModelType::Qwen2, models/llama2/mod.rs:25-30) */
 } ifo_config;
 
 typedef struct {
@@ -136,6 +137,8 @@ typedef struct {
 typedef struct {
     ifo_tensor attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down;
     const float *attn_norm, *ffn_norm;
+    /* Qwen2's QKV biases (transformer.rs:434-442); NULL when absent */
+    const float *q_bias, *k_bias, *v_bias;
 } ifo_layer;
 
 typedef struct {

@@ -218,9 +218,12 @@ def test_config_from_gguf(tmp_path):
     llama_file(p, dict(BASE), tokens=None)
     with pytest.raises(I.HipError, match="tokens"):
         I.Llama2Config.from_gguf(I.Gguf(p))
-    q = dict(BASE)
-    q["arch"] = "qwen2"
-    llama_file(p, q)
-    with pytest.raises(I.HipError) as e:
+    # qwen2: the keys carry its prefix and the RoPE pairing is NeoX (models/llama2/mod.rs:18-30)
+    q = {k.replace("llama.", "qwen2."): v for k, v in BASE.items()}
+    q["arch"] = "Qwen2"
+    llama_file(p, q, tokens=100)
+    c = I.Llama2Config.from_gguf(I.Gguf(p))
+    assert c.rope_variant == I.ROPE_NEOX and c.n_layers == 2 and c.vocab == 100 and c.rope_theta == 500000.0
+    llama_file(p, dict(BASE, arch="qwen2"))  # llama.* keys under a qwen2 architecture are not read
+    with pytest.raises(I.HipError, match="qwen2.embedding_length"):
         I.Llama2Config.from_gguf(I.Gguf(p))
-    assert e.value.status == 2  # IFR_EUNSUPPORTED

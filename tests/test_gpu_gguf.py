@@ -97,3 +97,29 @@ def test_tied_embeddings_and_bad_files(ctx, tmp_path):
         lib_destroy(tied.h)
         tied.h = None
         w.close()
+
+
+def test_qwen2_model_round_trips_through_gguf(ctx, tmp_path):
+    """A Qwen2-style model (NeoX RoPE, QKV biases) written under
+    general.architecture = qwen2 reads back with the qwen2.* keys, the NeoX
+    variant and its biases, and decodes bit-identically."""
+    cfg = I.Llama2Config(n_layers=2, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=512, max_pos=32,
+                         rope_theta=1000000.0, rms_eps=1e-6, kv_dtype=I.F16, rope_variant=I.ROPE_NEOX)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=17, qkv_bias=True, std=0.05)
+    path = str(tmp_path / "qwen.gguf")
+    w.to_gguf(path)
+    g = I.Gguf(path)
+    assert g.get("general.architecture") == "qwen2" and "qwen2.block_count" in g.keys()
+    assert "blk.1.attn_k.bias" in g.tensor_names()
+    c2 = I.Llama2Config.from_gguf(g)
+    assert c2.rope_variant == I.ROPE_NEOX
+    c2.kv_dtype = I.F16
+    w2 = I.Llama2Weights.from_gguf(ctx, g, c2)
+    try:
+        a, ta = decode(ctx, cfg, w, [9, 4], 5)
+        b, tb = decode(ctx, c2, w2, [9, 4], 5)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)) and np.array_equal(ta, tb)
+    finally:
+        g.close()
+        w2.close()
+        w.close()

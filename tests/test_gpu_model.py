@@ -30,12 +30,12 @@ def oracle_model(cfg, weights):
     import inferi_amd as I
 
     host = {}
-    for name in cfg.shapes():
+    for name in weights.buffers:
         dt, arr, rows, cols = weights.download(name)
         host[name] = arr if dt == I.F32 else (dt, arr, rows, cols)
     c = dict(hidden=cfg.hidden, ffn=cfg.ffn, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
              vocab=cfg.vocab, max_pos=cfg.max_pos, rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps,
-             kv_f16=int(cfg.kv_dtype == I.F16))
+             kv_f16=int(cfg.kv_dtype == I.F16), rope_neox=int(cfg.rope_variant == I.ROPE_NEOX))
     return O.Model(c, host)
 
 
@@ -76,6 +76,32 @@ def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv, exact):
     cfg = tiny_cfg(kv_dtype=dt[kv])
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=11, mat_dtype=dt[mat], head_dtype=dt[head], embd_dtype=dt[mat],
                                   std=0.05)
+    try:
+        check_steps_vs_oracle(ctx, cfg, w, mode)
+    finally:
+        ctx.set_option("gemv_exact", 0)
+        w.close()
+
+
+@pytest.mark.parametrize("mode", ["fused", "unfused", "graph"])
+def test_qwen2_style_step_by_step(ctx, oracle_lib, mode):
+    """Qwen2's differences (transformer.rs:434-445, models/llama2/mod.rs:25-30):
+    QKV biases added before RoPE, and NeoX RoPE pairs."""
+    import inferi_amd as I
+
+    cfg = tiny_cfg(rope_variant=I.ROPE_NEOX)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=13, std=0.05, qkv_bias=True)
+    try:
+        check_steps_vs_oracle(ctx, cfg, w, mode)
+    finally:
+        w.close()
+
+
+def check_steps_vs_oracle(ctx, cfg, w, mode):
+    """20 steps (a 5-token prompt, then greedy): every step's logits and the
+    KV-cache rows against the oracle, the generated ids identical."""
+    import inferi_amd as I
+
     s = I.Llama2State(ctx, cfg)
     prompt = [3, 999, 41, 0, 512]
     try:
@@ -102,9 +128,7 @@ def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv, exact):
                     got, ref = O.decode_f16(got), O.decode_f16(ref)
                 assert_close(got, ref, tol=2e-3, what=f"{which} cache layer {layer}")
     finally:
-        ctx.set_option("gemv_exact", 0)
         s.close()
-        w.close()
 
 
 def test_paths_agree_and_continuation(ctx):

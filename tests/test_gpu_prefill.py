@@ -145,6 +145,20 @@ def test_prefill_chunks_and_gqa4_hs128(ctx, oracle_lib):
         w.close()
 
 
+def test_prefill_qwen2_style(ctx, oracle_lib):
+    """NeoX RoPE pairs and QKV biases (Qwen2) in the prefill's RoPE/KV kernel."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=600, max_pos=160,
+                         rope_theta=1000000.0, rms_eps=1e-6, kv_dtype=I.F16, rope_variant=I.ROPE_NEOX)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=43, std=0.05, qkv_bias=True)
+    try:
+        prompt = np.random.default_rng(5).integers(0, cfg.vocab, 130).tolist()
+        assert _prefill_vs_decode(ctx, cfg, w, prompt, 8) > 0
+    finally:
+        w.close()
+
+
 def test_prefill_rejects_unsupported(ctx):
     import inferi_amd as I
 

@@ -186,8 +186,9 @@ def tiny_config(**kw):
     return c
 
 
-def random_weights(c, rng, mat_dtype=O.Q8_0, head_dtype=O.Q8_0, embd_dtype=O.Q8_0, zero_layers=False):
-    """Random model in GGUF block form.  Hidden 64 only fits 32-element blocks."""
+def random_weights(c, rng, mat_dtype=O.Q8_0, head_dtype=O.Q8_0, embd_dtype=O.Q8_0, zero_layers=False, bias=False):
+    """Random model in GGUF block form.  Hidden 64 only fits 32-element blocks.
+    bias: Qwen2's attn_{q,k,v}.bias vectors."""
     hd, kv = c["hidden"], c["hidden"] * c["n_kv_heads"] // c["n_heads"]
     shapes = {"attn_q": (hd, hd), "attn_k": (kv, hd), "attn_v": (kv, hd), "attn_output": (hd, hd),
               "ffn_gate": (c["ffn"], hd), "ffn_up": (c["ffn"], hd), "ffn_down": (hd, c["ffn"])}
@@ -204,6 +205,9 @@ def random_weights(c, rng, mat_dtype=O.Q8_0, head_dtype=O.Q8_0, embd_dtype=O.Q8_
             w[f"blk.{l}.{m}.weight"] = qt(mat_dtype, r, cc, zero=zero_layers)
         w[f"blk.{l}.attn_norm.weight"] = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
         w[f"blk.{l}.ffn_norm.weight"] = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+        if bias:
+            for b, n in (("q", hd), ("k", kv), ("v", kv)):
+                w[f"blk.{l}.attn_{b}.bias"] = (0.5 * rng.standard_normal(n)).astype(np.float32)
     w["token_embd.weight"] = qt(embd_dtype, c["vocab"], hd, 1.0)
     w["output.weight"] = qt(head_dtype, c["vocab"], hd)
     w["output_norm.weight"] = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
@@ -229,12 +233,16 @@ def numpy_forward(c, w, tokens):
         return x / np.sqrt(np.mean(x * x) + c["rms_eps"]) * g
 
     def rope(v, pos):
+        # original: pairs (2j, 2j+1); NeoX (rope.rs:97-141): pairs (j, j + hs/2)
+        # within each head; both rotate by pos * base^(-2j/hs)
         v = v.copy()
-        for i in range(0, v.size, 2):
-            th = np.float32(c["rope_theta"]) ** (-np.float32(i % hs) / np.float32(hs))
-            a = np.float64(np.float32(pos) * np.float32(th))
-            x0, x1 = v[i], v[i + 1]
-            v[i], v[i + 1] = np.cos(a) * x0 - np.sin(a) * x1, np.sin(a) * x0 + np.cos(a) * x1
+        for h in range(v.size // hs):
+            for j in range(hs // 2):
+                th = np.float32(c["rope_theta"]) ** (-np.float32(2 * j) / np.float32(hs))
+                a = np.float64(np.float32(pos) * np.float32(th))
+                i0, i1 = (h * hs + j, h * hs + j + hs // 2) if c.get("rope_neox") else (h * hs + 2 * j, h * hs + 2 * j + 1)
+                x0, x1 = v[i0], v[i1]
+                v[i0], v[i1] = np.cos(a) * x0 - np.sin(a) * x1, np.sin(a) * x0 + np.cos(a) * x1
         return v
 
     all_logits = []
@@ -243,9 +251,10 @@ def numpy_forward(c, w, tokens):
         for l in range(c["n_layers"]):
             g = lambda m: deq[f"blk.{l}.{m}.weight"]
             xb = rms(x, g("attn_norm"))
-            q = rope(g("attn_q") @ xb, pos)
-            k = rope(g("attn_k") @ xb, pos)
-            v = g("attn_v") @ xb
+            bq, bk, bv = (deq.get(f"blk.{l}.attn_{b}.bias", 0.0) for b in "qkv")
+            q = rope(g("attn_q") @ xb + bq, pos)
+            k = rope(g("attn_k") @ xb + bk, pos)
+            v = g("attn_v") @ xb + bv
             f = (lambda a: a.astype(np.float16).astype(np.float64)) if c["kv_f16"] else (lambda a: a)
             kc[l, pos], vc[l, pos] = f(k), f(v)
             att = np.zeros(hd)
@@ -261,11 +270,13 @@ def numpy_forward(c, w, tokens):
     return all_logits
 
 
-@pytest.mark.parametrize("kv_f16", [1, 0])
-def test_forward_vs_numpy_rederivation(oracle_lib, kv_f16):
-    c = tiny_config(kv_f16=kv_f16)
+@pytest.mark.parametrize("kv_f16,qwen2", [(1, 0), (0, 0), (1, 1)], ids=["f16", "f32", "qwen2"])
+def test_forward_vs_numpy_rederivation(oracle_lib, kv_f16, qwen2):
+    """qwen2: QKV biases added before RoPE (transformer.rs:434-442) and the
+    NeoX RoPE pairing (models/llama2/mod.rs:25-30)."""
+    c = tiny_config(kv_f16=kv_f16, rope_neox=qwen2)
     rng = np.random.default_rng(1234)
-    w = random_weights(c, rng)
+    w = random_weights(c, rng, bias=bool(qwen2))
     m = O.Model(c, w)
     tokens = [3, 17, 42, 0, 49, 8, 8, 21]
     ref = numpy_forward(c, w, tokens)
