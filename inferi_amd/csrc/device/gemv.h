@@ -270,6 +270,7 @@ struct XQ {
           xs((const float *)(base + 3 * K)), xsum((const float *)(base + 3 * K + K / 4)) {}
 };
 
+
 constexpr float XQ_MAXCODE = 2097151.0f; // 2^21 - 1
 
 // Quantizes one value per lane into XQ at element i; the 16 lanes of a DPP
@@ -824,7 +825,16 @@ __device__ void gemv_int_body(const GemvArgs &a) {
 
     // the wave index is uniform across the wave: row addresses stay scalar
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t W = blockDim.x >> 6, KS = a.ks, RW = W / KS;
+    // Every argument the prologue needs, read in one batch: left to itself
+    // the compiler loads each field next to its first use and waits each
+    // time, three dependent round trips before the first weight load.  (An
+    // empty asm that takes them in scalar registers; it emits nothing.)
+    asm volatile("" ::"s"(a.w0), "s"(a.w1), "s"(a.w2), "s"(a.rows0), "s"(a.rows1), "s"(a.total_rows), "s"(a.cols),
+                 "s"(a.nb), "s"(a.row_bytes), "s"(a.n_ss), "s"(a.xq), "s"(a.ss_part), "s"(a.ks), "s"(a.y),
+                 "s"(a.gamma_next), "s"(a.rope_tab), "s"(a.ctl), "s"(a.head_size), "s"(a.nwaves));
+    // the launch shape comes from the arguments: reading blockDim costs a
+    // vector load of the dispatch packet and a full wait at kernel entry
+    const uint32_t W = a.nwaves, NT = W * 64, KS = a.ks, RW = W / KS;
     const uint32_t ks = (uint32_t)wave % KS, rw = (uint32_t)wave / KS;
     // a geometry that does not tile the group would never advance: the host
     // never launches one, and the workgroup exits as a whole if it did
@@ -866,32 +876,40 @@ __device__ void gemv_int_body(const GemvArgs &a) {
 
     Item cur{blockIdx.x, 0, ks};
     CH A, B;
-    // the first item's weights do not depend on x: in flight before staging
     if (cur.g >= ngroups) { // no work for this workgroup (the host never launches one)
         if constexpr (MODE == GEMV_HEAD)
             if (tid == 0 && a.part_keys) a.part_keys[blockIdx.x] = 0;
         return;
     }
-    load(A, cur);
-    {
-        const uint4 *src = (const uint4 *)a.xq;
-        uint4 *dst = (uint4 *)lds;
-        const uint32_t n16 = xq_bytes(a.cols) / 16;
-        for (uint32_t i = (uint32_t)tid; i < n16; i += blockDim.x) dst[i] = src[i];
-    }
-    float rs = 1.0f;
+    // Prologue order.  Loads complete in issue order, so every small input
+    // (x's XQ copy, the RMSNorm partial sums, the RoPE thetas, the first
+    // group's residual) is requested before the first item's weights: staging
+    // x then waits for those few loads only, while the weights stream in.
+    // The first XC chunks per thread and SC partial sums per lane are
+    // straight-line loads of clamped (valid) addresses; loops cover larger
+    // inputs.
+    constexpr uint32_t XC = 4, SC = 4;
+    const uint32_t n16 = xq_bytes(a.cols) / 16;
+    const uint4 *xsrc = (const uint4 *)a.xq;
+    static_assert(XC == 4, "four named chunks");
+    const uint32_t xi0 = min((uint32_t)tid, n16 - 1), xi1 = min((uint32_t)tid + NT, n16 - 1);
+    const uint32_t xi2 = min((uint32_t)tid + 2 * NT, n16 - 1), xi3 = min((uint32_t)tid + 3 * NT, n16 - 1);
+    const uint4 xv0 = xsrc[xi0], xv1 = xsrc[xi1], xv2 = xsrc[xi2], xv3 = xsrc[xi3];
+    float sv[SC];
     if constexpr (NORM) {
-        float t = 0.0f;
-        for (uint32_t i = (uint32_t)lane; i < a.n_ss; i += 64) t += a.ss_part[i];
-        t = wave_sum(t);
-        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+        // with no partial sums, a harmless read of x instead (never added)
+        const float *ssp = a.n_ss ? a.ss_part : (const float *)a.xq;
+        const uint32_t last = a.n_ss ? a.n_ss - 1 : 0;
+#pragma unroll
+        for (uint32_t j = 0; j < SC; j++) sv[j] = ssp[min((uint32_t)lane + 64 * j, last)];
     }
     uint32_t pos = 0;
     // QKV: the RoPE theta table (head_size/2 <= 64 values) read once into LDS
     __shared__ float theta_lds[64];
+    float th = 0.0f;
     if constexpr (MODE == GEMV_QKV) {
         pos = a.ctl->pos;
-        if (tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = a.rope_tab[tid];
+        th = a.rope_tab[min((uint32_t)tid & 63u, a.head_size / 2 - 1)];
     }
     // RESID: wave 0 reads the group's residual and next RMSNorm weight before
     // the weights, so the epilogue waits for no load of its own
@@ -906,6 +924,31 @@ __device__ void gemv_int_body(const GemvArgs &a) {
         }
     };
     preload(cur.g);
+    // keeps the small loads ahead of the weights (a scheduling fence only)
+    __builtin_amdgcn_sched_barrier(0);
+    load(A, cur);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        uint4 *dst = (uint4 *)lds;
+        // unconditional stores (a thread past the end rewrites the last
+        // chunk with its own value), so no load is moved behind a branch
+        dst[xi0] = xv0;
+        dst[xi1] = xv1;
+        dst[xi2] = xv2;
+        dst[xi3] = xv3;
+        for (uint32_t i = (uint32_t)tid + XC * NT; i < n16; i += NT) dst[i] = xsrc[i];
+    }
+    float rs = 1.0f;
+    if constexpr (NORM) {
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < SC; j++) t += (uint32_t)lane + 64 * j < a.n_ss ? sv[j] : 0.0f;
+        for (uint32_t i = (uint32_t)lane + 64 * SC; i < a.n_ss; i += 64) t += a.ss_part[i];
+        t = wave_sum(t);
+        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+    }
+    if constexpr (MODE == GEMV_QKV)
+        if (tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = th;
     __syncthreads();
     const XQ xq(lds, a.cols);
 

@@ -231,6 +231,7 @@ static ifr_status launch_gemv(ifr_ctx *c, const char *fmt, const char *mode, Gem
     if (!a.xq || (a.total_rows && a.cols % 16)) return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
     const IntGeom g = int_geom(c, fmt, mode, a, cap);
     a.ks = g.ks;
+    a.nwaves = g.waves;
     if (grid_out) *grid_out = g.grid;
     return c->launch(name, dim3(g.grid), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
 }

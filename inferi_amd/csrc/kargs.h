@@ -76,7 +76,7 @@ struct GemvArgs {
     const StepCtl *ctl;  // QKV: position
     uint32_t kv_dim, head_size;
     int32_t kv_f16;      // QKV: cache element type
-    uint32_t pad1;
+    uint32_t nwaves;     // integer path: waves per workgroup (blockDim.x / 64)
     uint64_t *part_keys; // HEAD: one argmax key per workgroup (may be null)
 };
 
