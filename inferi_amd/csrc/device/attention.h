@@ -15,9 +15,11 @@
 // head.  The per-thread states are combined through LDS; the chunk's partial
 // (m, l, o) goes to global memory.  A second, small kernel (attn_merge_body) combines the
 // partials of each query head: out = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
-// The kernel boundary orders the two: merging inside the first kernel would
-// need device-scope fences, which on this chip write back and invalidate the
-// whole L2 of the XCD for every workgroup.
+// The kernel boundary orders the two.  (Merging in the last split workgroup
+// of each KV head instead, with an arrival counter, measured slower: with
+// device-scope release fences every workgroup writes back its XCD's L2, and
+// even with write-through partial stores one workgroup per KV head reading
+// all splits' partials takes longer than the second launch.)
 #pragma once
 #include "gemv.h"
 
@@ -28,21 +30,39 @@ constexpr int ATTN_CMAX = 256; // longest chunk a workgroup accepts
 constexpr int ATTN_MERGE_MAX = 256;  // most splits one KV head may have
 constexpr int ATTN_BATCH = 4;  // positions per thread whose K and V are loaded together
 
+// Eight consecutive cache elements of one row, kept raw until used (f16:
+// u; f32: u and w), so a batch's loads are issued back to back and the
+// conversions wait for the data only where the scores need it.
 template <bool F16>
-IFR_DEV void load_kv8(const void *cache, size_t off, float *v) {
+struct KV8 {
+    uint4 u, w;
+};
+template <bool F16>
+IFR_DEV void kv8_load(const void *cache, size_t off, KV8<F16> &r) {
     if constexpr (F16) {
-        const uint4 u = *(const uint4 *)((const uint16_t *)cache + off);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            v[2 * i] = f16_to_f32(w[i] & 0xFFFFu);
-            v[2 * i + 1] = f16_to_f32(w[i] >> 16);
-        }
+        r.u = *(const uint4 *)((const uint16_t *)cache + off);
     } else {
-        const float4 a = *(const float4 *)((const float *)cache + off);
-        const float4 b = *(const float4 *)((const float *)cache + off + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        r.u = *(const uint4 *)((const float *)cache + off);
+        r.w = *(const uint4 *)((const float *)cache + off + 4);
+    }
+}
+template <bool F16>
+IFR_DEV void kv8_zero(KV8<F16> &r) {
+    r.u = make_uint4(0u, 0u, 0u, 0u);
+    r.w = r.u;
+}
+// element e (0..7) as f32, read where it is multiplied (an f16 element
+// widened inside the FMA, which the compiler folds into a mixed-precision
+// FMA, so no converted copy of the batch is kept)
+template <bool F16>
+IFR_DEV float kv8_at(const KV8<F16> &r, int e) {
+    const uint32_t w = e < 2 ? r.u.x : e < 4 ? r.u.y : e < 6 ? r.u.z : r.u.w;
+    if constexpr (F16) {
+        return f16_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+    } else {
+        const uint32_t w2 = e == 0 ? r.u.x : e == 1 ? r.u.y : e == 2 ? r.u.z : e == 3 ? r.u.w
+                          : e == 4 ? r.w.x : e == 5 ? r.w.y : e == 6 ? r.w.z : r.w.w;
+        return __uint_as_float(w2);
     }
 }
 
@@ -82,6 +102,14 @@ __device__ void attn_body(const AttnArgs &a) {
     __shared__ float mg[NPG][G], lg[NPG][G];
     __shared__ float wg[NPG][G], Mh[G];
 
+    // arguments in one batch of scalar loads (the compiler would otherwise
+    // fetch them in dependent round trips next to their first uses); an
+    // empty asm that emits nothing
+    asm volatile("" ::"s"(a.q), "s"(a.k_cache), "s"(a.v_cache), "s"(a.part_o), "s"(a.part_ml), "s"(a.pos),
+                 "s"(a.kv_dim), "s"(a.n_splits), "s"(a.seq_cap));
+    // the device position, as a vector load issued before every other load:
+    // loads complete in issue order, so waiting for it waits for nothing else
+    const uint32_t pos_dev = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = blockIdx.x, s = blockIdx.y, S = a.n_splits;
     constexpr uint32_t Qb = attn_quantum<HS>();
@@ -106,19 +134,20 @@ __device__ void attn_body(const AttnArgs &a) {
     // arrives: the first batch's K and V loads go out together with the
     // position load (rows clamped into the cache, masked below).
     const bool fixed = S * Qb >= a.seq_cap;
-    float kr[ATTN_BATCH][8], vr[ATTN_BATCH][8];
+    KV8<F16> kr[ATTN_BATCH], vr[ATTN_BATCH];
     auto load_batch = [&](uint32_t t0, uint32_t base, uint32_t n) {
 #pragma unroll
         for (int u = 0; u < ATTN_BATCH; u++) {
             const uint32_t tt = base + pg + PPP * u;
             const uint32_t row = n ? t0 + (tt < n ? tt : 0) : min(t0 + tt, a.seq_cap - 1);
             const size_t off = (size_t)row * a.kv_dim + head_off;
-            load_kv8<F16>(a.k_cache, off, kr[u]);
-            load_kv8<F16>(a.v_cache, off, vr[u]);
+            kv8_load<F16>(a.k_cache, off, kr[u]);
+            kv8_load<F16>(a.v_cache, off, vr[u]);
         }
     };
     if (fixed) load_batch(s * Qb, 0, 0);
-    const uint32_t T = min(*a.pos + 1, a.seq_cap);
+    __builtin_amdgcn_sched_barrier(0); // the batch's loads stay together
+    const uint32_t T = min(__builtin_amdgcn_readfirstlane(pos_dev) + 1, a.seq_cap);
     const uint32_t C = fixed ? Qb : attn_chunk<HS>(T, S);
     const uint32_t t0 = s * C;
     if (t0 >= T) {
@@ -142,12 +171,12 @@ __device__ void attn_body(const AttnArgs &a) {
 
     for (uint32_t base = 0; base < n; base += PPP * U) {
         if (!fixed || base) load_batch(t0, base, n);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; u++)
             if (base + pg + PPP * u >= n) {
                 // a masked row (possibly never written): its values must not reach the sums
-#pragma unroll
-                for (int e = 0; e < 8; e++) vr[u][e] = 0.0f;
+                kv8_zero<F16>(vr[u]);
             }
 #pragma unroll
         for (int j = 0; j < G; j++) {
@@ -157,7 +186,7 @@ __device__ void attn_body(const AttnArgs &a) {
             for (int u = 0; u < U; u++) {
                 float d = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 8; e++) d = fmaf(q[j][e], kr[u][e], d);
+                for (int e = 0; e < 8; e++) d = fmaf(q[j][e], kv8_at<F16>(kr[u], e), d);
                 d = group_sum<TPP>(d);
                 sc[u] = (base + pg + PPP * u < n) ? d : -INFINITY;
                 mb = fmaxf(mb, sc[u]);
@@ -173,7 +202,7 @@ __device__ void attn_body(const AttnArgs &a) {
                 const float p = exp2f(sc[u] - mn); // 0 for a masked position
                 lsum += p;
 #pragma unroll
-                for (int e = 0; e < 8; e++) ov[e] = fmaf(p, vr[u][e], ov[e]);
+                for (int e = 0; e < 8; e++) ov[e] = fmaf(p, kv8_at<F16>(vr[u], e), ov[e]);
             }
             m[j] = mn;
             l[j] = lsum;
