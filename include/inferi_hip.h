@@ -42,10 +42,15 @@ typedef int32_t ifr_status;
 /* GGUF tensor type ids (crates/inferi/src/gguf.rs:74-104). */
 #define IFR_F32 0
 #define IFR_F16 1
+#define IFR_Q4_0 2
+#define IFR_Q4_1 3
+#define IFR_Q5_0 6
+#define IFR_Q5_1 7
 #define IFR_Q8_0 8
 #define IFR_Q4_K 12
 #define IFR_Q5_K 13
 #define IFR_Q6_K 14
+#define IFR_Q8_K 15
 
 /* RoPEVariant (crates/inferi/src/ops/rope.rs:7-13). */
 #define IFR_ROPE_ORIGINAL 0
@@ -112,8 +117,9 @@ IFR_API ifr_status ifr_event_elapsed(ifr_ctx *ctx, int32_t start_slot, int32_t e
 /* -------------------------------------------------------------------- ops */
 
 /* out[0..n_elems) = dequantize(blocks), bit-exact with the reference's
- * Block*::dequantize (crates/inferi/src/quantization.rs:47-55, 224-257,
- * 287-330, 358-392) and decode_f16 (:405-422).  dtype: any IFR_* above;
+ * Block*::dequantize (crates/inferi/src/quantization.rs:47-55, 66-82,
+ * 94-112, 123-143, 155-177, 204-212, 224-257, 287-330, 358-392) and
+ * decode_f16 (:405-422).  dtype: any IFR_* above;
  * n_elems a multiple of the block size. */
 IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int32_t dtype, uint64_t n_elems);
 
@@ -126,8 +132,9 @@ IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int
  * the "gemv_exact" option is set.
  * Requirements: cols % QK == 0; cols <= 18432 (integer path; 16320 with
  * "gemv_exact"), as x is staged in one workgroup's LDS; W 16-byte aligned
- * for Q4_K and Q5_K, 4-byte aligned for Q6_K and Q8_0 (GGUF data is
- * 32-aligned). */
+ * for Q4_K and Q5_K, 4-byte aligned for the other formats (GGUF data is
+ * 32-aligned).  dtype Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K or
+ * Q8_K (the reference's GEMV shaders, crates/inferi-shaders/src/gemv_quant_*.rs). */
 IFR_API ifr_status ifr_matmul_quant(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
                                     uint32_t cols, const float *v);
 
@@ -217,7 +224,7 @@ IFR_API ifr_status ifr_gemm_quant(ifr_ctx *ctx, float *y, const void *w, int32_t
 
 /* GGUF blocks from f32 values on the device: the deterministic min/max
  * quantizer used for the synthetic models (the reference only dequantizes;
- * crates/inferi/src/quantization.rs:1-426).  dtype Q8_0/Q4_K/Q5_K/Q6_K/F16/F32. */
+ * crates/inferi/src/quantization.rs:1-426).  dtype any IFR_* type above. */
 IFR_API ifr_status ifr_quantize(ifr_ctx *ctx, void *out_blocks, const float *x, int32_t dtype, uint64_t n_elems);
 
 /* Synthetic weights: out[i] = mean + std * z_i, z_i ~ N(0,1) from a

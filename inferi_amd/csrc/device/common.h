@@ -112,7 +112,17 @@ IFR_DEV uint4 ld16_a2(const uint8_t *p) {
     return r;
 }
 
+// 16 bytes at a 4-byte aligned address.
+IFR_DEV uint4 ld16_a4(const uint8_t *p) {
+    u32x4_a4 v = *(const u32x4_a4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 IFR_DEV uint32_t ld_u16(const uint8_t *p) { return *(const uint16_t *)p; }
+
+// Bit 4 of byte k set to bit k of b (k = 0..3): the fifth bits of four
+// 5-bit codes moved next to their low nibbles.
+IFR_DEV uint32_t spread4_b4(uint32_t b) { return ((b * 0x00204081u) & 0x01010101u) << 4; }
 
 // Byte k (0..11) of the 12-byte K-quant scale field held in three words.
 IFR_DEV uint32_t sbyte(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t k) {

@@ -2,6 +2,7 @@
 // deterministic block quantizer.
 //
 // Dequantization follows crates/inferi/src/quantization.rs (Q8_0 :47-55,
+// Q4_0 :66-82, Q4_1 :94-112, Q5_0 :123-143, Q5_1 :155-177, Q8_K :204-212,
 // Q6_K :224-257, Q5_K :287-330, Q4_K :358-392, get_scale_min_k4 :394-402,
 // decode_f16 :405-422).  Rust evaluates `d1 * q - m1` as three separately
 // rounded f32 operations and never contracts them into an FMA, so
@@ -72,14 +73,70 @@ IFR_DEV float deq_q8_0(const uint8_t *blk, uint32_t e) {
     return (float)(int8_t)rd8(blk + 2 + e) * d;
 }
 
-IFR_DEV int fmt_qk(int fmt) { return fmt == Q8_0 ? 32 : (fmt == F32 || fmt == F16) ? 1 : 256; }
+// Q4_0: d@0 qs[16]@2; byte j holds element j (low nibble) and j+16 (high);
+// y = (q - 8) * d.
+IFR_DEV float deq_q4_0(const uint8_t *blk, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t b = rd8(blk + 2 + (e & 15u));
+    const int q = (int)((e < 16) ? (b & 15u) : (b >> 4)) - 8;
+    return (float)q * f16_to_f32(ld_u16(blk));
+}
+
+// Q4_1: d@0 m@2 qs[16]@4; y = q * d + m (two roundings).
+IFR_DEV float deq_q4_1(const uint8_t *blk, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t b = rd8(blk + 4 + (e & 15u));
+    const uint32_t q = (e < 16) ? (b & 15u) : (b >> 4);
+    return (float)q * f16_to_f32(ld_u16(blk)) + f16_to_f32(ld_u16(blk + 2));
+}
+
+// Fifth bit of element e of a Q5_0/Q5_1 block: bit e of the little-endian
+// word qh (element j and j+16 of byte j read bits j and j+16).
+IFR_DEV uint32_t q5_high(const uint8_t *qh, uint32_t e) { return (rd8(qh + (e >> 3)) >> (e & 7u)) & 1u; }
+
+// Q5_0: d@0 qh[4]@2 qs[16]@6; y = (q - 16) * d.
+IFR_DEV float deq_q5_0(const uint8_t *blk, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t b = rd8(blk + 6 + (e & 15u));
+    const uint32_t lo = (e < 16) ? (b & 15u) : (b >> 4);
+    const int q = (int)(lo | (q5_high(blk + 2, e) << 4)) - 16;
+    return (float)q * f16_to_f32(ld_u16(blk));
+}
+
+// Q5_1: d@0 m@2 qh[4]@4 qs[16]@8; y = q * d + m.
+IFR_DEV float deq_q5_1(const uint8_t *blk, uint32_t e) {
+#pragma clang fp contract(off)
+    const uint32_t b = rd8(blk + 8 + (e & 15u));
+    const uint32_t lo = (e < 16) ? (b & 15u) : (b >> 4);
+    const uint32_t q = lo | (q5_high(blk + 4, e) << 4);
+    return (float)q * f16_to_f32(ld_u16(blk)) + f16_to_f32(ld_u16(blk + 2));
+}
+
+// Q8_K: d:f32@0 qs:i8[256]@4 bsums:i16[16]@260; y = d * q.
+IFR_DEV float deq_q8_k(const uint8_t *blk, uint32_t e) {
+#pragma clang fp contract(off)
+    return *(const float *)blk * (float)(int8_t)rd8(blk + 4 + e);
+}
+
+IFR_DEV int fmt_qk(int fmt) {
+    switch (fmt) {
+    case F32: case F16: return 1;
+    case Q4_0: case Q4_1: case Q5_0: case Q5_1: case Q8_0: return 32;
+    default: return 256;
+    }
+}
 IFR_DEV int fmt_bytes(int fmt) {
     switch (fmt) {
     case F32: return 4;
     case F16: return 2;
+    case Q4_0: return 18;
+    case Q4_1: return 20;
+    case Q5_0: return 22;
+    case Q5_1: return 24;
     case Q8_0: return 34;
     case Q4_K: return 144;
     case Q5_K: return 176;
+    case Q8_K: return 292;
     default: return 210;
     }
 }
@@ -93,9 +150,14 @@ IFR_DEV float deq_elem(int fmt, const uint8_t *base, uint64_t idx) {
     switch (fmt) {
     case F32: return *(const float *)blk;
     case F16: return f16_to_f32(ld_u16(blk));
+    case Q4_0: return deq_q4_0(blk, e);
+    case Q4_1: return deq_q4_1(blk, e);
+    case Q5_0: return deq_q5_0(blk, e);
+    case Q5_1: return deq_q5_1(blk, e);
     case Q8_0: return deq_q8_0(blk, e);
     case Q4_K: return deq_q4k(blk, e);
     case Q5_K: return deq_q5k(blk, e);
+    case Q8_K: return deq_q8_k(blk, e);
     default: return deq_q6k(blk, e);
     }
 }
@@ -111,6 +173,13 @@ IFR_DEV float deq_elem(int fmt, const uint8_t *base, uint64_t idx) {
 //         q = clamp(rint((x + dmin*m) / (d*sc)), 0, L)
 //   Q6_K: per 16-element sub-block s = amax/31; d = f16(max s/127);
 //         sc = clamp(rint(s/d), 0, 127); q = clamp(rint(x/(d*sc)), -32, 31) + 32
+//   Q4_0/Q5_0 (H = 8/16): v = the element of largest magnitude (first one),
+//         d = f16(v / -H) (+0 when v = 0); q = clamp(rint(x * (1/d)), -H, H-1) + H
+//   Q4_1/Q5_1 (L = 15/31): lo = min x, hi = max x; d = f16((hi-lo)/L),
+//         m = f16(lo); q = clamp(rint((x - m) / d), 0, L)
+//   Q8_K: d = amax/127 (f32); q = clamp(rint(x * (1/d)), -127, 127),
+//         bsums = the sums of q over each 16 elements
+// (d and m above are the decoded f16 values wherever codes are formed.)
 // Comparisons are explicit (no fmin/fmax) so signed zeros resolve identically.
 
 IFR_DEV float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
@@ -131,6 +200,103 @@ IFR_DEV void quant_q8_0(const float *x, uint8_t *blk) {
     float id = d != 0.0f ? 1.0f / d : 0.0f;
     wr16(blk, f32_to_f16(d));
     for (int l = 0; l < 32; l++) blk[2 + l] = (uint8_t)(int8_t)qround(x[l] * id, -127.0f, 127.0f);
+}
+
+// Q4_0 / Q5_0: symmetric codes around H with the block's extreme at -H.
+IFR_DEV void quant_sym32(const float *x, int H, uint16_t *dh_out, int *q) {
+#pragma clang fp contract(off)
+    float amax = 0.0f, v = 0.0f;
+    for (int l = 0; l < 32; l++) {
+        const float a = fabsf(x[l]);
+        if (a > amax) {
+            amax = a;
+            v = x[l];
+        }
+    }
+    // an all-zero block gets d = +0 (stated, not left to how 0/-H is folded)
+    const uint16_t dh = f32_to_f16(v == 0.0f ? 0.0f : v / -(float)H);
+    const float d = f16_to_f32(dh);
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int l = 0; l < 32; l++) q[l] = qround(x[l] * id, -(float)H, (float)(H - 1)) + H;
+    *dh_out = dh;
+}
+
+// Q4_1 / Q5_1: affine codes from the block's min.
+IFR_DEV void quant_aff32(const float *x, int L, uint16_t *dh_out, uint16_t *mh_out, int *q) {
+#pragma clang fp contract(off)
+    float lo = x[0], hi = x[0];
+    for (int l = 1; l < 32; l++) {
+        lo = x[l] < lo ? x[l] : lo;
+        hi = x[l] > hi ? x[l] : hi;
+    }
+    const uint16_t dh = f32_to_f16((hi - lo) / (float)L), mh = f32_to_f16(lo);
+    const float d = f16_to_f32(dh), m = f16_to_f32(mh);
+    for (int l = 0; l < 32; l++) q[l] = d > 0.0f ? qround((x[l] - m) / d, 0.0f, (float)L) : 0;
+    *dh_out = dh;
+    *mh_out = mh;
+}
+
+IFR_DEV void pack_nibbles16(const int *q, uint8_t *qs) {
+    for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 15) | ((q[j + 16] & 15) << 4));
+}
+IFR_DEV void pack_high32(const int *q, uint8_t *qh) {
+    uint32_t h = 0;
+    for (int j = 0; j < 32; j++) h |= (uint32_t)((q[j] >> 4) & 1) << j;
+    for (int b = 0; b < 4; b++) qh[b] = (uint8_t)(h >> (8 * b));
+}
+
+IFR_DEV void quant_q4_0(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh;
+    quant_sym32(x, 8, &dh, q);
+    wr16(blk, dh);
+    pack_nibbles16(q, blk + 2);
+}
+IFR_DEV void quant_q5_0(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh;
+    quant_sym32(x, 16, &dh, q);
+    wr16(blk, dh);
+    pack_high32(q, blk + 2);
+    pack_nibbles16(q, blk + 6);
+}
+IFR_DEV void quant_q4_1(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh, mh;
+    quant_aff32(x, 15, &dh, &mh, q);
+    wr16(blk, dh);
+    wr16(blk + 2, mh);
+    pack_nibbles16(q, blk + 4);
+}
+IFR_DEV void quant_q5_1(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh, mh;
+    quant_aff32(x, 31, &dh, &mh, q);
+    wr16(blk, dh);
+    wr16(blk + 2, mh);
+    pack_high32(q, blk + 4);
+    pack_nibbles16(q, blk + 8);
+}
+IFR_DEV void quant_q8_k(const float *x, uint8_t *blk) {
+#pragma clang fp contract(off)
+    float amax = 0.0f;
+    for (int l = 0; l < 256; l++) {
+        const float a = fabsf(x[l]);
+        amax = a > amax ? a : amax;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const uint32_t db = __float_as_uint(d);
+    for (int b = 0; b < 4; b++) blk[b] = (uint8_t)(db >> (8 * b));
+    for (int j = 0; j < 16; j++) {
+        int sum = 0;
+        for (int l = 0; l < 16; l++) {
+            const int v = qround(x[16 * j + l] * id, -127.0f, 127.0f);
+            blk[4 + 16 * j + l] = (uint8_t)(int8_t)v;
+            sum += v;
+        }
+        wr16(blk + 260 + 2 * j, (uint16_t)(int16_t)sum);
+    }
 }
 
 IFR_DEV void pack_scales_k4(const uint8_t *sc, const uint8_t *mn, uint8_t *q) {

@@ -200,9 +200,14 @@ __device__ void quantize_body(const QuantArgs &a) {
     switch (a.fmt) {
     case F32: *(float *)out = x[0]; break;
     case F16: wr16(out, f32_to_f16(x[0])); break;
+    case Q4_0: quant_q4_0(x, out); break;
+    case Q4_1: quant_q4_1(x, out); break;
+    case Q5_0: quant_q5_0(x, out); break;
+    case Q5_1: quant_q5_1(x, out); break;
     case Q8_0: quant_q8_0(x, out); break;
     case Q4_K: quant_q4_k(x, out); break;
     case Q5_K: quant_q5_k(x, out); break;
+    case Q8_K: quant_q8_k(x, out); break;
     default: quant_q6_k(x, out); break;
     }
 }

@@ -93,6 +93,59 @@ template <>
 struct QFmt<Q6_K> { static constexpr int QK = 256, BB = 210, LPB = 8; };
 template <>
 struct QFmt<Q8_0> { static constexpr int QK = 32, BB = 34, LPB = 2; };
+template <>
+struct QFmt<Q4_0> { static constexpr int QK = 32, BB = 18, LPB = 2; };
+template <>
+struct QFmt<Q4_1> { static constexpr int QK = 32, BB = 20, LPB = 2; };
+template <>
+struct QFmt<Q5_0> { static constexpr int QK = 32, BB = 22, LPB = 2; };
+template <>
+struct QFmt<Q5_1> { static constexpr int QK = 32, BB = 24, LPB = 2; };
+template <>
+struct QFmt<Q8_K> { static constexpr int QK = 256, BB = 292, LPB = 16; };
+
+// Codes of lane half c (elements 16c..16c+15) of a 32-element block whose
+// qs byte j holds element j (low nibble) and j+16 (high), with the fifth bits
+// (Q5_0/Q5_1: bit e of the word qh) when `qh` is given.
+IFR_DEV uint4 codes32(uint4 qs, uint32_t c, bool five, uint32_t qh) {
+    const uint32_t M = 0x0F0F0F0Fu, sh = 4u * c;
+    uint4 r = make_uint4((qs.x >> sh) & M, (qs.y >> sh) & M, (qs.z >> sh) & M, (qs.w >> sh) & M);
+    if (five) {
+        const uint32_t h = qh >> (16u * c);
+        r.x |= spread4_b4(h & 15u);
+        r.y |= spread4_b4((h >> 4) & 15u);
+        r.z |= spread4_b4((h >> 8) & 15u);
+        r.w |= spread4_b4((h >> 12) & 15u);
+    }
+    return r;
+}
+
+// Header and codes of the 32-element formats (Q4_0 :66-82, Q4_1 :94-112,
+// Q5_0 :123-143, Q5_1 :155-177 of crates/inferi/src/quantization.rs):
+// d (and m) as f32, the 16 qs bytes and the 32 fifth bits.  Field offsets:
+// Q4_0 d@0 qs@2; Q4_1 d@0 m@2 qs@4; Q5_0 d@0 qh@2 qs@6; Q5_1 d@0 m@2 qh@4 qs@8.
+template <int FMT>
+struct Blk32 {
+    static constexpr bool FIVE = FMT == Q5_0 || FMT == Q5_1;  // a fifth bit per code
+    static constexpr bool AFF = FMT == Q4_1 || FMT == Q5_1;   // y = q d + m, else (q - H) d
+    static constexpr float H = FMT == Q4_0 ? 8.0f : 16.0f;    // the symmetric formats' offset
+    static constexpr int QS = FMT == Q4_0 ? 2 : FMT == Q4_1 ? 4 : FMT == Q5_0 ? 6 : 8;
+    uint4 qs;
+    uint32_t dm, qh; // dm: d | m << 16
+    IFR_DEV void load(const uint8_t *b) {
+        if constexpr (QS % 4 == 0) qs = ld16_a4(b + QS);
+        else qs = ld16_a2(b + QS);
+        dm = AFF ? (ld_u16(b) | ld_u16(b + 2) << 16) : ld_u16(b);
+        if constexpr (FMT == Q5_0) qh = ld_u16(b + 2) | ld_u16(b + 4) << 16;
+        else if constexpr (FMT == Q5_1) qh = *(const uint32_t *)(b + 4);
+        else qh = 0;
+    }
+    IFR_DEV float d() const { return f16_to_f32(dm & 0xFFFFu); }
+    IFR_DEV float m() const { return f16_to_f32(dm >> 16); }
+    IFR_DEV uint4 codes(uint32_t c) const { return codes32(qs, c, FIVE, qh); }
+    // sum over the lane's 16 elements of y * x, from dq = sum q x and sx = sum x
+    IFR_DEV float apply(float dq, float sx) const { return AFF ? d() * dq + m() * sx : d() * (dq - H * sx); }
+};
 
 // One lane's share of one block step for R rows: the raw bytes (load) and
 // their dot with x (compute), split so the next step's loads can be in
@@ -248,6 +301,62 @@ struct Chunk<Q8_0, R> {
     }
 };
 
+// 32-element formats, lane half c of block kb (elements 16c..16c+15).
+template <int FMT, int R>
+struct Chunk32 {
+    Blk32<FMT> b[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t) {
+#pragma unroll
+        for (int r = 0; r < R; r++) b[r].load(rowp[r] + (size_t)kb * QFmt<FMT>::BB);
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        float xv[16];
+        lds16(xs + kb * 32 + 16 * c, xv);
+        const float sx = sum16v(xv);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint4 q = b[r].codes(c);
+            acc[r] += b[r].apply(dot16u(q.x, q.y, q.z, q.w, xv), sx);
+        }
+    }
+};
+template <int R>
+struct Chunk<Q4_0, R> : Chunk32<Q4_0, R> {};
+template <int R>
+struct Chunk<Q4_1, R> : Chunk32<Q4_1, R> {};
+template <int R>
+struct Chunk<Q5_0, R> : Chunk32<Q5_0, R> {};
+template <int R>
+struct Chunk<Q5_1, R> : Chunk32<Q5_1, R> {};
+
+// Q8_K (quantization.rs:204-212): d:f32@0 qs:i8[256]@4; lane c of 16 reads
+// qs[16c, 16c+16).
+template <int R>
+struct Chunk<Q8_K, R> {
+    uint4 qv[R];
+    float dv[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 292;
+            dv[r] = *(const float *)b;
+            qv[r] = ld16_a4(b + 4 + 16 * c);
+        }
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        float xv[16];
+        lds16(xs + kb * 256 + 16 * c, xv);
+        const float sx = sum16v(xv);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint4 q = qv[r];
+            const uint32_t F = 0x80808080u;
+            const float dq = dot16u(q.x ^ F, q.y ^ F, q.z ^ F, q.w ^ F, xv);
+            acc[r] += dv[r] * (dq - 128.0f * sx);
+        }
+    }
+};
+
 // ------------------------------------------------------------------------
 // Integer path.  An activation vector of K values is kept as XQ (K % 16 == 0):
 //   XA, XB, XC int8[K] @0, @K, @2K;  XS f32[K/16] @3K;  XSUM f32[K/16] @3K+K/4.
@@ -345,6 +454,7 @@ struct ChunkI;
 template <int R>
 struct ChunkI<Q4_K, R> {
     static constexpr int LPB = 4;
+    static constexpr bool DIRECT = false;
     uint4 hv[R], q0[R], q1[R];
     IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t g) {
 #pragma unroll
@@ -385,6 +495,7 @@ struct ChunkI<Q4_K, R> {
 template <int R>
 struct ChunkI<Q5_K, R> {
     static constexpr int LPB = 4;
+    static constexpr bool DIRECT = false;
     uint4 hv[R], q0[R], q1[R], e0[R], e1[R];
     IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t g) {
 #pragma unroll
@@ -434,6 +545,7 @@ struct ChunkI<Q5_K, R> {
 template <int R>
 struct ChunkI<Q6_K, R> {
     static constexpr int LPB = 4;
+    static constexpr bool DIRECT = false;
     uint4 l0[R], l1[R], h0[R], h1[R];
     uint32_t sc_lo[R], sc_hi[R], dd[R];
     IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
@@ -492,6 +604,7 @@ struct ChunkI<Q6_K, R> {
 template <int R>
 struct ChunkI<Q8_0, R> {
     static constexpr int LPB = 2;
+    static constexpr bool DIRECT = true; // compute() does the whole step
     uint4 qv[R];
     uint32_t dd[R];
     IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
@@ -514,11 +627,81 @@ struct ChunkI<Q8_0, R> {
     }
 };
 
+// 32-element formats, 2 lanes per block: lane c owns elements 16c..16c+15,
+// exactly one activation group.  The codes (at most 31) times the x digits
+// form one exact int32 (gdot_u); the block affine map is applied in fp32:
+//   sum (q - H) x = s*sum q v - H*S,  sum (q d + m) x = d*(s*sum q v) + m*S
+// with s, S the group's scale and sum of x.
+template <int FMT, int R>
+struct ChunkI32 {
+    static constexpr int LPB = 2;
+    static constexpr bool DIRECT = true;
+    Blk32<FMT> b[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t) {
+#pragma unroll
+        for (int r = 0; r < R; r++) b[r].load(rowp[r] + (size_t)kb * QFmt<FMT>::BB);
+    }
+    IFR_DEV void compute(const XQ &x, uint32_t kb, uint32_t c, bool valid, float *acc) const {
+        const uint32_t e = kb * 32 + 16 * c;
+        const XG xg = xg_load(x, e);
+        const float s = x.xs[e / 16], S = x.xsum[e / 16];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float v = b[r].apply((float)gdot_u(b[r].codes(c), xg) * s, S);
+            acc[r] += valid ? v : 0.0f;
+        }
+    }
+};
+template <int R>
+struct ChunkI<Q4_0, R> : ChunkI32<Q4_0, R> {};
+template <int R>
+struct ChunkI<Q4_1, R> : ChunkI32<Q4_1, R> {};
+template <int R>
+struct ChunkI<Q5_0, R> : ChunkI32<Q5_0, R> {};
+template <int R>
+struct ChunkI<Q5_1, R> : ChunkI32<Q5_1, R> {};
+
+// Q8_K, 4 lanes per block: lane c owns elements 64c..64c+63 (four groups),
+// signed codes times the x digits as two exact int parts (gdot_s), times the
+// group scale, then d.
+template <int R>
+struct ChunkI<Q8_K, R> {
+    static constexpr int LPB = 4;
+    static constexpr bool DIRECT = true;
+    uint4 q[R][4];
+    float dv[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 292;
+            dv[r] = *(const float *)b;
+#pragma unroll
+            for (int k = 0; k < 4; k++) q[r][k] = ld16_a4(b + 4 + 64 * c + 16 * k);
+        }
+    }
+    IFR_DEV void compute(const XQ &x, uint32_t kb, uint32_t c, bool valid, float *acc) const {
+        const uint32_t e0 = kb * 256 + 64 * c;
+        const float4 s4 = *(const float4 *)__builtin_assume_aligned(x.xs + e0 / 16, 16);
+        const float s[4] = {s4.x, s4.y, s4.z, s4.w};
+        float t[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) t[r] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const XG xg = xg_load(x, e0 + 16 * k);
+#pragma unroll
+            for (int r = 0; r < R; r++) t[r] = fmaf(gdot_s(q[r][k], xg), s[k], t[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] += valid ? dv[r] * t[r] : 0.0f;
+    }
+};
+
 // One step of a lane for R rows (K-quants group by group), added to acc
 // when `valid` (a select, not a branch).
 template <int FMT, int R>
 IFR_DEV void chunk_step(const ChunkI<FMT, R> &w, const XQ &x, uint32_t kb, uint32_t c, bool valid, float *acc) {
-    if constexpr (FMT == Q8_0) {
+    if constexpr (ChunkI<FMT, R>::DIRECT) {
         w.compute(x, kb, c, valid, acc);
     } else {
         const XS4 sc = ChunkI<FMT, R>::xscales(x, kb, c);

@@ -49,8 +49,8 @@ constexpr uint32_t PF_CHUNK = 512;        // prompt tokens per prefill pass
 int qk_of(int32_t dt) {
     switch (dt) {
     case IFR_F32: case IFR_F16: return 1;
-    case IFR_Q8_0: return 32;
-    case IFR_Q4_K: case IFR_Q5_K: case IFR_Q6_K: return 256;
+    case IFR_Q4_0: case IFR_Q4_1: case IFR_Q5_0: case IFR_Q5_1: case IFR_Q8_0: return 32;
+    case IFR_Q4_K: case IFR_Q5_K: case IFR_Q6_K: case IFR_Q8_K: return 256;
     default: return 0;
     }
 }
@@ -58,22 +58,35 @@ int bytes_of(int32_t dt) {
     switch (dt) {
     case IFR_F32: return 4;
     case IFR_F16: return 2;
+    case IFR_Q4_0: return 18;
+    case IFR_Q4_1: return 20;
+    case IFR_Q5_0: return 22;
+    case IFR_Q5_1: return 24;
     case IFR_Q8_0: return 34;
     case IFR_Q4_K: return 144;
     case IFR_Q5_K: return 176;
     case IFR_Q6_K: return 210;
+    case IFR_Q8_K: return 292;
     default: return 0;
     }
 }
 const char *gemv_fmt_name(int32_t dt) {
     switch (dt) {
+    case IFR_Q4_0: return "q4_0";
+    case IFR_Q4_1: return "q4_1";
+    case IFR_Q5_0: return "q5_0";
+    case IFR_Q5_1: return "q5_1";
     case IFR_Q8_0: return "q8_0";
     case IFR_Q4_K: return "q4_k";
     case IFR_Q5_K: return "q5_k";
     case IFR_Q6_K: return "q6_k";
+    case IFR_Q8_K: return "q8_k";
     default: return nullptr;
     }
 }
+// Blocks one 64-lane step of the integer GEMV covers: 32 for the 32-element
+// formats (2 lanes per block), 16 for the 256-element ones (4 lanes).
+uint32_t int_blocks_per_step(int32_t dt) { return qk_of(dt) == 32 ? 32u : 16u; }
 
 } // namespace
 
@@ -164,6 +177,7 @@ struct ifr_ctx {
 struct GemvPlan {
     const char *fmt;
     uint32_t nb, row_bytes;
+    uint32_t bpi; // blocks per integer-path step (int_blocks_per_step)
 };
 
 static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const void *w, GemvPlan &p) {
@@ -177,6 +191,7 @@ static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const voi
     if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "matmul_quant: weights not %u-byte aligned", (unsigned)need);
     p.nb = cols / (uint32_t)qk;
     p.row_bytes = p.nb * (uint32_t)bytes_of(dtype);
+    p.bpi = int_blocks_per_step(dtype);
     return IFR_OK;
 }
 
@@ -194,8 +209,7 @@ static GemvGeomT geom_of(const char *mode) {
 struct IntGeom {
     uint32_t ks, waves, grid;
 };
-static IntGeom int_geom(const ifr_ctx *c, const char *fmt, const char *mode, const GemvArgs &a, uint32_t cap) {
-    const uint32_t bpi = !strcmp(fmt, "q8_0") ? 32 : 16;
+static IntGeom int_geom(const ifr_ctx *c, uint32_t bpi, const char *mode, const GemvArgs &a, uint32_t cap) {
     const uint32_t steps = (a.nb + bpi - 1) / bpi;
     IntGeom g;
     g.ks = steps <= 1 ? 1 : steps <= 2 ? 2 : 4;
@@ -214,10 +228,10 @@ static IntGeom int_geom(const ifr_ctx *c, const char *fmt, const char *mode, con
     return g;
 }
 
-static ifr_status launch_gemv(ifr_ctx *c, const char *fmt, const char *mode, GemvArgs &a, uint32_t cap = 0,
+static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, GemvArgs &a, uint32_t cap = 0,
                               uint32_t *grid_out = nullptr) {
     const bool exact = c->gemv_exact != 0;
-    std::string name = std::string("gemv_") + fmt + "_" + mode + (exact ? "_f32" : "");
+    std::string name = std::string("gemv_") + p.fmt + "_" + mode + (exact ? "_f32" : "");
     if (exact) {
         const GemvGeomT ge = geom_of(mode);
         const uint32_t tr = (uint32_t)(ge.R * ge.W);
@@ -229,7 +243,7 @@ static ifr_status launch_gemv(ifr_ctx *c, const char *fmt, const char *mode, Gem
         return c->launch(name, dim3(g), dim3((uint32_t)ge.W * 64u), a.cols * 4, a);
     }
     if (!a.xq || (a.total_rows && a.cols % 16)) return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
-    const IntGeom g = int_geom(c, fmt, mode, a, cap);
+    const IntGeom g = int_geom(c, p.bpi, mode, a, cap);
     a.ks = g.ks;
     a.nwaves = g.waves;
     if (grid_out) *grid_out = g.grid;
@@ -263,7 +277,7 @@ static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtyp
         if ((st = launch_quant_act(c, v, nullptr, cols, xq, nullptr))) return st;
         a.xq = xq;
     }
-    return launch_gemv(c, p.fmt, "plain", a);
+    return launch_gemv(c, p, "plain", a);
 }
 
 // ------------------------------------------------------------- attention --
@@ -459,7 +473,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.kv_dim = kv_dim;
             a.head_size = s->head_size;
             a.kv_f16 = cfg.kv_dtype == IFR_F16;
-            if ((st = launch_gemv(c, p.fmt, "qkv", a))) return st;
+            if ((st = launch_gemv(c, p, "qkv", a))) return st;
         } else {
             EltArgs n{};
             n.a = s->xb;
@@ -531,7 +545,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.xq_out = s->xq_f;
             a.ss_out = s->ss_f;
             a.gamma_next = (const float *)Lw.ffn_norm.data;
-            if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
+            if ((st = launch_gemv(c, p, "resid", a))) return st;
         } else {
             if ((st = gemv_plain(c, s->xb2, Lw.attn_output.data, Lw.attn_output.dtype, hidden, hidden, s->att, s->xq_u)))
                 return st;
@@ -560,7 +574,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.eps = cfg.rms_eps;
             a.y = s->hb;
             a.xq_out = s->xq_h;
-            if ((st = launch_gemv(c, p.fmt, "gateup", a))) return st;
+            if ((st = launch_gemv(c, p, "gateup", a))) return st;
         } else {
             EltArgs n{};
             n.a = s->xb;
@@ -594,7 +608,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.xq_out = s->xq_a;
             a.ss_out = s->ss_a;
             a.gamma_next = next_norm;
-            if ((st = launch_gemv(c, p.fmt, "resid", a))) return st;
+            if ((st = launch_gemv(c, p, "resid", a))) return st;
             n_ss_a = n_ss_res;
         } else {
             if ((st = gemv_plain(c, s->xb2, Lw.ffn_down.data, Lw.ffn_down.dtype, hidden, ffn, s->hb, s->xq_u))) return st;
@@ -629,7 +643,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         a.eps = cfg.rms_eps;
         a.y = s->logits;
         a.part_keys = s->part_keys;
-        if ((st = launch_gemv(c, p.fmt, "head", a, MAX_PARTS, &n_parts))) return st;
+        if ((st = launch_gemv(c, p, "head", a, MAX_PARTS, &n_parts))) return st;
     } else {
         EltArgs n{};
         n.a = s->xb;
@@ -826,7 +840,8 @@ IFR_API ifr_status ifr_dequant(ifr_ctx *c, float *out, const void *blocks, int32
     if (n % (uint64_t)qk) return c->fail(IFR_EINVAL, "dequant: %llu elements not a multiple of %d", (unsigned long long)n, qk);
     if (!n) return IFR_OK;
     if (!out || !blocks) return c->fail(IFR_EINVAL, "dequant: null pointer");
-    if ((uintptr_t)blocks % (dtype == IFR_F32 ? 4 : 2)) return c->fail(IFR_EINVAL, "dequant: misaligned blocks");
+    // f32 fields (F32, Q8_K's d) need 4-byte alignment, f16 fields 2
+    if ((uintptr_t)blocks % ((dtype == IFR_F32 || dtype == IFR_Q8_K) ? 4 : 2)) return c->fail(IFR_EINVAL, "dequant: misaligned blocks");
     DequantArgs a{out, (const uint8_t *)blocks, n, dtype, 0};
     const uint64_t g = std::min<uint64_t>((n + 255) / 256, 65536);
     return c->launch("dequant_k", dim3((uint32_t)g), dim3(256), 0, a);
@@ -874,7 +889,7 @@ IFR_API ifr_status ifr_matmul_quant_xq(ifr_ctx *c, float *out, const void *w, in
     a.row_bytes = p.row_bytes;
     a.xq = (const uint8_t *)xq;
     a.y = out;
-    return launch_gemv(c, p.fmt, "plain", a);
+    return launch_gemv(c, p, "plain", a);
 }
 
 IFR_API ifr_status ifr_rms_norm(ifr_ctx *c, const ifr_rms_norm_config *cfg, float *out, const float *value,

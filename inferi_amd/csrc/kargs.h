@@ -7,7 +7,8 @@
 
 namespace ifr {
 
-enum Fmt : int32_t { F32 = 0, F16 = 1, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14 };
+// GGUF tensor type ids (ggml_type)
+enum Fmt : int32_t { F32 = 0, F16 = 1, Q4_0 = 2, Q4_1 = 3, Q5_0 = 6, Q5_1 = 7, Q8_0 = 8, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15 };
 
 // GEMV epilogue/prologue modes.
 enum GemvMode : int32_t {

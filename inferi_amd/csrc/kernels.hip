@@ -38,6 +38,11 @@ GEMV_ALL_MODES(q4_k, Q4_K)
 GEMV_ALL_MODES(q5_k, Q5_K)
 GEMV_ALL_MODES(q6_k, Q6_K)
 GEMV_ALL_MODES(q8_0, Q8_0)
+GEMV_ALL_MODES(q4_0, Q4_0)
+GEMV_ALL_MODES(q4_1, Q4_1)
+GEMV_ALL_MODES(q5_0, Q5_0)
+GEMV_ALL_MODES(q5_1, Q5_1)
+GEMV_ALL_MODES(q8_k, Q8_K)
 
 #define ATTN_KERNEL(HS, G)                                                                          \
     extern "C" __global__ void __launch_bounds__(256) attn_f16_h##HS##_g##G(AttnArgs a) {           \

@@ -20,8 +20,8 @@
 int ifo_block_elems(int dtype) {
     switch (dtype) {
     case IFO_F32: case IFO_F16: return 1;
-    case IFO_Q8_0: return 32;
-    case IFO_Q4_K: case IFO_Q5_K: case IFO_Q6_K: return QK_K;
+    case IFO_Q4_0: case IFO_Q4_1: case IFO_Q5_0: case IFO_Q5_1: case IFO_Q8_0: return 32;
+    case IFO_Q4_K: case IFO_Q5_K: case IFO_Q6_K: case IFO_Q8_K: return QK_K;
     default: return 0;
     }
 }
@@ -30,7 +30,12 @@ int ifo_block_bytes(int dtype) {
     switch (dtype) {
     case IFO_F32: return 4;
     case IFO_F16: return 2;
+    case IFO_Q4_0: return 18;   /* quantization.rs:60-63 */
+    case IFO_Q4_1: return 20;   /* quantization.rs:87-91 */
+    case IFO_Q5_0: return 22;   /* quantization.rs:116-120 */
+    case IFO_Q5_1: return 24;   /* quantization.rs:147-152 */
     case IFO_Q8_0: return 34;   /* quantization.rs:42-45 */
+    case IFO_Q8_K: return 292;  /* quantization.rs:183-187 */
     case IFO_Q4_K: return 144;  /* quantization.rs:335-340 */
     case IFO_Q5_K: return 176;  /* quantization.rs:262-268 */
     case IFO_Q6_K: return 210;  /* quantization.rs:217-222 */
@@ -187,6 +192,65 @@ void ifo_dequant_q6_k(const uint8_t *blk, float *y) {
     }
 }
 
+/* quantization.rs:66-82.  Layout: d @0, qs[16] @2; byte j holds element j
+ * (low nibble) and j+16 (high); y = (q - 8) * d. */
+void ifo_dequant_q4_0(const uint8_t *blk, float *y) {
+    float d = ifo_decode_f16(rd16(blk));
+    for (int j = 0; j < 16; j++) {
+        int x0 = (blk[2 + j] & 0x0F) - 8, x1 = (blk[2 + j] >> 4) - 8;
+        y[j] = (float)x0 * d;
+        y[j + 16] = (float)x1 * d;
+    }
+}
+
+/* quantization.rs:94-112.  Layout: d @0, m @2, qs[16] @4; y = q * d + m. */
+void ifo_dequant_q4_1(const uint8_t *blk, float *y) {
+    float d = ifo_decode_f16(rd16(blk)), m = ifo_decode_f16(rd16(blk + 2));
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)(blk[4 + j] & 0x0F) * d + m;
+        y[j + 16] = (float)(blk[4 + j] >> 4) * d + m;
+    }
+}
+
+static inline uint32_t rd32(const uint8_t *p) {
+    return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+
+/* quantization.rs:123-143.  Layout: d @0, qh[4] @2 (read as a little-endian
+ * u32), qs[16] @6; y = (q - 16) * d. */
+void ifo_dequant_q5_0(const uint8_t *blk, float *y) {
+    float d = ifo_decode_f16(rd16(blk));
+    uint32_t qh = rd32(blk + 2);
+    for (uint32_t j = 0; j < 16; j++) {
+        uint32_t xh_0 = ((qh >> j) << 4) & 0x10, xh_1 = (qh >> (j + 12)) & 0x10;
+        int x0 = (int)(((uint32_t)blk[6 + j] & 0x0F) | xh_0) - 16;
+        int x1 = (int)(((uint32_t)blk[6 + j] >> 4) | xh_1) - 16;
+        y[j] = (float)x0 * d;
+        y[j + 16] = (float)x1 * d;
+    }
+}
+
+/* quantization.rs:155-177.  Layout: d @0, m @2, qh[4] @4, qs[16] @8;
+ * y = q * d + m. */
+void ifo_dequant_q5_1(const uint8_t *blk, float *y) {
+    float d = ifo_decode_f16(rd16(blk)), m = ifo_decode_f16(rd16(blk + 2));
+    uint32_t qh = rd32(blk + 4);
+    for (uint32_t j = 0; j < 16; j++) {
+        uint32_t xh_0 = ((qh >> j) << 4) & 0x10, xh_1 = (qh >> (j + 12)) & 0x10;
+        uint32_t x0 = ((uint32_t)blk[8 + j] & 0x0F) | xh_0, x1 = ((uint32_t)blk[8 + j] >> 4) | xh_1;
+        y[j] = (float)x0 * d + m;
+        y[j + 16] = (float)x1 * d + m;
+    }
+}
+
+/* quantization.rs:204-212.  Layout: d:f32 @0, qs:i8[256] @4, bsums:i16[16]
+ * @260 (not read by dequantize); y = d * q. */
+void ifo_dequant_q8_k(const uint8_t *blk, float *y) {
+    float d;
+    memcpy(&d, blk, 4);
+    for (int j = 0; j < QK_K; j++) y[j] = d * (float)(int8_t)blk[4 + j];
+}
+
 int ifo_dequant(int dtype, const void *data, size_t n_elems, float *y) {
     const uint8_t *p = (const uint8_t *)data;
     int qk = ifo_block_elems(dtype), bb = ifo_block_bytes(dtype);
@@ -196,10 +260,15 @@ int ifo_dequant(int dtype, const void *data, size_t n_elems, float *y) {
         switch (dtype) {
         case IFO_F32: memcpy(y, p, 4); break;
         case IFO_F16: y[0] = ifo_decode_f16(rd16(p)); break;
+        case IFO_Q4_0: ifo_dequant_q4_0(p, y); break;
+        case IFO_Q4_1: ifo_dequant_q4_1(p, y); break;
+        case IFO_Q5_0: ifo_dequant_q5_0(p, y); break;
+        case IFO_Q5_1: ifo_dequant_q5_1(p, y); break;
         case IFO_Q8_0: ifo_dequant_q8_0(p, y); break;
         case IFO_Q4_K: ifo_dequant_q4_k(p, y); break;
         case IFO_Q5_K: ifo_dequant_q5_k(p, y); break;
         case IFO_Q6_K: ifo_dequant_q6_k(p, y); break;
+        case IFO_Q8_K: ifo_dequant_q8_k(p, y); break;
         }
     }
     return 0;
@@ -226,6 +295,12 @@ int ifo_dequant(int dtype, const void *data, size_t n_elems, float *y) {
  *   Q6_K: per 16-element sub-block, s_j = amax_j/31; d = max s/127 as f16;
  *         sc_j = clamp(rint(s_j/d'), 0, 127);
  *         q = clamp(rint(x/(d'*sc_j)), -32, 31) + 32.
+ *   Q4_0/Q5_0 (H = 8/16): v = the first element of largest magnitude;
+ *         d = v/-H as f16 (+0 when v = 0); q = clamp(rint(x * (1/d')), -H, H-1) + H.
+ *   Q4_1/Q5_1 (L = 15/31): lo = min x, hi = max x; d = (hi-lo)/L and
+ *         m = lo as f16; q = clamp(rint((x - m') / d'), 0, L) (0 when d' = 0).
+ *   Q8_K: d = amax/127 kept in f32; q = clamp(rint(x * (1/d)), -127, 127);
+ *         bsums_j = the sum of q over elements 16j..16j+15.
  */
 static inline float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
 /* clamp in the float domain first, then round half to even: defined for every
@@ -243,6 +318,101 @@ static void quant_q8_0(const float *x, uint8_t *blk) {
     uint16_t dh = ifo_encode_f16(d);
     wr16(blk, dh);
     for (int l = 0; l < 32; l++) blk[2 + l] = (uint8_t)(int8_t)qround(x[l] * id, -127.0f, 127.0f);
+}
+
+static void quant_sym32(const float *x, int H, uint16_t *dh_out, int *q) {
+    float amax = 0.0f, v = 0.0f;
+    for (int l = 0; l < 32; l++) {
+        float a = fabsf(x[l]);
+        if (a > amax) {
+            amax = a;
+            v = x[l];
+        }
+    }
+    uint16_t dh = ifo_encode_f16(v == 0.0f ? 0.0f : v / -(float)H); /* +0 for an all-zero block */
+    float d = ifo_decode_f16(dh);
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int l = 0; l < 32; l++) q[l] = qround(x[l] * id, -(float)H, (float)(H - 1)) + H;
+    *dh_out = dh;
+}
+
+static void quant_aff32(const float *x, int L, uint16_t *dh_out, uint16_t *mh_out, int *q) {
+    float lo = x[0], hi = x[0];
+    for (int l = 1; l < 32; l++) {
+        lo = x[l] < lo ? x[l] : lo;
+        hi = x[l] > hi ? x[l] : hi;
+    }
+    uint16_t dh = ifo_encode_f16((hi - lo) / (float)L), mh = ifo_encode_f16(lo);
+    float d = ifo_decode_f16(dh), m = ifo_decode_f16(mh);
+    for (int l = 0; l < 32; l++) q[l] = d > 0.0f ? qround((x[l] - m) / d, 0.0f, (float)L) : 0;
+    *dh_out = dh;
+    *mh_out = mh;
+}
+
+static void pack_nibbles16(const int *q, uint8_t *qs) {
+    for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 15) | ((q[j + 16] & 15) << 4));
+}
+
+static void pack_high32(const int *q, uint8_t *qh) {
+    uint32_t h = 0;
+    for (int j = 0; j < 32; j++) h |= (uint32_t)((q[j] >> 4) & 1) << j;
+    for (int b = 0; b < 4; b++) qh[b] = (uint8_t)(h >> (8 * b));
+}
+
+static void quant_q4_0(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh;
+    quant_sym32(x, 8, &dh, q);
+    wr16(blk, dh);
+    pack_nibbles16(q, blk + 2);
+}
+
+static void quant_q5_0(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh;
+    quant_sym32(x, 16, &dh, q);
+    wr16(blk, dh);
+    pack_high32(q, blk + 2);
+    pack_nibbles16(q, blk + 6);
+}
+
+static void quant_q4_1(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh, mh;
+    quant_aff32(x, 15, &dh, &mh, q);
+    wr16(blk, dh);
+    wr16(blk + 2, mh);
+    pack_nibbles16(q, blk + 4);
+}
+
+static void quant_q5_1(const float *x, uint8_t *blk) {
+    int q[32];
+    uint16_t dh, mh;
+    quant_aff32(x, 31, &dh, &mh, q);
+    wr16(blk, dh);
+    wr16(blk + 2, mh);
+    pack_high32(q, blk + 4);
+    pack_nibbles16(q, blk + 8);
+}
+
+static void quant_q8_k(const float *x, uint8_t *blk) {
+    float amax = 0.0f;
+    for (int l = 0; l < QK_K; l++) {
+        float a = fabsf(x[l]);
+        amax = a > amax ? a : amax;
+    }
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    memcpy(blk, &d, 4);
+    for (int j = 0; j < 16; j++) {
+        int sum = 0;
+        for (int l = 0; l < 16; l++) {
+            int v = qround(x[16 * j + l] * id, -127.0f, 127.0f);
+            blk[4 + 16 * j + l] = (uint8_t)(int8_t)v;
+            sum += v;
+        }
+        wr16(blk + 260 + 2 * j, (uint16_t)(int16_t)sum);
+    }
 }
 
 /* Pack 8 six-bit scales and mins into the 12-byte K-quant layout read by
@@ -362,10 +532,15 @@ int ifo_quantize(int dtype, const float *x, size_t n_elems, void *out) {
         switch (dtype) {
         case IFO_F32: memcpy(p, x, 4); break;
         case IFO_F16: wr16(p, ifo_encode_f16(x[0])); break;
+        case IFO_Q4_0: quant_q4_0(x, p); break;
+        case IFO_Q4_1: quant_q4_1(x, p); break;
+        case IFO_Q5_0: quant_q5_0(x, p); break;
+        case IFO_Q5_1: quant_q5_1(x, p); break;
         case IFO_Q8_0: quant_q8_0(x, p); break;
         case IFO_Q4_K: quant_q4_k(x, p); break;
         case IFO_Q5_K: quant_q5_k(x, p); break;
         case IFO_Q6_K: quant_q6_k(x, p); break;
+        case IFO_Q8_K: quant_q8_k(x, p); break;
         }
     }
     return 0;

@@ -42,10 +42,15 @@ extern "C" {
 enum {
     IFO_F32 = 0,
     IFO_F16 = 1,
+    IFO_Q4_0 = 2,
+    IFO_Q4_1 = 3,
+    IFO_Q5_0 = 6,
+    IFO_Q5_1 = 7,
     IFO_Q8_0 = 8,
     IFO_Q4_K = 12,
     IFO_Q5_K = 13,
     IFO_Q6_K = 14,
+    IFO_Q8_K = 15,
 };
 
 /* Elements and bytes per block (quantization.rs:42-45, 217-222, 262-268, 335-340). */
@@ -68,6 +73,11 @@ void ifo_dequant_q8_0(const uint8_t *blk, float *y);
 void ifo_dequant_q4_k(const uint8_t *blk, float *y);
 void ifo_dequant_q5_k(const uint8_t *blk, float *y);
 void ifo_dequant_q6_k(const uint8_t *blk, float *y);
+void ifo_dequant_q4_0(const uint8_t *blk, float *y);
+void ifo_dequant_q4_1(const uint8_t *blk, float *y);
+void ifo_dequant_q5_0(const uint8_t *blk, float *y);
+void ifo_dequant_q5_1(const uint8_t *blk, float *y);
+void ifo_dequant_q8_k(const uint8_t *blk, float *y);
 /* n_elems must be a multiple of the block size; F32/F16 are accepted too. */
 int ifo_dequant(int dtype, const void *data, size_t n_elems, float *y);
 

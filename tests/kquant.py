@@ -1,8 +1,9 @@
 """Hand-built GGUF K-quant blocks for known-answer tests.
 
 The builders below write blocks field by field from the GGUF block layouts
-(crates/inferi/src/quantization.rs:42-45, 217-222, 262-268, 335-340 in the
-reference, i.e. ggml's block_q8_0 / block_q6_K / block_q5_K / block_q4_K), so
+(crates/inferi/src/quantization.rs:42-45, 60-63, 87-91, 116-120, 147-152,
+183-187, 217-222, 262-268, 335-340 in the reference, i.e. ggml's block_q8_0,
+q4_0, q4_1, q5_0, q5_1, q8_K, q6_K, q5_K and q4_K), so
 that a test can state the expected dequantized values in closed form.  They
 share no code with the oracle.
 """
@@ -80,6 +81,51 @@ def q8_0_block(d16: int, q) -> bytes:
     return d16.to_bytes(2, "little") + bytes(int(v) & 0xFF for v in q)
 
 
+def _nibbles16(u) -> bytes:
+    """Byte j holds code j (low nibble) and code j+16 (high)."""
+    return bytes((int(u[j]) & 15) | ((int(u[j + 16]) & 15) << 4) for j in range(16))
+
+
+def _high32(u) -> bytes:
+    """Bit j of the little-endian word is bit 4 of code j."""
+    h = 0
+    for j in range(32):
+        h |= ((int(u[j]) >> 4) & 1) << j
+    return h.to_bytes(4, "little")
+
+
+def q4_0_block(d16: int, q) -> bytes:
+    """q: 32 ints in -8..7 (stored +8); layout d@0 qs[16]@2 (ggml block_q4_0)."""
+    u = [int(v) + 8 for v in q]
+    return d16.to_bytes(2, "little") + _nibbles16(u)
+
+
+def q4_1_block(d16: int, m16: int, q) -> bytes:
+    """q: 32 ints in 0..15; layout d@0 m@2 qs[16]@4 (block_q4_1)."""
+    return d16.to_bytes(2, "little") + m16.to_bytes(2, "little") + _nibbles16(q)
+
+
+def q5_0_block(d16: int, q) -> bytes:
+    """q: 32 ints in -16..15 (stored +16); layout d@0 qh[4]@2 qs[16]@6 (block_q5_0)."""
+    u = [int(v) + 16 for v in q]
+    return d16.to_bytes(2, "little") + _high32(u) + _nibbles16(u)
+
+
+def q5_1_block(d16: int, m16: int, q) -> bytes:
+    """q: 32 ints in 0..31; layout d@0 m@2 qh[4]@4 qs[16]@8 (block_q5_1)."""
+    return d16.to_bytes(2, "little") + m16.to_bytes(2, "little") + _high32(q) + _nibbles16(q)
+
+
+def q8_k_block(d: float, q, bsums=None) -> bytes:
+    """q: 256 ints in -128..127; layout d:f32@0 qs[256]@4 bsums:i16[16]@260
+    (block_q8_K; bsums default to the sums of q over 16 elements)."""
+    q = [int(v) for v in q]
+    if bsums is None:
+        bsums = [sum(q[16 * j:16 * j + 16]) for j in range(16)]
+    return (np.array([d], np.float32).tobytes() + bytes(v & 0xFF for v in q)
+            + np.array(bsums, np.int16).astype("<i2").tobytes())
+
+
 def f16_value(code: int) -> float:
     return float(np.array([code], np.uint16).view(np.float16)[0])
 
@@ -97,7 +143,7 @@ def random_blocks(dtype: int, n_blocks: int, rng: np.random.Generator) -> np.nda
     """Raw random bits with valid (finite, often subnormal) f16 scales, the
     shape of the reference's rand_block_* test generators
     (gemv_quant.rs:367-430)."""
-    from oracle import BLOCK_BYTES, Q4_K, Q5_K, Q6_K, Q8_0
+    from oracle import BLOCK_BYTES, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, Q8_K
 
     bb = BLOCK_BYTES[dtype]
     raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
@@ -112,6 +158,12 @@ def random_blocks(dtype: int, n_blocks: int, rng: np.random.Generator) -> np.nda
         raw[:, 2:4] = scales(n_blocks)
     elif dtype == Q6_K:
         raw[:, 208:210] = scales(n_blocks)
-    elif dtype == Q8_0:
+    elif dtype in (Q8_0, Q4_0, Q5_0):
         raw[:, 0:2] = scales(n_blocks)
+    elif dtype in (Q4_1, Q5_1):
+        raw[:, 0:2] = scales(n_blocks)
+        raw[:, 2:4] = scales(n_blocks)
+    elif dtype == Q8_K:
+        # d: f32 uniform in [-1, 1] (gemv_quant.rs:381-387)
+        raw[:, 0:4] = (rng.random(n_blocks) * 2.0 - 1.0).astype(np.float32).view(np.uint8).reshape(n_blocks, 4)
     return raw.reshape(-1)

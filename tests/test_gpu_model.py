@@ -67,12 +67,14 @@ def run_steps(ctx, state, weights, prompt, n_total, mode):
 @pytest.mark.parametrize("exact", [False, True], ids=["int", "exact"])
 @pytest.mark.parametrize("mode", ["fused", "unfused", "graph"])
 @pytest.mark.parametrize("mat,head,kv", [("Q4_K", "Q6_K", "F16"), ("Q8_0", "Q8_0", "F32"), ("Q5_K", "Q4_K", "F16"),
-                                         ("Q6_K", "Q5_K", "F32")])
+                                         ("Q6_K", "Q5_K", "F32"), ("Q4_0", "Q8_K", "F16"), ("Q5_1", "Q4_1", "F32"),
+                                         ("Q5_0", "Q5_1", "F16")])
 def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv, exact):
     import inferi_amd as I
 
     ctx.set_option("gemv_exact", int(exact))
-    dt = {"Q4_K": I.Q4_K, "Q5_K": I.Q5_K, "Q6_K": I.Q6_K, "Q8_0": I.Q8_0, "F16": I.F16, "F32": I.F32}
+    dt = {"Q4_K": I.Q4_K, "Q5_K": I.Q5_K, "Q6_K": I.Q6_K, "Q8_0": I.Q8_0, "F16": I.F16, "F32": I.F32,
+          "Q4_0": I.Q4_0, "Q4_1": I.Q4_1, "Q5_0": I.Q5_0, "Q5_1": I.Q5_1, "Q8_K": I.Q8_K}
     cfg = tiny_cfg(kv_dtype=dt[kv])
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=11, mat_dtype=dt[mat], head_dtype=dt[head], embd_dtype=dt[mat],
                                   std=0.05)

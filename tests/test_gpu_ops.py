@@ -14,8 +14,9 @@ from tests import kquant as K
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K]
-FNAME = {O.Q8_0: "Q8_0", O.Q4_K: "Q4_K", O.Q5_K: "Q5_K", O.Q6_K: "Q6_K"}
+FMTS = [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q8_K]
+FNAME = {O.Q8_0: "Q8_0", O.Q4_K: "Q4_K", O.Q5_K: "Q5_K", O.Q6_K: "Q6_K", O.Q4_0: "Q4_0", O.Q4_1: "Q4_1",
+         O.Q5_0: "Q5_0", O.Q5_1: "Q5_1", O.Q8_K: "Q8_K"}
 TOL = 1e-3
 
 
@@ -36,7 +37,7 @@ def bits(a):
 @pytest.mark.parametrize("dtype", FMTS, ids=FNAME.get)
 def test_dequant_bit_exact_random_blocks(ctx, oracle_lib, dtype):
     rng = np.random.default_rng(1000 + dtype)
-    nblk = 4096 if dtype == O.Q8_0 else 512
+    nblk = 4096 if O.BLOCK_ELEMS[dtype] == 32 else 512
     blocks = K.random_blocks(dtype, nblk, rng)
     n = nblk * O.BLOCK_ELEMS[dtype]
     db, dy = ctx.upload(blocks), ctx.alloc(n * 4)
@@ -59,6 +60,17 @@ def test_dequant_bit_exact_known_answer_blocks(ctx, oracle_lib, dtype):
             blks.append(K.q5k_block(d16, 0x0003, rng.integers(0, 64, 8), rng.integers(0, 64, 8), rng.integers(0, 32, 256)))
         elif dtype == O.Q6_K:
             blks.append(K.q6k_block(d16, rng.integers(-128, 128, 16), rng.integers(-32, 32, 256)))
+        elif dtype == O.Q4_0:
+            blks.extend(K.q4_0_block(d16, rng.integers(-8, 8, 32)) for _ in range(8))
+        elif dtype == O.Q4_1:
+            blks.extend(K.q4_1_block(d16, 0x8001, rng.integers(0, 16, 32)) for _ in range(8))
+        elif dtype == O.Q5_0:
+            blks.extend(K.q5_0_block(d16, rng.integers(-16, 16, 32)) for _ in range(8))
+        elif dtype == O.Q5_1:
+            blks.extend(K.q5_1_block(d16, 0x3555, rng.integers(0, 32, 32)) for _ in range(8))
+        elif dtype == O.Q8_K:
+            d = float(np.array([d16], np.uint16).view(np.float16)[0])
+            blks.append(K.q8_k_block(d, rng.integers(-128, 128, 256)))
         else:
             blks.extend(K.q8_0_block(d16, rng.integers(-128, 128, 32)) for _ in range(8))
     blks.append(b"\xff" * O.BLOCK_BYTES[dtype])

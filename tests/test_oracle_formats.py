@@ -1,8 +1,8 @@
 """Pins the oracle's f16 codec, scale unpacking, dequantizers and quantizers.
 
 Reference behaviour: crates/inferi/src/quantization.rs (decode_f16 :405-422,
-get_scale_min_k4 :394-402, Block*::dequantize :47-55, :224-257, :287-330,
-:358-392).  Every check compares against something the oracle does not share
+get_scale_min_k4 :394-402, Block*::dequantize :47-55, :66-82, :94-112,
+:123-143, :155-177, :204-212, :224-257, :287-330, :358-392).  Every check compares against something the oracle does not share
 code with: numpy's IEEE binary16 codec, hand-built blocks with closed-form
 outputs (tests/kquant.py), one-hot blocks that fix the element order, or
 round-trip error bounds.
@@ -152,7 +152,81 @@ def test_dequant_q8_0_known_answer(oracle_lib):
     assert y[0] == -128 * 2.0**-24 and y[1] == 127 * 2.0**-24 and not y[2:].any()
 
 
-@pytest.mark.parametrize("dtype,tol", [(O.Q8_0, 0.012), (O.Q4_K, 0.13), (O.Q5_K, 0.065), (O.Q6_K, 0.045)])
+def test_dequant_q4_0_order_and_offset(oracle_lib):
+    """quantization.rs:66-82: byte j holds element j (low nibble) and j+16
+    (high); stored code 8 is zero."""
+    for e in range(32):
+        q = [0] * 32
+        q[e] = 5
+        y = O.dequant(O.Q4_0, K.q4_0_block(K.F16_ONE, q), 32)
+        hot = np.zeros(32, np.float32)
+        hot[e] = 5.0
+        assert np.array_equal(y, hot), e
+    q = list(range(-8, 8)) * 2
+    y = O.dequant(O.Q4_0, K.q4_0_block(K.F16_HALF, q), 32)
+    assert np.array_equal(y, np.array(q, np.float32) * 0.5)
+
+
+def test_dequant_q4_1_order_and_min(oracle_lib):
+    """quantization.rs:94-112: y = q * d + m, two roundings (no FMA)."""
+    for e in (0, 7, 15, 16, 31):
+        q = [0] * 32
+        q[e] = 7
+        y = O.dequant(O.Q4_1, K.q4_1_block(K.F16_HALF, K.F16_QUARTER, q), 32)
+        want = np.full(32, 0.25, np.float32)
+        want[e] = 3.75
+        assert np.array_equal(y, want), e
+    rng = np.random.default_rng(3)
+    q = rng.integers(0, 16, 32)
+    d16, m16 = 0x2E66, 0xB4CD  # about 0.1 and -0.3: the products round
+    y = O.dequant(O.Q4_1, K.q4_1_block(d16, m16, q), 32)
+    d, m = np.float32(K.f16_value(d16)), np.float32(K.f16_value(m16))
+    want = (q.astype(np.float32) * d).astype(np.float32) + m
+    assert np.array_equal(y, want.astype(np.float32))
+
+
+def test_dequant_q5_0_fifth_bit_placement(oracle_lib):
+    """quantization.rs:123-143: bit j of qh is the fifth bit of element j and
+    bit j+16 of element j+16 (xh_1 = (qh >> (j+12)) & 0x10); stored 16 is zero."""
+    for e in range(32):
+        q = [-16] * 32  # stored 0
+        q[e] = 0  # stored 16: only the fifth bit
+        y = O.dequant(O.Q5_0, K.q5_0_block(K.F16_ONE, q), 32)
+        want = np.full(32, -16.0, np.float32)
+        want[e] = 0.0
+        assert np.array_equal(y, want), e
+    q = list(range(-16, 16))
+    y = O.dequant(O.Q5_0, K.q5_0_block(K.F16_QUARTER, q), 32)
+    assert np.array_equal(y, np.array(q, np.float32) * 0.25)
+
+
+def test_dequant_q5_1_fifth_bit_and_min(oracle_lib):
+    """quantization.rs:155-177."""
+    for e in (0, 3, 15, 16, 17, 31):
+        q = [0] * 32
+        q[e] = 16
+        y = O.dequant(O.Q5_1, K.q5_1_block(K.F16_ONE, K.F16_HALF, q), 32)
+        want = np.full(32, 0.5, np.float32)
+        want[e] = 16.5
+        assert np.array_equal(y, want), e
+    q = np.arange(32)
+    y = O.dequant(O.Q5_1, K.q5_1_block(K.F16_TWO, 0xBC00, q), 32)  # d 2, m -1
+    assert np.array_equal(y, q.astype(np.float32) * 2 - 1)
+
+
+def test_dequant_q8_k_known_answer(oracle_lib):
+    """quantization.rs:204-212: y = d * q with d an f32; bsums are not read."""
+    rng = np.random.default_rng(4)
+    q = rng.integers(-128, 128, 256)
+    for d in (0.5, 0.1, -3.0e-5):
+        y = O.dequant(O.Q8_K, K.q8_k_block(d, q, bsums=rng.integers(-30000, 30000, 16)), 256)
+        want = np.float32(d) * q.astype(np.float32)
+        assert np.array_equal(y, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype,tol", [(O.Q8_0, 0.012), (O.Q4_K, 0.13), (O.Q5_K, 0.065), (O.Q6_K, 0.045),
+                                       (O.Q4_0, 0.13), (O.Q4_1, 0.1), (O.Q5_0, 0.065), (O.Q5_1, 0.05),
+                                       (O.Q8_K, 0.012)])
 def test_quantize_round_trip(oracle_lib, dtype, tol):
     rng = np.random.default_rng(100 + dtype)
     x = (rng.standard_normal(256 * 64) * 0.02).astype(np.float32)
@@ -162,14 +236,15 @@ def test_quantize_round_trip(oracle_lib, dtype, tol):
     rel = np.sqrt(np.mean((y - x) ** 2)) / np.sqrt(np.mean(x**2))
     assert rel < tol, rel
     # every element lands within one quantization step of its input
-    step = {O.Q8_0: 1 / 127, O.Q4_K: 1 / 15 * 2, O.Q5_K: 1 / 31 * 2, O.Q6_K: 1 / 31 * 2}[dtype]
+    step = {O.Q8_0: 1 / 127, O.Q4_K: 1 / 15 * 2, O.Q5_K: 1 / 31 * 2, O.Q6_K: 1 / 31 * 2, O.Q4_0: 1 / 8,
+            O.Q4_1: 2 / 15, O.Q5_0: 1 / 16, O.Q5_1: 2 / 31, O.Q8_K: 1 / 127}[dtype]
     qk = O.BLOCK_ELEMS[dtype]
     amax = np.abs(x).reshape(-1, qk).max(axis=1).repeat(qk)
     assert np.all(np.abs(y - x) <= step * amax * 1.05 + 1e-7)
 
 
 def test_quantize_zero_and_constant_blocks(oracle_lib):
-    for dtype in (O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K):
+    for dtype in (O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q8_K):
         z = np.zeros(256, np.float32)
         assert not O.dequant(dtype, O.quantize(dtype, z), 256).any()
     # a Q4_K sub-block of a constant negative value is represented exactly via the min
