@@ -215,10 +215,13 @@ IFR_API ifr_status ifr_sample(ifr_ctx *ctx, const float *logits, float *probs, u
  * the prompt one token at a time through GemvQuant,
  * crates/inferi/src/ops/gemv_quant.rs:183-340):
  * y[m][rows] (+)= x[m][cols] . dequant(W)[rows x cols]^T, x f16 (IEEE
- * binary16, row-major, 16-byte aligned), W Q4_K rows as a GGUF file stores
- * them, y f32 row-major with leading dimension `rows`.  The weights are
- * dequantized into f16 tiles and multiplied on the matrix cores
- * (v_mfma_f32_32x32x16_f16, f32 accumulation); accumulate != 0 adds to y. */
+ * binary16, row-major, 16-byte aligned), W rows of any quantized GGUF type
+ * (Q4_0 .. Q8_K) as a GGUF file stores them (16-byte aligned for Q4_K and
+ * Q5_K, 4 otherwise; cols a multiple of 64 and of the block size), y f32
+ * row-major with leading dimension `rows`.  The weights are dequantized with
+ * the reference's arithmetic into f16 tiles and multiplied on the matrix
+ * cores (v_mfma_f32_32x32x16_f16, f32 accumulation); accumulate != 0 adds
+ * to y. */
 IFR_API ifr_status ifr_gemm_quant(ifr_ctx *ctx, float *y, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
                                   const void *x_f16, uint32_t m, int32_t accumulate);
 
@@ -296,9 +299,9 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const 
  * the matrix cores (ifr_gemm_quant) and causal attention over the cache;
  * their KV-cache rows are written and the position advances by n_tokens.
  * No logits are formed: the next decode step, at the prompt's last token,
- * produces them.  Waits for queued work (it reads the position).  Requires
- * Q4_K attention and FFN matrices; both RoPE variants and QKV biases are
- * handled. */
+ * produces them.  Waits for queued work (it reads the position).  The
+ * attention and FFN matrices may be of any quantized GGUF type that
+ * ifr_gemm_quant takes; both RoPE variants and QKV biases are handled. */
 IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
                                       uint32_t n_tokens);
 /* Sampling at the end of each decode step, as sample_next_token does

@@ -1359,18 +1359,31 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
     g.K = w.cols;
     g.ldx = ldx;
     g.ldy = ldy;
-    g.row_bytes = (w.cols / 256) * 144;
+    g.row_bytes = (w.cols / (uint32_t)qk_of(w.dtype)) * (uint32_t)bytes_of(w.dtype);
     const dim3 grid((w.rows + PF_GEMM_TILE - 1) / PF_GEMM_TILE, (M + PF_GEMM_TILE - 1) / PF_GEMM_TILE);
-    return c->launch(accumulate ? "gemm_q4_k_f16_add" : "gemm_q4_k_f16_store", grid, dim3(256), 0, g);
+    return c->launch(std::string("gemm_") + gemv_fmt_name(w.dtype) + (accumulate ? "_f16_add" : "_f16_store"), grid,
+                     dim3(256), 0, g);
+}
+
+// A matrix the prefill GEMM takes: a quantized GGUF type, K a whole number
+// of its 64-element steps, rows aligned for the tile loads (16 bytes for
+// Q4_K/Q5_K, 4 for the others).
+static ifr_status check_pf_matrix(ifr_ctx *c, int32_t dtype, uint32_t cols, const void *w) {
+    if (!gemv_fmt_name(dtype)) return c->fail(IFR_EUNSUPPORTED, "prefill GEMM: dtype %d is not a quantized GGUF type", dtype);
+    if (cols % 64 || cols % (uint32_t)qk_of(dtype)) return c->fail(IFR_EUNSUPPORTED, "prefill GEMM: cols %u not a multiple of 64 and of the block", cols);
+    const uintptr_t need = (dtype == IFR_Q4_K || dtype == IFR_Q5_K) ? 16 : 4;
+    if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "prefill GEMM: weights not %u-byte aligned", (unsigned)need);
+    return IFR_OK;
 }
 
 IFR_API ifr_status ifr_gemm_quant(ifr_ctx *c, float *y, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
                                   const void *x_f16, uint32_t m, int32_t accumulate) {
     if (!c) return IFR_EINVAL;
     if (!y || !w || !x_f16) return c->fail(IFR_EINVAL, "gemm_quant: null pointer");
-    if (dtype != IFR_Q4_K) return c->fail(IFR_EUNSUPPORTED, "gemm_quant: dtype %d (Q4_K only)", dtype);
-    if (!rows || !m || !cols || cols % 256) return c->fail(IFR_EINVAL, "gemm_quant: rows, m > 0 and cols %% 256 == 0");
-    if ((uintptr_t)w % 16 || (uintptr_t)x_f16 % 16) return c->fail(IFR_EINVAL, "gemm_quant: w and x must be 16-byte aligned");
+    if (!rows || !m || !cols) return c->fail(IFR_EINVAL, "gemm_quant: rows, m and cols must be > 0");
+    ifr_status st = check_pf_matrix(c, dtype, cols, w);
+    if (st) return st;
+    if ((uintptr_t)x_f16 % 16) return c->fail(IFR_EINVAL, "gemm_quant: x must be 16-byte aligned");
     Tens t;
     t.dtype = dtype;
     t.data = (const uint8_t *)w;
@@ -1406,7 +1419,7 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     for (const LayerW &L : w->layers) {
         const Tens *mats[] = {&L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
         for (const Tens *t : mats)
-            if (t->dtype != IFR_Q4_K) return c->fail(IFR_EUNSUPPORTED, "prefill: matrices must be Q4_K (found dtype %d)", t->dtype);
+            if ((st = check_pf_matrix(c, t->dtype, t->cols, t->data))) return st;
     }
     if (!n) return IFR_OK;
     if ((st = pf_ensure_scratch(s))) return st;

@@ -217,7 +217,7 @@ struct KvStoreArgs {
 // halves), W Q4_K rows, Y f32.
 struct PfGemmArgs {
     const void *x;       // f16 [M][ldx]
-    const uint8_t *w;    // Q4_K rows
+    const uint8_t *w;    // rows of K/QK GGUF blocks
     float *y;            // f32 [M][ldy]
     uint32_t M, N, K, ldx, ldy, row_bytes;
 };

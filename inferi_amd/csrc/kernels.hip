@@ -82,8 +82,18 @@ extern "C" __global__ void __launch_bounds__(64) quantize_k(QuantArgs a) { quant
 extern "C" __global__ void __launch_bounds__(256) fill_normal_k(FillArgs a) { fill_normal_body(a); }
 
 // prompt (prefill) path
-extern "C" __global__ void __launch_bounds__(256) gemm_q4_k_f16_store(PfGemmArgs a) { gemm_q4k_f16_body<0>(a); }
-extern "C" __global__ void __launch_bounds__(256) gemm_q4_k_f16_add(PfGemmArgs a) { gemm_q4k_f16_body<1>(a); }
+#define GEMM_KERNELS(FMTNAME, FMT)                                                                          \
+    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_store(PfGemmArgs a) { gemm_f16_body<FMT, 0>(a); } \
+    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_add(PfGemmArgs a) { gemm_f16_body<FMT, 1>(a); }
+GEMM_KERNELS(q4_k, Q4_K)
+GEMM_KERNELS(q5_k, Q5_K)
+GEMM_KERNELS(q6_k, Q6_K)
+GEMM_KERNELS(q8_k, Q8_K)
+GEMM_KERNELS(q8_0, Q8_0)
+GEMM_KERNELS(q4_0, Q4_0)
+GEMM_KERNELS(q4_1, Q4_1)
+GEMM_KERNELS(q5_0, Q5_0)
+GEMM_KERNELS(q5_1, Q5_1)
 extern "C" __global__ void __launch_bounds__(256) pf_embed_k(PfArgs a) { pf_embed_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { pf_rmsnorm_f16_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }

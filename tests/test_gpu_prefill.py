@@ -1,8 +1,9 @@
 """GPU parity of the prompt (prefill) path.
 
-ifr_gemm_quant multiplies f16 activations by Q4_K weights dequantized to f16
-tiles on the matrix cores: it is checked against an f64 product of the same
-f16-rounded operands (only the f32 accumulation order may differ).
+ifr_gemm_quant multiplies f16 activations by weights of any quantized GGUF
+type dequantized to f16 tiles on the matrix cores: it is checked against an
+f64 product of the same f16-rounded operands (only the f32 accumulation
+order may differ).
 
 ifr_llama2_prefill runs a prompt through every layer in chunks; the state it
 leaves (KV-cache rows, position) must continue exactly like a state that
@@ -21,16 +22,40 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def synthetic_q4k(ctx, rows, cols, seed):
+def synthetic_q(ctx, rows, cols, seed, dtype):
     import inferi_amd as I
 
     n = rows * cols
     tmp = ctx.alloc(n * 4)
     ctx.fill_normal(tmp, n, seed, 0, 0.0, 0.02)
-    w = ctx.alloc(rows * I.row_bytes(I.Q4_K, cols))
-    ctx.quantize(w, tmp, I.Q4_K, n)
+    w = ctx.alloc(rows * I.row_bytes(dtype, cols))
+    ctx.quantize(w, tmp, dtype, n)
     tmp.free()
     return w
+
+
+def _gemm_case(ctx, dtype, rows, cols, m, w, rng):
+    """y = x . deq(W)^T against the f64 product of the same f16-rounded
+    operands (bound 2e-5 * sum |x w|), then the accumulating form."""
+    import inferi_amd as I
+
+    rb = I.row_bytes(dtype, cols)
+    deq = O.dequant(dtype, w.download(np.uint8, rows * rb), rows * cols).reshape(rows, cols)
+    wh = deq.astype(np.float16).astype(np.float64)
+    x = rng.standard_normal((m, cols)).astype(np.float16)
+    dx = ctx.upload(x)
+    y = ctx.alloc(m * rows * 4)
+    ctx.gemm_quant(y, w, dtype, rows, cols, dx, m)
+    got = y.download(np.float32, m * rows).reshape(m, rows).astype(np.float64)
+    xd = x.astype(np.float64)
+    ref = xd @ wh.T
+    bound = 2e-5 * (np.abs(xd) @ np.abs(wh).T) + 1e-30
+    assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) - bound):.3e}"
+    ctx.gemm_quant(y, w, dtype, rows, cols, dx, m, accumulate=True)
+    got2 = y.download(np.float32, m * rows).reshape(m, rows).astype(np.float64)
+    assert np.all(np.abs(got2 - 2 * ref) <= 2 * bound)
+    for b in (dx, y):
+        b.free()
 
 
 @pytest.mark.parametrize("rows,cols,m", [(128, 256, 128), (300, 512, 70), (1000, 1024, 257), (4096, 4096, 128),
@@ -39,24 +64,32 @@ def test_gemm_quant_matches_f64(ctx, oracle_lib, rows, cols, m):
     import inferi_amd as I
 
     rng = np.random.default_rng(rows * 7 + cols + m)
-    w = synthetic_q4k(ctx, rows, cols, seed=rows + m)
-    rb = I.row_bytes(I.Q4_K, cols)
-    deq = O.dequant(I.Q4_K, w.download(np.uint8, rows * rb), rows * cols).reshape(rows, cols)
-    wh = deq.astype(np.float16).astype(np.float64)
-    x = rng.standard_normal((m, cols)).astype(np.float16)
-    dx = ctx.upload(x)
-    y = ctx.alloc(m * rows * 4)
-    ctx.gemm_quant(y, w, I.Q4_K, rows, cols, dx, m)
-    got = y.download(np.float32, m * rows).reshape(m, rows).astype(np.float64)
-    xd = x.astype(np.float64)
-    ref = xd @ wh.T
-    bound = 2e-5 * (np.abs(xd) @ np.abs(wh).T) + 1e-30
-    assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) - bound):.3e}"
-    ctx.gemm_quant(y, w, I.Q4_K, rows, cols, dx, m, accumulate=True)
-    got2 = y.download(np.float32, m * rows).reshape(m, rows).astype(np.float64)
-    assert np.all(np.abs(got2 - 2 * ref) <= 2 * bound)
-    for b in (w, dx, y):
-        b.free()
+    w = synthetic_q(ctx, rows, cols, rows + m, I.Q4_K)
+    _gemm_case(ctx, I.Q4_K, rows, cols, m, w, rng)
+    w.free()
+
+
+FMTS = ["Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q8_K"]
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("rows,cols,m", [(300, 512, 70), (130, 2048, 129)])
+def test_gemm_quant_every_format(ctx, oracle_lib, fmt, rows, cols, m):
+    """Each GGUF type's tile loader: quantized synthetic weights and raw
+    random blocks with a quarter of the scales subnormal (the reference's
+    GEMV test generator, gemv_quant.rs:354-430)."""
+    import inferi_amd as I
+    from tests import kquant as K
+
+    dtype = getattr(I, fmt)
+    rng = np.random.default_rng(rows + cols + dtype)
+    w = synthetic_q(ctx, rows, cols, rows * 3 + dtype, dtype)
+    _gemm_case(ctx, dtype, rows, cols, m, w, rng)
+    w.free()
+    raw = K.random_blocks(dtype, rows * cols // O.BLOCK_ELEMS[dtype], rng)
+    w = ctx.upload(raw)
+    _gemm_case(ctx, dtype, rows, cols, m, w, rng)
+    w.free()
 
 
 def test_gemm_quant_rejects_bad_input(ctx):
@@ -64,9 +97,13 @@ def test_gemm_quant_rejects_bad_input(ctx):
 
     buf = ctx.alloc(1 << 16)
     with pytest.raises(I.HipError):
-        ctx.gemm_quant(buf, buf, I.Q6_K, 16, 256, buf, 4)  # Q4_K only
+        ctx.gemm_quant(buf, buf, I.F32, 16, 256, buf, 4)  # not a quantized type
     with pytest.raises(I.HipError):
         ctx.gemm_quant(buf, buf, I.Q4_K, 16, 100, buf, 4)  # cols % 256
+    with pytest.raises(I.HipError):
+        ctx.gemm_quant(buf, buf, I.Q8_0, 16, 96, buf, 4)  # cols % 64
+    with pytest.raises(I.HipError):
+        ctx.gemm_quant(buf, buf.at(4), I.Q4_K, 16, 256, buf, 4)  # K-quant rows 16-byte aligned
     buf.free()
 
 
@@ -159,23 +196,35 @@ def test_prefill_qwen2_style(ctx, oracle_lib):
         w.close()
 
 
+@pytest.mark.parametrize("mat,head", [("Q8_0", "Q8_0"), ("Q5_K", "Q6_K"), ("Q6_K", "Q4_K"), ("Q4_0", "Q8_K"),
+                                      ("Q5_1", "Q4_1"), ("Q8_K", "Q5_0")])
+def test_prefill_other_formats(ctx, oracle_lib, mat, head):
+    """Prefill with every layer matrix of another GGUF type."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=700, max_pos=128,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=47, std=0.05, mat_dtype=getattr(I, mat), head_dtype=getattr(I, head),
+                                  embd_dtype=getattr(I, mat))
+    try:
+        prompt = np.random.default_rng(6).integers(0, cfg.vocab, 100).tolist()
+        assert _prefill_vs_decode(ctx, cfg, w, prompt, 8) > 0
+    finally:
+        w.close()
+
+
 def test_prefill_rejects_unsupported(ctx):
     import inferi_amd as I
 
     cfg = I.Llama2Config(n_layers=1, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=300, max_pos=64,
                          rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
-    w = I.Llama2Weights.synthetic(ctx, cfg, seed=5, mat_dtype=I.Q8_0, head_dtype=I.Q8_0, embd_dtype=I.Q8_0)
     s = I.Llama2State(ctx, cfg)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=5)
     try:
         s.reset([1, 2, 3], 0)
         with pytest.raises(I.HipError):
-            I.Llama2.prefill(ctx, s, w, 2)  # Q8_0 matrices
-        w2 = I.Llama2Weights.synthetic(ctx, cfg, seed=5)
-        try:
-            with pytest.raises(I.HipError):
-                I.Llama2.prefill(ctx, s, w2, 5)  # only 3 prompt tokens
-        finally:
-            w2.close()
+            I.Llama2.prefill(ctx, s, w, 5)  # only 3 prompt tokens
     finally:
+        w.close()
         s.close()
         w.close()
