@@ -166,6 +166,7 @@ def run_decode(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
+    ctx.set_option("persistent", args.persistent)
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
@@ -390,6 +391,8 @@ def main() -> None:
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
+    ap.add_argument("--persistent", type=int, default=1,
+                    help="1: the GEMV stages between attentions in one persistent launch per layer")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU; the multi-GPU sharding of the decode path is designed "

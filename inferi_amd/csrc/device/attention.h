@@ -90,17 +90,33 @@ IFR_DEV uint32_t attn_chunk(uint32_t T, uint32_t S) {
 // Scores are kept in base-2 units: q is pre-scaled by log2(e)/sqrt(hs), so
 // e^(s - m) of the reference's softmax is 2^(s2 - m2) here, and the partial
 // maxima handed to the merge are in the same units.
-template <int HS, int G, bool F16>
-__device__ void attn_body(const AttnArgs &a) {
+// LDS of one attention item (one split of one KV head).
+template <int HS, int G>
+struct AttnLds {
+    static constexpr int NPG = ATTN_THREADS / 64 * (64 / (HS / 8)); // position groups
+    float og[NPG][G][HS]; // per position group: unnormalised o
+    float mg[NPG][G], lg[NPG][G];
+    float wg[NPG][G], Mh[G];
+};
+
+// One split s of KV head kvh, computed by the ATTN_THREADS threads tid of a
+// workgroup that call it together.  Every thread of the workgroup passes the
+// same barriers: threads of an inactive item (active false) take part in
+// them and do nothing else, so several items can share one workgroup.  COH:
+// partials written with coherent stores (read in the same launch).
+template <int HS, int G, bool F16, bool COH>
+__device__ void attn_item(const AttnArgs &a, uint32_t kvh, uint32_t s, int tid, bool active, AttnLds<HS, G> &L) {
     constexpr int TPP = HS / 8;             // lanes per position (8 dims each)
     constexpr int PPW = 64 / TPP;           // positions per wave and pass
     constexpr int NW = ATTN_THREADS / 64;   // waves
     constexpr int PPP = NW * PPW;           // positions per workgroup and pass
     constexpr int NPG = PPP;                // position groups (threads sharing a dim slice)
     constexpr int U = ATTN_BATCH;
-    __shared__ float og[NPG][G][HS];        // per position group: unnormalised o
-    __shared__ float mg[NPG][G], lg[NPG][G];
-    __shared__ float wg[NPG][G], Mh[G];
+    auto &og = L.og;
+    auto &mg = L.mg;
+    auto &lg = L.lg;
+    auto &wg = L.wg;
+    auto &Mh = L.Mh;
 
     // arguments in one batch of scalar loads (the compiler would otherwise
     // fetch them in dependent round trips next to their first uses); an
@@ -110,8 +126,8 @@ __device__ void attn_body(const AttnArgs &a) {
     // the device position, as a vector load issued before every other load:
     // loads complete in issue order, so waiting for it waits for nothing else
     const uint32_t pos_dev = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kvh = blockIdx.x, s = blockIdx.y, S = a.n_splits;
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint32_t S = a.n_splits;
     constexpr uint32_t Qb = attn_quantum<HS>();
     const int dc = lane % TPP;
     const uint32_t pg = (uint32_t)(wave * PPW + lane / TPP);
@@ -145,20 +161,18 @@ __device__ void attn_body(const AttnArgs &a) {
             kv8_load<F16>(a.v_cache, off, vr[u]);
         }
     };
-    if (fixed) load_batch(s * Qb, 0, 0);
+    if (fixed && active) load_batch(s * Qb, 0, 0);
     __builtin_amdgcn_sched_barrier(0); // the batch's loads stay together
     const uint32_t T = min(__builtin_amdgcn_readfirstlane(pos_dev) + 1, a.seq_cap);
     const uint32_t C = fixed ? Qb : attn_chunk<HS>(T, S);
     const uint32_t t0 = s * C;
-    if (t0 >= T) {
+    if (active && t0 >= T && tid < G) {
         // an empty split: a partial the merge gives weight 0
-        if (tid < G) {
-            a.part_ml[(pidx + tid) * 2] = -INFINITY;
-            a.part_ml[(pidx + tid) * 2 + 1] = 0.0f;
-        }
-        return;
+        st_out<COH>(a.part_ml + (pidx + tid) * 2, -INFINITY);
+        st_out<COH>(a.part_ml + (pidx + tid) * 2 + 1, 0.0f);
     }
-    const uint32_t n = min(C, T - t0);
+    const bool live = active && t0 < T;
+    const uint32_t n = live ? min(C, T - t0) : 0u;
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -213,42 +227,52 @@ __device__ void attn_body(const AttnArgs &a) {
 
     // combine the NPG position groups through LDS: states, then per-head
     // maxima and weights 2^(m_g - M), then the weighted sums of o
+    if (live) {
 #pragma unroll
-    for (int j = 0; j < G; j++) {
+        for (int j = 0; j < G; j++) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) og[pg][j][dc * 8 + e] = o[j][e];
-        if (dc == 0) {
-            mg[pg][j] = m[j];
-            lg[pg][j] = l[j];
+            for (int e = 0; e < 8; e++) og[pg][j][dc * 8 + e] = o[j][e];
+            if (dc == 0) {
+                mg[pg][j] = m[j];
+                lg[pg][j] = l[j];
+            }
         }
     }
     __syncthreads();
-    if (tid < G) {
+    if (live && tid < G) {
         float M = -INFINITY;
         for (int g = 0; g < NPG; g++) M = fmaxf(M, mg[g][tid]);
         Mh[tid] = M;
     }
     __syncthreads();
-    for (int i = tid; i < NPG * G; i += ATTN_THREADS) {
-        const int g = i / G, j = i % G;
-        wg[g][j] = exp2f(mg[g][j] - Mh[j]); // 0 for a group that saw no position
-    }
+    if (live)
+        for (int i = tid; i < NPG * G; i += ATTN_THREADS) {
+            const int g = i / G, j = i % G;
+            wg[g][j] = exp2f(mg[g][j] - Mh[j]); // 0 for a group that saw no position
+        }
     __syncthreads();
 
-    for (int i = tid; i < G * HS; i += ATTN_THREADS) {
-        const int j = i / HS, d = i % HS;
-        float v = 0.0f;
+    if (live)
+        for (int i = tid; i < G * HS; i += ATTN_THREADS) {
+            const int j = i / HS, d = i % HS;
+            float v = 0.0f;
 #pragma unroll
-        for (int g = 0; g < NPG; g++) v = fmaf(wg[g][j], og[g][j][d], v);
-        a.part_o[(pidx + j) * HS + d] = v;
-        if (d == 0) {
-            float L = 0.0f;
+            for (int g = 0; g < NPG; g++) v = fmaf(wg[g][j], og[g][j][d], v);
+            st_out<COH>(a.part_o + (pidx + j) * HS + d, v);
+            if (d == 0) {
+                float Ls = 0.0f;
 #pragma unroll
-            for (int g = 0; g < NPG; g++) L = fmaf(wg[g][j], lg[g][j], L);
-            a.part_ml[(pidx + j) * 2] = Mh[j];
-            a.part_ml[(pidx + j) * 2 + 1] = L;
+                for (int g = 0; g < NPG; g++) Ls = fmaf(wg[g][j], lg[g][j], Ls);
+                st_out<COH>(a.part_ml + (pidx + j) * 2, Mh[j]);
+                st_out<COH>(a.part_ml + (pidx + j) * 2 + 1, Ls);
+            }
         }
-    }
+}
+
+template <int HS, int G, bool F16>
+__device__ void attn_body(const AttnArgs &a) {
+    __shared__ AttnLds<HS, G> L;
+    attn_item<HS, G, F16, false>(a, blockIdx.x, blockIdx.y, (int)threadIdx.x, true, L);
 }
 
 // Merge of the split partials: one workgroup of ATTN_MERGE_THREADS per query
@@ -258,14 +282,26 @@ __device__ void attn_body(const AttnArgs &a) {
 // start.  Split weights are 2^(m_s - M) (base-2 units).
 constexpr int ATTN_MERGE_THREADS = 512;
 
-template <int HS, int G>
-__device__ void attn_merge_body(const AttnArgs &a) {
+template <int HS>
+struct MergeLds {
+    static constexpr int Q = ATTN_MERGE_THREADS / HS;
+    float wm[ATTN_MERGE_MAX], wl[ATTN_MERGE_MAX], wt[ATTN_MERGE_MAX];
+    float part[Q][HS];
+};
+
+// Merge of query head h by the ATTN_MERGE_THREADS threads tid of a
+// workgroup (all of its threads pass the same barriers; active false: only
+// the barriers).  COH: the quantized output written with coherent stores.
+template <int HS, int G, bool COH>
+__device__ void attn_merge_item(const AttnArgs &a, uint32_t h, int tid, bool active, MergeLds<HS> &Lm) {
     constexpr int Q = ATTN_MERGE_THREADS / HS;             // split groups
     constexpr int PER = (ATTN_MERGE_MAX + Q - 1) / Q;      // splits per thread at most
-    __shared__ float wm[ATTN_MERGE_MAX], wl[ATTN_MERGE_MAX], wt[ATTN_MERGE_MAX];
-    __shared__ float part[Q][HS];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const uint32_t h = blockIdx.x, kvh = h / G, j = h % G, S = a.n_splits;
+    auto &wm = Lm.wm;
+    auto &wl = Lm.wl;
+    auto &wt = Lm.wt;
+    auto &part = Lm.part;
+    const int lane = tid & 63;
+    const uint32_t kvh = h / G, j = h % G, S = active ? a.n_splits : 0u;
     const int d = tid % HS, qg = tid / HS;
     const float *po = a.part_o + ((size_t)kvh * S * G + j) * HS + d; // split t at po[t * G * HS]
     float v[PER];
@@ -299,21 +335,27 @@ __device__ void attn_merge_body(const AttnArgs &a) {
             if (w != 0.0f) O = fmaf(v[u], w, O);
         }
     }
-    part[qg][d] = O;
+    if (tid < ATTN_MERGE_THREADS) part[qg][d] = O;
     __syncthreads();
     // head dims are written (and quantized for the next GEMV: a head is
     // HS/16 whole activation groups) by the first HS threads
-    if (tid < ((HS + 63) / 64) * 64) {
+    if (active && tid < ((HS + 63) / 64) * 64) {
         const bool ok = tid < HS;
         float r = 0.0f;
         if (ok) {
 #pragma unroll
             for (int k = 0; k < Q; k++) r += part[k][tid];
             r /= L;
-            a.out[(size_t)h * HS + tid] = r;
+            if (a.out) st_out<COH>(a.out + (size_t)h * HS + tid, r);
         }
-        if (a.xq_out) quant16(r, ok, a.xq_out, a.n_out, (uint32_t)(h * HS + tid), tid & 63);
+        if (a.xq_out) quant16<COH>(r, ok, a.xq_out, a.n_out, (uint32_t)(h * HS + tid), tid & 63);
     }
+}
+
+template <int HS, int G>
+__device__ void attn_merge_body(const AttnArgs &a) {
+    __shared__ MergeLds<HS> Lm;
+    attn_merge_item<HS, G, false>(a, blockIdx.x, (int)threadIdx.x, true, Lm);
 }
 
 } // namespace ifr

@@ -87,6 +87,16 @@ IFR_DEV void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Stores that another workgroup of the same launch reads after a grid
+// barrier (COH): agent-scope atomic stores, which are written through to the
+// device-coherent level instead of staying in this XCD's L2.  Plain stores
+// otherwise (the kernel boundary makes them visible).
+template <bool COH, typename T>
+IFR_DEV void st_out(T *p, T v) {
+    if constexpr (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
 // 16 bytes at a 16-byte aligned address.
 IFR_DEV uint4 ld16(const uint8_t *p) {
     u32x4_a16 v = *(const u32x4_a16 *)p;

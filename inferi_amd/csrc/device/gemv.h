@@ -385,6 +385,7 @@ constexpr float XQ_MAXCODE = 2097151.0f; // 2^21 - 1
 // Quantizes one value per lane into XQ at element i; the 16 lanes of a DPP
 // row form one group (i % 16 == lane % 16).  Every lane of the wave must call
 // it (the reductions read neighbours); `ok` gates the stores.
+template <bool COH = false>
 IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int lane) {
     const float am = max16(fabsf(v));
     const float sc = am / XQ_MAXCODE;
@@ -397,12 +398,12 @@ IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int 
     const int da = (q1 - db) >> 8;
     const float sq = sum16((float)q);
     if (ok) {
-        xq[i] = (uint8_t)(int8_t)da;
-        xq[K + i] = (uint8_t)(int8_t)db;
-        xq[2 * K + i] = (uint8_t)(int8_t)dc;
+        st_out<COH>(xq + i, (uint8_t)(int8_t)da);
+        st_out<COH>(xq + K + i, (uint8_t)(int8_t)db);
+        st_out<COH>(xq + 2 * K + i, (uint8_t)(int8_t)dc);
         if ((lane & 15) == 0) {
-            ((float *)(xq + 3 * K))[i / 16] = sc;
-            ((float *)(xq + 3 * K + K / 4))[i / 16] = sc * sq;
+            st_out<COH>((float *)(xq + 3 * K) + i / 16, sc);
+            st_out<COH>((float *)(xq + 3 * K + K / 4) + i / 16, sc * sq);
         }
     }
 }
@@ -995,14 +996,17 @@ __device__ void gemv_f32_body(const GemvArgs &a) {
 //    once per group and wave 0 adds the K-slices and runs the epilogue on the
 //    group's 16 outputs (residual add and quantization of x * gamma_next for
 //    the next GEMV, or silu(gate) * up and its quantization).
-template <int FMT, int MODE, bool PIPE>
+template <int FMT, int MODE, bool PIPE, int NI = 1>
 __device__ void gemv_int_body(const GemvArgs &a) {
     constexpr int R = 2;
     using CH = ChunkI<FMT, R>;
     constexpr int LPB = CH::LPB, BPI = 64 / LPB;
     constexpr bool NORM = (MODE == GEMV_QKV || MODE == GEMV_GATEUP || MODE == GEMV_HEAD);
     constexpr bool QOUT = (MODE == GEMV_RESID || MODE == GEMV_GATEUP);
-    constexpr uint32_t GR = MODE == GEMV_GATEUP ? 32 : 16;
+    // output group: 16 values (32 virtual rows for GATEUP) where a group is
+    // quantized or its K-slices are added; where waves finish their own rows
+    // (one K-slice, no quantized output) a group is just the workgroup's rows
+    constexpr uint32_t GRQ = MODE == GEMV_GATEUP ? 32 : 16;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float part[2][GEMV_KS_MAX][32];
 
@@ -1021,6 +1025,8 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     const uint32_t ks = (uint32_t)wave % KS, rw = (uint32_t)wave / KS;
     // a geometry that does not tile the group would never advance: the host
     // never launches one, and the workgroup exits as a whole if it did
+    const bool local_rows = !QOUT && KS == 1;
+    const uint32_t GR = local_rows ? RW * R : GRQ;
     if (KS == 0 || KS > GEMV_KS_MAX || RW == 0 || RW * KS != W || GR % (RW * R) != 0) return;
     const uint32_t SUBR = RW * R, SUB = GR / SUBR;
     const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
@@ -1110,6 +1116,10 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     // keeps the small loads ahead of the weights (a scheduling fence only)
     __builtin_amdgcn_sched_barrier(0);
     load(A, cur);
+    // NI = 2: the second item's weights are requested up front as well (a
+    // workgroup whose second item lies past the end re-reads its first one)
+    Item c2 = next(cur);
+    if constexpr (NI >= 2) load(B, c2.g < ngroups ? c2 : cur);
     __builtin_amdgcn_sched_barrier(0);
     {
         uint4 *dst = (uint4 *)lds;
@@ -1278,6 +1288,15 @@ __device__ void gemv_int_body(const GemvArgs &a) {
         }
     } else {
         bool first = true;
+        if constexpr (NI >= 2) {
+            compute(A, cur);
+            cur = c2;
+            if (cur.g < ngroups) {
+                compute(B, cur);
+                cur = next(cur);
+            }
+            first = false;
+        }
         while (cur.g < ngroups) {
             if (!first) load(A, cur);
             first = false;

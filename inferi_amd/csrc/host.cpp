@@ -111,6 +111,10 @@ struct ifr_ctx {
     // GEMV arithmetic: 0 = x as 16-bit fixed point with int8 dot products,
     // 1 = exact fp32 x and FMAs
     int gemv_exact = 0;
+    // decode step: 1 = the GEMV stages between attentions in one persistent
+    // launch per layer (device/pk.h) where the model allows it
+    int persistent = 0;
+    int pk_trace_layer = -1; // layer whose persistent launch records its stage timeline
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -217,11 +221,17 @@ static IntGeom int_geom(const ifr_ctx *c, uint32_t bpi, const char *mode, const 
     // gateup: 8 waves (two sub-tiles per group) and three workgroups per CU
     // measured fastest; the others: as many row waves as a group allows
     const bool gateup = !strcmp(mode, "gateup");
-    uint32_t rw = gateup ? 8 / g.ks : std::min(GEMV_INT_MAX_WAVES / g.ks, gr / 2);
+    // waves that finish their own rows (one K-slice, no quantized output):
+    // four waves of two rows per workgroup, one workgroup per 8 rows, every
+    // workgroup resident at once (measured fastest); the groups are then
+    // the workgroups' 8 rows
+    const bool local = g.ks == 1 && (!strcmp(mode, "plain") || !strcmp(mode, "qkv") || !strcmp(mode, "head"));
+    uint32_t rw = gateup ? 8 / g.ks : local ? 4 : std::min(GEMV_INT_MAX_WAVES / g.ks, gr / 2);
     if (c->gemv_waves) rw = std::max(1u, std::min(std::min(GEMV_INT_MAX_WAVES / g.ks, gr / 2), c->gemv_waves / g.ks));
     g.waves = g.ks * rw;
-    const uint32_t ngroups = (a.total_rows + gr - 1) / gr;
-    uint32_t grid = gateup ? c->n_cu * 3 : c->n_cu * (GEMV_INT_MAX_WAVES / g.waves);
+    const uint32_t gr_eff = local ? rw * 2 : gr;
+    const uint32_t ngroups = (a.total_rows + gr_eff - 1) / gr_eff;
+    uint32_t grid = gateup ? c->n_cu * 3 : local ? ngroups : c->n_cu * (GEMV_INT_MAX_WAVES / g.waves);
     if (c->gemv_max_grid) grid = c->gemv_max_grid;
     if (cap) grid = std::min(grid, cap);
     g.grid = std::max(std::min(grid, ngroups), 1u);
@@ -355,8 +365,14 @@ struct ifr_llama2_state {
     float temperature = 0.0f, topp = 0.0f;
     uint64_t seed = 0;
     uint32_t sampler_gen = 0;
+    // persistent layer tail: the residual after attention, barrier words and
+    // the error word
+    float *pk_xmid = nullptr;
+    uint32_t *pk_bar = nullptr, *pk_err = nullptr;
+    uint64_t *pk_ts = nullptr; // stage timeline of one launch
     // captured decode step
     hipGraphExec_t graph = nullptr;
+    int graph_pk = -1;
     uint32_t graph_sampler = 0;
     const ifr_llama2_weights *graph_w = nullptr;
     int graph_fused = -1;
@@ -411,7 +427,121 @@ static ifr_status launch_keys_of_y(ifr_ctx *c, const float *logits, uint32_t n, 
     return c->launch("argmax_part_k", dim3(parts), dim3(256), 0, k);
 }
 
+static ifr_status enqueue_head(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused, uint32_t n_ss_a);
+
+// The persistent layer tail runs a model when every matrix is Q4_K, the
+// layers have no QKV bias, RoPE pairs adjacent dims (the fused QKV epilogue),
+// and one workgroup per CU holds each stage's rows and its input in LDS.
+static bool pk_supported(ifr_ctx *c, const ifr_llama2_state *s, const ifr_llama2_weights *w) {
+    const ifr_llama2_config &cfg = s->cfg;
+    if (!c->persistent || c->gemv_exact || cfg.rope_variant != IFR_ROPE_ORIGINAL) return false;
+    for (const LayerW &L : w->layers) {
+        const Tens *m[7] = {&L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
+        for (const Tens *t : m)
+            if (t->dtype != IFR_Q4_K || ((uintptr_t)t->data & 15)) return false;
+        if (L.q_bias.data || L.k_bias.data || L.v_bias.data) return false;
+    }
+    const uint32_t H = cfg.hidden, F = cfg.ffn, nwg = (uint32_t)c->n_cu;
+    if (H % 256 || F % 256 || H / 256 > 16 * PK_KSTEPS || F / 256 > 16 * PK_KSTEPS) return false;
+    auto rows_per_wg = [&](uint32_t units, uint32_t gu) { return (units + nwg - 1) / nwg * gu; };
+    if (rows_per_wg((H + 2 * s->kv_dim) / 2, 2) > PK_PART_ROWS || rows_per_wg(H / 16, 16) > PK_PART_ROWS ||
+        rows_per_wg(F / 16, 32) > PK_PART_ROWS)
+        return false;
+    const uint32_t lds = pk_lds_bytes(std::max(H, F));
+    if (lds > GEMV_MAX_LDS) return false;
+    hipFunction_t f = c->fn("pk_tail_q4_k");
+    int occ = 0;
+    if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, f, PK_WAVES * 64, lds) != hipSuccess || occ < 1)
+        return false;
+    return true;
+}
+
+// One decode step with the persistent layer tail: per layer the attention
+// split and merge kernels, then one launch for O, gate/up, down and the next
+// layer's QKV (mode 0: the embedding and the first QKV).
+static ifr_status enqueue_step_pk(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w) {
+    const ifr_llama2_config &cfg = s->cfg;
+    const uint32_t hidden = cfg.hidden, L = cfg.n_layers;
+    const uint32_t lds = pk_lds_bytes(std::max(hidden, cfg.ffn));
+    ifr_status st;
+    PkArgs base{};
+    base.table = w->token_embd.data;
+    base.emb_row_bytes = hidden / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
+    base.emb_fmt = w->token_embd.dtype;
+    base.emb_gamma = (const float *)w->layers[0].attn_norm.data;
+    base.tokens = s->tokens;
+    base.ctl = s->ctl;
+    base.rope_tab = s->rope_tab;
+    base.x = s->x;
+    base.x_mid = s->pk_xmid;
+    base.q = s->q;
+    base.xq_att = s->xq_att;
+    base.xq_f = s->xq_f;
+    base.xq_h = s->xq_h;
+    base.xq_a = s->xq_a;
+    base.ss_f = s->ss_f;
+    base.ss_a = s->ss_a;
+    base.n_ss_a = (hidden + 255) / 256;
+    base.hidden = hidden;
+    base.ffn = cfg.ffn;
+    base.head_size = s->head_size;
+    base.kv_dim = s->kv_dim;
+    base.nb_h = hidden / 256;
+    base.rb_h = base.nb_h * 144;
+    base.nb_f = cfg.ffn / 256;
+    base.rb_f = base.nb_f * 144;
+    base.eps = cfg.rms_eps;
+    base.kv_f16 = cfg.kv_dtype == IFR_F16;
+    base.bar = s->pk_bar;
+    base.err = s->pk_err;
+    auto set_qkv = [&](PkArgs &a, uint32_t l) {
+        const LayerW &Lw = w->layers[l];
+        a.wq = Lw.attn_q.data;
+        a.wk = Lw.attn_k.data;
+        a.wv = Lw.attn_v.data;
+        a.kc = s->kcache + (size_t)l * s->layer_kv_bytes;
+        a.vc = s->vcache + (size_t)l * s->layer_kv_bytes;
+    };
+    const dim3 grid((uint32_t)c->n_cu), block(PK_WAVES * 64);
+    {
+        PkArgs a = base;
+        a.mode = 0;
+        set_qkv(a, 0);
+        if ((st = c->launch("pk_tail_q4_k", grid, block, lds, a))) return st;
+    }
+    for (uint32_t l = 0; l < L; l++) {
+        AttnArgs t{};
+        t.q = s->q;
+        t.k_cache = s->kcache + (size_t)l * s->layer_kv_bytes;
+        t.v_cache = s->vcache + (size_t)l * s->layer_kv_bytes;
+        t.out = s->att;
+        t.xq_out = s->xq_att;
+        t.part_o = s->part_o;
+        t.part_ml = s->part_ml;
+        t.pos = &s->ctl->pos;
+        t.kv_dim = s->kv_dim;
+        t.n_splits = s->n_splits;
+        t.seq_cap = cfg.max_pos;
+        t.n_out = hidden;
+        if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, t, cfg.n_kv_heads))) return st;
+        const LayerW &Lw = w->layers[l];
+        PkArgs a = base;
+        a.mode = 1;
+        a.wo = Lw.attn_output.data;
+        a.wg = Lw.ffn_gate.data;
+        a.wu = Lw.ffn_up.data;
+        a.wd = Lw.ffn_down.data;
+        a.ffn_norm = (const float *)Lw.ffn_norm.data;
+        a.next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
+        if (l + 1 < L) set_qkv(a, l + 1);
+        if ((int)l == c->pk_trace_layer) a.ts = s->pk_ts;
+        if ((st = c->launch("pk_tail_q4_k", grid, block, lds, a))) return st;
+    }
+    return enqueue_head(c, s, w, 1, hidden / 16);
+}
+
 static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
+    if (fused && pk_supported(c, s, w)) return enqueue_step_pk(c, s, w);
     const ifr_llama2_config &cfg = s->cfg;
     const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn, L = cfg.n_layers;
     const uint32_t n_ss_res = hidden / 16; // partial sums written by a RESID GEMV (one per 16-row tile)
@@ -623,6 +753,16 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         }
     }
 
+    return enqueue_head(c, s, w, fused, n_ss_a);
+}
+
+// Final RMSNorm, output head, then the argmax (or the sampler) that writes
+// the next token and advances the position.  n_ss_a: partial sums of x^2 in
+// ss_a (fused path).
+static ifr_status enqueue_head(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused, uint32_t n_ss_a) {
+    const ifr_llama2_config &cfg = s->cfg;
+    const uint32_t hidden = cfg.hidden;
+    ifr_status st;
     // ---- final norm, output head, argmax, advance
     const Tens &out = w->output.data ? w->output : w->token_embd; // transformer.rs:376-382
     GemvPlan p;
@@ -767,6 +907,14 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
     }
     if (!strcmp(key, "gemv_exact")) {
         c->gemv_exact = value ? 1 : 0;
+        return IFR_OK;
+    }
+    if (!strcmp(key, "persistent")) {
+        c->persistent = value ? 1 : 0;
+        return IFR_OK;
+    }
+    if (!strcmp(key, "pk_trace_layer")) {
+        c->pk_trace_layer = (int)value;
         return IFR_OK;
     }
     if (!strcmp(key, "gemv_waves")) {
@@ -1289,6 +1437,8 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     A(s->xq_u, xq_bytes(std::max(H, F))) A(s->ss_a, H / 16 * 4) A(s->ss_f, H / 16 * 4)
     A(s->kcache, s->layer_kv_bytes * cfg->n_layers)
     A(s->vcache, s->layer_kv_bytes * cfg->n_layers)
+    A(s->pk_xmid, H * 4) A(s->pk_bar, PK_BAR_WORDS * 4) A(s->pk_err, 4)
+    A(s->pk_ts, (size_t)c->n_cu * PK_TS_EVENTS * 8)
 #undef A
     ifr_rms_norm_config rc{cfg->rms_eps};
     if ((st = c->hip(hipMemcpy(s->rms_cfg, &rc, sizeof rc, hipMemcpyHostToDevice), "hipMemcpy"))) { state_free(s); return st; }
@@ -1513,7 +1663,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         return IFR_OK;
     }
     if (!s->graph || s->graph_w != w || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
-        s->graph_sampler != s->sampler_gen) {
+        s->graph_sampler != s->sampler_gen || s->graph_pk != c->persistent) {
         if (s->graph) {
             hipStreamSynchronize(c->stream);
             hipGraphExecDestroy(s->graph);
@@ -1536,6 +1686,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         s->graph_fused = 1;
         s->graph_exact = c->gemv_exact;
         s->graph_sampler = s->sampler_gen;
+        s->graph_pk = c->persistent;
     }
     for (uint32_t i = 0; i < n_steps; i++)
         if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;
@@ -1572,6 +1723,8 @@ IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name
     else if (n == "logits") { *p = s->logits; b = (size_t)cfg.vocab * 4; }
     else if (n == "probs") { *p = s->probs; b = (size_t)cfg.vocab * 4; }
     else if (n == "pos") { *p = &s->ctl->pos; b = 4; }
+    else if (n == "pk_err") { *p = s->pk_err; b = 4; }
+    else if (n == "pk_ts") { *p = s->pk_ts; b = (size_t)s->ctx->n_cu * PK_TS_EVENTS * 8; }
     else if (n == "tokens") { *p = s->tokens; b = ((size_t)cfg.max_pos + 1) * 4; }
     else if (n == "key_cache" || n == "value_cache") {
         if (layer < 0 || (uint32_t)layer >= cfg.n_layers) return s->ctx->fail(IFR_EINVAL, "layer out of range");

@@ -5,6 +5,7 @@
 #include "device/attention.h"
 #include "device/elementwise.h"
 #include "device/gemv.h"
+#include "device/pk.h"
 #include "device/prefill.h"
 #include "device/sample.h"
 
@@ -15,8 +16,8 @@ using namespace ifr;
 // Four waves per SIMD (at most 128 VGPRs) keeps enough loads in flight.
 #define GEMV_KERNEL(NAME, FMT, MODE)                                                                   \
     extern "C" __global__ void __launch_bounds__(GEMV_INT_MAX_WAVES * 64)                            \
-        __attribute__((amdgpu_waves_per_eu(4, 8))) NAME(GemvArgs a) {                                \
-        gemv_int_body<FMT, MODE, GEMV_INT_PIPE>(a);                                                  \
+        __attribute__((amdgpu_waves_per_eu(GEMV_INT_WPE, 8))) NAME(GemvArgs a) {                     \
+        gemv_int_body<FMT, MODE, GEMV_INT_PIPE, GEMV_INT_NI>(a);                                     \
     }                                                                                                \
     extern "C" __global__ void __launch_bounds__(GemvGeom<MODE>::W * 64)                             \
         __attribute__((amdgpu_waves_per_eu(4, 8))) NAME##_f32(GemvArgs a) {                          \
@@ -25,6 +26,12 @@ using namespace ifr;
 
 #ifndef GEMV_INT_PIPE
 #define GEMV_INT_PIPE false
+#endif
+#ifndef GEMV_INT_NI
+#define GEMV_INT_NI 1
+#endif
+#ifndef GEMV_INT_WPE
+#define GEMV_INT_WPE 4
 #endif
 
 #define GEMV_ALL_MODES(FMTNAME, FMT)                  \
@@ -115,3 +122,10 @@ PF_ATTN_KERNEL(128, 1)
 PF_ATTN_KERNEL(128, 2)
 PF_ATTN_KERNEL(128, 4)
 PF_ATTN_KERNEL(128, 8)
+
+// persistent layer tail (device/pk.h)
+#define PK_KERNEL(FMTNAME, FMT)                                                                   \
+    extern "C" __global__ void __launch_bounds__(PK_THREADS) pk_tail_##FMTNAME(PkArgs a) {         \
+        pk_tail_body<FMT>(a);                                                                     \
+    }
+PK_KERNEL(q4_k, Q4_K)
