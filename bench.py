@@ -391,7 +391,7 @@ def main() -> None:
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
-    ap.add_argument("--persistent", type=int, default=1,
+    ap.add_argument("--persistent", type=int, default=0,
                     help="1: the GEMV stages between attentions in one persistent launch per layer")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -275,87 +275,63 @@ __device__ void attn_body(const AttnArgs &a) {
     attn_item<HS, G, F16, false>(a, blockIdx.x, blockIdx.y, (int)threadIdx.x, true, L);
 }
 
-// Merge of the split partials: one workgroup of ATTN_MERGE_THREADS per query
-// head; thread (q, d) sums splits q, q + Q, ... for head dim d.  Every split
-// of the launch is read (an empty one carries m = -inf and weight 0), so the
-// merge does not wait for the device position: all loads go out at the
-// start.  Split weights are 2^(m_s - M) (base-2 units).
-constexpr int ATTN_MERGE_THREADS = 512;
+// Merge of the split partials, one wave per 16 output values (dims
+// 16c..16c+15 of one query head): lane = (subset r = lane / 16, dim
+// 16c + lane % 16); subset r folds splits r, r + 4, ... into a running
+// (M, L, O) with base-2 weights, then the four subsets combine through lane
+// shuffles: out = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s.  No LDS and no
+// barrier.  Every split of the launch is read (an empty one carries m = -inf
+// and is skipped), so no load waits for the position.
+constexpr uint32_t ATTN_MERGE_SUBSETS = 4;
+constexpr uint32_t ATTN_MERGE_CHUNK = 24; // splits of a subset whose loads are in flight together
 
-template <int HS>
-struct MergeLds {
-    static constexpr int Q = ATTN_MERGE_THREADS / HS;
-    float wm[ATTN_MERGE_MAX], wl[ATTN_MERGE_MAX], wt[ATTN_MERGE_MAX];
-    float part[Q][HS];
-};
-
-// Merge of query head h by the ATTN_MERGE_THREADS threads tid of a
-// workgroup (all of its threads pass the same barriers; active false: only
-// the barriers).  COH: the quantized output written with coherent stores.
-template <int HS, int G, bool COH>
-__device__ void attn_merge_item(const AttnArgs &a, uint32_t h, int tid, bool active, MergeLds<HS> &Lm) {
-    constexpr int Q = ATTN_MERGE_THREADS / HS;             // split groups
-    constexpr int PER = (ATTN_MERGE_MAX + Q - 1) / Q;      // splits per thread at most
-    auto &wm = Lm.wm;
-    auto &wl = Lm.wl;
-    auto &wt = Lm.wt;
-    auto &part = Lm.part;
-    const int lane = tid & 63;
-    const uint32_t kvh = h / G, j = h % G, S = active ? a.n_splits : 0u;
-    const int d = tid % HS, qg = tid / HS;
-    const float *po = a.part_o + ((size_t)kvh * S * G + j) * HS + d; // split t at po[t * G * HS]
-    float v[PER];
-#pragma unroll
-    for (int u = 0; u < PER; u++) {
-        const uint32_t t = (uint32_t)(qg + Q * u);
-        v[u] = t < S ? po[(size_t)t * G * HS] : 0.0f;
-    }
-    if ((uint32_t)tid < S) {
-        const float *ml = a.part_ml + (((size_t)kvh * S + tid) * G + j) * 2;
-        wm[tid] = ml[0];
-        wl[tid] = ml[1];
-    }
-    __syncthreads();
-    // every wave forms M itself; split weights 2^(m_s - M) once, in LDS
-    float M = -INFINITY;
-    for (uint32_t t = lane; t < S; t += 64) M = fmaxf(M, wm[t]);
-    M = wave_max(M);
-    if ((uint32_t)tid < S) wt[tid] = wm[tid] == -INFINITY ? 0.0f : exp2f(wm[tid] - M);
-    __syncthreads();
-    float L = 0.0f;
-    for (uint32_t t = lane; t < S; t += 64) L = fmaf(wl[t], wt[t], L);
-    L = wave_sum(L);
-    float O = 0.0f;
-#pragma unroll
-    for (int u = 0; u < PER; u++) {
-        const uint32_t t = (uint32_t)(qg + Q * u);
-        if (t < S) {
-            const float w = wt[t];
-            // an empty split's o was never written: skipped, not multiplied by 0
-            if (w != 0.0f) O = fmaf(v[u], w, O);
-        }
-    }
-    if (tid < ATTN_MERGE_THREADS) part[qg][d] = O;
-    __syncthreads();
-    // head dims are written (and quantized for the next GEMV: a head is
-    // HS/16 whole activation groups) by the first HS threads
-    if (active && tid < ((HS + 63) / 64) * 64) {
-        const bool ok = tid < HS;
-        float r = 0.0f;
-        if (ok) {
-#pragma unroll
-            for (int k = 0; k < Q; k++) r += part[k][tid];
-            r /= L;
-            if (a.out) st_out<COH>(a.out + (size_t)h * HS + tid, r);
-        }
-        if (a.xq_out) quant16<COH>(r, ok, a.xq_out, a.n_out, (uint32_t)(h * HS + tid), tid & 63);
-    }
+IFR_DEV void merge_fold(float &M, float &L, float &O, float m, float l, float o) {
+    if (m == -INFINITY) return; // an empty split (its o was never written)
+    const float Mn = fmaxf(M, m);
+    const float a = exp2f(M - Mn), b = exp2f(m - Mn); // a = 0 while M is -inf
+    L = fmaf(l, b, L * a);
+    O = fmaf(o, b, O * a);
+    M = Mn;
 }
 
 template <int HS, int G>
 __device__ void attn_merge_body(const AttnArgs &a) {
-    __shared__ MergeLds<HS> Lm;
-    attn_merge_item<HS, G, false>(a, blockIdx.x, (int)threadIdx.x, true, Lm);
+    constexpr uint32_t NR = ATTN_MERGE_SUBSETS, CH = ATTN_MERGE_CHUNK;
+    const int lane = (int)threadIdx.x;
+    const uint32_t grp = blockIdx.x, h = grp / (HS / 16), c = grp % (HS / 16);
+    const uint32_t kvh = h / G, j = h % G, S = a.n_splits;
+    const uint32_t r = (uint32_t)lane / 16, d = c * 16 + (uint32_t)lane % 16;
+    const float *po = a.part_o + ((size_t)kvh * S * G + j) * HS + d; // split t at po[t * G * HS]
+    const float *pml = a.part_ml + ((size_t)kvh * S * G + j) * 2;    // split t at pml[t * G * 2]
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (uint32_t t0 = r; t0 < S; t0 += NR * CH) {
+        float mv[CH], lv[CH], ov[CH];
+#pragma unroll
+        for (uint32_t u = 0; u < CH; u++) {
+            const uint32_t t = t0 + NR * u;
+            const bool ok = t < S;
+            mv[u] = ok ? pml[(size_t)t * G * 2] : -INFINITY;
+            lv[u] = ok ? pml[(size_t)t * G * 2 + 1] : 0.0f;
+            ov[u] = ok ? po[(size_t)t * G * HS] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < CH; u++) merge_fold(M, L, O, mv[u], lv[u], ov[u]);
+    }
+    // the four subsets of each dim: lanes d, d + 16, d + 32, d + 48
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+        const float Mo = __shfl_xor(M, off, 64), Lo = __shfl_xor(L, off, 64), Oo = __shfl_xor(O, off, 64);
+        const float Mn = fmaxf(M, Mo);
+        const float wa = M == -INFINITY ? 0.0f : exp2f(M - Mn), wb = Mo == -INFINITY ? 0.0f : exp2f(Mo - Mn);
+        L = fmaf(Lo, wb, L * wa);
+        O = fmaf(Oo, wb, O * wa);
+        M = Mn;
+    }
+    const float res = O / L;
+    const uint32_t oi = h * HS + d;
+    const bool ok = lane < 16;
+    if (ok && a.out) a.out[oi] = res;
+    if (a.xq_out) quant16(ok ? res : 0.0f, ok, a.xq_out, a.n_out, oi, lane);
 }
 
 } // namespace ifr

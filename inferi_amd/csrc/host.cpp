@@ -309,7 +309,7 @@ static ifr_status launch_attn(ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, i
     ifr_status st = c->launch(name, dim3(n_kv_heads, a.n_splits), dim3(256), 0, a);
     if (st) return st;
     snprintf(name, sizeof name, "attn_merge_h%u_g%u", head_size, kv_mul);
-    return c->launch(name, dim3(n_kv_heads * kv_mul), dim3(512), 0, a);
+    return c->launch(name, dim3(n_kv_heads * kv_mul * (head_size / 16)), dim3(64), 0, a);
 }
 
 // ----------------------------------------------------------------- model --

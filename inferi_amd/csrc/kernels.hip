@@ -58,7 +58,7 @@ GEMV_ALL_MODES(q8_k, Q8_K)
     extern "C" __global__ void __launch_bounds__(256) attn_f32_h##HS##_g##G(AttnArgs a) {           \
         attn_body<HS, G, false>(a);                                                                 \
     }                                                                                               \
-    extern "C" __global__ void __launch_bounds__(512) attn_merge_h##HS##_g##G(AttnArgs a) {         \
+    extern "C" __global__ void __launch_bounds__(64) attn_merge_h##HS##_g##G(AttnArgs a) {          \
         attn_merge_body<HS, G>(a);                                                                  \
     }
 
