@@ -1325,4 +1325,106 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// One-item form of the integer path for the modes whose waves finish their
+// own rows (PLAIN, QKV) when a row is one 64-lane step (K <= 64/LPB blocks):
+// workgroups of GEMV_ONE_WAVES waves of two rows each, one workgroup per
+// 2*GEMV_ONE_WAVES rows, launched all at once.  Each wave requests x, then
+// its rows' weights, then stages x and computes: no item loop, no buffers
+// carried between items.  Same arithmetic and order as gemv_int_body.
+template <int FMT, int MODE>
+__device__ void gemv_one_body(const GemvArgs &a) {
+    constexpr int R = 2;
+    using CH = ChunkI<FMT, R>;
+    constexpr int LPB = CH::LPB;
+    constexpr bool NORM = MODE == GEMV_QKV;
+    static_assert(MODE == GEMV_PLAIN || MODE == GEMV_QKV, "local modes only");
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float theta_lds[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    constexpr uint32_t NT = GEMV_ONE_WAVES * 64;
+    const uint32_t v0 = (blockIdx.x * GEMV_ONE_WAVES + (uint32_t)wave) * R;
+    const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
+    // x first (loads complete in issue order: staging waits for these only)
+    const uint32_t n16 = xq_bytes(a.cols) / 16;
+    const uint4 *xsrc = (const uint4 *)a.xq;
+    // four named chunks (an array here ends up in scratch memory)
+    constexpr uint32_t XC = 4;
+    const uint32_t xi0 = min((uint32_t)tid, n16 - 1), xi1 = min((uint32_t)tid + NT, n16 - 1);
+    const uint32_t xi2 = min((uint32_t)tid + 2 * NT, n16 - 1), xi3 = min((uint32_t)tid + 3 * NT, n16 - 1);
+    const uint4 xv0 = xsrc[xi0], xv1 = xsrc[xi1], xv2 = xsrc[xi2], xv3 = xsrc[xi3];
+    float sv[4];
+    uint32_t pos = 0;
+    float th = 0.0f;
+    if constexpr (NORM) {
+        const float *ssp = a.n_ss ? a.ss_part : (const float *)a.xq;
+        const uint32_t last = a.n_ss ? a.n_ss - 1 : 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) sv[j] = ssp[min((uint32_t)lane + 64 * j, last)];
+        pos = a.ctl->pos;
+        th = a.rope_tab[min((uint32_t)tid & 63u, a.head_size / 2 - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    CH w;
+    {
+        const uint8_t *rowp[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) rowp[r] = gemv_row_ptr<MODE>(a, min(v0 + r, a.total_rows - 1));
+        w.load(rowp, min(bsub, a.nb - 1), c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        uint4 *dst = (uint4 *)lds;
+        dst[xi0] = xv0;
+        dst[xi1] = xv1;
+        dst[xi2] = xv2;
+        dst[xi3] = xv3;
+        for (uint32_t i = (uint32_t)tid + XC * NT; i < n16; i += NT) dst[i] = xsrc[i];
+    }
+    float rs = 1.0f;
+    if constexpr (NORM) {
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) t += (uint32_t)lane + 64 * j < a.n_ss ? sv[j] : 0.0f;
+        for (uint32_t i = (uint32_t)lane + 256; i < a.n_ss; i += 64) t += a.ss_part[i];
+        t = wave_sum(t);
+        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+        if (tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = th;
+    }
+    __syncthreads();
+    const XQ xq(lds, a.cols);
+    float acc[R] = {0.0f, 0.0f};
+    chunk_step<FMT, R>(w, xq, min(bsub, a.nb - 1), c, bsub < a.nb, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    if constexpr (MODE == GEMV_QKV) {
+        if (lane == 0 && v0 + 1 < a.total_rows) {
+            float x0 = acc[0] * rs, x1 = acc[1] * rs;
+            const uint32_t v = v0;
+            if (v < a.rows0) {
+                rope_pair(x0, x1, v, a.head_size, pos, theta_lds);
+                a.y[v] = x0;
+                a.y[v + 1] = x1;
+            } else {
+                const bool is_k = v < a.rows0 + a.rows1;
+                const uint32_t idx = is_k ? v - a.rows0 : v - a.rows0 - a.rows1;
+                if (is_k) rope_pair(x0, x1, idx, a.head_size, pos, theta_lds);
+                const size_t off = (size_t)pos * a.kv_dim + idx;
+                void *cache = is_k ? a.k_cache : a.v_cache;
+                if (a.kv_f16) {
+                    const uint32_t packed = (uint32_t)f32_to_f16(x0) | ((uint32_t)f32_to_f16(x1) << 16);
+                    *(uint32_t *)((uint16_t *)cache + off) = packed;
+                } else {
+                    ((float *)cache)[off] = x0;
+                    ((float *)cache)[off + 1] = x1;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (lane == r && v0 + r < a.total_rows) a.y[v0 + r] = acc[r] * rs;
+    }
+}
+
 } // namespace ifr

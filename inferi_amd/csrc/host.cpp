@@ -253,6 +253,16 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
         return c->launch(name, dim3(g), dim3((uint32_t)ge.W * 64u), a.cols * 4, a);
     }
     if (!a.xq || (a.total_rows && a.cols % 16)) return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
+    // plain and qkv rows of one 64-lane step: the one-item kernel, every
+    // workgroup launched at once
+    const bool one_mode = !strcmp(mode, "plain") || !strcmp(mode, "qkv");
+    if (one_mode && a.nb <= p.bpi && !c->gemv_waves && !c->gemv_max_grid && a.total_rows) {
+        const uint32_t rows_per = GEMV_ONE_WAVES * 2, g = (a.total_rows + rows_per - 1) / rows_per;
+        a.ks = 1;
+        a.nwaves = GEMV_ONE_WAVES;
+        if (grid_out) *grid_out = g;
+        return c->launch(name + "_one", dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a);
+    }
     const IntGeom g = int_geom(c, p.bpi, mode, a, cap);
     a.ks = g.ks;
     a.nwaves = g.waves;

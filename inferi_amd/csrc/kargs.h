@@ -49,6 +49,10 @@ struct StepCtl {
     uint32_t pad;
 };
 
+// Integer-path GEMV, one-item form (device/gemv.h gemv_one_body): waves per
+// workgroup (two rows each).
+constexpr uint32_t GEMV_ONE_WAVES = 4;
+
 // Integer-path GEMV: at most this many K-slices and 16 waves per workgroup.
 constexpr uint32_t GEMV_KS_MAX = 4;
 constexpr uint32_t GEMV_INT_MAX_WAVES = 16;

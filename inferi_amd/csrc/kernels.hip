@@ -34,7 +34,15 @@ using namespace ifr;
 #define GEMV_INT_WPE 4
 #endif
 
+// one-item form of the local modes (plain, qkv)
+#define GEMV_ONE_KERNEL(NAME, FMT, MODE)                                                               \
+    extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) NAME##_one(GemvArgs a) {         \
+        gemv_one_body<FMT, MODE>(a);                                                                 \
+    }
+
 #define GEMV_ALL_MODES(FMTNAME, FMT)                  \
+    GEMV_ONE_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN) \
+    GEMV_ONE_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)     \
     GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)   \
     GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID)   \
     GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)       \
