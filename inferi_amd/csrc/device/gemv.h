@@ -1427,4 +1427,124 @@ __device__ void gemv_one_body(const GemvArgs &a) {
     }
 }
 
+// One-item form of the grouped modes (RESID, GATEUP): a workgroup owns one
+// output group (16 values: RESID 16 rows, GATEUP 16 gate/up pairs) with RW
+// row waves of R rows times KS K-slices; every wave computes one item (its R
+// rows over one 64-lane K step), the slices are added in LDS in slice
+// order, and wave 0 runs gemv_int_body's epilogue.  Same arithmetic and
+// order as gemv_int_body.
+template <int FMT, int MODE, int R, int RW, int KS>
+__device__ void gemv_grp_body(const GemvArgs &a) {
+    static_assert(MODE == GEMV_RESID || MODE == GEMV_GATEUP, "grouped modes only");
+    constexpr uint32_t GR = RW * R;
+    static_assert(GR == (MODE == GEMV_GATEUP ? 32u : 16u), "one output group per workgroup");
+    constexpr bool NORM = MODE == GEMV_GATEUP;
+    using CH = ChunkI<FMT, R>;
+    constexpr int LPB = CH::LPB, BPI = 64 / LPB;
+    constexpr uint32_t NT = RW * KS * 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float part[KS][GR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t ks = (uint32_t)wave % KS, rw = (uint32_t)wave / KS, g = blockIdx.x;
+    const uint32_t v0 = g * GR + rw * R;
+    const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
+    // x first (four named chunks: an array ends up in scratch memory)
+    const uint32_t n16 = xq_bytes(a.cols) / 16;
+    const uint4 *xsrc = (const uint4 *)a.xq;
+    constexpr uint32_t XC = 4;
+    const uint32_t xi0 = min((uint32_t)tid, n16 - 1), xi1 = min((uint32_t)tid + NT, n16 - 1);
+    const uint32_t xi2 = min((uint32_t)tid + 2 * NT, n16 - 1), xi3 = min((uint32_t)tid + 3 * NT, n16 - 1);
+    const uint4 xv0 = xsrc[xi0], xv1 = xsrc[xi1], xv2 = xsrc[xi2], xv3 = xsrc[xi3];
+    float sv[4];
+    if constexpr (NORM) {
+        const float *ssp = a.n_ss ? a.ss_part : (const float *)a.xq;
+        const uint32_t last = a.n_ss ? a.n_ss - 1 : 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) sv[j] = ssp[min((uint32_t)lane + 64 * j, last)];
+    }
+    // RESID: wave 0 reads the group's residual and next RMSNorm weight
+    float y_pre = 0.0f, g_pre = 1.0f;
+    if constexpr (MODE == GEMV_RESID) {
+        const uint32_t v = g * 16 + ((uint32_t)lane & 15u);
+        if (wave == 0 && lane < 16 && v < a.total_rows) {
+            y_pre = a.y[v];
+            if (a.gamma_next) g_pre = a.gamma_next[v];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    CH w;
+    const uint32_t kb = ks * BPI + bsub;
+    {
+        const uint8_t *rowp[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) rowp[r] = gemv_row_ptr<MODE>(a, min(v0 + r, a.total_rows - 1));
+        w.load(rowp, min(kb, a.nb - 1), c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        uint4 *dst = (uint4 *)lds;
+        dst[xi0] = xv0;
+        dst[xi1] = xv1;
+        dst[xi2] = xv2;
+        dst[xi3] = xv3;
+        for (uint32_t i = (uint32_t)tid + XC * NT; i < n16; i += NT) dst[i] = xsrc[i];
+    }
+    float rs = 1.0f;
+    if constexpr (NORM) {
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) t += (uint32_t)lane + 64 * j < a.n_ss ? sv[j] : 0.0f;
+        for (uint32_t i = (uint32_t)lane + 256; i < a.n_ss; i += 64) t += a.ss_part[i];
+        t = wave_sum(t);
+        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+    }
+    __syncthreads();
+    const XQ xq(lds, a.cols);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    chunk_step<FMT, R>(w, xq, min(kb, a.nb - 1), c, kb < a.nb, acc);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) part[ks][rw * R + r] = acc[r];
+    }
+    lds_barrier();
+    if (wave != 0) return;
+    auto val = [&](uint32_t i) {
+        float t = part[0][i];
+#pragma unroll
+        for (uint32_t k = 1; k < KS; k++) t += part[k][i];
+        return t * rs;
+    };
+    const uint32_t l = (uint32_t)lane & 15u;
+    if constexpr (MODE == GEMV_RESID) {
+        // x += W v, then x * gamma_next quantized for the next GEMV
+        const uint32_t v = g * 16 + l;
+        const bool ok = lane < 16 && v < a.total_rows;
+        float xn = 0.0f;
+        if (ok) {
+            xn = y_pre + val(l);
+            a.y[v] = xn;
+        }
+        if (a.xq_out) {
+            quant16(xn * g_pre, ok, a.xq_out, a.total_rows, v, lane);
+            const float sq = sum16(xn * xn);
+            if (lane == 0) a.ss_out[g] = sq;
+        }
+    } else {
+        // h[j] = up * silu(gate), quantized for the down GEMV
+        const uint32_t K = a.total_rows / 2, v = g * 16 + l;
+        const bool ok = lane < 16 && v < K;
+        float h = 0.0f;
+        if (ok) {
+            const float gt = val(2 * l), up = val(2 * l + 1);
+            h = up * (gt / (1.0f + expf(-gt)));
+            a.y[v] = h;
+        }
+        if (a.xq_out) quant16(h, ok, a.xq_out, K, v, lane);
+    }
+}
+
 } // namespace ifr

@@ -115,6 +115,10 @@ struct ifr_ctx {
     // launch per layer (device/pk.h) where the model allows it
     int persistent = 0;
     int pk_trace_layer = -1; // layer whose persistent launch records its stage timeline
+    // grouped one-item GEMV forms in use: bit 0 resid with one K step (O),
+    // bit 1 resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16
+    // waves of two rows (else 8 waves of four)
+    int gemv_grp = 1;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -263,6 +267,27 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
         if (grid_out) *grid_out = g;
         return c->launch(name + "_one", dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a);
     }
+    // resid and gateup: one output group per workgroup, one item per wave,
+    // where the code object has the form for this format and K
+    const bool resid = !strcmp(mode, "resid"), gateup = !strcmp(mode, "gateup");
+    if ((resid || gateup) && !c->gemv_waves && !c->gemv_max_grid && a.total_rows) {
+        const uint32_t steps = (a.nb + p.bpi - 1) / p.bpi;
+        char kn[96] = {0};
+        const bool alt = c->gemv_grp & 8;
+        if (resid && steps == 1 && (c->gemv_grp & 1)) snprintf(kn, sizeof kn, "gemv_%s_resid_r2w8k1", p.fmt);
+        else if (resid && steps > 1 && steps <= 4 && (c->gemv_grp & 2)) snprintf(kn, sizeof kn, "gemv_%s_resid_r4w4k4", p.fmt);
+        else if (gateup && steps == 1 && (c->gemv_grp & 4))
+            snprintf(kn, sizeof kn, alt ? "gemv_%s_gateup_r2w16k1" : "gemv_%s_gateup_r4w8k1", p.fmt);
+        hipFunction_t f = kn[0] ? c->fn(kn) : nullptr;
+        if (f) {
+            const uint32_t gr = gateup ? 32 : 16, g = (a.total_rows + gr - 1) / gr;
+            const uint32_t waves = resid && steps == 1 ? 8 : resid ? 16 : alt ? 16 : 8;
+            a.ks = steps;
+            a.nwaves = waves;
+            if (grid_out) *grid_out = g;
+            return c->launch(kn, dim3(g), dim3(waves * 64), (uint32_t)xq_bytes(a.cols), a);
+        }
+    }
     const IntGeom g = int_geom(c, p.bpi, mode, a, cap);
     a.ks = g.ks;
     a.nwaves = g.waves;
@@ -383,6 +408,7 @@ struct ifr_llama2_state {
     // captured decode step
     hipGraphExec_t graph = nullptr;
     int graph_pk = -1;
+    int graph_grp = -1;
     uint32_t graph_sampler = 0;
     const ifr_llama2_weights *graph_w = nullptr;
     int graph_fused = -1;
@@ -921,6 +947,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
     }
     if (!strcmp(key, "persistent")) {
         c->persistent = value ? 1 : 0;
+        return IFR_OK;
+    }
+    if (!strcmp(key, "gemv_grp")) {
+        c->gemv_grp = (int)value;
         return IFR_OK;
     }
     if (!strcmp(key, "pk_trace_layer")) {
@@ -1673,7 +1703,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         return IFR_OK;
     }
     if (!s->graph || s->graph_w != w || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
-        s->graph_sampler != s->sampler_gen || s->graph_pk != c->persistent) {
+        s->graph_sampler != s->sampler_gen || s->graph_pk != c->persistent || s->graph_grp != c->gemv_grp) {
         if (s->graph) {
             hipStreamSynchronize(c->stream);
             hipGraphExecDestroy(s->graph);
@@ -1697,6 +1727,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         s->graph_exact = c->gemv_exact;
         s->graph_sampler = s->sampler_gen;
         s->graph_pk = c->persistent;
+        s->graph_grp = c->gemv_grp;
     }
     for (uint32_t i = 0; i < n_steps; i++)
         if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;

@@ -40,6 +40,16 @@ using namespace ifr;
         gemv_one_body<FMT, MODE>(a);                                                                 \
     }
 
+// one-item form of the grouped modes: R rows per wave, RW row waves, KS K-slices
+#define GEMV_GRP_KERNEL(NAME, FMT, MODE, R, RW, KS)                                                     \
+    extern "C" __global__ void __launch_bounds__(RW * KS * 64) NAME##_r##R##w##RW##k##KS(GemvArgs a) { \
+        gemv_grp_body<FMT, MODE, R, RW, KS>(a);                                                         \
+    }
+GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 2, 8, 1)
+GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 4, 4, 4)
+GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 4, 8, 1)
+GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 2, 16, 1)
+
 #define GEMV_ALL_MODES(FMTNAME, FMT)                  \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN) \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)     \
