@@ -87,10 +87,17 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
 
 /* Knobs (no reference counterpart): "gemv_max_grid" sets the number of GEMV
  * workgroups (0 = chosen by shape, the default); "gemv_waves" caps the
- * waves per GEMV workgroup (1, 2, 4, 8 or 16; 0 = chosen by shape); "gemv_exact" = 1
+ * waves per GEMV workgroup (1, 2, 4, 8 or 16; 0 = chosen by shape); either
+ * one also turns off the one-item GEMV forms.  "gemv_exact" = 1
  * makes every GEMV keep x in fp32 and use fp32 FMAs, instead of the default
  * path that takes x as 22-bit fixed point per 16 elements and multiplies
- * with int8 dot products (see ifr_quantize_activation). */
+ * with int8 dot products (see ifr_quantize_activation).  "gemv_grp" selects
+ * the one-item forms of the grouped decode GEMVs (bit 0 attention output,
+ * the default; bit 1 FFN down; bit 2 gate/up, bit 3 with 16 waves of two
+ * rows; bit 4 the output head).  "persistent" = 1 runs the decode step's
+ * GEMV stages between two attentions (O, gate/up, down, the next QKV) as one
+ * persistent launch per layer with grid barriers (Q4_K models; results
+ * identical to the default path). */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */

@@ -1337,8 +1337,8 @@ __device__ void gemv_one_body(const GemvArgs &a) {
     constexpr int R = 2;
     using CH = ChunkI<FMT, R>;
     constexpr int LPB = CH::LPB;
-    constexpr bool NORM = MODE == GEMV_QKV;
-    static_assert(MODE == GEMV_PLAIN || MODE == GEMV_QKV, "local modes only");
+    constexpr bool NORM = MODE == GEMV_QKV || MODE == GEMV_HEAD;
+    static_assert(MODE == GEMV_PLAIN || MODE == GEMV_QKV || MODE == GEMV_HEAD, "local modes only");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float theta_lds[64];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1361,8 +1361,10 @@ __device__ void gemv_one_body(const GemvArgs &a) {
         const uint32_t last = a.n_ss ? a.n_ss - 1 : 0;
 #pragma unroll
         for (uint32_t j = 0; j < 4; j++) sv[j] = ssp[min((uint32_t)lane + 64 * j, last)];
-        pos = a.ctl->pos;
-        th = a.rope_tab[min((uint32_t)tid & 63u, a.head_size / 2 - 1)];
+        if constexpr (MODE == GEMV_QKV) {
+            pos = a.ctl->pos;
+            th = a.rope_tab[min((uint32_t)tid & 63u, a.head_size / 2 - 1)];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     CH w;
@@ -1389,7 +1391,7 @@ __device__ void gemv_one_body(const GemvArgs &a) {
         for (uint32_t i = (uint32_t)lane + 256; i < a.n_ss; i += 64) t += a.ss_part[i];
         t = wave_sum(t);
         rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
-        if (tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = th;
+        if (MODE == GEMV_QKV && tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = th;
     }
     __syncthreads();
     const XQ xq(lds, a.cols);
@@ -1421,9 +1423,29 @@ __device__ void gemv_one_body(const GemvArgs &a) {
             }
         }
     } else {
+        uint64_t best = 0;
 #pragma unroll
         for (int r = 0; r < R; r++)
-            if (lane == r && v0 + r < a.total_rows) a.y[v0 + r] = acc[r] * rs;
+            if (v0 + r < a.total_rows) {
+                const float y = acc[r] * rs;
+                if (lane == r) a.y[v0 + r] = y;
+                if constexpr (MODE == GEMV_HEAD) {
+                    const uint64_t k = argmax_key(y, v0 + r);
+                    best = k > best ? k : best;
+                }
+            }
+        if constexpr (MODE == GEMV_HEAD) {
+            // the workgroup's key (every lane of a wave holds its wave's)
+            __shared__ uint64_t kred[GEMV_ONE_WAVES];
+            if (lane == 0) kred[wave] = best;
+            __syncthreads();
+            if (tid == 0 && a.part_keys) {
+                uint64_t b = kred[0];
+#pragma unroll
+                for (uint32_t w2 = 1; w2 < GEMV_ONE_WAVES; w2++) b = kred[w2] > b ? kred[w2] : b;
+                a.part_keys[blockIdx.x] = b;
+            }
+        }
     }
 }
 

@@ -381,6 +381,7 @@ struct ifr_llama2_state {
     ifr_rope_config *rope_cfg;
     ifr_attn_params *attn_params;
     uint64_t *part_keys;
+    uint32_t part_keys_cap = 0; // entries of part_keys
     float *part_o, *part_ml;
     float *rope_tab;
     // quantized activations passed between the fused kernels, and the
@@ -819,7 +820,17 @@ static ifr_status enqueue_head(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         a.eps = cfg.rms_eps;
         a.y = s->logits;
         a.part_keys = s->part_keys;
-        if ((st = launch_gemv(c, p, "head", a, MAX_PARTS, &n_parts))) return st;
+        // one item per wave and a key per workgroup when the state holds them
+        const uint32_t one_grid = (cfg.vocab + GEMV_ONE_WAVES * 2 - 1) / (GEMV_ONE_WAVES * 2);
+        const std::string one = std::string("gemv_") + p.fmt + "_head_one";
+        if ((c->gemv_grp & 16) && !c->gemv_exact && p.nb <= p.bpi && one_grid <= s->part_keys_cap && c->fn(one)) {
+            a.ks = 1;
+            a.nwaves = GEMV_ONE_WAVES;
+            if ((st = c->launch(one, dim3(one_grid), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a))) return st;
+            n_parts = one_grid;
+        } else if ((st = launch_gemv(c, p, "head", a, MAX_PARTS, &n_parts))) {
+            return st;
+        }
     } else {
         EltArgs n{};
         n.a = s->xb;
@@ -1469,7 +1480,8 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     A(s->tokens, ((size_t)cfg->max_pos + 1) * 4)
     A(s->ctl, sizeof(StepCtl)) A(s->rms_cfg, sizeof(ifr_rms_norm_config)) A(s->rope_cfg, sizeof(ifr_rope_config))
     A(s->attn_params, sizeof(ifr_attn_params))
-    A(s->part_keys, MAX_PARTS * 8)
+    s->part_keys_cap = std::max(MAX_PARTS, (uint32_t)((cfg->vocab + GEMV_ONE_WAVES * 2 - 1) / (GEMV_ONE_WAVES * 2)));
+    A(s->part_keys, (size_t)s->part_keys_cap * 8)
     A(s->part_o, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * s->head_size * 4)
     A(s->part_ml, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * 2 * 4)
     A(s->rope_tab, (size_t)s->head_size / 2 * 4)

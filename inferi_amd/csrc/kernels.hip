@@ -53,6 +53,7 @@ GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 2, 16, 1)
 #define GEMV_ALL_MODES(FMTNAME, FMT)                  \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN) \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)     \
+    GEMV_ONE_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD)   \
     GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)   \
     GEMV_KERNEL(gemv_##FMTNAME##_resid, FMT, GEMV_RESID)   \
     GEMV_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)       \

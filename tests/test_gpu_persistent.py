@@ -132,3 +132,31 @@ def test_c5_shape_same_as_fused(ctx):
         check_same_as_fused(ctx, cfg, w, [17, 128255, 0, 4242], 8)
     finally:
         w.close()
+
+
+@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31])
+def test_gemv_forms_same_results(ctx, grp):
+    """Every GEMV form the gemv_grp option selects (the looping body, the
+    one-item forms of O, down, gate/up and the head) gives the default
+    path's logits, tokens and KV rows bit for bit (same arithmetic, same
+    reduction orders), on the C4 shape."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=4, hidden=2048, ffn=5632, n_heads=32, n_kv_heads=4, vocab=32000, max_pos=32,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=1000)
+    try:
+        prompt = [5, 31999, 7, 1234]
+        ref = decode(ctx, cfg, w, prompt, 12, persistent=False)
+        ctx.set_option("gemv_grp", grp)
+        try:
+            got = decode(ctx, cfg, w, prompt, 12, persistent=False)
+        finally:
+            ctx.set_option("gemv_grp", 1)
+        assert_same(got[0], ref[0], "logits")
+        assert np.array_equal(got[1], ref[1]), "tokens"
+        for k in ref[2]:
+            assert_same(got[2][k], ref[2][k], f"{k[0]} layer {k[1]}")
+        assert_same(got[3], ref[3], "residual x")
+    finally:
+        w.close()
