@@ -88,7 +88,7 @@ struct Pk {
         : a(args), lds(l), tid((int)threadIdx.x), lane((int)threadIdx.x & 63),
           wave(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)), b(blockIdx.x), nwg(gridDim.x) {}
 
-    IFR_DEV uint32_t xq_off_part() const { return (xq_bytes(max(a.hidden, a.ffn)) + 15u) & ~15u; }
+    IFR_DEV uint32_t xq_off_part() const { return pk_xq_region(max(a.hidden, a.ffn)); }
     IFR_DEV float *part() const { return (float *)(lds + xq_off_part()); } // [PK_PART_ROWS][PK_KSTEPS]
 
     // ------------------------------------------------------------ barrier
@@ -116,24 +116,35 @@ struct Pk {
         }
     }
 
-    // End of a stage: every thread's stores complete, one arrival, the next
-    // stage's weights requested by the compute waves (pf), the barrier, then
-    // the next stage's input staged into LDS (stage).
-    template <typename PF, typename ST>
-    IFR_DEV void stage_end(PF &&pf, ST &&stage, uint32_t n_total) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // The boundary after a stage's items.  The compute waves store nothing
+    // (wave 0 writes every output), so once the items' sums are in LDS they
+    // request the next stage's first items (pf); wave 0 runs the stage's
+    // epilogue (epi) meanwhile, waits
+    // for its stores, arrives and waits for every workgroup, then stages
+    // the next stage's input into LDS by itself (st: its loads do not queue
+    // behind the prefetch, since a wave's loads return in order).
+    template <typename PF, typename EPI, typename ST>
+    IFR_DEV void stage_boundary(PF &&pf, EPI &&epi, ST &&stage, uint32_t n_total) {
         __syncthreads();
-        if (tid == 0) arrive();
+        stamp(4 * nbar + 2);
+        // (issuing the prefetch can stall while the memory pipeline is
+        // full: the epilogue runs meanwhile)
         if (wave != 0) pf();
-        if (tid == 0) {
-            wait_all();
+        if (wave == 0) {
+            epi();
+            stamp(4 * nbar + 3);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            if (lane == 0) {
+                arrive();
+                wait_all();
+                // every workgroup has read the epoch: advance it for the next launch
+                if (nbar == 0 && b == 0)
+                    __hip_atomic_store(a.bar + PK_BAR_EPOCH, epoch + n_total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             stamp(4 * nbar + 4);
-            // every workgroup has read the epoch: advance it for the next launch
-            if (nbar == 0 && b == 0) __hip_atomic_store(a.bar + PK_BAR_EPOCH, epoch + n_total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            stage();
         }
         nbar++;
-        __syncthreads();
-        stage();
         __syncthreads();
         stamp(4 * nbar + 1);
     }
@@ -203,23 +214,19 @@ struct Pk {
         load_item<MODE>(B, g, cw + PK_CW);
     }
 
-    // The input XQ of K values into LDS (all threads), and for a normalising
-    // stage wave 0's RMSNorm scale from the n_ss partial sums of x^2.
+    // Wave 0: the input XQ of K values into LDS with LDS-direct loads (1 KB
+    // per instruction, none waits on another; the last chunk's lanes past
+    // the end re-read the last 16 bytes, the LDS region is whole KBs), and
+    // for a normalising stage the RMSNorm scale from the n_ss partial sums
+    // of x^2.
     IFR_DEV void stage_xq(const uint8_t *src, uint32_t K, const float *ss, uint32_t n_ss) {
-        const uint32_t n16 = xq_bytes(K) / 16;
+        const uint32_t n16 = xq_bytes(K) / 16, nk = (n16 + 63) / 64;
         const uint4 *s4 = (const uint4 *)src;
-        uint4 *d4 = (uint4 *)lds;
-        constexpr uint32_t NC = 5;
-        uint4 v[NC];
-        for (uint32_t base = 0; base < n16; base += NC * PK_THREADS) {
-#pragma unroll
-            for (uint32_t j = 0; j < NC; j++) v[j] = s4[min(base + (uint32_t)tid + j * PK_THREADS, n16 - 1u)];
-#pragma unroll
-            for (uint32_t j = 0; j < NC; j++)
-                if (base + (uint32_t)tid + j * PK_THREADS < n16) d4[base + tid + j * PK_THREADS] = v[j];
-        }
-        if (!ss) rs = 1.0f;
-        if (ss && wave == 0) {
+        for (uint32_t k = 0; k < nk; k++)
+            __builtin_amdgcn_global_load_lds((const void *)(s4 + min(k * 64 + (uint32_t)lane, n16 - 1)),
+                                             (__attribute__((address_space(3))) void *)(lds + k * 1024), 16, 0, 0);
+        rs = 1.0f;
+        if (ss) {
             // the order of gemv_int_body's prologue
             constexpr uint32_t SC = 4;
             float sv[SC];
@@ -233,6 +240,7 @@ struct Pk {
             t = wave_sum(t);
             rs = 1.0f / sqrtf(t / (float)K + a.eps); // rms_norm.rs:115
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
 
     // Compute waves: every item, partial row sums into LDS part[row][step].
@@ -375,51 +383,44 @@ struct Pk {
         epoch = a.bar[PK_BAR_EPOCH];
         pos = a.ctl->pos;
         const bool has_qkv = a.wq != nullptr;
+        auto none = [] {};
         if (a.mode == 0) {
             const PkGemv gq = desc_qkv();
             embed();
-            stage_end([&] { prefetch<GEMV_QKV>(gq); }, [&] { stage_xq(a.xq_a, a.hidden, a.ss_a, a.n_ss_a); }, 1u);
+            // the embedding's stores are every storing wave's: complete before the arrival
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            stage_boundary([&] { prefetch<GEMV_QKV>(gq); }, none,
+                           [&] { stage_xq(a.xq_a, a.hidden, a.ss_a, a.n_ss_a); }, 1u);
             qkv_stage(gq);
             return;
         }
         const uint32_t n_total = has_qkv ? 3u : 2u;
         stamp(0);
-        {   // O: its input comes from the previous kernel
-            const PkGemv go = desc_o();
-            if (wave != 0) prefetch<GEMV_RESID>(go);
-            stage_xq(a.xq_att, a.hidden, nullptr, 0);
-            __syncthreads();
-            stamp(1);
-            gemv_items<GEMV_RESID>(go);
-            __syncthreads();
-            stamp(2);
-            if (wave == 0) epi_resid(go, a.x, a.x_mid, a.ffn_norm, a.xq_f, a.ss_f);
-            stamp(3);
-        }
-        {
-            const PkGemv gg = desc_gateup();
-            stage_end([&] { prefetch<GEMV_GATEUP>(gg); }, [&] { stage_xq(a.xq_f, a.hidden, a.ss_f, a.hidden / 16); },
-                      n_total);
-            gemv_items<GEMV_GATEUP>(gg);
-            __syncthreads();
-            stamp(6);
-            if (wave == 0) epi_gateup(gg);
-            stamp(7);
-        }
-        {
-            const PkGemv gd = desc_down();
-            stage_end([&] { prefetch<GEMV_RESID>(gd); }, [&] { stage_xq(a.xq_h, a.ffn, nullptr, 0); }, n_total);
-            gemv_items<GEMV_RESID>(gd);
-            __syncthreads();
-            stamp(10);
-            if (wave == 0) epi_resid(gd, a.x_mid, a.x, a.next_norm, a.xq_a, a.ss_a);
-            stamp(11);
-        }
+        const PkGemv go = desc_o();
+        // O: its input comes from the previous kernel
+        if (wave != 0) prefetch<GEMV_RESID>(go);
+        else stage_xq(a.xq_att, a.hidden, nullptr, 0);
+        __syncthreads();
+        stamp(1);
+        gemv_items<GEMV_RESID>(go);
+        const PkGemv gg = desc_gateup();
+        stage_boundary([&] { prefetch<GEMV_GATEUP>(gg); },
+                       [&] { epi_resid(go, a.x, a.x_mid, a.ffn_norm, a.xq_f, a.ss_f); },
+                       [&] { stage_xq(a.xq_f, a.hidden, a.ss_f, a.hidden / 16); }, n_total);
+        gemv_items<GEMV_GATEUP>(gg);
+        const PkGemv gd = desc_down();
+        stage_boundary([&] { prefetch<GEMV_RESID>(gd); }, [&] { epi_gateup(gg); },
+                       [&] { stage_xq(a.xq_h, a.ffn, nullptr, 0); }, n_total);
+        gemv_items<GEMV_RESID>(gd);
         if (has_qkv) {
             const PkGemv gq = desc_qkv();
-            stage_end([&] { prefetch<GEMV_QKV>(gq); }, [&] { stage_xq(a.xq_a, a.hidden, a.ss_a, a.hidden / 16); },
-                      n_total);
+            stage_boundary([&] { prefetch<GEMV_QKV>(gq); },
+                           [&] { epi_resid(gd, a.x_mid, a.x, a.next_norm, a.xq_a, a.ss_a); },
+                           [&] { stage_xq(a.xq_a, a.hidden, a.ss_a, a.hidden / 16); }, n_total);
             qkv_stage(gq);
+        } else {
+            __syncthreads();
+            if (wave == 0) epi_resid(gd, a.x_mid, a.x, a.next_norm, a.xq_a, a.ss_a);
         }
     }
 };

@@ -260,7 +260,9 @@ constexpr uint32_t PK_BAR_EPOCH = 32;
 constexpr uint32_t PK_BAR_WORDS = 64 * 9;
 // dynamic LDS: the input XQ (K values, K the larger of hidden and ffn) and
 // the item partials
-constexpr uint32_t pk_lds_bytes(uint32_t kmax) { return ((3 * kmax + kmax / 2 + 15) & ~15u) + PK_PART_ROWS * PK_KSTEPS * 4; }
+// (the XQ region in whole KBs: it is filled 1 KB per wave instruction)
+constexpr uint32_t pk_xq_region(uint32_t kmax) { return (3 * kmax + kmax / 2 + 1023) & ~1023u; }
+constexpr uint32_t pk_lds_bytes(uint32_t kmax) { return pk_xq_region(kmax) + PK_PART_ROWS * PK_KSTEPS * 4; }
 
 struct PkArgs {
     int32_t mode;                  // 0: embedding + QKV of layer 0; 1: O, gate/up, down (+ the next QKV)
