@@ -233,7 +233,7 @@ def run_decode(args) -> None:
     # the dominant kernel: Q4_K GEMV, measured on its plain form at the
     # 14336x4096 shape of the FFN projections
     g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
-    log(f"bench: gemv_q4_k_plain 14336x4096: {g['us']:.2f} us/launch, {g['gbs']:.0f} GB/s")
+    log(f"bench: gemv_q4_k_plain_one 14336x4096: {g['us']:.2f} us/launch, {g['gbs']:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -270,7 +270,7 @@ def run_decode(args) -> None:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_q4_k_plain 14336x4096 (Q4_K, 33,103,872 algorithmic bytes per launch)",
+            "kernel": "gemv_q4_k_plain_one 14336x4096 (Q4_K, 33,103,872 algorithmic bytes per launch)",
             "achieved": round(g["gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -306,7 +306,7 @@ def run_pmc_sample(args) -> None:
     """Workload for the rocprofv3 --pmc passes behind roofline.traffic: the
     element-wise add kernel (add_k) over 64 Mi floats, whose HBM traffic is
     known (reads 2 x 256 MiB, writes 256 MiB), calibrates FETCH_SIZE and
-    WRITE_SIZE; then the roofline kernel (gemv_q4_k_plain 14336x4096) on
+    WRITE_SIZE; then the roofline kernel (gemv_q4_k_plain_one 14336x4096) on
     weight copies rotated past the Infinity Cache."""
     ctx = I.LlmContext(0, args.code_object)
     n = 64 << 20
@@ -319,7 +319,7 @@ def run_pmc_sample(args) -> None:
     a.free()
     b.free()
     g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
-    log(f"pmc sample: add_k {3} x {n} floats; gemv_q4_k_plain 14336x4096 {g['us']:.2f} us")
+    log(f"pmc sample: add_k {3} x {n} floats; gemv_q4_k_plain_one 14336x4096 {g['us']:.2f} us")
     ctx.close()
 
 
