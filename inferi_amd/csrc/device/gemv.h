@@ -408,6 +408,47 @@ IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int 
     }
 }
 
+// The same quantization with four consecutive values per lane: a quad of
+// lanes holds one 16-value group (lane & 3 = which four).  The maximum, the
+// scale and every digit are quant16's; the sum of codes is formed as
+// quant16's is (exact 8-value halves, one final rounding), so the bytes are
+// identical.  Writes through a generic pointer (LDS or global memory); the
+// caller's quad holds elements 4c .. 4c+15 with c % 4 == 0 at lane & 3 == 0.
+IFR_DEV void quant4x4(float4 v, bool ok, uint8_t *xq, uint32_t K, uint32_t c) {
+    float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    am = fmaxf(am, dpp_f<DPP_QUAD_XOR1>(am));
+    am = fmaxf(am, dpp_f<DPP_QUAD_XOR2>(am));
+    const float sc = am / XQ_MAXCODE;
+    const float inv = am > 0.0f ? XQ_MAXCODE / am : 0.0f;
+    const float vals[4] = {v.x, v.y, v.z, v.w};
+    uint32_t wa = 0, wb = 0, wc = 0;
+    float qf[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int q = (int)rintf(clampf(vals[e] * inv, -XQ_MAXCODE, XQ_MAXCODE));
+        const int dc = ((q + 128) & 0xFF) - 128;
+        const int q1 = (q - dc) >> 8;
+        const int db = ((q1 + 128) & 0xFF) - 128;
+        const int da = (q1 - db) >> 8;
+        wa |= ((uint32_t)da & 0xFFu) << (8 * e);
+        wb |= ((uint32_t)db & 0xFFu) << (8 * e);
+        wc |= ((uint32_t)dc & 0xFFu) << (8 * e);
+        qf[e] = (float)q;
+    }
+    const float s4 = (qf[0] + qf[1]) + (qf[2] + qf[3]);
+    const float s8 = s4 + dpp_f<DPP_QUAD_XOR1>(s4);
+    const float sq = s8 + dpp_f<DPP_QUAD_XOR2>(s8);
+    if (ok) {
+        *(uint32_t *)(xq + 4 * c) = wa;
+        *(uint32_t *)(xq + K + 4 * c) = wb;
+        *(uint32_t *)(xq + 2 * K + 4 * c) = wc;
+        if ((c & 3u) == 0) {
+            ((float *)(xq + 3 * K))[c / 4] = sc;
+            ((float *)(xq + 3 * K + K / 4))[c / 4] = sc * sq;
+        }
+    }
+}
+
 IFR_DEV uint4 ld_u4(const int8_t *p) { return *(const uint4 *)__builtin_assume_aligned(p, 16); }
 IFR_DEV int sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
 // c + sum over four words of codes q and x digits
@@ -996,7 +1037,7 @@ __device__ void gemv_f32_body(const GemvArgs &a) {
 //    once per group and wave 0 adds the K-slices and runs the epilogue on the
 //    group's 16 outputs (residual add and quantization of x * gamma_next for
 //    the next GEMV, or silu(gate) * up and its quantization).
-template <int FMT, int MODE, bool PIPE, int NI = 1>
+template <int FMT, int MODE, bool PIPE, int NI = 1, bool XF = false>
 __device__ void gemv_int_body(const GemvArgs &a) {
     constexpr int R = 2;
     using CH = ChunkI<FMT, R>;
@@ -1077,9 +1118,11 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     // The first XC chunks per thread and SC partial sums per lane are
     // straight-line loads of clamped (valid) addresses; loops cover larger
     // inputs.
+    // XF: x arrives in f32 (four values per thread and chunk) and this
+    // kernel quantizes it into LDS itself (quant4x4, quant16's bytes)
     constexpr uint32_t XC = 4, SC = 4;
-    const uint32_t n16 = xq_bytes(a.cols) / 16;
-    const uint4 *xsrc = (const uint4 *)a.xq;
+    const uint32_t n16 = XF ? a.cols / 4 : xq_bytes(a.cols) / 16;
+    const uint4 *xsrc = XF ? (const uint4 *)a.x : (const uint4 *)a.xq;
     static_assert(XC == 4, "four named chunks");
     const uint32_t xi0 = min((uint32_t)tid, n16 - 1), xi1 = min((uint32_t)tid + NT, n16 - 1);
     const uint32_t xi2 = min((uint32_t)tid + 2 * NT, n16 - 1), xi3 = min((uint32_t)tid + 3 * NT, n16 - 1);
@@ -1121,7 +1164,22 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     Item c2 = next(cur);
     if constexpr (NI >= 2) load(B, c2.g < ngroups ? c2 : cur);
     __builtin_amdgcn_sched_barrier(0);
-    {
+    if constexpr (XF) {
+        // every quad of lanes quantizes one 16-value group per chunk; a
+        // thread past the end quantizes the last chunk again (stores off)
+        auto qc = [&](uint4 u, uint32_t i, uint32_t c) {
+            quant4x4(make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)),
+                     i < n16, lds, a.cols, c);
+        };
+        qc(xv0, (uint32_t)tid, xi0);
+        qc(xv1, (uint32_t)tid + NT, xi1);
+        qc(xv2, (uint32_t)tid + 2 * NT, xi2);
+        qc(xv3, (uint32_t)tid + 3 * NT, xi3);
+        for (uint32_t base = XC * NT; base < n16; base += NT) {
+            const uint32_t i = base + (uint32_t)tid;
+            qc(xsrc[min(i, n16 - 1)], i, min(i, n16 - 1));
+        }
+    } else {
         uint4 *dst = (uint4 *)lds;
         // unconditional stores (a thread past the end rewrites the last
         // chunk with its own value), so no load is moved behind a branch
@@ -1337,8 +1395,9 @@ __device__ void gemv_one_body(const GemvArgs &a) {
     constexpr int R = 2;
     using CH = ChunkI<FMT, R>;
     constexpr int LPB = CH::LPB;
-    constexpr bool NORM = MODE == GEMV_QKV || MODE == GEMV_HEAD;
-    static_assert(MODE == GEMV_PLAIN || MODE == GEMV_QKV || MODE == GEMV_HEAD, "local modes only");
+    constexpr bool NORM = MODE == GEMV_QKV || MODE == GEMV_HEAD || MODE == GEMV_GATEUP;
+    static_assert(MODE == GEMV_PLAIN || MODE == GEMV_QKV || MODE == GEMV_HEAD || MODE == GEMV_GATEUP,
+                  "modes whose waves finish their own rows");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float theta_lds[64];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1399,7 +1458,14 @@ __device__ void gemv_one_body(const GemvArgs &a) {
     chunk_step<FMT, R>(w, xq, min(bsub, a.nb - 1), c, bsub < a.nb, acc);
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
-    if constexpr (MODE == GEMV_QKV) {
+    if constexpr (MODE == GEMV_GATEUP) {
+        // virtual rows v0 (gate j), v0 + 1 (up j): h[j] = up * silu(gate), in
+        // f32 (the down GEMV quantizes it)
+        if (lane == 0 && v0 + 1 < a.total_rows) {
+            const float gt = acc[0] * rs, up = acc[1] * rs;
+            a.y[v0 >> 1] = up * (gt / (1.0f + expf(-gt)));
+        }
+    } else if constexpr (MODE == GEMV_QKV) {
         if (lane == 0 && v0 + 1 < a.total_rows) {
             float x0 = acc[0] * rs, x1 = acc[1] * rs;
             const uint32_t v = v0;

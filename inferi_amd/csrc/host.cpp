@@ -115,10 +115,11 @@ struct ifr_ctx {
     // launch per layer (device/pk.h) where the model allows it
     int persistent = 0;
     int pk_trace_layer = -1; // layer whose persistent launch records its stage timeline
-    // grouped one-item GEMV forms in use: bit 0 resid with one K step (O),
-    // bit 1 resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16
-    // waves of two rows (else 8 waves of four)
-    int gemv_grp = 1;
+    // one-item GEMV forms in use: bit 0 resid with one K step (O), bit 1
+    // resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16 waves of
+    // two rows (else 8 waves of four), bit 4 the output head, bit 5 gateup
+    // with h in f32 and the down GEMV quantizing it (default: bits 0 and 5)
+    int gemv_grp = 33;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -609,6 +610,11 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype &&
                               cfg.rope_variant == IFR_ROPE_ORIGINAL && !has_bias;
         const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
+        // gate/up as one item per wave with h in f32, quantized by the down
+        // GEMV itself (Q4_K, rows of one K step; option gemv_grp bit 5)
+        const bool h32 = fuse_ffn && (c->gemv_grp & 32) && !c->gemv_exact && !c->gemv_waves && !c->gemv_max_grid &&
+                         Lw.ffn_gate.dtype == IFR_Q4_K && Lw.ffn_down.dtype == IFR_Q4_K && hidden <= 4096 &&
+                         hidden % 256 == 0 && c->fn("gemv_q4_k_gateup_one") && c->fn("gemv_q4_k_resid_xf");
         const float *next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
         GemvPlan p;
 
@@ -741,7 +747,17 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.eps = cfg.rms_eps;
             a.y = s->hb;
             a.xq_out = s->xq_h;
-            if ((st = launch_gemv(c, p, "gateup", a))) return st;
+            if (h32) {
+                a.xq_out = nullptr;
+                a.ks = 1;
+                a.nwaves = GEMV_ONE_WAVES;
+                const uint32_t g = (a.total_rows + GEMV_ONE_WAVES * 2 - 1) / (GEMV_ONE_WAVES * 2);
+                if ((st = c->launch("gemv_q4_k_gateup_one", dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols),
+                                    a)))
+                    return st;
+            } else if ((st = launch_gemv(c, p, "gateup", a))) {
+                return st;
+            }
         } else {
             EltArgs n{};
             n.a = s->xb;
@@ -775,7 +791,16 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.xq_out = s->xq_a;
             a.ss_out = s->ss_a;
             a.gamma_next = next_norm;
-            if ((st = launch_gemv(c, p, "resid", a))) return st;
+            if (h32) {
+                a.xq = nullptr; // h arrives in f32 (a.x) and is quantized in LDS
+                const IntGeom g = int_geom(c, p.bpi, "resid", a, 0);
+                a.ks = g.ks;
+                a.nwaves = g.waves;
+                if ((st = c->launch("gemv_q4_k_resid_xf", dim3(g.grid), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a)))
+                    return st;
+            } else if ((st = launch_gemv(c, p, "resid", a))) {
+                return st;
+            }
             n_ss_a = n_ss_res;
         } else {
             if ((st = gemv_plain(c, s->xb2, Lw.ffn_down.data, Lw.ffn_down.dtype, hidden, ffn, s->hb, s->xq_u))) return st;

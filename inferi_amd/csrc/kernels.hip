@@ -45,6 +45,14 @@ using namespace ifr;
     extern "C" __global__ void __launch_bounds__(RW * KS * 64) NAME##_r##R##w##RW##k##KS(GemvArgs a) { \
         gemv_grp_body<FMT, MODE, R, RW, KS>(a);                                                         \
     }
+// gate/up with h in f32, and the down GEMV that quantizes its f32 input itself
+extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) gemv_q4_k_gateup_one(GemvArgs a) {
+    gemv_one_body<Q4_K, GEMV_GATEUP>(a);
+}
+extern "C" __global__ void __launch_bounds__(GEMV_INT_MAX_WAVES * 64)
+    __attribute__((amdgpu_waves_per_eu(GEMV_INT_WPE, 8))) gemv_q4_k_resid_xf(GemvArgs a) {
+    gemv_int_body<Q4_K, GEMV_RESID, GEMV_INT_PIPE, GEMV_INT_NI, true>(a);
+}
 GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 2, 8, 1)
 GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 4, 4, 4)
 GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 4, 8, 1)

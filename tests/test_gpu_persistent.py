@@ -134,7 +134,7 @@ def test_c5_shape_same_as_fused(ctx):
         w.close()
 
 
-@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31])
+@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31, 33, 63])
 def test_gemv_forms_same_results(ctx, grp):
     """Every GEMV form the gemv_grp option selects (the looping body, the
     one-item forms of O, down, gate/up and the head) gives the default
@@ -152,7 +152,7 @@ def test_gemv_forms_same_results(ctx, grp):
         try:
             got = decode(ctx, cfg, w, prompt, 12, persistent=False)
         finally:
-            ctx.set_option("gemv_grp", 1)
+            ctx.set_option("gemv_grp", 33)
         assert_same(got[0], ref[0], "logits")
         assert np.array_equal(got[1], ref[1]), "tokens"
         for k in ref[2]:
