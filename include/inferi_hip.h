@@ -98,7 +98,10 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * the FFN down GEMV quantizing h itself).  "persistent" = 1 runs the decode step's
  * GEMV stages between two attentions (O, gate/up, down, the next QKV) as one
  * persistent launch per layer with grid barriers (Q4_K models; results
- * identical to the default path). */
+ * identical to the default path).  "attn_mfma" = 1 makes decode states
+ * created afterwards (and ifr_attention) use the attention split kernel that
+ * forms q.k on the matrix cores (f16 caches, head size 128, at most 4 query
+ * heads per KV head; same results within the decode tolerance). */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */

@@ -99,6 +99,15 @@ struct AttnLds {
     float wg[NPG][G], Mh[G];
 };
 
+// Positions of the split [t0, t0 + C) below T.  Written without a select
+// on t0 < T: hipcc (ROCm 7.2) folds `t0 < T ? min(C, T - t0) : 0`, when the
+// result is only compared with other values, into min(C, T - t0) and the
+// subtraction then wraps for an empty split.
+IFR_DEV uint32_t split_len(uint32_t t0, uint32_t C, uint32_t T) {
+    const uint32_t end = min(T, t0 + C);
+    return end - min(end, t0);
+}
+
 // One split s of KV head kvh, computed by the ATTN_THREADS threads tid of a
 // workgroup that call it together.  Every thread of the workgroup passes the
 // same barriers: threads of an inactive item (active false) take part in
@@ -163,7 +172,7 @@ __device__ void attn_item(const AttnArgs &a, uint32_t kvh, uint32_t s, int tid, 
     };
     if (fixed && active) load_batch(s * Qb, 0, 0);
     __builtin_amdgcn_sched_barrier(0); // the batch's loads stay together
-    const uint32_t T = min(__builtin_amdgcn_readfirstlane(pos_dev) + 1, a.seq_cap);
+    const uint32_t T = min((uint32_t)__builtin_amdgcn_readfirstlane(pos_dev) + 1u, a.seq_cap);
     const uint32_t C = fixed ? Qb : attn_chunk<HS>(T, S);
     const uint32_t t0 = s * C;
     if (active && t0 >= T && tid < G) {
@@ -172,7 +181,7 @@ __device__ void attn_item(const AttnArgs &a, uint32_t kvh, uint32_t s, int tid, 
         st_out<COH>(a.part_ml + (pidx + tid) * 2 + 1, 0.0f);
     }
     const bool live = active && t0 < T;
-    const uint32_t n = live ? min(C, T - t0) : 0u;
+    const uint32_t n = active ? split_len(t0, C, T) : 0u;
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -273,6 +282,214 @@ template <int HS, int G, bool F16>
 __device__ void attn_body(const AttnArgs &a) {
     __shared__ AttnLds<HS, G> L;
     attn_item<HS, G, F16, false>(a, blockIdx.x, blockIdx.y, (int)threadIdx.x, true, L);
+}
+
+// The split kernel with q.k on the matrix cores (head size 128, f16 cache,
+// G <= 4 query heads per KV head).  Workgroup (h, s): 4 waves of 32
+// positions, chunk C (a multiple of 128) from s*C.  Per block of 32
+// positions a wave forms the scores with v_mfma_f32_32x32x16_f16, A = the
+// query as 2G rows (the f16 high part of 256*q of every head, then the f16
+// low part, so hi + lo carries ~22 bits), B = the 32 K rows straight from
+// the cache (lane l: row l % 32, dims 16k + 8(l / 32)..+8): lane l then holds
+// the high-part sums of position l % 32 (l < 32) or the low-part sums
+// (l >= 32), added across the two halves.  The wave's running softmax and
+// P.V stay in fp32 on the vector ALUs: 16 lanes span a row's 128 dims, the
+// four lane groups take 8 positions each and are summed by lane shuffles.
+// The four waves' states combine through LDS into the split's partial.
+// Scores are in base-2 units as in attn_body.
+constexpr int ATTN2_WAVES = 4, ATTN2_PW = 32;
+constexpr uint32_t ATTN2_QB = ATTN2_WAVES * ATTN2_PW; // positions per block of a workgroup
+
+template <int G>
+__device__ void attn2_body(const AttnArgs &a) {
+    constexpr int HS = 128;
+    static_assert(G <= 4, "2G query rows in the first 8 rows of the 32-row operand");
+    __shared__ float pl[ATTN2_WAVES][G][ATTN2_PW];
+    __shared__ float ow[ATTN2_WAVES][G][HS];
+    __shared__ float mw[ATTN2_WAVES][G], lw[ATTN2_WAVES][G], wt[ATTN2_WAVES][G], Mh[G];
+    asm volatile("" ::"s"(a.q), "s"(a.k_cache), "s"(a.v_cache), "s"(a.part_o), "s"(a.part_ml), "s"(a.pos),
+                 "s"(a.kv_dim), "s"(a.n_splits), "s"(a.seq_cap));
+    const uint32_t pos_dev = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t kvh = blockIdx.x, s = blockIdx.y, S = a.n_splits;
+    const uint32_t li = (uint32_t)lane & 31u, lk = 8u * ((uint32_t)lane >> 5);
+    const uint32_t vg = (uint32_t)lane >> 4, vd = 8u * ((uint32_t)lane & 15u); // P.V: positions 8vg.., dims vd..
+    const size_t pidx = ((size_t)kvh * S + s) * G;
+    const uint16_t *kc = (const uint16_t *)a.k_cache, *vc = (const uint16_t *)a.v_cache;
+    const uint32_t C = a.chunk, t0 = s * C;
+    const uint32_t nblk = C / ATTN2_QB;
+
+    // this block's K (MFMA layout) and V (P.V layout) rows, clamped into the cache
+    uint4 kb[8], vb[8];
+    auto load_block = [&](uint32_t blk) {
+        const uint32_t p0 = t0 + blk * ATTN2_QB + (uint32_t)wave * ATTN2_PW;
+        const uint32_t kr = min(p0 + li, a.seq_cap - 1);
+        const uint16_t *krow = kc + (size_t)kr * a.kv_dim + (size_t)kvh * HS + lk;
+#pragma unroll
+        for (int k = 0; k < 8; k++) kb[k] = *(const uint4 *)(krow + 16 * k);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t vr = min(p0 + 8 * vg + (uint32_t)u, a.seq_cap - 1);
+            vb[u] = *(const uint4 *)(vc + (size_t)vr * a.kv_dim + (size_t)kvh * HS + vd);
+        }
+    };
+    load_block(0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the query operand: row li < G: hi(256 q_li), G <= li < 2G: lo, else 0
+    // (scaled by log2(e)/sqrt(hs) and by 2^8, undone on the scores exactly)
+    half8v aq[8];
+    {
+        const float qs = 1.44269504088896341f / sqrtf((float)HS) * 256.0f;
+        const uint32_t h = li < (uint32_t)G ? li : li - G;
+        const bool used = li < 2u * G;
+        const float *qrow = a.q + (size_t)(kvh * G + (used ? h : 0u)) * HS + lk;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float4 x0 = *(const float4 *)(qrow + 16 * k), x1 = *(const float4 *)(qrow + 16 * k + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = xv[e] * qs;
+                const _Float16 hi = (_Float16)v;
+                const _Float16 lo = (_Float16)(v - (float)hi);
+                aq[k][e] = !used ? (_Float16)0.0f : li < (uint32_t)G ? hi : lo;
+            }
+        }
+    }
+
+    const uint32_t T = min((uint32_t)__builtin_amdgcn_readfirstlane(pos_dev) + 1u, a.seq_cap);
+    const uint32_t n = split_len(t0, C, T);
+
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[j][e] = 0.0f;
+    }
+    for (uint32_t blk = 0; blk * ATTN2_QB < n; blk++) {
+        const uint32_t b0 = blk * ATTN2_QB + (uint32_t)wave * ATTN2_PW; // this wave's first position in the chunk
+        float16v acc;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            half8v bv;
+            __builtin_memcpy(&bv, &kb[k], 16);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[k], bv, acc, 0, 0, 0);
+        }
+        // rows 0..3 of lanes < 32 and 4..7 of lanes >= 32 (registers 0..3):
+        // G = 4: hi of head e in lanes < 32, lo of head e in lanes >= 32
+        const bool pos_ok = b0 + li < n;
+        float sc[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            // row j (hi) sits in register j of lanes < 32 when j < 4; row G + j
+            // (lo) in register (G + j) - 4 of lanes >= 32 when G + j >= 4,
+            // else in register G + j of lanes < 32
+            const float mine = acc[j];
+            const float hi = __shfl(mine, (int)li, 64);
+            float lo;
+            if constexpr (G == 4) {
+                lo = __shfl(acc[j], (int)li + 32, 64);
+            } else {
+                const int r = G + j;
+                const float cand = r < 4 ? acc[r < 4 ? r : 0] : acc[r >= 4 ? r - 4 : 0];
+                lo = __shfl(cand, r < 4 ? (int)li : (int)li + 32, 64);
+            }
+            sc[j] = pos_ok ? (hi + lo) * (1.0f / 256.0f) : -INFINITY;
+        }
+        // the wave's new maxima, probabilities and their sums (positions in lanes 0..31)
+        float p[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            const float bm = wave_max(lane < 32 ? sc[j] : -INFINITY);
+            const float mn = fmaxf(m[j], bm);
+            const float al = mn == -INFINITY ? 1.0f : exp2f(m[j] - mn);
+            p[j] = (lane < 32 && sc[j] != -INFINITY) ? exp2f(sc[j] - mn) : 0.0f;
+            l[j] = l[j] * al + wave_sum(p[j]);
+            m[j] = mn;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[j][e] *= al;
+        }
+        if (lane < 32) {
+#pragma unroll
+            for (int j = 0; j < G; j++) pl[wave][j][li] = p[j];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): this wave's LDS writes are visible to it
+        // P.V: lane group vg takes positions 8vg..8vg+7 of the wave's 32, 8 dims
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const bool vok = b0 + 8 * vg + (uint32_t)u < n;
+            const uint4 w = vok ? vb[u] : make_uint4(0u, 0u, 0u, 0u); // masked rows never reach the sums
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+                const float pj = pl[wave][j][8 * vg + u];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t hb = (e & 1) ? (ww[e >> 1] >> 16) : (ww[e >> 1] & 0xFFFFu);
+                    o[j][e] = fmaf(pj, f16_to_f32(hb), o[j][e]);
+                }
+            }
+        }
+        // next block's rows (none past the chunk's positions)
+        if ((blk + 1) * ATTN2_QB < n) load_block(blk + 1);
+    }
+    // the four lane groups of the wave hold disjoint positions of the same dims
+#pragma unroll
+    for (int j = 0; j < G; j++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            o[j][e] += __shfl_xor(o[j][e], 16, 64);
+            o[j][e] += __shfl_xor(o[j][e], 32, 64);
+        }
+    if (lane < 16) {
+#pragma unroll
+        for (int j = 0; j < G; j++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) ow[wave][j][vd + e] = o[j][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            mw[wave][j] = m[j];
+            lw[wave][j] = l[j];
+        }
+    }
+    __syncthreads();
+    if (tid < G) {
+        float M = -INFINITY;
+        for (int w = 0; w < ATTN2_WAVES; w++) M = fmaxf(M, mw[w][tid]);
+        Mh[tid] = M;
+        for (int w = 0; w < ATTN2_WAVES; w++) wt[w][tid] = mw[w][tid] == -INFINITY ? 0.0f : exp2f(mw[w][tid] - M);
+    }
+    __syncthreads();
+    if (n == 0) {
+        // an empty split: a partial the merge gives weight 0
+        if (tid < G) {
+            a.part_ml[(pidx + tid) * 2] = -INFINITY;
+            a.part_ml[(pidx + tid) * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+    for (int i = tid; i < G * HS; i += ATTN2_WAVES * 64) {
+        const int j = i / HS, d = i % HS;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < ATTN2_WAVES; w++) v = fmaf(wt[w][j], ow[w][j][d], v);
+        a.part_o[(pidx + j) * HS + d] = v;
+        if (d == 0) {
+            float L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < ATTN2_WAVES; w++) L = fmaf(wt[w][j], lw[w][j], L);
+            a.part_ml[(pidx + j) * 2] = Mh[j];
+            a.part_ml[(pidx + j) * 2 + 1] = L;
+        }
+    }
 }
 
 // Merge of the split partials, one wave per 16 output values (dims

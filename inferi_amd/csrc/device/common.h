@@ -12,6 +12,9 @@
 namespace ifr {
 
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+// matrix-core operand and accumulator vectors (v_mfma_f32_32x32x16_f16)
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_a16 __attribute__((ext_vector_type(4), aligned(16)));
 
 // binary16 -> binary32.  v_cvt_f32_f16 is exact for every finite code,

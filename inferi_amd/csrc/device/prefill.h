@@ -14,8 +14,6 @@
 
 namespace ifr {
 
-typedef _Float16 half8v __attribute__((ext_vector_type(8)));
-typedef float float16v __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------------------------ GEMM --
 // Y[m][n] = sum_k X[m][k] * deq(W)[n][k]   (EPI 0: Y =, EPI 1: Y +=)

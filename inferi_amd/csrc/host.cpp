@@ -120,6 +120,9 @@ struct ifr_ctx {
     // two rows (else 8 waves of four), bit 4 the output head, bit 5 gateup
     // with h in f32 and the down GEMV quantizing it (default: bits 0 and 5)
     int gemv_grp = 33;
+    // attention split on the matrix cores where it applies (read when a
+    // decode state is created)
+    int attn_mfma = 0;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -337,11 +340,23 @@ static uint32_t attn_splits_for(uint32_t T, uint32_t head_size) {
     return std::max(1u, std::min(ATTN_MERGE_MAX, (T + q - 1) / q));
 }
 
+// The matrix-core split kernel (device/attention.h attn2_body) serves f16
+// caches of head size 128 with at most 4 query heads per KV head: splits of
+// a fixed chunk of whole 128-position blocks, at most ATTN_MERGE_MAX.
+static bool attn2_ok(const ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, int32_t kv_dtype) {
+    return c->attn_mfma && kv_dtype == IFR_F16 && head_size == 128 && kv_mul <= 4;
+}
+static uint32_t attn2_chunk(uint32_t seq_cap) {
+    const uint32_t nb = (seq_cap + 127) / 128, per = (nb + ATTN_MERGE_MAX - 1) / ATTN_MERGE_MAX;
+    return per * 128;
+}
+
 // Split pass over the KV sequence, then the merge of the partials.
 static ifr_status launch_attn(ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, int32_t kv_dtype, AttnArgs &a,
-                              uint32_t n_kv_heads) {
+                              uint32_t n_kv_heads, bool mfma = false) {
     char name[64];
     snprintf(name, sizeof name, "attn_%s_h%u_g%u", kv_dtype == IFR_F16 ? "f16" : "f32", head_size, kv_mul);
+    if (mfma) snprintf(name, sizeof name, "attn2_f16_h128_g%u", kv_mul);
     ifr_status st = c->launch(name, dim3(n_kv_heads, a.n_splits), dim3(256), 0, a);
     if (st) return st;
     snprintf(name, sizeof name, "attn_merge_h%u_g%u", head_size, kv_mul);
@@ -373,6 +388,8 @@ struct ifr_llama2_state {
     ifr_ctx *ctx;
     ifr_llama2_config cfg;
     uint32_t kv_dim, head_size, kv_mul, n_splits;
+    bool attn2 = false;      // matrix-core attention split kernel
+    uint32_t attn_chunk = 0; // its positions per split
     std::vector<void *> allocs;
     float *x, *xb, *xb2, *q, *ktmp, *vtmp, *hb, *hb2, *att, *logits, *probs;
     uint8_t *smp_work;
@@ -559,9 +576,10 @@ static ifr_status enqueue_step_pk(ifr_ctx *c, ifr_llama2_state *s, const ifr_lla
         t.pos = &s->ctl->pos;
         t.kv_dim = s->kv_dim;
         t.n_splits = s->n_splits;
+        t.chunk = s->attn_chunk;
         t.seq_cap = cfg.max_pos;
         t.n_out = hidden;
-        if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, t, cfg.n_kv_heads))) return st;
+        if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, t, cfg.n_kv_heads, s->attn2))) return st;
         const LayerW &Lw = w->layers[l];
         PkArgs a = base;
         a.mode = 1;
@@ -700,9 +718,10 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.pos = &s->ctl->pos;
             a.kv_dim = kv_dim;
             a.n_splits = s->n_splits;
+            a.chunk = s->attn_chunk;
             a.seq_cap = cfg.max_pos;
             a.n_out = hidden;
-            if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, a, cfg.n_kv_heads))) return st;
+            if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, a, cfg.n_kv_heads, s->attn2))) return st;
         }
         if (fused) {   // x += Wo att; x * ffn_norm quantized for gate/up
             if ((st = check_gemv(c, Lw.attn_output.dtype, hidden, Lw.attn_output.data, p))) return st;
@@ -985,6 +1004,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->persistent = value ? 1 : 0;
         return IFR_OK;
     }
+    if (!strcmp(key, "attn_mfma")) {
+        c->attn_mfma = value ? 1 : 0;
+        return IFR_OK;
+    }
     if (!strcmp(key, "gemv_grp")) {
         c->gemv_grp = (int)value;
         return IFR_OK;
@@ -1186,7 +1209,9 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     if (p->pos >= ATTN_CMAX * ATTN_MERGE_MAX) return c->fail(IFR_EUNSUPPORTED, "attention: pos %u too large", p->pos);
     if ((uintptr_t)q % 16 || (uintptr_t)kc % 16 || (uintptr_t)vc % 16)
         return c->fail(IFR_EINVAL, "attention: q and caches must be 16-byte aligned");
-    const uint32_t T = p->pos + 1, S = attn_splits_for(T, p->head_size);
+    const uint32_t T = p->pos + 1;
+    const bool mfma = attn2_ok(c, p->head_size, g, kv_dtype);
+    const uint32_t chunk = mfma ? attn2_chunk(T) : 0, S = mfma ? (T + chunk - 1) / chunk : attn_splits_for(T, p->head_size);
     const size_t part_o = (size_t)n_kv * S * g * p->head_size, part_ml = (size_t)n_kv * S * g * 2;
     ifr_status st = c->ensure_scratch((part_o + part_ml) * sizeof(float));
     if (st) return st;
@@ -1200,8 +1225,9 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     a.pos = &dev_p->pos;
     a.kv_dim = p->kv_dim;
     a.n_splits = S;
+    a.chunk = chunk;
     a.seq_cap = T;
-    return launch_attn(c, p->head_size, g, kv_dtype, a, n_kv);
+    return launch_attn(c, p->head_size, g, kv_dtype, a, n_kv, mfma);
 }
 
 IFR_API ifr_status ifr_argmax(ifr_ctx *c, const float *v, uint32_t n, uint32_t *dev_index) {
@@ -1488,7 +1514,13 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     s->head_size = cfg->hidden / cfg->n_heads;
     s->kv_dim = s->head_size * cfg->n_kv_heads;
     s->kv_mul = cfg->n_heads / cfg->n_kv_heads;
-    s->n_splits = attn_splits_for(cfg->max_pos, s->head_size);
+    s->attn2 = attn2_ok(c, s->head_size, s->kv_mul, cfg->kv_dtype);
+    if (s->attn2) {
+        s->attn_chunk = attn2_chunk(cfg->max_pos);
+        s->n_splits = (cfg->max_pos + s->attn_chunk - 1) / s->attn_chunk;
+    } else {
+        s->n_splits = attn_splits_for(cfg->max_pos, s->head_size);
+    }
     auto alloc = [&](size_t bytes, void **p) -> ifr_status {
         ifr_status e = c->hip(hipMalloc(p, std::max<size_t>(bytes, 16)), "hipMalloc(state)");
         if (e) return e;
@@ -1801,6 +1833,8 @@ IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name
     else if (n == "logits") { *p = s->logits; b = (size_t)cfg.vocab * 4; }
     else if (n == "probs") { *p = s->probs; b = (size_t)cfg.vocab * 4; }
     else if (n == "pos") { *p = &s->ctl->pos; b = 4; }
+    else if (n == "part_ml") { *p = s->part_ml; b = (size_t)cfg.n_kv_heads * s->n_splits * s->kv_mul * 2 * 4; }
+    else if (n == "part_o") { *p = s->part_o; b = (size_t)cfg.n_kv_heads * s->n_splits * s->kv_mul * s->head_size * 4; }
     else if (n == "pk_err") { *p = s->pk_err; b = 4; }
     else if (n == "pk_ts") { *p = s->pk_ts; b = (size_t)s->ctx->n_cu * PK_TS_EVENTS * 8; }
     else if (n == "tokens") { *p = s->tokens; b = ((size_t)cfg.max_pos + 1) * 4; }

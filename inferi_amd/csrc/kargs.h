@@ -98,6 +98,7 @@ struct AttnArgs {
     uint32_t n_splits;        // gridDim.y
     uint32_t seq_cap;         // positions attended never exceed this (cache rows)
     uint32_t n_out;           // n_heads * head_size (length of xq_out)
+    uint32_t chunk;           // matrix-core split kernel: positions per split (a multiple of 128)
 };
 
 struct EltArgs {

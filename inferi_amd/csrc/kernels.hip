@@ -89,6 +89,11 @@ GEMV_ALL_MODES(q8_k, Q8_K)
         attn_merge_body<HS, G>(a);                                                                  \
     }
 
+// q.k on the matrix cores (head size 128, f16 cache)
+extern "C" __global__ void __launch_bounds__(256) attn2_f16_h128_g1(AttnArgs a) { attn2_body<1>(a); }
+extern "C" __global__ void __launch_bounds__(256) attn2_f16_h128_g2(AttnArgs a) { attn2_body<2>(a); }
+extern "C" __global__ void __launch_bounds__(256) attn2_f16_h128_g4(AttnArgs a) { attn2_body<4>(a); }
+
 ATTN_KERNEL(64, 1)
 ATTN_KERNEL(64, 2)
 ATTN_KERNEL(64, 4)
