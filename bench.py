@@ -167,6 +167,7 @@ def run_decode(args) -> None:
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
     ctx.set_option("persistent", args.persistent)
+    ctx.set_option("attn_mfma", args.attn_mfma)
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
@@ -327,10 +328,11 @@ def run_attn(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
+    ctx.set_option("attn_mfma", args.attn_mfma)
     out = []
     nh, nkv, hs = 32, 8, 128
     kv_dim = nkv * hs
-    for L in (512, 2048, 4352, 8192):
+    for L in (512, 2048, 4352, 8192, 16384, 32768):
         copies = max(2, -(-ROT_BYTES // (2 * L * kv_dim * 2)))
         caches = []
         for i in range(copies):
@@ -387,6 +389,7 @@ def main() -> None:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")
+    ap.add_argument("--attn-mfma", type=int, default=0, help="attention split with q.k on the matrix cores")
     ap.add_argument("--pmc-sample", action="store_true", help="workload for the rocprofv3 --pmc traffic passes")
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")

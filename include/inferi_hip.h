@@ -95,7 +95,8 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * the one-item forms of the grouped decode GEMVs (bit 0 attention output,
  * a default; bit 1 FFN down; bit 2 gate/up, bit 3 with 16 waves of two
  * rows; bit 4 the output head; bit 5, a default, gate/up with h in f32 and
- * the FFN down GEMV quantizing h itself).  "persistent" = 1 runs the decode step's
+ * the FFN down GEMV quantizing h itself; bit 6, a default, the Q6_K output
+ * head in 4-wave workgroups of up to 256 VGPRs, two per CU).  Default 97.  "persistent" = 1 runs the decode step's
  * GEMV stages between two attentions (O, gate/up, down, the next QKV) as one
  * persistent launch per layer with grid barriers (Q4_K models; results
  * identical to the default path).  "attn_mfma" = 1 makes decode states

@@ -119,7 +119,7 @@ struct ifr_ctx {
     // resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16 waves of
     // two rows (else 8 waves of four), bit 4 the output head, bit 5 gateup
     // with h in f32 and the down GEMV quantizing it (default: bits 0 and 5)
-    int gemv_grp = 33;
+    int gemv_grp = 97;
     // attention split on the matrix cores where it applies (read when a
     // decode state is created)
     int attn_mfma = 0;
@@ -296,6 +296,14 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
     a.ks = g.ks;
     a.nwaves = g.waves;
     if (grid_out) *grid_out = g.grid;
+    // the head's form with up to 256 VGPRs, where the code object has it:
+    // two workgroups per CU, each looping over its share of the row groups
+    // (measured fastest: 3 or 4 per CU and the 128-VGPR form are slower)
+    if (!strcmp(mode, "head") && (c->gemv_grp & 64) && g.waves <= 4 && !c->gemv_max_grid && c->fn(name + "_w2")) {
+        const uint32_t gg = std::min(g.grid, (uint32_t)c->n_cu * 2);
+        if (grid_out) *grid_out = gg;
+        return c->launch(name + "_w2", dim3(gg), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
+    }
     return c->launch(name, dim3(g.grid), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
 }
 

@@ -53,6 +53,12 @@ extern "C" __global__ void __launch_bounds__(GEMV_INT_MAX_WAVES * 64)
     __attribute__((amdgpu_waves_per_eu(GEMV_INT_WPE, 8))) gemv_q4_k_resid_xf(GemvArgs a) {
     gemv_int_body<Q4_K, GEMV_RESID, GEMV_INT_PIPE, GEMV_INT_NI, true>(a);
 }
+// the output head in workgroups of at most 4 waves with up to 256 VGPRs (the
+// Q6_K integer step spills at 128)
+extern "C" __global__ void __launch_bounds__(4 * 64) __attribute__((amdgpu_waves_per_eu(2, 8)))
+gemv_q6_k_head_w2(GemvArgs a) {
+    gemv_int_body<Q6_K, GEMV_HEAD, GEMV_INT_PIPE, GEMV_INT_NI>(a);
+}
 GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 2, 8, 1)
 GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 4, 4, 4)
 GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 4, 8, 1)

@@ -134,12 +134,12 @@ def test_c5_shape_same_as_fused(ctx):
         w.close()
 
 
-@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31, 33, 63])
+@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31, 33, 63, 64, 97])
 def test_gemv_forms_same_results(ctx, grp):
     """Every GEMV form the gemv_grp option selects (the looping body, the
-    one-item forms of O, down, gate/up and the head) gives the default
-    path's logits, tokens and KV rows bit for bit (same arithmetic, same
-    reduction orders), on the C4 shape."""
+    one-item forms of O, down, gate/up and the head, the head's 256-VGPR
+    form) gives the default path's logits, tokens and KV rows bit for bit
+    (same arithmetic, same reduction orders), on the C4 shape."""
     import inferi_amd as I
 
     cfg = I.Llama2Config(n_layers=4, hidden=2048, ffn=5632, n_heads=32, n_kv_heads=4, vocab=32000, max_pos=32,
@@ -152,7 +152,7 @@ def test_gemv_forms_same_results(ctx, grp):
         try:
             got = decode(ctx, cfg, w, prompt, 12, persistent=False)
         finally:
-            ctx.set_option("gemv_grp", 33)
+            ctx.set_option("gemv_grp", 97)
         assert_same(got[0], ref[0], "logits")
         assert np.array_equal(got[1], ref[1]), "tokens"
         for k in ref[2]:
