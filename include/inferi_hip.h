@@ -102,7 +102,10 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * identical to the default path).  "attn_mfma" = 1 makes decode states
  * created afterwards (and ifr_attention) use the attention split kernel that
  * forms q.k on the matrix cores (f16 caches, head size 128, at most 4 query
- * heads per KV head; same results within the decode tolerance). */
+ * heads per KV head; same results within the decode tolerance).  "pf_chunk"
+ * sets the prompt tokens per ifr_llama2_prefill pass (a multiple of 64, at
+ * most 16384; 0 = 4096), read at a state's first prefill: the results do
+ * not depend on it. */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */

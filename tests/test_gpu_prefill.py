@@ -168,18 +168,58 @@ def test_prefill_matches_sequential_decode_hs64(ctx, oracle_lib):
         w.close()
 
 
-def test_prefill_chunks_and_gqa4_hs128(ctx, oracle_lib):
-    """Two prefill chunks (512 + rest), head size 128, 4 query heads per KV head, f32 cache."""
+@pytest.mark.parametrize("chunk", [512, 0])
+def test_prefill_chunks_and_gqa4_hs128(ctx, oracle_lib, chunk):
+    """Two prefill passes (512 + rest) or one (the default pass length),
+    head size 128, 4 query heads per KV head, f32 cache."""
     import inferi_amd as I
 
     cfg = I.Llama2Config(n_layers=2, hidden=512, ffn=1024, n_heads=4, n_kv_heads=1, vocab=512, max_pos=700,
                          rope_theta=500000.0, rms_eps=1e-5, kv_dtype=I.F32)
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=41, std=0.05)
+    ctx.set_option("pf_chunk", chunk)
     try:
         prompt = np.random.default_rng(4).integers(0, cfg.vocab, 600).tolist()
         assert _prefill_vs_decode(ctx, cfg, w, prompt, 8) > 0
     finally:
+        ctx.set_option("pf_chunk", 0)
         w.close()
+
+
+def test_prefill_pass_length_gives_same_results(ctx):
+    """The prompt in passes of 64, 192 or all its tokens at once: the same
+    KV cache rows, logits and tokens bit for bit (each output row's GEMM sum
+    and each query's attention are computed the same way in any pass)."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, vocab=700, max_pos=400,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=43, std=0.05)
+    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 300).astype(np.uint32)
+    out = {}
+    try:
+        for chunk in (64, 192, 0):
+            ctx.set_option("pf_chunk", chunk)
+            s = I.Llama2State(ctx, cfg)
+            try:
+                s.reset(prompt, 0)
+                I.Llama2.prefill(ctx, s, w, 299)
+                I.Llama2.generate(ctx, s, w, 6, use_graph=True)
+                kv = [s.read(n, np.uint16, layer).copy() for layer in range(cfg.n_layers)
+                      for n in ("key_cache", "value_cache")]
+                out[chunk] = (s.read("logits"), s.tokens(0, 306), kv)
+            finally:
+                s.close()
+    finally:
+        ctx.set_option("pf_chunk", 0)
+        w.close()
+    ref = out[0]
+    for chunk in (64, 192):
+        got = out[chunk]
+        assert np.array_equal(got[0].view(np.uint32), ref[0].view(np.uint32)), f"logits, passes of {chunk}"
+        assert np.array_equal(got[1], ref[1]), f"tokens, passes of {chunk}"
+        for a, b in zip(got[2], ref[2]):
+            assert np.array_equal(a, b), f"KV cache, passes of {chunk}"
 
 
 def test_prefill_qwen2_style(ctx, oracle_lib):
