@@ -153,6 +153,20 @@ IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int
 IFR_API ifr_status ifr_matmul_quant(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
                                     uint32_t cols, const float *v);
 
+/* ifr_matmul_quant without allocation (no counterpart in the reference): for
+ * callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments, kernels and results as ifr_matmul_quant, but the quantized copy
+ * of v lives in a fixed device array of 65536 bytes (one per GPU, held until
+ * the process ends) instead of a buffer the library allocates; the call
+ * makes no hipMalloc, hipFree or other allocating call.  cols whose
+ * quantized input would not fit (cols > 18724 on the integer path) return
+ * IFR_EINVAL.  Every call on one GPU shares that array: calls that overlap
+ * on one GPU (two streams, two contexts) race; calls queued on one context's
+ * stream are ordered and safe. */
+IFR_API ifr_status ifr_matmul_quant_noalloc(ifr_ctx *ctx, float *out, const void *w, int32_t dtype, uint32_t rows,
+                                            uint32_t cols, const float *v);
+
 /* Activation pre-quantization (no reference counterpart: the reference
  * multiplies f32 vectors).  A caller that multiplies several matrices by the
  * same vector quantizes it once into `xq` (ifr_activation_bytes(n) bytes,

@@ -79,6 +79,7 @@ SIGNATURES = {
     "ifr_event_elapsed": (_i32, [_vp, _i32, _i32, C.POINTER(_f)]),
     "ifr_dequant": (_i32, [_vp, _vp, _vp, _i32, _u64]),
     "ifr_matmul_quant": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
+    "ifr_matmul_quant_noalloc": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
     "ifr_activation_bytes": (_u64, [_u32]),
     "ifr_quantize_activation": (_i32, [_vp, _vp, _vp, _vp, _u32, _vp]),
     "ifr_matmul_quant_xq": (_i32, [_vp, _vp, _vp, _i32, _u32, _u32, _vp]),
@@ -252,6 +253,11 @@ class LlmContext:
     def matmul_quant_assign(self, out, a, dtype: int, rows: int, cols: int, b) -> None:
         """out = deq(a)[rows x cols] . b (context.rs:441-456)."""
         self._check(lib().ifr_matmul_quant(self.h, _ptr(out), _ptr(a), dtype, rows, cols, _ptr(b)))
+
+    def matmul_quant_noalloc(self, out, a, dtype: int, rows: int, cols: int, b) -> None:
+        """matmul_quant_assign without allocation: the quantized input in the
+        device's fixed scratch array (ifr_matmul_quant_noalloc)."""
+        self._check(lib().ifr_matmul_quant_noalloc(self.h, _ptr(out), _ptr(a), dtype, rows, cols, _ptr(b)))
 
     def quantize_activation(self, xq, x, n: int, gamma=None, ss_out=None) -> None:
         """x (times gamma) -> the GEMV's quantized activation layout."""

@@ -52,10 +52,20 @@ def build_kernels(out: str = HSACO) -> str:
 
 def build_host(out: str = LIB) -> str:
     cxx = shutil.which("g++") or "g++"
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
     tmp = out + ".tmp"
+    obj_dir = os.path.join(ROOT, "_build")
+    os.makedirs(obj_dir, exist_ok=True)
+    # the fixed scratch of ifr_matmul_quant_noalloc: a device array, so this
+    # one file is compiled by hipcc (for gfx950) and linked into the library
+    noalloc_o = os.path.join(obj_dir, "noalloc.o")
+    _run([hipcc, "-c", "-fPIC", "--offload-arch=gfx950", "-O2", "-std=c++17", "-fvisibility=hidden",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          os.path.join(CSRC, "noalloc.hip"), "-o", noalloc_o])
     _run([cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-result",
           "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
-          os.path.join(CSRC, "host.cpp"), os.path.join(CSRC, "gguf.cpp"), f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
+          os.path.join(CSRC, "host.cpp"), os.path.join(CSRC, "gguf.cpp"), noalloc_o,
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
     os.replace(tmp, out)
     return out
 

@@ -23,6 +23,7 @@
 
 #include "../../include/inferi_hip.h"
 #include "kargs.h"
+#include "noalloc.h"
 
 using namespace ifr;
 
@@ -125,6 +126,8 @@ struct ifr_ctx {
     int attn_mfma = 0;
     // prompt tokens per prefill pass (0: PF_CHUNK), read at a state's first prefill
     uint32_t pf_chunk = 0;
+    // this device's fixed scratch of ifr_matmul_quant_noalloc (noalloc.hip)
+    void *noalloc_scratch = nullptr;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -944,7 +947,7 @@ IFR_API ifr_status ifr_create(int32_t device, const char *code_object_path, ifr_
     c->device = device;
     auto bail = [&](ifr_status st) {
         g_create_error = c->err;
-        if (c->module) hipModuleUnload(c->module);
+            if (c->module) hipModuleUnload(c->module);
         if (c->stream) hipStreamDestroy(c->stream);
         delete c;
         return st;
@@ -974,6 +977,7 @@ IFR_API ifr_status ifr_create(int32_t device, const char *code_object_path, ifr_
         return bail(st);
     for (auto &e : c->events)
         if ((st = c->hip(hipEventCreate(&e), "hipEventCreate"))) return bail(st);
+    if ((st = c->hip(ifr_noalloc_init(device, &c->noalloc_scratch), "hipGetSymbolAddress(scratch)"))) return bail(st);
     *out = c;
     return IFR_OK;
 }
@@ -1118,6 +1122,20 @@ IFR_API ifr_status ifr_matmul_quant(ifr_ctx *c, float *out, const void *w, int32
     ifr_status st = c->ensure_xq_scratch(xq_bytes(cols));
     if (st) return st;
     return gemv_plain(c, out, w, dtype, rows, cols, v, (uint8_t *)c->xq_scratch);
+}
+
+IFR_API ifr_status ifr_matmul_quant_noalloc(ifr_ctx *c, float *out, const void *w, int32_t dtype, uint32_t rows,
+                                            uint32_t cols, const float *v) {
+    if (!c) return IFR_EINVAL;
+    if (!out || !w || !v) return c->fail(IFR_EINVAL, "matmul_quant_noalloc: null pointer");
+    if (!rows) return IFR_OK;
+    if ((uintptr_t)v % 16) return c->fail(IFR_EINVAL, "matmul_quant_noalloc: v not 16-byte aligned");
+    if (!c->gemv_exact && xq_bytes(cols) > IFR_NOALLOC_SCRATCH_BYTES)
+        return c->fail(IFR_EINVAL, "matmul_quant_noalloc: cols %u needs %llu bytes of scratch, above the fixed %u", cols,
+                       (unsigned long long)xq_bytes(cols), (unsigned)IFR_NOALLOC_SCRATCH_BYTES);
+    // the same kernels as ifr_matmul_quant, with the quantized input in the
+    // device's fixed array (shared by every call on this device)
+    return gemv_plain(c, out, w, dtype, rows, cols, v, (uint8_t *)c->noalloc_scratch);
 }
 
 IFR_API uint64_t ifr_activation_bytes(uint32_t n) { return xq_bytes(n); }
