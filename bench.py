@@ -4,8 +4,10 @@
 One "step" is one decode token through the whole model (embedding, 32
 layers, final norm, Q6_K output head, greedy argmax), replayed from a HIP
 graph with the position on the device.  The timed region starts with the
-weights resident in HBM and the 4096-token prompt already in the KV cache
-(prefilled by sequential decode, untimed).
+weights resident in HBM and the 4096-token prompt already in the KV cache:
+its first 4095 tokens go through ifr_llama2_prefill (MFMA GEMMs and causal
+attention, in passes of up to 4096 tokens), which is timed on its own and
+reported as config.prefill, the last through the first decode step.
 
 Prints one JSON line.  Extra modes: --sweep (BASELINE config 2 GEMV sweep,
 GB/s per format and shape), --attn (config 3 attention GB/s).

@@ -318,7 +318,11 @@ IFR_API ifr_status ifr_llama2_state_reset(ifr_llama2_state *s, const uint32_t *p
 IFR_API ifr_status ifr_llama2_launch(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w, int32_t fused);
 /* n_steps decode steps; with use_graph the step is captured once into a HIP
  * graph and replayed (the position lives on the device, so one graph serves
- * every step). */
+ * every step).  The graph is captured again when it was made for another
+ * weights object or before an ifr_llama2_weights_set on this one, or when
+ * the options or the sampler changed; a caller that frees or overwrites a
+ * bound tensor's memory in place must rebind it (ifr_llama2_weights_set) or
+ * pass use_graph = 0. */
 IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
                                        uint32_t n_steps, int32_t use_graph);
 /* Prompt prefill (the reference runs a prompt through Llama2::launch one

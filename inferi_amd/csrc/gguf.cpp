@@ -241,9 +241,18 @@ ifr_status parse(ifr_gguf *g) {
             return gfail("gguf: tensor %s of type %u is not part of the supported gguf version", t.name.c_str(), type);
         t.dtype = (int32_t)type;
         t.offset = off;
-        unsigned __int128 elems = (unsigned __int128)t.dims[0] * t.dims[1] * t.dims[2] * t.dims[3];
-        if (elems >> 62) return gfail("gguf: tensor %s is too large", t.name.c_str());
-        t.bytes = known ? (uint64_t)(elems / be) * bb : 0;
+        // element count, multiplied step by step with an overflow check
+        uint64_t elems = 1;
+        for (int d = 0; d < 4; d++)
+            if (__builtin_mul_overflow(elems, t.dims[d], &elems) || (elems >> 62))
+                return gfail("gguf: tensor %s is too large", t.name.c_str());
+        if (known && elems % be)
+            return gfail("gguf: tensor %s has %llu elements, not a multiple of its block of %u", t.name.c_str(),
+                         (unsigned long long)elems, be);
+        uint64_t bytes = 0;
+        if (known && __builtin_mul_overflow(elems / be, (uint64_t)bb, &bytes))
+            return gfail("gguf: tensor %s is too large", t.name.c_str());
+        t.bytes = bytes;
         t.has_data = known;
         g->tensor_ix[t.name] = g->tensors.size(); // a repeated name keeps the last info, as a map insert does
         g->tensors.push_back(std::move(t));

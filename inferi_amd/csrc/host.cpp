@@ -13,6 +13,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -392,6 +393,9 @@ struct LayerW {
 struct ifr_llama2_weights {
     ifr_ctx *ctx;
     ifr_llama2_config cfg;
+    // identity of the tensor table for captured decode graphs: a process-wide
+    // id (never reused) and a generation every ifr_llama2_weights_set bumps
+    uint64_t id = 0, gen = 0;
     Tens token_embd, output_norm, output;
     std::vector<LayerW> layers;
     std::vector<void *> owned; // device copies made by ifr_llama2_weights_from_gguf
@@ -442,7 +446,7 @@ struct ifr_llama2_state {
     int graph_pk = -1;
     int graph_grp = -1;
     uint32_t graph_sampler = 0;
-    const ifr_llama2_weights *graph_w = nullptr;
+    uint64_t graph_wid = 0, graph_wgen = 0; // weights id and generation the graph was captured with
     int graph_fused = -1;
     int graph_exact = -1;
 };
@@ -1350,9 +1354,11 @@ IFR_API ifr_status ifr_llama2_weights_create(ifr_ctx *c, const ifr_llama2_config
     *out = nullptr;
     ifr_status st = validate_cfg(c, cfg);
     if (st) return st;
+    static std::atomic<uint64_t> next_id{0};
     auto *w = new ifr_llama2_weights();
     w->ctx = c;
     w->cfg = *cfg;
+    w->id = ++next_id;
     w->layers.resize(cfg->n_layers);
     *out = w;
     return IFR_OK;
@@ -1363,6 +1369,7 @@ IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *nam
     if (!w || !name) return IFR_EINVAL;
     ifr_ctx *c = w->ctx;
     const ifr_llama2_config &cfg = w->cfg;
+    w->gen++; // a graph captured with the table before this call is stale
     if (!data) return c->fail(IFR_EINVAL, "%s: null data", name);
     if (!qk_of(dtype)) return c->fail(IFR_EINVAL, "%s: unknown dtype %d", name, dtype);
     const uint32_t kv_dim = cfg.hidden / cfg.n_heads * cfg.n_kv_heads;
@@ -1603,6 +1610,7 @@ IFR_API ifr_status ifr_llama2_state_reset(ifr_llama2_state *s, const uint32_t *p
     if (!s) return IFR_EINVAL;
     ifr_ctx *c = s->ctx;
     const ifr_llama2_config &cfg = s->cfg;
+    if (n && !prompt) return c->fail(IFR_EINVAL, "null prompt");
     if (n > cfg.max_pos) return c->fail(IFR_EINVAL, "prompt longer than max_pos");
     if (pos >= cfg.max_pos) return c->fail(IFR_EINVAL, "pos %u >= max_pos %u", pos, cfg.max_pos);
     for (uint32_t i = 0; i < n; i++)
@@ -1808,7 +1816,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
             if ((st = enqueue_step(c, s, w, 1))) return st;
         return IFR_OK;
     }
-    if (!s->graph || s->graph_w != w || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
+    if (!s->graph || s->graph_wid != w->id || s->graph_wgen != w->gen || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
         s->graph_sampler != s->sampler_gen || s->graph_pk != c->persistent || s->graph_grp != c->gemv_grp) {
         if (s->graph) {
             hipStreamSynchronize(c->stream);
@@ -1828,7 +1836,8 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         st = c->hip(hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0), "hipGraphInstantiate");
         hipGraphDestroy(g);
         if (st) return st;
-        s->graph_w = w;
+        s->graph_wid = w->id;
+        s->graph_wgen = w->gen;
         s->graph_fused = 1;
         s->graph_exact = c->gemv_exact;
         s->graph_sampler = s->sampler_gen;

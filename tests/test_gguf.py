@@ -153,13 +153,14 @@ def test_truncated_and_malformed_files_fail_cleanly():
         I.Gguf(data=b"GGUX" + data[4:])
     assert I.Gguf(data=b"FUGG" + data[4:]).version == 3  # the other byte order is accepted (gguf.rs:19-20)
 
-    def one_tensor(rank=1, ttype=0, meta_type=None):
+    def one_tensor(rank=1, ttype=0, meta_type=None, dims=None):
+        dims = dims or [1] * rank
         b = bytearray(b"GGUF") + (3).to_bytes(4, "little") + (1).to_bytes(8, "little")
         b += (1 if meta_type is not None else 0).to_bytes(8, "little")
         if meta_type is not None:
             b += (1).to_bytes(8, "little") + b"k" + meta_type.to_bytes(4, "little") + (0).to_bytes(8, "little")
         b += (1).to_bytes(8, "little") + b"t" + rank.to_bytes(4, "little")
-        b += b"".join((1).to_bytes(8, "little") for _ in range(rank))
+        b += b"".join(int(d).to_bytes(8, "little") for d in dims)
         b += ttype.to_bytes(4, "little") + (0).to_bytes(8, "little")
         b += bytes((-len(b)) % 32) + bytes(32)
         return bytes(b)
@@ -173,6 +174,17 @@ def test_truncated_and_malformed_files_fail_cleanly():
         I.Gguf(data=one_tensor(meta_type=13))
     g = I.Gguf(data=one_tensor(ttype=10))  # Q2_K: listed, data not read (as the reference)
     assert g.tensor("t").data is None
+    # dims whose product wraps 64 bits (four dims of 2^32: 2^128) or exceeds
+    # 2^62, and element counts that are not whole blocks, are rejected before
+    # any byte count is formed from them
+    with pytest.raises(I.HipError, match="too large"):
+        I.Gguf(data=one_tensor(rank=4, dims=[1 << 32] * 4))
+    with pytest.raises(I.HipError, match="too large"):
+        I.Gguf(data=one_tensor(rank=2, dims=[1 << 31, 1 << 31]))
+    with pytest.raises(I.HipError, match="not a multiple"):
+        I.Gguf(data=one_tensor(rank=1, ttype=12, dims=[300]))  # Q4_K blocks are 256 elements
+    with pytest.raises(I.HipError, match="past the end"):
+        I.Gguf(data=one_tensor(rank=2, ttype=0, dims=[1 << 20, 1 << 20]))  # 4 TiB of F32 in a small file
 
 
 def llama_file(path, meta, tokens=8, drop=()):

@@ -264,3 +264,40 @@ def test_c5_8b_first_steps(ctx, oracle_lib, exact):
         ctx.set_option("gemv_exact", 0)
         s.close()
         w.close()
+
+
+def test_graph_recaptured_after_a_tensor_is_replaced(ctx):
+    """A captured decode step is keyed on the weights object's identity and
+    generation: replacing a bound tensor (ifr_llama2_weights_set) after a
+    graph step makes the next graph step use the new tensor, and a second
+    weights object never replays the first one's graph."""
+    import inferi_amd as I
+
+    cfg = tiny_cfg()
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=31)
+    s = I.Llama2State(ctx, cfg)
+    try:
+        prompt = [5, 77]
+        a, _ = run_steps(ctx, s, w, prompt, 2, "graph")
+        # new output norm: every logit changes
+        norm = ctx.alloc(cfg.hidden * 4)
+        ctx.fill_normal(norm, cfg.hidden, 99, 0, 2.0, 0.3)
+        w.buffers["output_norm.weight"][1].free()
+        w.set("output_norm.weight", I.F32, norm, 1, cfg.hidden)
+        b, _ = run_steps(ctx, s, w, prompt, 2, "graph")
+        c, _ = run_steps(ctx, s, w, prompt, 2, "fused")
+        for pos in range(2):
+            assert not np.array_equal(a[pos], b[pos]), "graph replayed the replaced tensor"
+            assert np.array_equal(b[pos], c[pos]), "graph step differs from the direct step"
+        # a second weights object (same config, other values): its own graph
+        w2 = I.Llama2Weights.synthetic(ctx, cfg, seed=32)
+        try:
+            d, _ = run_steps(ctx, s, w2, prompt, 2, "graph")
+            e, _ = run_steps(ctx, s, w2, prompt, 2, "fused")
+            assert all(np.array_equal(d[p], e[p]) for p in range(2))
+            assert not np.array_equal(d[1], b[1])
+        finally:
+            w2.close()
+    finally:
+        s.close()
+        w.close()
