@@ -273,7 +273,8 @@ def test_rope_matches_oracle(ctx, oracle_lib, neox):
     import inferi_amd as I
 
     rng = np.random.default_rng(4)
-    for hs, nq, nkv, theta, pos in ((128, 32, 8, 500000.0, 0), (128, 32, 8, 500000.0, 4095), (64, 32, 4, 10000.0, 77),
+    for hs, nq, nkv, theta, pos in ((128, 32, 8, 500000.0, 0), (128, 32, 8, 500000.0, 4095),
+                                    (128, 32, 8, 500000.0, 8191), (64, 32, 4, 10000.0, 77),
                                     (64, 16, 16, 10000.0, 1)):
         q = rng.standard_normal(nq * hs).astype(np.float32)
         k = rng.standard_normal(nkv * hs).astype(np.float32)
