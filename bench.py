@@ -150,7 +150,8 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
     host = {}
     for name in cfg.shapes():
         dt, arr, rows, cols = weights.download(name)
-        host[name] = arr if dt == I.F32 else (dt, arr, rows, cols)
+        vector = name.endswith(("norm.weight", ".bias"))
+        host[name] = arr if vector else (dt, np.ascontiguousarray(arr).view(np.uint8), rows, cols)
     c = dict(hidden=cfg.hidden, ffn=cfg.ffn, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
              vocab=cfg.vocab, max_pos=max(16, n_tokens + 1), rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps, kv_f16=1)
     m = O.Model(c, host)

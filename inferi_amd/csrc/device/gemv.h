@@ -103,6 +103,13 @@ template <>
 struct QFmt<Q5_1> { static constexpr int QK = 32, BB = 24, LPB = 2; };
 template <>
 struct QFmt<Q8_K> { static constexpr int QK = 256, BB = 292, LPB = 16; };
+// unquantized matrices (GpuQuantTensor::F32 and the F16 tensors the
+// reference converts to it, gemv_quant.rs:203-208, gguf.rs:113-128): a
+// 32-element virtual block per two lanes, as the 32-element formats
+template <>
+struct QFmt<F16> { static constexpr int QK = 32, BB = 64, LPB = 2; };
+template <>
+struct QFmt<F32> { static constexpr int QK = 32, BB = 128, LPB = 2; };
 
 // Codes of lane half c (elements 16c..16c+15) of a 32-element block whose
 // qs byte j holds element j (low nibble) and j+16 (high), with the fifth bits
@@ -298,6 +305,62 @@ struct Chunk<Q8_0, R> {
             const float dq = dot16u(q.x ^ F, q.y ^ F, q.z ^ F, q.w ^ F, xv);
             acc[r] += f16_to_f32(dsc[r]) * (dq - 128.0f * sx);
         }
+    }
+};
+
+// F16 / F32 rows: lane c owns elements 16c..16c+15 of the 32-element
+// virtual block kb, multiplied in fp32.
+template <int R>
+struct Chunk<F16, R> {
+    uint4 h0[R], h1[R];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t *b = rowp[r] + (size_t)kb * 64 + 32 * c;
+            h0[r] = ld16(b);
+            h1[r] = ld16(b + 16);
+        }
+    }
+    // row r's 16 weights times x[0..15]
+    IFR_DEV float dot(int r, const float *xv) const {
+        const uint32_t w[8] = {h0[r].x, h0[r].y, h0[r].z, h0[r].w, h1[r].x, h1[r].y, h1[r].z, h1[r].w};
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) t = fmaf(f16_to_f32((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu), xv[i], t);
+        return t;
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        float xv[16];
+        lds16(xs + kb * 32 + 16 * c, xv);
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] += dot(r, xv);
+    }
+};
+template <int R>
+struct Chunk<F32, R> {
+    uint4 v[R][4];
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[r][k] = ld16(rowp[r] + (size_t)kb * 128 + 64 * c + 16 * k);
+    }
+    IFR_DEV float dot(int r, const float *xv) const {
+        float t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            t = fmaf(__uint_as_float(v[r][k].x), xv[4 * k], t);
+            t = fmaf(__uint_as_float(v[r][k].y), xv[4 * k + 1], t);
+            t = fmaf(__uint_as_float(v[r][k].z), xv[4 * k + 2], t);
+            t = fmaf(__uint_as_float(v[r][k].w), xv[4 * k + 3], t);
+        }
+        return t;
+    }
+    IFR_DEV void compute(uint32_t kb, uint32_t c, const float *xs, float *acc) const {
+        float xv[16];
+        lds16(xs + kb * 32 + 16 * c, xv);
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] += dot(r, xv);
     }
 };
 
@@ -738,6 +801,41 @@ struct ChunkI<Q8_K, R> {
         for (int r = 0; r < R; r++) acc[r] += valid ? dv[r] * t[r] : 0.0f;
     }
 };
+
+// F16 / F32 rows on the integer path: lane c owns elements 16c..16c+15 of
+// the 32-element virtual block, exactly one activation group; the group's
+// 22-bit codes v (exact in f32) are rebuilt from the digit planes once and
+// multiplied by the weights in fp32, then by the group scale.
+IFR_DEV void xg_codes(const XG &g, float *v) {
+    const uint32_t a[4] = {g.a.x, g.a.y, g.a.z, g.a.w}, b[4] = {g.b.x, g.b.y, g.b.z, g.b.w},
+                   c[4] = {g.c.x, g.c.y, g.c.z, g.c.w};
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int sh = 24 - 8 * (i & 3);
+        const int da = (int32_t)(a[i >> 2] << sh) >> 24, db = (int32_t)(b[i >> 2] << sh) >> 24,
+                  dc = (int32_t)(c[i >> 2] << sh) >> 24;
+        v[i] = (float)(da * 65536 + db * 256 + dc);
+    }
+}
+template <int FMT, int R>
+struct ChunkIF {
+    static constexpr int LPB = 2;
+    static constexpr bool DIRECT = true;
+    Chunk<FMT, R> w;
+    IFR_DEV void load(const uint8_t *const *rowp, uint32_t kb, uint32_t c) { w.load(rowp, kb, c); }
+    IFR_DEV void compute(const XQ &x, uint32_t kb, uint32_t c, bool valid, float *acc) const {
+        const uint32_t e = kb * 32 + 16 * c;
+        float v[16];
+        xg_codes(xg_load(x, e), v);
+        const float s = x.xs[e / 16];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] += valid ? w.dot(r, v) * s : 0.0f;
+    }
+};
+template <int R>
+struct ChunkI<F16, R> : ChunkIF<F16, R> {};
+template <int R>
+struct ChunkI<F32, R> : ChunkIF<F32, R> {};
 
 // One step of a lane for R rows (K-quants group by group), added to acc
 // when `valid` (a select, not a branch).

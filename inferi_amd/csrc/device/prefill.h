@@ -151,6 +151,42 @@ struct PfTile<Q8_K> {
     }
 };
 
+// Unquantized rows (GpuQuantTensor::F32, and F16 which the reference
+// converts to F32 at load, gguf.rs:113-128): elements k0 + 32hs .. +32 taken
+// as they are (F16) or rounded to f16 (F32) for the matrix cores.
+template <>
+struct PfTile<F16> {
+    static constexpr int QK = 1, BB = 2;
+    uint4 v[4];
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
+        const uint8_t *b = wrow + 2 * (size_t)(k0 + 32 * hs);
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = ld16(b + 16 * k);
+    }
+    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const uint32_t w = pick4(v[l >> 3], (uint32_t)((l >> 1) & 3));
+            const uint16_t b = (uint16_t)((l & 1) ? (w >> 16) : (w & 0xFFFFu));
+            __builtin_memcpy(&h[l], &b, 2);
+        }
+    }
+};
+template <>
+struct PfTile<F32> {
+    static constexpr int QK = 1, BB = 4;
+    uint4 v[8];
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
+        const uint8_t *b = wrow + 4 * (size_t)(k0 + 32 * hs);
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = ld16(b + 16 * k);
+    }
+    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
+#pragma unroll
+        for (int l = 0; l < 32; l++) h[l] = (_Float16)__uint_as_float(pick4(v[l >> 2], (uint32_t)(l & 3)));
+    }
+};
+
 // The 32-element formats: the run is exactly block (k0 + 32hs)/32.
 // Q8_0 (quantization.rs:47-55): d@0 qs:i8[32]@2, y = q * d.
 template <>

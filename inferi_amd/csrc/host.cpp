@@ -83,12 +83,23 @@ const char *gemv_fmt_name(int32_t dt) {
     case IFR_Q5_K: return "q5_k";
     case IFR_Q6_K: return "q6_k";
     case IFR_Q8_K: return "q8_k";
+    case IFR_F16: return "f16";
+    case IFR_F32: return "f32";
     default: return nullptr;
     }
 }
+// The GEMV kernels' block: the GGUF block, or a virtual block of 32
+// elements for the unquantized types (device/gemv.h QFmt).
+int gemv_qk(int32_t dt) { return qk_of(dt) == 1 ? 32 : qk_of(dt); }
+uint32_t gemv_block_bytes(int32_t dt) { return (uint32_t)(qk_of(dt) == 1 ? 32 * bytes_of(dt) : bytes_of(dt)); }
+// Row alignment the GEMV and prefill tile loads need: 16 bytes for the
+// formats read with 16-byte loads, 4 (or the field alignment) otherwise.
+uintptr_t gemv_align(int32_t dt) {
+    return (dt == IFR_Q4_K || dt == IFR_Q5_K || dt == IFR_F16 || dt == IFR_F32) ? 16 : 4;
+}
 // Blocks one 64-lane step of the integer GEMV covers: 32 for the 32-element
 // formats (2 lanes per block), 16 for the 256-element ones (4 lanes).
-uint32_t int_blocks_per_step(int32_t dt) { return qk_of(dt) == 32 ? 32u : 16u; }
+uint32_t int_blocks_per_step(int32_t dt) { return gemv_qk(dt) == 32 ? 32u : 16u; }
 
 } // namespace
 
@@ -201,14 +212,14 @@ struct GemvPlan {
 static ifr_status check_gemv(ifr_ctx *c, int32_t dtype, uint32_t cols, const void *w, GemvPlan &p) {
     p.fmt = gemv_fmt_name(dtype);
     if (!p.fmt) return c->fail(IFR_EUNSUPPORTED, "matmul_quant: dtype %d has no GEMV kernel", dtype);
-    const int qk = qk_of(dtype);
+    const int qk = gemv_qk(dtype);
     if (cols == 0 || cols % (uint32_t)qk) return c->fail(IFR_EINVAL, "matmul_quant: cols %u not a multiple of %d", cols, qk);
     if ((c->gemv_exact ? (uint64_t)cols * 4 : xq_bytes(cols)) > GEMV_MAX_LDS)
         return c->fail(IFR_EUNSUPPORTED, "matmul_quant: cols %u too large for one workgroup's LDS", cols);
-    const uintptr_t need = (dtype == IFR_Q4_K || dtype == IFR_Q5_K) ? 16 : 4;
+    const uintptr_t need = gemv_align(dtype);
     if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "matmul_quant: weights not %u-byte aligned", (unsigned)need);
     p.nb = cols / (uint32_t)qk;
-    p.row_bytes = p.nb * (uint32_t)bytes_of(dtype);
+    p.row_bytes = p.nb * gemv_block_bytes(dtype);
     p.bpi = int_blocks_per_step(dtype);
     return IFR_OK;
 }
@@ -1669,9 +1680,9 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
 // of its 64-element steps, rows aligned for the tile loads (16 bytes for
 // Q4_K/Q5_K, 4 for the others).
 static ifr_status check_pf_matrix(ifr_ctx *c, int32_t dtype, uint32_t cols, const void *w) {
-    if (!gemv_fmt_name(dtype)) return c->fail(IFR_EUNSUPPORTED, "prefill GEMM: dtype %d is not a quantized GGUF type", dtype);
+    if (!gemv_fmt_name(dtype)) return c->fail(IFR_EUNSUPPORTED, "prefill GEMM: dtype %d has no tile loader", dtype);
     if (cols % 64 || cols % (uint32_t)qk_of(dtype)) return c->fail(IFR_EUNSUPPORTED, "prefill GEMM: cols %u not a multiple of 64 and of the block", cols);
-    const uintptr_t need = (dtype == IFR_Q4_K || dtype == IFR_Q5_K) ? 16 : 4;
+    const uintptr_t need = gemv_align(dtype);
     if ((uintptr_t)w % need) return c->fail(IFR_EINVAL, "prefill GEMM: weights not %u-byte aligned", (unsigned)need);
     return IFR_OK;
 }

@@ -83,6 +83,8 @@ GEMV_ALL_MODES(q4_1, Q4_1)
 GEMV_ALL_MODES(q5_0, Q5_0)
 GEMV_ALL_MODES(q5_1, Q5_1)
 GEMV_ALL_MODES(q8_k, Q8_K)
+GEMV_ALL_MODES(f16, F16)
+GEMV_ALL_MODES(f32, F32)
 
 #define ATTN_KERNEL(HS, G)                                                                          \
     extern "C" __global__ void __launch_bounds__(256) attn_f16_h##HS##_g##G(AttnArgs a) {           \
@@ -139,6 +141,8 @@ GEMM_KERNELS(q4_0, Q4_0)
 GEMM_KERNELS(q4_1, Q4_1)
 GEMM_KERNELS(q5_0, Q5_0)
 GEMM_KERNELS(q5_1, Q5_1)
+GEMM_KERNELS(f16, F16)
+GEMM_KERNELS(f32, F32)
 extern "C" __global__ void __launch_bounds__(256) pf_embed_k(PfArgs a) { pf_embed_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { pf_rmsnorm_f16_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }

@@ -145,6 +145,11 @@ def random_blocks(dtype: int, n_blocks: int, rng: np.random.Generator) -> np.nda
     (gemv_quant.rs:367-430)."""
     from oracle import BLOCK_BYTES, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, Q8_K
 
+    if dtype in (0, 1):  # F32 / F16: finite values, some tiny and some large
+        v = rng.standard_normal(n_blocks)
+        v[rng.integers(0, 256, size=n_blocks) < 16] *= 1e-5
+        v[rng.integers(0, 256, size=n_blocks) < 4] *= 100.0
+        return v.astype(np.float32 if dtype == 0 else np.float16).view(np.uint8)
     bb = BLOCK_BYTES[dtype]
     raw = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
 

@@ -31,8 +31,9 @@ def decode(ctx, cfg, w, prompt, n):
         s.close()
 
 
-@pytest.mark.parametrize("mat,head,embd", [(I.Q4_K, I.Q6_K, I.Q8_0), (I.Q4_0, I.Q8_K, I.Q5_1), (I.Q5_0, I.Q4_1, I.Q4_0)],
-                         ids=["k_quants", "q4_0_q8_k_q5_1", "q5_0_q4_1_q4_0"])
+@pytest.mark.parametrize("mat,head,embd", [(I.Q4_K, I.Q6_K, I.Q8_0), (I.Q4_0, I.Q8_K, I.Q5_1), (I.Q5_0, I.Q4_1, I.Q4_0),
+                                           (I.Q4_K, I.F16, I.F16), (I.F16, I.F32, I.F16)],
+                         ids=["k_quants", "q4_0_q8_k_q5_1", "q5_0_q4_1_q4_0", "f16_head", "f16_matrices"])
 def test_model_round_trips_through_gguf(ctx, tmp_path, mat, head, embd):
     cfg = tiny_cfg()
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=11, mat_dtype=mat, head_dtype=head, embd_dtype=embd)

@@ -32,7 +32,8 @@ def oracle_model(cfg, weights):
     host = {}
     for name in weights.buffers:
         dt, arr, rows, cols = weights.download(name)
-        host[name] = arr if dt == I.F32 else (dt, arr, rows, cols)
+        vector = name.endswith(("norm.weight", ".bias"))
+        host[name] = arr if vector else (dt, np.ascontiguousarray(arr).view(np.uint8), rows, cols)
     c = dict(hidden=cfg.hidden, ffn=cfg.ffn, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
              vocab=cfg.vocab, max_pos=cfg.max_pos, rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps,
              kv_f16=int(cfg.kv_dtype == I.F16), rope_neox=int(cfg.rope_variant == I.ROPE_NEOX))
@@ -68,7 +69,8 @@ def run_steps(ctx, state, weights, prompt, n_total, mode):
 @pytest.mark.parametrize("mode", ["fused", "unfused", "graph"])
 @pytest.mark.parametrize("mat,head,kv", [("Q4_K", "Q6_K", "F16"), ("Q8_0", "Q8_0", "F32"), ("Q5_K", "Q4_K", "F16"),
                                          ("Q6_K", "Q5_K", "F32"), ("Q4_0", "Q8_K", "F16"), ("Q5_1", "Q4_1", "F32"),
-                                         ("Q5_0", "Q5_1", "F16")])
+                                         ("Q5_0", "Q5_1", "F16"), ("F16", "F16", "F16"), ("F32", "F32", "F32"),
+                                         ("Q4_K", "F16", "F16")])
 def test_tiny_model_step_by_step(ctx, oracle_lib, mode, mat, head, kv, exact):
     import inferi_amd as I
 

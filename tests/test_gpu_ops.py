@@ -202,6 +202,23 @@ def test_gemv_selects_columns(ctx, oracle_lib, gemv_path, dtype):
         np.testing.assert_allclose(got, deq[:, k], rtol=2e-6, atol=1e-6 * np.abs(deq).max())
 
 
+@pytest.mark.parametrize("dtype", [O.F16, O.F32], ids=["F16", "F32"])
+@pytest.mark.parametrize("rows,cols", [(1, 32), (33, 1024), (100, 5632), (4096, 4096), (64, 14336)])
+def test_gemv_unquantized(ctx, oracle_lib, gemv_path, dtype, rows, cols):
+    """F32 matrices (GpuQuantTensor::F32 -> Gemm, gemv_quant.rs:203-208) and
+    F16 ones (converted to F32 at load by the reference, gguf.rs:113-128):
+    N(0, 0.02) values with a sprinkling of f16 subnormals and of large
+    magnitudes, against the oracle's f64 product of the same values."""
+    rng = np.random.default_rng(rows + cols + dtype)
+    wf = rng.standard_normal(rows * cols) * 0.02
+    wf[rng.integers(0, rows * cols, rows * cols // 50)] *= 1e-4  # f16 subnormal range
+    wf[rng.integers(0, rows * cols, rows * cols // 200)] *= 300.0
+    w = wf.astype(np.float16 if dtype == O.F16 else np.float32).view(np.uint8)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = _gemv_case(ctx, dtype, rows, cols, w, x)
+    assert_close(got, O.gemv_quant(dtype, w, rows, cols, x), what=f"{rows}x{cols}")
+
+
 def test_gemv_c1_q4k_4096(ctx, oracle_lib, gemv_path):
     """W 4096x4096 ~ N(0, 0.02) quantized to Q4_K, x ~ N(0, 1).
     Dequant bit-exact and y within 1e-3."""

@@ -69,7 +69,7 @@ def test_gemm_quant_matches_f64(ctx, oracle_lib, rows, cols, m):
     w.free()
 
 
-FMTS = ["Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q8_K"]
+FMTS = ["Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q8_K", "F16", "F32"]
 
 
 @pytest.mark.parametrize("fmt", FMTS)
@@ -237,7 +237,7 @@ def test_prefill_qwen2_style(ctx, oracle_lib):
 
 
 @pytest.mark.parametrize("mat,head", [("Q8_0", "Q8_0"), ("Q5_K", "Q6_K"), ("Q6_K", "Q4_K"), ("Q4_0", "Q8_K"),
-                                      ("Q5_1", "Q4_1"), ("Q8_K", "Q5_0")])
+                                      ("Q5_1", "Q4_1"), ("Q8_K", "Q5_0"), ("F16", "F16"), ("F32", "Q6_K")])
 def test_prefill_other_formats(ctx, oracle_lib, mat, head):
     """Prefill with every layer matrix of another GGUF type."""
     import inferi_amd as I
