@@ -169,8 +169,6 @@ def run_decode(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
-    ctx.set_option("persistent", args.persistent)
-    ctx.set_option("attn_mfma", args.attn_mfma)
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
@@ -331,7 +329,6 @@ def run_attn(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
-    ctx.set_option("attn_mfma", args.attn_mfma)
     out = []
     nh, nkv, hs = 32, 8, 128
     kv_dim = nkv * hs
@@ -392,13 +389,10 @@ def main() -> None:
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")
-    ap.add_argument("--attn-mfma", type=int, default=0, help="attention split with q.k on the matrix cores")
     ap.add_argument("--pmc-sample", action="store_true", help="workload for the rocprofv3 --pmc traffic passes")
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
-    ap.add_argument("--persistent", type=int, default=0,
-                    help="1: the GEMV stages between attentions in one persistent launch per layer")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU; the multi-GPU sharding of the decode path is designed "

@@ -96,13 +96,7 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * a default; bit 1 FFN down; bit 2 gate/up, bit 3 with 16 waves of two
  * rows; bit 4 the output head; bit 5, a default, gate/up with h in f32 and
  * the FFN down GEMV quantizing h itself; bit 6, a default, the Q6_K output
- * head in 4-wave workgroups of up to 256 VGPRs, two per CU).  Default 97.  "persistent" = 1 runs the decode step's
- * GEMV stages between two attentions (O, gate/up, down, the next QKV) as one
- * persistent launch per layer with grid barriers (Q4_K models; results
- * identical to the default path).  "attn_mfma" = 1 makes decode states
- * created afterwards (and ifr_attention) use the attention split kernel that
- * forms q.k on the matrix cores (f16 caches, head size 128, at most 4 query
- * heads per KV head; same results within the decode tolerance).  "pf_chunk"
+ * head in 4-wave workgroups of up to 256 VGPRs, two per CU).  Default 97.  "pf_chunk"
  * sets the prompt tokens per ifr_llama2_prefill pass (a multiple of 64, at
  * most 16384; 0 = 4096), read at a state's first prefill: the results do
  * not depend on it. */
@@ -211,7 +205,8 @@ IFR_API ifr_status ifr_silu(ifr_ctx *ctx, float *in_out_h1, const float *h2, uin
  * layout) or IFR_F16.  `params` (host) sizes the launch; `dev_params` is the
  * device copy the kernel reads.  BatchedMultiqueryAttention::launch
  * (crates/inferi/src/ops/batched_multiquery_attention.rs:87-110) ->
- * FusedAttention::launch (:27-76).  head_size in {64, 128}, kv_mul <= 8. */
+ * FusedAttention::launch (:27-76), which, like this call, takes any kv_mul.
+ * head_size is a multiple of 8, at most 128; pos below 2^30. */
 IFR_API ifr_status ifr_attention(ifr_ctx *ctx, const ifr_attn_params *params, const ifr_attn_params *dev_params,
                                  const float *q, const void *key_cache, const void *value_cache, int32_t kv_dtype,
                                  float *xb);
@@ -277,6 +272,10 @@ typedef struct {
     int32_t kv_dtype;     /* IFR_F16 or IFR_F32 */
     int32_t rope_variant; /* IFR_ROPE_ORIGINAL (llama) */
 } ifr_llama2_config;
+/* Accepted shapes: head size (hidden / n_heads) a multiple of 8, at most
+ * 128; n_heads / n_kv_heads (kv_mul) at most 64; hidden and ffn multiples of
+ * 32; max_pos up to 2^30 (the cache is sized to it, as transformer.rs:85-104
+ * sizes it to context_length). */
 
 typedef struct ifr_llama2_weights ifr_llama2_weights;
 typedef struct ifr_llama2_state ifr_llama2_state;

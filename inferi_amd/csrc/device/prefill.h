@@ -430,38 +430,43 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
 // ------------------------------------------------------------ attention --
 // Causal attention of the chunk's queries (positions p0 .. p0+M-1) over the
 // cache rows [0, position], on the matrix cores (flash attention).
-// Workgroup (h, qt): KV head h, its G query heads and 64/G queries, i.e. 64
-// rows r = qi * G + j.  Per key tile of 64 cache rows:
+// Workgroup (h, qt): KV head h, its G = kv_mul query heads and QT = 64 / G
+// queries, i.e. QT * G <= 64 rows r = qi * G + j (rows past QT * G hold
+// nothing).  Head dims run to HSP (the head size rounded up to 64 or 128;
+// dims past the head size are zeros).  Per key tile of 64 cache rows:
 //   S = Q K^T     (f16 operands from LDS, 4 waves x one 32x32 MFMA tile)
 //   running softmax per row in base-2 units (q pre-scaled by
 //   log2(e)/sqrt(hs)); P = 2^(S - m) as f16
-//   O = alpha O + P V   (4 waves x 32 rows x 64 dims)
+//   O = alpha O + P V   (4 waves x 32 rows x HSP/2 dims)
 // and out = O / l is written as f16 for the O GEMM.
 constexpr int PF_ROWS = 64, PF_KT = 64;
 
-template <int G>
-constexpr uint32_t pf_attn_queries() { return (uint32_t)(PF_ROWS / G); }
-
-template <int HS, int G, bool F16>
+template <int HSP, bool F16>
 __device__ void pf_attn_body(const PfArgs &a) {
-    constexpr int R = PF_ROWS, NT = 256, QT = PF_ROWS / G;
-    constexpr int HSP = HS + 8, KTP = PF_KT + 8; // padded LDS rows (halves)
-    constexpr int DT = HS / 64;                  // 32x32 O tiles per wave along the dims
-    __shared__ __attribute__((aligned(16))) _Float16 qh[R][HSP];
-    __shared__ __attribute__((aligned(16))) _Float16 kh[PF_KT][HSP];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[HS][KTP];
+    constexpr int R = PF_ROWS, NT = 256;
+    constexpr int HSL = HSP + 8, KTP = PF_KT + 8; // padded LDS rows (halves)
+    constexpr int DT = HSP / 64;                  // 32x32 O tiles per wave along the dims
+    __shared__ __attribute__((aligned(16))) _Float16 qh[R][HSL];
+    __shared__ __attribute__((aligned(16))) _Float16 kh[PF_KT][HSL];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[HSP][KTP];
     __shared__ __attribute__((aligned(16))) _Float16 ph[R][KTP];
     __shared__ float sf[R][PF_KT + 1];
     __shared__ float alpha_s[R], l_s[R];
+    __shared__ int32_t qpos_s[R]; // position of row r's query, -1 for an unused row
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t G = a.kv_mul, hs = a.head_size, QT = (uint32_t)PF_ROWS / G;
     const uint32_t kvh = blockIdx.x, qt0 = blockIdx.y * QT;
-    const uint32_t nq = min((uint32_t)QT, a.M - qt0);
-    const float qscale = 1.44269504088896341f / sqrtf((float)HS);
+    const uint32_t nq = min(QT, a.M - qt0);
+    const float qscale = 1.44269504088896341f / sqrtf((float)hs);
     const float *qbase = (const float *)a.qkv;
-    for (uint32_t i = tid; i < (uint32_t)R * HS; i += NT) {
-        const uint32_t rr = i / HS, d = i % HS, qi = rr / G, j = rr % G;
-        const float v = qi < nq ? qbase[(size_t)(qt0 + qi) * a.ld_qkv + (kvh * G + j) * HS + d] : 0.0f;
+    for (uint32_t i = tid; i < (uint32_t)R * HSP; i += NT) {
+        const uint32_t rr = i / HSP, d = i % HSP, qi = rr / G, j = rr % G;
+        const float v = (qi < nq && d < hs) ? qbase[(size_t)(qt0 + qi) * a.ld_qkv + (kvh * G + j) * hs + d] : 0.0f;
         qh[rr][d] = (_Float16)(v * qscale);
+    }
+    if (tid < R) {
+        const uint32_t qi = (uint32_t)tid / G;
+        qpos_s[tid] = qi < nq ? (int32_t)(a.p0 + qt0 + qi) : -1;
     }
     // softmax ownership: row sr, keys [16 * sq, 16 * sq + 16)
     const uint32_t sr = (uint32_t)tid >> 2, sq = (uint32_t)tid & 3u;
@@ -469,7 +474,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
     // MFMA roles
     const uint32_t li = (uint32_t)lane & 31u, lk = 8 * ((uint32_t)lane >> 5);
     const uint32_t srow = 32 * (uint32_t)(wave >> 1), skey = 32 * (uint32_t)(wave & 1); // S tile of this wave
-    const uint32_t orow = 32 * (uint32_t)(wave >> 1), odim = (HS / 2) * (uint32_t)(wave & 1); // O block
+    const uint32_t orow = 32 * (uint32_t)(wave >> 1), odim = (HSP / 2) * (uint32_t)(wave & 1); // O block
     float16v oacc[DT];
 #pragma unroll
     for (int t = 0; t < DT; t++)
@@ -479,11 +484,11 @@ __device__ void pf_attn_body(const PfArgs &a) {
     const uint32_t last = a.p0 + qt0 + nq - 1; // largest query position of the tile
     for (uint32_t k0 = 0; k0 <= last; k0 += PF_KT) {
         __syncthreads(); // previous tile's operands are consumed
-        for (uint32_t i = tid; i < (uint32_t)PF_KT * HS; i += NT) {
-            const uint32_t kr = i / HS, d = i % HS, kp = k0 + kr;
+        for (uint32_t i = tid; i < (uint32_t)PF_KT * HSP; i += NT) {
+            const uint32_t kr = i / HSP, d = i % HSP, kp = k0 + kr;
             _Float16 kk = (_Float16)0.0f, vv = (_Float16)0.0f;
-            if (kp <= last) {
-                const size_t off = (size_t)kp * a.kv_dim + (size_t)kvh * HS + d;
+            if (kp <= last && d < hs) {
+                const size_t off = (size_t)kp * a.kv_dim + (size_t)kvh * hs + d;
                 if constexpr (F16) {
                     const uint16_t kb = ((const uint16_t *)a.k_cache)[off], vb = ((const uint16_t *)a.v_cache)[off];
                     __builtin_memcpy(&kk, &kb, 2);
@@ -503,7 +508,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
 #pragma unroll
             for (int e = 0; e < 16; e++) sacc[e] = 0.0f;
 #pragma unroll
-            for (int kk = 0; kk < HS; kk += 16) {
+            for (int kk = 0; kk < HSP; kk += 16) {
                 const half8v av = *(const half8v *)&qh[srow + li][kk + lk];
                 const half8v bv = *(const half8v *)&kh[skey + li][kk + lk];
                 sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, sacc, 0, 0, 0);
@@ -512,8 +517,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
             for (int e = 0; e < 16; e++) {
                 const uint32_t row = srow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
                 const uint32_t key = skey + li;
-                const uint32_t qi = row / G, qpos = a.p0 + qt0 + qi;
-                sf[row][key] = (k0 + key <= qpos && qi < nq) ? sacc[e] : -INFINITY;
+                sf[row][key] = ((int32_t)(k0 + key) <= qpos_s[row]) ? sacc[e] : -INFINITY;
             }
         }
         __syncthreads();
@@ -567,8 +571,8 @@ __device__ void pf_attn_body(const PfArgs &a) {
         for (int e = 0; e < 16; e++) {
             const uint32_t row = orow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
             const uint32_t qi = row / G, dim = odim + 32 * t + li;
-            if (qi < nq)
-                ((_Float16 *)a.xh)[(size_t)(qt0 + qi) * a.ldh + (kvh * G + row % G) * HS + dim] =
+            if (qpos_s[row] >= 0 && dim < hs)
+                ((_Float16 *)a.xh)[(size_t)(qt0 + qi) * a.ldh + (kvh * G + row % G) * hs + dim] =
                     (_Float16)(oacc[t][e] / l_s[row]);
         }
 }

@@ -42,8 +42,8 @@ constexpr uint32_t GEMV_MAX_LDS = 65536 - 256;
 uint64_t xq_bytes(uint64_t n) { return 3 * n + n / 2; }
 
 // Dynamic LDS of a GEMV launch: x as f32, or its XQ copy.
-constexpr uint32_t ATTN_CMAX = 256;       // device/attention.h
-constexpr uint32_t ATTN_MERGE_MAX = 256;  // device/attention.h: most splits per KV head
+constexpr uint32_t ATTN_SPLITS_MAX = 256; // attention splits per KV head (at most)
+constexpr uint32_t ATTN_GT_MAX = 8;       // device/attention.h: query heads per workgroup
 constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
 constexpr uint32_t PF_GEMM_TILE = 128;    // device/prefill.h: PF_BM = PF_BN
 constexpr uint32_t PF_CHUNK = 4096;       // prompt tokens per prefill pass (at most)
@@ -124,18 +124,11 @@ struct ifr_ctx {
     // GEMV arithmetic: 0 = x as 16-bit fixed point with int8 dot products,
     // 1 = exact fp32 x and FMAs
     int gemv_exact = 0;
-    // decode step: 1 = the GEMV stages between attentions in one persistent
-    // launch per layer (device/pk.h) where the model allows it
-    int persistent = 0;
-    int pk_trace_layer = -1; // layer whose persistent launch records its stage timeline
     // one-item GEMV forms in use: bit 0 resid with one K step (O), bit 1
     // resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16 waves of
     // two rows (else 8 waves of four), bit 4 the output head, bit 5 gateup
     // with h in f32 and the down GEMV quantizing it (default: bits 0 and 5)
     int gemv_grp = 97;
-    // attention split on the matrix cores where it applies (read when a
-    // decode state is created)
-    int attn_mfma = 0;
     // prompt tokens per prefill pass (0: PF_CHUNK), read at a state's first prefill
     uint32_t pf_chunk = 0;
     // this device's fixed scratch of ifr_matmul_quant_noalloc (noalloc.hip)
@@ -356,36 +349,34 @@ static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtyp
 
 // ------------------------------------------------------------- attention --
 
+// Head sizes run on kernels for 64 or 128 dims (device/attention.h pads the
+// head to them).
+static uint32_t attn_hsp(uint32_t head_size) { return head_size <= 64 ? 64u : 128u; }
 // Splits of the attention over the sequence for T positions: one batch of
-// the split kernel each (8192/head_size positions, device/attention.h
-// attn_quantum), at most ATTN_MERGE_MAX; longer chunks beyond that.
-static uint32_t attn_quantum(uint32_t head_size) { return 8192u / head_size; }
+// the split kernel each (8192/HSP positions, device/attention.h
+// attn_quantum), at most ATTN_SPLITS_MAX; longer chunks beyond that.
 static uint32_t attn_splits_for(uint32_t T, uint32_t head_size) {
-    const uint32_t q = attn_quantum(head_size);
-    return std::max(1u, std::min(ATTN_MERGE_MAX, (T + q - 1) / q));
+    const uint32_t q = 8192u / attn_hsp(head_size);
+    return std::max(1u, std::min(ATTN_SPLITS_MAX, (uint32_t)(((uint64_t)T + q - 1) / q)));
+}
+// A KV head's query heads go to n_sub workgroups of gt heads each (gt <= 8,
+// the last workgroup holding the rest).
+static void attn_groups(uint32_t kv_mul, uint32_t &n_sub, uint32_t &gt) {
+    n_sub = (kv_mul + ATTN_GT_MAX - 1) / ATTN_GT_MAX;
+    gt = (kv_mul + n_sub - 1) / n_sub;
 }
 
-// The matrix-core split kernel (device/attention.h attn2_body) serves f16
-// caches of head size 128 with at most 4 query heads per KV head: splits of
-// a fixed chunk of whole 128-position blocks, at most ATTN_MERGE_MAX.
-static bool attn2_ok(const ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, int32_t kv_dtype) {
-    return c->attn_mfma && kv_dtype == IFR_F16 && head_size == 128 && kv_mul <= 4;
-}
-static uint32_t attn2_chunk(uint32_t seq_cap) {
-    const uint32_t nb = (seq_cap + 127) / 128, per = (nb + ATTN_MERGE_MAX - 1) / ATTN_MERGE_MAX;
-    return per * 128;
-}
-
-// Split pass over the KV sequence, then the merge of the partials.
-static ifr_status launch_attn(ifr_ctx *c, uint32_t head_size, uint32_t kv_mul, int32_t kv_dtype, AttnArgs &a,
-                              uint32_t n_kv_heads, bool mfma = false) {
+// Split pass over the KV sequence, then the merge of the partials.  `a`
+// carries head_size, kv_mul, n_splits and n_out; n_sub is set here.
+static ifr_status launch_attn(ifr_ctx *c, int32_t kv_dtype, AttnArgs &a, uint32_t n_kv_heads) {
+    uint32_t n_sub, gt;
+    attn_groups(a.kv_mul, n_sub, gt);
+    a.n_sub = n_sub;
     char name[64];
-    snprintf(name, sizeof name, "attn_%s_h%u_g%u", kv_dtype == IFR_F16 ? "f16" : "f32", head_size, kv_mul);
-    if (mfma) snprintf(name, sizeof name, "attn2_f16_h128_g%u", kv_mul);
-    ifr_status st = c->launch(name, dim3(n_kv_heads, a.n_splits), dim3(256), 0, a);
+    snprintf(name, sizeof name, "attn_%s_h%u_g%u", kv_dtype == IFR_F16 ? "f16" : "f32", attn_hsp(a.head_size), gt);
+    ifr_status st = c->launch(name, dim3(n_kv_heads * n_sub, a.n_splits), dim3(256), 0, a);
     if (st) return st;
-    snprintf(name, sizeof name, "attn_merge_h%u_g%u", head_size, kv_mul);
-    return c->launch(name, dim3(n_kv_heads * kv_mul * (head_size / 16)), dim3(64), 0, a);
+    return c->launch("attn_merge", dim3((a.n_out + 15) / 16), dim3(64), 0, a);
 }
 
 // ----------------------------------------------------------------- model --
@@ -416,8 +407,6 @@ struct ifr_llama2_state {
     ifr_ctx *ctx;
     ifr_llama2_config cfg;
     uint32_t kv_dim, head_size, kv_mul, n_splits;
-    bool attn2 = false;      // matrix-core attention split kernel
-    uint32_t attn_chunk = 0; // its positions per split
     std::vector<void *> allocs;
     float *x, *xb, *xb2, *q, *ktmp, *vtmp, *hb, *hb2, *att, *logits, *probs;
     uint8_t *smp_work;
@@ -447,14 +436,8 @@ struct ifr_llama2_state {
     float temperature = 0.0f, topp = 0.0f;
     uint64_t seed = 0;
     uint32_t sampler_gen = 0;
-    // persistent layer tail: the residual after attention, barrier words and
-    // the error word
-    float *pk_xmid = nullptr;
-    uint32_t *pk_bar = nullptr, *pk_err = nullptr;
-    uint64_t *pk_ts = nullptr; // stage timeline of one launch
     // captured decode step
     hipGraphExec_t graph = nullptr;
-    int graph_pk = -1;
     int graph_grp = -1;
     uint32_t graph_sampler = 0;
     uint64_t graph_wid = 0, graph_wgen = 0; // weights id and generation the graph was captured with
@@ -469,14 +452,13 @@ static ifr_status validate_cfg(ifr_ctx *c, const ifr_llama2_config *cfg) {
     if (cfg->hidden % cfg->n_heads || cfg->n_heads % cfg->n_kv_heads)
         return c->fail(IFR_EINVAL, "hidden %% n_heads or n_heads %% n_kv_heads != 0");
     const uint32_t hs = cfg->hidden / cfg->n_heads, kv_mul = cfg->n_heads / cfg->n_kv_heads;
-    if (hs != 64 && hs != 128) return c->fail(IFR_EUNSUPPORTED, "head_size %u (64 or 128 supported)", hs);
-    if (kv_mul != 1 && kv_mul != 2 && kv_mul != 4 && kv_mul != 8)
-        return c->fail(IFR_EUNSUPPORTED, "kv_mul %u (1, 2, 4 or 8 supported)", kv_mul);
+    if (hs % 8 || hs > 128) return c->fail(IFR_EUNSUPPORTED, "head_size %u (a multiple of 8, at most 128)", hs);
+    if (kv_mul > 64) return c->fail(IFR_EUNSUPPORTED, "kv_mul %u (at most 64 query heads per KV head)", kv_mul);
     if (cfg->hidden % 32 || cfg->ffn % 32) return c->fail(IFR_EUNSUPPORTED, "hidden and ffn must be multiples of 32");
     if (cfg->kv_dtype != IFR_F16 && cfg->kv_dtype != IFR_F32) return c->fail(IFR_EINVAL, "kv_dtype must be F16 or F32");
     if (cfg->rope_variant != IFR_ROPE_ORIGINAL && cfg->rope_variant != IFR_ROPE_NEOX)
         return c->fail(IFR_EINVAL, "bad rope_variant");
-    if (cfg->max_pos > ATTN_CMAX * ATTN_MERGE_MAX) return c->fail(IFR_EUNSUPPORTED, "max_pos too large");
+    if (cfg->max_pos > (1u << 30)) return c->fail(IFR_EUNSUPPORTED, "max_pos %u too large", cfg->max_pos);
     return IFR_OK;
 }
 
@@ -512,120 +494,7 @@ static ifr_status launch_keys_of_y(ifr_ctx *c, const float *logits, uint32_t n, 
 
 static ifr_status enqueue_head(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused, uint32_t n_ss_a);
 
-// The persistent layer tail runs a model when every matrix is Q4_K, the
-// layers have no QKV bias, RoPE pairs adjacent dims (the fused QKV epilogue),
-// and one workgroup per CU holds each stage's rows and its input in LDS.
-static bool pk_supported(ifr_ctx *c, const ifr_llama2_state *s, const ifr_llama2_weights *w) {
-    const ifr_llama2_config &cfg = s->cfg;
-    if (!c->persistent || c->gemv_exact || cfg.rope_variant != IFR_ROPE_ORIGINAL) return false;
-    for (const LayerW &L : w->layers) {
-        const Tens *m[7] = {&L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
-        for (const Tens *t : m)
-            if (t->dtype != IFR_Q4_K || ((uintptr_t)t->data & 15)) return false;
-        if (L.q_bias.data || L.k_bias.data || L.v_bias.data) return false;
-    }
-    const uint32_t H = cfg.hidden, F = cfg.ffn, nwg = (uint32_t)c->n_cu;
-    if (H % 256 || F % 256 || H / 256 > 16 * PK_KSTEPS || F / 256 > 16 * PK_KSTEPS) return false;
-    auto rows_per_wg = [&](uint32_t units, uint32_t gu) { return (units + nwg - 1) / nwg * gu; };
-    if (rows_per_wg((H + 2 * s->kv_dim) / 2, 2) > PK_PART_ROWS || rows_per_wg(H / 16, 16) > PK_PART_ROWS ||
-        rows_per_wg(F / 16, 32) > PK_PART_ROWS)
-        return false;
-    const uint32_t lds = pk_lds_bytes(std::max(H, F));
-    if (lds > GEMV_MAX_LDS) return false;
-    hipFunction_t f = c->fn("pk_tail_q4_k");
-    int occ = 0;
-    if (!f || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&occ, f, PK_WAVES * 64, lds) != hipSuccess || occ < 1)
-        return false;
-    return true;
-}
-
-// One decode step with the persistent layer tail: per layer the attention
-// split and merge kernels, then one launch for O, gate/up, down and the next
-// layer's QKV (mode 0: the embedding and the first QKV).
-static ifr_status enqueue_step_pk(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w) {
-    const ifr_llama2_config &cfg = s->cfg;
-    const uint32_t hidden = cfg.hidden, L = cfg.n_layers;
-    const uint32_t lds = pk_lds_bytes(std::max(hidden, cfg.ffn));
-    ifr_status st;
-    PkArgs base{};
-    base.table = w->token_embd.data;
-    base.emb_row_bytes = hidden / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
-    base.emb_fmt = w->token_embd.dtype;
-    base.emb_gamma = (const float *)w->layers[0].attn_norm.data;
-    base.tokens = s->tokens;
-    base.ctl = s->ctl;
-    base.rope_tab = s->rope_tab;
-    base.x = s->x;
-    base.x_mid = s->pk_xmid;
-    base.q = s->q;
-    base.xq_att = s->xq_att;
-    base.xq_f = s->xq_f;
-    base.xq_h = s->xq_h;
-    base.xq_a = s->xq_a;
-    base.ss_f = s->ss_f;
-    base.ss_a = s->ss_a;
-    base.n_ss_a = (hidden + 255) / 256;
-    base.hidden = hidden;
-    base.ffn = cfg.ffn;
-    base.head_size = s->head_size;
-    base.kv_dim = s->kv_dim;
-    base.nb_h = hidden / 256;
-    base.rb_h = base.nb_h * 144;
-    base.nb_f = cfg.ffn / 256;
-    base.rb_f = base.nb_f * 144;
-    base.eps = cfg.rms_eps;
-    base.kv_f16 = cfg.kv_dtype == IFR_F16;
-    base.bar = s->pk_bar;
-    base.err = s->pk_err;
-    auto set_qkv = [&](PkArgs &a, uint32_t l) {
-        const LayerW &Lw = w->layers[l];
-        a.wq = Lw.attn_q.data;
-        a.wk = Lw.attn_k.data;
-        a.wv = Lw.attn_v.data;
-        a.kc = s->kcache + (size_t)l * s->layer_kv_bytes;
-        a.vc = s->vcache + (size_t)l * s->layer_kv_bytes;
-    };
-    const dim3 grid((uint32_t)c->n_cu), block(PK_WAVES * 64);
-    {
-        PkArgs a = base;
-        a.mode = 0;
-        set_qkv(a, 0);
-        if ((st = c->launch("pk_tail_q4_k", grid, block, lds, a))) return st;
-    }
-    for (uint32_t l = 0; l < L; l++) {
-        AttnArgs t{};
-        t.q = s->q;
-        t.k_cache = s->kcache + (size_t)l * s->layer_kv_bytes;
-        t.v_cache = s->vcache + (size_t)l * s->layer_kv_bytes;
-        t.out = s->att;
-        t.xq_out = s->xq_att;
-        t.part_o = s->part_o;
-        t.part_ml = s->part_ml;
-        t.pos = &s->ctl->pos;
-        t.kv_dim = s->kv_dim;
-        t.n_splits = s->n_splits;
-        t.chunk = s->attn_chunk;
-        t.seq_cap = cfg.max_pos;
-        t.n_out = hidden;
-        if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, t, cfg.n_kv_heads, s->attn2))) return st;
-        const LayerW &Lw = w->layers[l];
-        PkArgs a = base;
-        a.mode = 1;
-        a.wo = Lw.attn_output.data;
-        a.wg = Lw.ffn_gate.data;
-        a.wu = Lw.ffn_up.data;
-        a.wd = Lw.ffn_down.data;
-        a.ffn_norm = (const float *)Lw.ffn_norm.data;
-        a.next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
-        if (l + 1 < L) set_qkv(a, l + 1);
-        if ((int)l == c->pk_trace_layer) a.ts = s->pk_ts;
-        if ((st = c->launch("pk_tail_q4_k", grid, block, lds, a))) return st;
-    }
-    return enqueue_head(c, s, w, 1, hidden / 16);
-}
-
 static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
-    if (fused && pk_supported(c, s, w)) return enqueue_step_pk(c, s, w);
     const ifr_llama2_config &cfg = s->cfg;
     const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn, L = cfg.n_layers;
     const uint32_t n_ss_res = hidden / 16; // partial sums written by a RESID GEMV (one per 16-row tile)
@@ -746,10 +615,11 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.pos = &s->ctl->pos;
             a.kv_dim = kv_dim;
             a.n_splits = s->n_splits;
-            a.chunk = s->attn_chunk;
             a.seq_cap = cfg.max_pos;
             a.n_out = hidden;
-            if ((st = launch_attn(c, s->head_size, s->kv_mul, cfg.kv_dtype, a, cfg.n_kv_heads, s->attn2))) return st;
+            a.head_size = s->head_size;
+            a.kv_mul = s->kv_mul;
+            if ((st = launch_attn(c, cfg.kv_dtype, a, cfg.n_kv_heads))) return st;
         }
         if (fused) {   // x += Wo att; x * ffn_norm quantized for gate/up
             if ((st = check_gemv(c, Lw.attn_output.dtype, hidden, Lw.attn_output.data, p))) return st;
@@ -1029,25 +899,13 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->gemv_exact = value ? 1 : 0;
         return IFR_OK;
     }
-    if (!strcmp(key, "persistent")) {
-        c->persistent = value ? 1 : 0;
-        return IFR_OK;
-    }
     if (!strcmp(key, "pf_chunk")) {
         if (value < 0 || value > 16384 || value % 64) return c->fail(IFR_EINVAL, "pf_chunk must be a multiple of 64 in [0, 16384]");
         c->pf_chunk = (uint32_t)value;
         return IFR_OK;
     }
-    if (!strcmp(key, "attn_mfma")) {
-        c->attn_mfma = value ? 1 : 0;
-        return IFR_OK;
-    }
     if (!strcmp(key, "gemv_grp")) {
         c->gemv_grp = (int)value;
-        return IFR_OK;
-    }
-    if (!strcmp(key, "pk_trace_layer")) {
-        c->pk_trace_layer = (int)value;
         return IFR_OK;
     }
     if (!strcmp(key, "gemv_waves")) {
@@ -1247,20 +1105,19 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     if (!c) return IFR_EINVAL;
     if (!p || !dev_p || !q || !kc || !vc || !xb) return c->fail(IFR_EINVAL, "attention: null pointer");
     if (kv_dtype != IFR_F16 && kv_dtype != IFR_F32) return c->fail(IFR_EINVAL, "attention: kv dtype F16 or F32");
-    if (p->head_size != 64 && p->head_size != 128) return c->fail(IFR_EUNSUPPORTED, "attention: head_size %u", p->head_size);
-    if (!p->kv_mul || p->n_heads % p->kv_mul) return c->fail(IFR_EINVAL, "attention: n_heads %% kv_mul");
+    if (!p->head_size || p->head_size % 8 || p->head_size > 128)
+        return c->fail(IFR_EUNSUPPORTED, "attention: head_size %u (a multiple of 8, at most 128)", p->head_size);
+    if (!p->n_heads || !p->kv_mul || p->n_heads % p->kv_mul) return c->fail(IFR_EINVAL, "attention: n_heads %% kv_mul");
     const uint32_t g = p->kv_mul;
-    if (g != 1 && g != 2 && g != 4 && g != 8) return c->fail(IFR_EUNSUPPORTED, "attention: kv_mul %u", g);
     const uint32_t n_kv = p->n_heads / g;
     if (p->kv_dim != n_kv * p->head_size) return c->fail(IFR_EINVAL, "attention: kv_dim != n_kv_heads * head_size");
     if (p->pos >= p->seq_len) return c->fail(IFR_EINVAL, "attention: pos %u >= seq_len %u", p->pos, p->seq_len);
-    if (p->pos >= ATTN_CMAX * ATTN_MERGE_MAX) return c->fail(IFR_EUNSUPPORTED, "attention: pos %u too large", p->pos);
+    if (p->pos >= (1u << 30)) return c->fail(IFR_EUNSUPPORTED, "attention: pos %u too large", p->pos);
     if ((uintptr_t)q % 16 || (uintptr_t)kc % 16 || (uintptr_t)vc % 16)
         return c->fail(IFR_EINVAL, "attention: q and caches must be 16-byte aligned");
     const uint32_t T = p->pos + 1;
-    const bool mfma = attn2_ok(c, p->head_size, g, kv_dtype);
-    const uint32_t chunk = mfma ? attn2_chunk(T) : 0, S = mfma ? (T + chunk - 1) / chunk : attn_splits_for(T, p->head_size);
-    const size_t part_o = (size_t)n_kv * S * g * p->head_size, part_ml = (size_t)n_kv * S * g * 2;
+    const uint32_t S = attn_splits_for(T, p->head_size);
+    const size_t part_o = (size_t)p->n_heads * S * p->head_size, part_ml = (size_t)p->n_heads * S * 2;
     ifr_status st = c->ensure_scratch((part_o + part_ml) * sizeof(float));
     if (st) return st;
     AttnArgs a{};
@@ -1273,9 +1130,11 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     a.pos = &dev_p->pos;
     a.kv_dim = p->kv_dim;
     a.n_splits = S;
-    a.chunk = chunk;
     a.seq_cap = T;
-    return launch_attn(c, p->head_size, g, kv_dtype, a, n_kv, mfma);
+    a.n_out = p->n_heads * p->head_size;
+    a.head_size = p->head_size;
+    a.kv_mul = g;
+    return launch_attn(c, kv_dtype, a, n_kv);
 }
 
 IFR_API ifr_status ifr_argmax(ifr_ctx *c, const float *v, uint32_t n, uint32_t *dev_index) {
@@ -1565,13 +1424,7 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     s->head_size = cfg->hidden / cfg->n_heads;
     s->kv_dim = s->head_size * cfg->n_kv_heads;
     s->kv_mul = cfg->n_heads / cfg->n_kv_heads;
-    s->attn2 = attn2_ok(c, s->head_size, s->kv_mul, cfg->kv_dtype);
-    if (s->attn2) {
-        s->attn_chunk = attn2_chunk(cfg->max_pos);
-        s->n_splits = (cfg->max_pos + s->attn_chunk - 1) / s->attn_chunk;
-    } else {
-        s->n_splits = attn_splits_for(cfg->max_pos, s->head_size);
-    }
+    s->n_splits = attn_splits_for(cfg->max_pos, s->head_size);
     auto alloc = [&](size_t bytes, void **p) -> ifr_status {
         ifr_status e = c->hip(hipMalloc(p, std::max<size_t>(bytes, 16)), "hipMalloc(state)");
         if (e) return e;
@@ -1590,15 +1443,13 @@ IFR_API ifr_status ifr_llama2_state_create(ifr_ctx *c, const ifr_llama2_config *
     A(s->attn_params, sizeof(ifr_attn_params))
     s->part_keys_cap = std::max(MAX_PARTS, (uint32_t)((cfg->vocab + GEMV_ONE_WAVES * 2 - 1) / (GEMV_ONE_WAVES * 2)));
     A(s->part_keys, (size_t)s->part_keys_cap * 8)
-    A(s->part_o, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * s->head_size * 4)
-    A(s->part_ml, (size_t)cfg->n_kv_heads * s->n_splits * s->kv_mul * 2 * 4)
+    A(s->part_o, (size_t)cfg->n_heads * s->n_splits * s->head_size * 4)
+    A(s->part_ml, (size_t)cfg->n_heads * s->n_splits * 2 * 4)
     A(s->rope_tab, (size_t)s->head_size / 2 * 4)
     A(s->xq_a, xq_bytes(H)) A(s->xq_f, xq_bytes(H)) A(s->xq_att, xq_bytes(H)) A(s->xq_h, xq_bytes(F))
     A(s->xq_u, xq_bytes(std::max(H, F))) A(s->ss_a, H / 16 * 4) A(s->ss_f, H / 16 * 4)
     A(s->kcache, s->layer_kv_bytes * cfg->n_layers)
     A(s->vcache, s->layer_kv_bytes * cfg->n_layers)
-    A(s->pk_xmid, H * 4) A(s->pk_bar, PK_BAR_WORDS * 4) A(s->pk_err, 4)
-    A(s->pk_ts, (size_t)c->n_cu * PK_TS_EVENTS * 8)
 #undef A
     ifr_rms_norm_config rc{cfg->rms_eps};
     if ((st = c->hip(hipMemcpy(s->rms_cfg, &rc, sizeof rc, hipMemcpyHostToDevice), "hipMemcpy"))) { state_free(s); return st; }
@@ -1749,8 +1600,8 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     const uint32_t H = cfg.hidden, F = cfg.ffn, hs = s->head_size, kvd = s->kv_dim, qd = cfg.n_heads * hs;
     const uint32_t G = s->kv_mul, ldq = qd + 2 * kvd, ldh = s->pf_ldh;
     char attn_name[64];
-    snprintf(attn_name, sizeof attn_name, "pf_attn_%s_h%u_g%u", cfg.kv_dtype == IFR_F16 ? "f16" : "f32", hs, G);
-    const uint32_t attn_qt = 64 / G;
+    snprintf(attn_name, sizeof attn_name, "pf_attn_%s_h%u", cfg.kv_dtype == IFR_F16 ? "f16" : "f32", attn_hsp(hs));
+    const uint32_t attn_qt = 64 / G; // device/prefill.h: PF_ROWS / kv_mul queries per workgroup
     for (uint32_t c0 = 0; c0 < n; c0 += s->pf_chunk) {
         const uint32_t M = std::min(s->pf_chunk, n - c0), p0 = pos0 + c0;
         PfArgs a{};
@@ -1775,6 +1626,7 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
         a.ffn = F;
         a.gu = s->pf_gu;
         a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
+        a.kv_mul = G;
         if ((st = c->launch("pf_embed_k", dim3(M), dim3(256), 0, a))) return st;
         for (uint32_t l = 0; l < cfg.n_layers; l++) {
             const LayerW &L = w->layers[l];
@@ -1828,7 +1680,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         return IFR_OK;
     }
     if (!s->graph || s->graph_wid != w->id || s->graph_wgen != w->gen || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
-        s->graph_sampler != s->sampler_gen || s->graph_pk != c->persistent || s->graph_grp != c->gemv_grp) {
+        s->graph_sampler != s->sampler_gen || s->graph_grp != c->gemv_grp) {
         if (s->graph) {
             hipStreamSynchronize(c->stream);
             hipGraphExecDestroy(s->graph);
@@ -1852,7 +1704,6 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
         s->graph_fused = 1;
         s->graph_exact = c->gemv_exact;
         s->graph_sampler = s->sampler_gen;
-        s->graph_pk = c->persistent;
         s->graph_grp = c->gemv_grp;
     }
     for (uint32_t i = 0; i < n_steps; i++)
@@ -1892,8 +1743,6 @@ IFR_API ifr_status ifr_llama2_state_buffer(ifr_llama2_state *s, const char *name
     else if (n == "pos") { *p = &s->ctl->pos; b = 4; }
     else if (n == "part_ml") { *p = s->part_ml; b = (size_t)cfg.n_kv_heads * s->n_splits * s->kv_mul * 2 * 4; }
     else if (n == "part_o") { *p = s->part_o; b = (size_t)cfg.n_kv_heads * s->n_splits * s->kv_mul * s->head_size * 4; }
-    else if (n == "pk_err") { *p = s->pk_err; b = 4; }
-    else if (n == "pk_ts") { *p = s->pk_ts; b = (size_t)s->ctx->n_cu * PK_TS_EVENTS * 8; }
     else if (n == "tokens") { *p = s->tokens; b = ((size_t)cfg.max_pos + 1) * 4; }
     else if (n == "key_cache" || n == "value_cache") {
         if (layer < 0 || (uint32_t)layer >= cfg.n_layers) return s->ctx->fail(IFR_EINVAL, "layer out of range");

@@ -91,14 +91,16 @@ struct AttnArgs {
     const void *v_cache;
     float *out;               // [n_heads * head_size]
     uint8_t *xq_out;          // merge: the output quantized for the next GEMV (may be null)
-    float *part_o;            // [n_kv_heads][n_splits][kv_mul][head_size]
-    float *part_ml;           // [n_kv_heads][n_splits][kv_mul][2]
+    float *part_o;            // [n_heads][n_splits][head_size]
+    float *part_ml;           // [n_heads][n_splits][2]
     const uint32_t *pos;      // device position
     uint32_t kv_dim;
     uint32_t n_splits;        // gridDim.y
     uint32_t seq_cap;         // positions attended never exceed this (cache rows)
-    uint32_t n_out;           // n_heads * head_size (length of xq_out)
-    uint32_t chunk;           // matrix-core split kernel: positions per split (a multiple of 128)
+    uint32_t n_out;           // n_heads * head_size (length of out and xq_out)
+    uint32_t head_size;       // a multiple of 8, at most 128
+    uint32_t kv_mul;          // query heads per KV head
+    uint32_t n_sub;           // workgroups per KV head and split (gridDim.x / n_kv_heads)
 };
 
 struct EltArgs {
@@ -249,48 +251,7 @@ struct PfArgs {
     void *gu;            // f32 [M][2*ffn]: gate | up
     const float *q_bias, *k_bias, *v_bias; // QKV biases (may be null)
     int32_t neox;        // RoPE pairs (j, j + hs/2) instead of (2j, 2j+1)
+    uint32_t kv_mul;     // attention: query heads per KV head
 };
-
-// Persistent layer tail (device/pk.h): one launch of one workgroup of
-// PK_WAVES waves per CU runs several GEMV stages with grid barriers between.
-constexpr uint32_t PK_WAVES = 12;
-constexpr uint32_t PK_PART_ROWS = 256; // virtual GEMV rows a workgroup may own in one stage
-constexpr uint32_t PK_KSTEPS = 4;      // 64-lane K steps of a row at most
-constexpr uint32_t PK_BAR_CLASS = 64;  // counter words: [0] all classes, [64 (x + 1)] class x, [32] epoch
-constexpr uint32_t PK_BAR_EPOCH = 32;
-constexpr uint32_t PK_BAR_WORDS = 64 * 9;
-// dynamic LDS: the input XQ (K values, K the larger of hidden and ffn) and
-// the item partials
-// (the XQ region in whole KBs: it is filled 1 KB per wave instruction)
-constexpr uint32_t pk_xq_region(uint32_t kmax) { return (3 * kmax + kmax / 2 + 1023) & ~1023u; }
-constexpr uint32_t pk_lds_bytes(uint32_t kmax) { return pk_xq_region(kmax) + PK_PART_ROWS * PK_KSTEPS * 4; }
-
-struct PkArgs {
-    int32_t mode;                  // 0: embedding + QKV of layer 0; 1: O, gate/up, down (+ the next QKV)
-    const uint8_t *wq, *wk, *wv;   // QKV of the layer that follows (mode 1; null: none) or of layer 0
-    const uint8_t *wo, *wg, *wu, *wd;
-    const float *ffn_norm;         // this layer's FFN RMSNorm weight (x_mid * it quantized for gate/up)
-    const float *next_norm;        // RMSNorm weight after down (next attn_norm, or output_norm)
-    void *kc, *vc;                 // KV cache of the QKV's layer
-    const uint8_t *table;          // mode 0: token_embd rows
-    uint32_t emb_row_bytes;
-    int32_t emb_fmt;
-    const float *emb_gamma;        // mode 0: attn_norm of layer 0
-    const uint32_t *tokens;
-    const StepCtl *ctl;
-    const float *rope_tab;
-    float *x, *x_mid, *q;          // residual stream, its value after attention, q of the QKV
-    uint8_t *xq_att, *xq_f, *xq_h, *xq_a;
-    float *ss_f, *ss_a;
-    uint32_t n_ss_a;               // mode 0: partial sums the embedding writes
-    uint32_t hidden, ffn, head_size, kv_dim;
-    uint32_t nb_h, rb_h, nb_f, rb_f; // blocks and bytes of a weight row with K = hidden / K = ffn
-    float eps;
-    int32_t kv_f16;
-    uint32_t *bar;                 // PK_BAR_WORDS barrier words
-    uint32_t *err;                 // raised by a barrier that gave up
-    uint64_t *ts;                  // null, or PK_TS_EVENTS s_memrealtime stamps per workgroup
-};
-constexpr uint32_t PK_TS_EVENTS = 16;
 
 } // namespace ifr

@@ -5,7 +5,6 @@
 #include "device/attention.h"
 #include "device/elementwise.h"
 #include "device/gemv.h"
-#include "device/pk.h"
 #include "device/prefill.h"
 #include "device/sample.h"
 
@@ -86,30 +85,20 @@ GEMV_ALL_MODES(q8_k, Q8_K)
 GEMV_ALL_MODES(f16, F16)
 GEMV_ALL_MODES(f32, F32)
 
-#define ATTN_KERNEL(HS, G)                                                                          \
-    extern "C" __global__ void __launch_bounds__(256) attn_f16_h##HS##_g##G(AttnArgs a) {           \
-        attn_body<HS, G, true>(a);                                                                  \
+// decode attention: head sizes padded to 64 or 128, 1..8 query heads per workgroup
+#define ATTN_KERNEL(HSP, GT)                                                                        \
+    extern "C" __global__ void __launch_bounds__(256) attn_f16_h##HSP##_g##GT(AttnArgs a) {         \
+        attn_split_body<HSP, GT, true>(a);                                                          \
     }                                                                                               \
-    extern "C" __global__ void __launch_bounds__(256) attn_f32_h##HS##_g##G(AttnArgs a) {           \
-        attn_body<HS, G, false>(a);                                                                 \
-    }                                                                                               \
-    extern "C" __global__ void __launch_bounds__(64) attn_merge_h##HS##_g##G(AttnArgs a) {          \
-        attn_merge_body<HS, G>(a);                                                                  \
+    extern "C" __global__ void __launch_bounds__(256) attn_f32_h##HSP##_g##GT(AttnArgs a) {         \
+        attn_split_body<HSP, GT, false>(a);                                                         \
     }
-
-// q.k on the matrix cores (head size 128, f16 cache)
-extern "C" __global__ void __launch_bounds__(256) attn2_f16_h128_g1(AttnArgs a) { attn2_body<1>(a); }
-extern "C" __global__ void __launch_bounds__(256) attn2_f16_h128_g2(AttnArgs a) { attn2_body<2>(a); }
-extern "C" __global__ void __launch_bounds__(256) attn2_f16_h128_g4(AttnArgs a) { attn2_body<4>(a); }
-
-ATTN_KERNEL(64, 1)
-ATTN_KERNEL(64, 2)
-ATTN_KERNEL(64, 4)
-ATTN_KERNEL(64, 8)
-ATTN_KERNEL(128, 1)
-ATTN_KERNEL(128, 2)
-ATTN_KERNEL(128, 4)
-ATTN_KERNEL(128, 8)
+#define ATTN_KERNELS(HSP) \
+    ATTN_KERNEL(HSP, 1) ATTN_KERNEL(HSP, 2) ATTN_KERNEL(HSP, 3) ATTN_KERNEL(HSP, 4) \
+    ATTN_KERNEL(HSP, 5) ATTN_KERNEL(HSP, 6) ATTN_KERNEL(HSP, 7) ATTN_KERNEL(HSP, 8)
+ATTN_KERNELS(64)
+ATTN_KERNELS(128)
+extern "C" __global__ void __launch_bounds__(64) attn_merge(AttnArgs a) { attn_merge_body(a); }
 
 extern "C" __global__ void __launch_bounds__(1024) rms_norm_k(EltArgs a) { rms_norm_body(a); }
 extern "C" __global__ void __launch_bounds__(256) rope_k(EltArgs a) { rope_body(a); }
@@ -148,26 +137,12 @@ extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { p
 extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_silu_k(PfArgs a) { pf_silu_body(a); }
 
-#define PF_ATTN_KERNEL(HS, G)                                                                    \
-    extern "C" __global__ void __launch_bounds__(256) pf_attn_f16_h##HS##_g##G(PfArgs a) {       \
-        pf_attn_body<HS, G, true>(a);                                                            \
+#define PF_ATTN_KERNEL(HSP)                                                                     \
+    extern "C" __global__ void __launch_bounds__(256) pf_attn_f16_h##HSP(PfArgs a) {             \
+        pf_attn_body<HSP, true>(a);                                                              \
     }                                                                                            \
-    extern "C" __global__ void __launch_bounds__(256) pf_attn_f32_h##HS##_g##G(PfArgs a) {       \
-        pf_attn_body<HS, G, false>(a);                                                           \
+    extern "C" __global__ void __launch_bounds__(256) pf_attn_f32_h##HSP(PfArgs a) {             \
+        pf_attn_body<HSP, false>(a);                                                             \
     }
-
-PF_ATTN_KERNEL(64, 1)
-PF_ATTN_KERNEL(64, 2)
-PF_ATTN_KERNEL(64, 4)
-PF_ATTN_KERNEL(64, 8)
-PF_ATTN_KERNEL(128, 1)
-PF_ATTN_KERNEL(128, 2)
-PF_ATTN_KERNEL(128, 4)
-PF_ATTN_KERNEL(128, 8)
-
-// persistent layer tail (device/pk.h)
-#define PK_KERNEL(FMTNAME, FMT)                                                                   \
-    extern "C" __global__ void __launch_bounds__(PK_THREADS) pk_tail_##FMTNAME(PkArgs a) {         \
-        pk_tail_body<FMT>(a);                                                                     \
-    }
-PK_KERNEL(q4_k, Q4_K)
+PF_ATTN_KERNEL(64)
+PF_ATTN_KERNEL(128)

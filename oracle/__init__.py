@@ -393,6 +393,18 @@ class Model:
         buf = (C.c_char * (n * np.dtype(dt).itemsize)).from_address(ptr)
         return np.frombuffer(buf, dt).reshape(c["max_pos"], kv_dim).copy()
 
+    def set_kv_rows(self, layer: int, which: str, rows: np.ndarray) -> None:
+        """Writes cache rows 0 .. len(rows)-1 of one layer (uint16 f16 bits or
+        float32, as the cache holds), for tests that start decoding late."""
+        c = self.cfg
+        kv_dim = c["hidden"] * c["n_kv_heads"] // c["n_heads"]
+        dt = np.dtype(np.uint16 if c.get("kv_f16", 1) else np.float32)
+        rows = np.ascontiguousarray(rows, dt)
+        if rows.ndim != 2 or rows.shape[1] != kv_dim or rows.shape[0] > c["max_pos"]:
+            raise ValueError("kv rows shape")
+        ptr = lib().ifo_state_buffer(self._state, 1 if which == "k" else 2, layer)
+        C.memmove(ptr, rows.ctypes.data, rows.nbytes)
+
     def generate(self, prompt: list[int], n_new: int, nthreads: int = 0, margins: list | None = None) -> list[int]:
         """Greedy token loop of chat_llama2.rs:137-160 with forced prompt tokens.
 

@@ -165,7 +165,11 @@ def test_rejects_bad_inputs(ctx):
     import inferi_amd as I
 
     with pytest.raises(I.HipError):
-        I.Llama2State(ctx, tiny_cfg(hidden=256, n_heads=8))  # head_size 32
+        I.Llama2State(ctx, tiny_cfg(hidden=512, n_heads=2, n_kv_heads=1))  # head_size 256
+    with pytest.raises(I.HipError):
+        I.Llama2State(ctx, tiny_cfg(hidden=320, n_heads=16, n_kv_heads=2))  # head_size 20
+    with pytest.raises(I.HipError):
+        I.Llama2State(ctx, tiny_cfg(hidden=2080, n_heads=260, n_kv_heads=4))  # 65 query heads per KV head
     cfg = tiny_cfg()
     s = I.Llama2State(ctx, cfg)
     try:

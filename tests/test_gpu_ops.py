@@ -266,8 +266,11 @@ def test_gemv_rejects_bad_shapes(ctx):
         ctx.matmul_quant_assign(y, w.at(8), I.Q4_K, 4, 256, x)  # misaligned weights
     assert e.value.status == 1
     with pytest.raises(I.HipError) as e:
-        ctx.matmul_quant_assign(y, w, I.F32, 4, 256, x)
-    assert e.value.status == 2
+        ctx.matmul_quant_assign(y, w.at(4), I.F32, 4, 256, x)  # f32 rows must be 16-byte aligned
+    assert e.value.status == 1
+    with pytest.raises(I.HipError) as e:
+        ctx.matmul_quant_assign(y, w, 5, 4, 256, x)  # no GGUF type 5
+    assert e.value.status in (1, 2)
 
 
 # ------------------------------------------------------- elementwise ops --

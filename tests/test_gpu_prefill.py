@@ -97,7 +97,7 @@ def test_gemm_quant_rejects_bad_input(ctx):
 
     buf = ctx.alloc(1 << 16)
     with pytest.raises(I.HipError):
-        ctx.gemm_quant(buf, buf, I.F32, 16, 256, buf, 4)  # not a quantized type
+        ctx.gemm_quant(buf, buf, 5, 16, 256, buf, 4)  # no GGUF type 5
     with pytest.raises(I.HipError):
         ctx.gemm_quant(buf, buf, I.Q4_K, 16, 100, buf, 4)  # cols % 256
     with pytest.raises(I.HipError):

@@ -168,6 +168,21 @@ def test_attention_closed_forms_and_brute_force(oracle_lib, kv_f16):
         assert np.allclose(out, _attn_numpy(q, kc, vc, nh, nkv, hs, pos), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("nh,nkv,hs", [(14, 2, 64), (24, 8, 128), (24, 2, 32), (20, 2, 80), (6, 3, 40), (4, 4, 8)])
+def test_attention_any_group_and_head_size(oracle_lib, nh, nkv, hs):
+    """The group sizes (7, 3, 12, 10, 2, 1) and head sizes the device kernels
+    take, against numpy in f64, including a position past 65,536."""
+    rng = np.random.default_rng(nh * 100 + hs)
+    L = 70001 if hs == 8 else 300
+    kv_dim = nkv * hs
+    kc = rng.standard_normal((L, kv_dim)).astype(np.float32)
+    vc = rng.standard_normal((L, kv_dim)).astype(np.float32)
+    q = rng.standard_normal(nh * hs).astype(np.float32)
+    for pos in (0, 17, L - 1):
+        out = O.attention(q, kc, vc, nh, nkv, hs, pos, False)
+        assert np.allclose(out, _attn_numpy(q, kc, vc, nh, nkv, hs, pos), rtol=1e-5, atol=1e-6)
+
+
 def test_argmax_ties_lowest_index(oracle_lib):
     v = np.array([1.0, 3.0, -2.0, 3.0, 3.0], np.float32)
     assert O.argmax(v) == 1
