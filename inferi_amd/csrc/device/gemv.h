@@ -862,9 +862,20 @@ IFR_DEV void chunk_step(const ChunkI<FMT, R> &w, const XQ &x, uint32_t kb, uint3
     }
 }
 
+// QKV with NeoX RoPE (rope.rs:97-141): virtual rows 2j and 2j+1 of a q or
+// k head are its rows j and j + hs/2, so that the two outputs one lane
+// rotates together stay adjacent in the launch; v rows keep their order.
+IFR_DEV uint32_t qkv_phys(const GemvArgs &a, uint32_t v) {
+    if (!a.neox || v >= a.rows0 + a.rows1) return v;
+    const uint32_t base = v < a.rows0 ? 0u : a.rows0, u = v - base, hs = a.head_size;
+    const uint32_t r = u % hs;
+    return base + (u - r) + (r >> 1) + (r & 1u) * (hs / 2);
+}
+
 template <int MODE>
 IFR_DEV const uint8_t *gemv_row_ptr(const GemvArgs &a, uint32_t v) {
     if constexpr (MODE == GEMV_QKV) {
+        v = qkv_phys(a, v);
         if (v < a.rows0) return a.w0 + (size_t)v * a.row_bytes;
         v -= a.rows0;
         if (v < a.rows1) return a.w1 + (size_t)v * a.row_bytes;
@@ -888,6 +899,47 @@ IFR_DEV void rope_pair(float &a, float &b, uint32_t idx, uint32_t hs, uint32_t p
     const float x = a, y = b;
     a = cs * x - sn * y;
     b = sn * x + cs * y;
+}
+
+// QKV epilogue of virtual rows v, v+1 (v even, one pair of one head): the
+// Qwen2 biases added first, then RoPE on q and k (transformer.rs:434-445),
+// q to a.y, k and v to this position's cache row.  Physical indices follow
+// qkv_phys; the theta index of the pair is (v mod hs) / 2 in both variants.
+IFR_DEV void qkv_store_pair(const GemvArgs &a, uint32_t v, float x0, float x1, uint32_t pos, const float *theta) {
+    const bool is_q = v < a.rows0, is_k = !is_q && v < a.rows0 + a.rows1;
+    const uint32_t base = is_q ? 0u : is_k ? a.rows0 : a.rows0 + a.rows1;
+    const uint32_t idx = v - base;
+    uint32_t i0 = idx, i1 = idx + 1;
+    if (a.neox && (is_q || is_k)) {
+        const uint32_t hs = a.head_size, r = idx % hs;
+        i0 = idx - r + (r >> 1);
+        i1 = i0 + hs / 2;
+    }
+    const float *bias = is_q ? a.q_bias : is_k ? a.k_bias : a.v_bias;
+    if (bias) {
+        x0 = x0 + bias[i0];
+        x1 = x1 + bias[i1];
+    }
+    if (is_q || is_k) rope_pair(x0, x1, idx, a.head_size, pos, theta);
+    if (is_q) {
+        a.y[i0] = x0;
+        a.y[i1] = x1;
+        return;
+    }
+    const size_t off = (size_t)pos * a.kv_dim;
+    void *cache = is_k ? a.k_cache : a.v_cache;
+    if (a.kv_f16) {
+        uint16_t *c16 = (uint16_t *)cache + off;
+        if (i1 == i0 + 1) {
+            *(uint32_t *)(c16 + i0) = (uint32_t)f32_to_f16(x0) | ((uint32_t)f32_to_f16(x1) << 16);
+        } else {
+            c16[i0] = f32_to_f16(x0);
+            c16[i1] = f32_to_f16(x1);
+        }
+    } else {
+        ((float *)cache)[off + i0] = x0;
+        ((float *)cache)[off + i1] = x1;
+    }
 }
 
 // Stages x (times gamma for the normalising modes) into LDS as f32 and
@@ -1028,27 +1080,7 @@ __device__ void gemv_f32_body(const GemvArgs &a) {
 #pragma unroll
             for (int p = 0; p < R / 2; p++) {
                 const uint32_t v = v0 + 2 * p;
-                if (lane == p && v + 1 < a.total_rows) {
-                    float x0 = acc[2 * p], x1 = acc[2 * p + 1];
-                    if (v < a.rows0) {
-                        rope_pair(x0, x1, v, a.head_size, pos, a.rope_tab);
-                        a.y[v] = x0;
-                        a.y[v + 1] = x1;
-                    } else {
-                        const bool is_k = v < a.rows0 + a.rows1;
-                        const uint32_t idx = is_k ? v - a.rows0 : v - a.rows0 - a.rows1;
-                        if (is_k) rope_pair(x0, x1, idx, a.head_size, pos, a.rope_tab);
-                        const size_t off = (size_t)pos * a.kv_dim + idx;
-                        void *cache = is_k ? a.k_cache : a.v_cache;
-                        if (a.kv_f16) {
-                            const uint32_t packed = (uint32_t)f32_to_f16(x0) | ((uint32_t)f32_to_f16(x1) << 16);
-                            *(uint32_t *)((uint16_t *)cache + off) = packed;
-                        } else {
-                            ((float *)cache)[off] = x0;
-                            ((float *)cache)[off + 1] = x1;
-                        }
-                    }
-                }
+                if (lane == p && v + 1 < a.total_rows) qkv_store_pair(a, v, acc[2 * p], acc[2 * p + 1], pos, a.rope_tab);
             }
         }
 #pragma unroll
@@ -1309,26 +1341,7 @@ __device__ void gemv_int_body(const GemvArgs &a) {
 
     // outputs v, v+1 of a QKV launch (an even pair of one head): q, or RoPE'd
     // k / v into the cache row of this position
-    auto qkv_store = [&](uint32_t v, float x0, float x1) {
-        if (v < a.rows0) {
-            rope_pair(x0, x1, v, a.head_size, pos, theta_lds);
-            a.y[v] = x0;
-            a.y[v + 1] = x1;
-        } else {
-            const bool is_k = v < a.rows0 + a.rows1;
-            const uint32_t idx = is_k ? v - a.rows0 : v - a.rows0 - a.rows1;
-            if (is_k) rope_pair(x0, x1, idx, a.head_size, pos, theta_lds);
-            const size_t off = (size_t)pos * a.kv_dim + idx;
-            void *cache = is_k ? a.k_cache : a.v_cache;
-            if (a.kv_f16) {
-                const uint32_t packed = (uint32_t)f32_to_f16(x0) | ((uint32_t)f32_to_f16(x1) << 16);
-                *(uint32_t *)((uint16_t *)cache + off) = packed;
-            } else {
-                ((float *)cache)[off] = x0;
-                ((float *)cache)[off + 1] = x1;
-            }
-        }
-    };
+    auto qkv_store = [&](uint32_t v, float x0, float x1) { qkv_store_pair(a, v, x0, x1, pos, theta_lds); };
 
     // wave 0, after the group's barrier: the group's outputs
     auto epilogue = [&](uint32_t g) {
@@ -1564,28 +1577,7 @@ __device__ void gemv_one_body(const GemvArgs &a) {
             a.y[v0 >> 1] = up * (gt / (1.0f + expf(-gt)));
         }
     } else if constexpr (MODE == GEMV_QKV) {
-        if (lane == 0 && v0 + 1 < a.total_rows) {
-            float x0 = acc[0] * rs, x1 = acc[1] * rs;
-            const uint32_t v = v0;
-            if (v < a.rows0) {
-                rope_pair(x0, x1, v, a.head_size, pos, theta_lds);
-                a.y[v] = x0;
-                a.y[v + 1] = x1;
-            } else {
-                const bool is_k = v < a.rows0 + a.rows1;
-                const uint32_t idx = is_k ? v - a.rows0 : v - a.rows0 - a.rows1;
-                if (is_k) rope_pair(x0, x1, idx, a.head_size, pos, theta_lds);
-                const size_t off = (size_t)pos * a.kv_dim + idx;
-                void *cache = is_k ? a.k_cache : a.v_cache;
-                if (a.kv_f16) {
-                    const uint32_t packed = (uint32_t)f32_to_f16(x0) | ((uint32_t)f32_to_f16(x1) << 16);
-                    *(uint32_t *)((uint16_t *)cache + off) = packed;
-                } else {
-                    ((float *)cache)[off] = x0;
-                    ((float *)cache)[off + 1] = x1;
-                }
-            }
-        }
+        if (lane == 0 && v0 + 1 < a.total_rows) qkv_store_pair(a, v0, acc[0] * rs, acc[1] * rs, pos, theta_lds);
     } else {
         uint64_t best = 0;
 #pragma unroll

@@ -521,9 +521,7 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
         const LayerW &Lw = w->layers[l];
         uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
         uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
-        const bool has_bias = Lw.q_bias.data || Lw.k_bias.data || Lw.v_bias.data;
-        const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype &&
-                              cfg.rope_variant == IFR_ROPE_ORIGINAL && !has_bias;
+        const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype;
         const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
         // gate/up as one item per wave with h in f32, quantized by the down
         // GEMV itself (Q4_K, rows of one K step; option gemv_grp bit 5)
@@ -561,6 +559,10 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.kv_dim = kv_dim;
             a.head_size = s->head_size;
             a.kv_f16 = cfg.kv_dtype == IFR_F16;
+            a.q_bias = (const float *)Lw.q_bias.data;
+            a.k_bias = (const float *)Lw.k_bias.data;
+            a.v_bias = (const float *)Lw.v_bias.data;
+            a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
             if ((st = launch_gemv(c, p, "qkv", a))) return st;
         } else {
             EltArgs n{};
@@ -726,9 +728,6 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             e.b = s->xb2;
             e.n = hidden;
             if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
-        }
-        if (fused && !fuse_qkv && l + 1 < L) {
-            // the next layer's unfused QKV reads f32 xb; nothing to quantize
         }
     }
 

@@ -83,6 +83,8 @@ struct GemvArgs {
     int32_t kv_f16;      // QKV: cache element type
     uint32_t nwaves;     // integer path: waves per workgroup (blockDim.x / 64)
     uint64_t *part_keys; // HEAD: one argmax key per workgroup (may be null)
+    const float *q_bias, *k_bias, *v_bias; // QKV: Qwen2 biases (may be null)
+    int32_t neox;        // QKV: RoPE pairs (j, j + hs/2) instead of (2j, 2j+1)
 };
 
 struct AttnArgs {
