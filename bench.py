@@ -9,8 +9,11 @@ its first 4095 tokens go through ifr_llama2_prefill (MFMA GEMMs and causal
 attention, in passes of up to 4096 tokens), which is timed on its own and
 reported as config.prefill, the last through the first decode step.
 
-Prints one JSON line.  Extra modes: --sweep (BASELINE config 2 GEMV sweep,
-GB/s per format and shape), --attn (config 3 attention GB/s).
+Prints one JSON line.  Besides the decode rate it carries each decode
+stage's time and HBM rate (config.stages), the exact-GEMV-path decode rate,
+the sampled decode rate and the prefill.  Extra modes: --sweep (BASELINE
+config 2 GEMV sweep, GB/s per format and shape), --attn (config 3 attention
+GB/s), --pmc-sample / --pf-sample (workloads for rocprofv3 counter passes).
 """
 
 from __future__ import annotations
@@ -97,6 +100,7 @@ MFMA_F16_PEAK = 2.5e15  # MI355X dense f16 matrix-core FLOP/s
 
 
 SAMPLE_WARMUP = 4
+EXACT_WARMUP = 3
 
 
 def time_sampler(ctx: I.LlmContext, n: int, iters: int = 50) -> float:
@@ -128,21 +132,50 @@ def prefill_flops(cfg: I.Llama2Config, n: int) -> float:
     return cfg.n_layers * (2.0 * n * mats + attn)
 
 
-def measured_traffic():
-    """HBM bytes per launch of the roofline kernel from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (calibrated on add_k), or None."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_q4_k_14336x4096_traffic.json")
+STAGES = ("qkv", "attention", "attn_output", "ffn_gate_up", "ffn_down")
+# the decode step's kernel behind each stage (Q4_K matrices, f16 cache, head size 128, 4 query heads per KV head)
+STAGE_KERNELS = {"qkv": "gemv_q4_k_qkv_one", "attention": "attn_f16_h128_g4 + attn_merge",
+                 "attn_output": "gemv_q4_k_resid_r2w8k1", "ffn_gate_up": "gemv_q4_k_gateup_one",
+                 "ffn_down": "gemv_q4_k_resid_xf"}
+ROOFLINE_STAGE = "ffn_gate_up"  # the decode step's dominant kernel
+
+
+def stage_bytes(cfg: I.Llama2Config, stage: str, ctx_len: float, mat=I.Q4_K) -> int:
+    """Algorithmic HBM bytes of one layer's decode stage: its weight blocks
+    once, the vectors it reads and writes once (quantized activations at
+    3.5 bytes per value, f32 vectors at 4), and for attention the f16 K and V
+    rows of ctx_len positions."""
+    h, kv, f = cfg.hidden, cfg.kv_dim, cfg.ffn
+    xq = lambda n: 3.5 * n  # noqa: E731  (XQ layout: three digit planes, a scale and a sum per 16)
+    if stage == "qkv":
+        return int(I.row_bytes(mat, h) * (h + 2 * kv) + xq(h) + 4 * h + 2 * 2 * kv)
+    if stage == "attention":
+        return int(2 * kv * 2 * ctx_len + 4 * h + 4 * h + xq(h))
+    if stage == "attn_output":
+        return int(I.row_bytes(mat, h) * h + xq(h) + 2 * 4 * h + xq(h))
+    if stage == "ffn_gate_up":
+        return int(I.row_bytes(mat, h) * 2 * f + xq(h) + 4 * f)
+    if stage == "ffn_down":
+        return int(I.row_bytes(mat, f) * h + 4 * f + 2 * 4 * h + xq(h))
+    raise ValueError(stage)
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of a decode kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (calibrated on add_k), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_8b_q4k_traffic.json")
     try:
         with open(path) as f:
-            return int(json.load(f)["hbm_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
+            return int(json.load(f)["kernels"][kernel]["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
-def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, threads: int) -> dict:
+def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, threads: int, pos0: int) -> dict:
     """The CPU oracle (a C restatement of the reference's forward) timed on
     the host cores on a bounded sample: n_tokens decode steps of the same
-    model bytes."""
+    model bytes at the GPU leg's positions pos0.. (the oracle's cache rows
+    below pos0 are zeros, which cost the same attention work)."""
     import oracle as O
 
     if not os.path.exists(O.LIB_PATH):
@@ -153,16 +186,23 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
         vector = name.endswith(("norm.weight", ".bias"))
         host[name] = arr if vector else (dt, np.ascontiguousarray(arr).view(np.uint8), rows, cols)
     c = dict(hidden=cfg.hidden, ffn=cfg.ffn, n_layers=cfg.n_layers, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
-             vocab=cfg.vocab, max_pos=max(16, n_tokens + 1), rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps, kv_f16=1)
+             vocab=cfg.vocab, max_pos=pos0 + n_tokens + 1, rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps,
+             kv_f16=1)
     m = O.Model(c, host)
-    m.forward(1, 0, threads)  # warm the pages
+    m.forward(1, pos0, threads)  # warm the pages
     t0 = time.perf_counter()
-    for p in range(1, n_tokens + 1):
-        m.forward(p, p, threads)
+    for p in range(pos0 + 1, pos0 + n_tokens + 1):
+        m.forward(p % cfg.vocab, p, threads)
     dt = time.perf_counter() - t0
-    return {"value": n_tokens / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n_tokens} decode tokens of the same 8B-shape model bytes (positions 1-{n_tokens}) "
-                      f"through oracle/oracle.c ifo_forward, {threads} threads"}
+    try:
+        host_cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        host_cores = os.cpu_count()
+    return {"value": n_tokens / dt, "unit": "tok/s", "cores": threads, "host_cores": host_cores,
+            "host_cpu_count": os.cpu_count(), "kind": "port",
+            "sample": f"{n_tokens} decode tokens of the same 8B-shape model bytes at positions {pos0 + 1}-"
+                      f"{pos0 + n_tokens} (the GPU leg's context) through oracle/oracle.c ifo_forward, "
+                      f"{threads} threads on {host_cores} available cores"}
 
 
 def run_decode(args) -> None:
@@ -172,7 +212,8 @@ def run_decode(args) -> None:
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
-    max_pos = prompt_len + args.warmup + args.steps + SAMPLE_WARMUP + args.sample_steps + 1
+    n_exact = args.exact_steps + (EXACT_WARMUP if args.exact_steps else 0)
+    max_pos = prompt_len + args.warmup + args.steps + SAMPLE_WARMUP + args.sample_steps + n_exact + 1
     cfg = I.Llama2Config(max_pos=max_pos, kv_dtype=I.F16, **base)
     t0 = time.perf_counter()
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=args.seed)
@@ -232,8 +273,34 @@ def run_decode(args) -> None:
         log(f"bench: sampled decode (T 0.7, top-p 0.95): {sms:.4f} ms/token, {1000.0 / sms:.1f} tok/s; "
             f"sampler alone {sampled['sampler_us']:.1f} us")
 
-    # the dominant kernel: Q4_K GEMV, measured on its plain form at the
-    # 14336x4096 shape of the FFN projections
+    # the same loop on the exact GEMV path (x kept in f32, fp32 FMAs)
+    exact = None
+    if args.exact_steps > 0:
+        ctx.set_option("gemv_exact", 1)
+        I.Llama2.generate(ctx, s, w, EXACT_WARMUP, use_graph=not args.no_graph)
+        ctx.sync()
+        ctx.event_record(2)
+        I.Llama2.generate(ctx, s, w, args.exact_steps, use_graph=not args.no_graph)
+        ctx.event_record(3)
+        ems = ctx.event_elapsed(2, 3) / args.exact_steps
+        ctx.set_option("gemv_exact", 0)
+        exact = {"steps": args.exact_steps, "ms_per_step": round(ems, 5), "tok_s": round(1000.0 / ems, 2)}
+        log(f"bench: exact-path decode (gemv_exact): {ems:.4f} ms/token, {1000.0 / ems:.1f} tok/s")
+
+    # every stage of the step on its own (the step's own launches, each layer
+    # in turn, so no weights are reused from the caches), at this context
+    ctx_now = int(s.read("pos", np.uint32)[0]) + 1
+    stages = {}
+    for st in STAGES:
+        us = I.Llama2.time_stage(ctx, s, w, st, args.stage_iters)
+        nb = stage_bytes(cfg, st, ctx_now)
+        stages[st] = {"kernel": STAGE_KERNELS[st], "us": round(us, 3), "bytes": nb,
+                      "gbs": round(nb / (us * 1e-6) / 1e9, 1), "frac": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                      "us_per_token": round(us * cfg.n_layers, 1)}
+        log(f"bench: stage {st} ({STAGE_KERNELS[st]}): {us:.2f} us/layer, {stages[st]['gbs']:.0f} GB/s")
+    dom = stages[ROOFLINE_STAGE]
+
+    # the op-level Q4_K GEMV (ifr_matmul_quant_xq) at the 14336x4096 FFN shape
     g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
     log(f"bench: gemv_q4_k_plain_one 14336x4096: {g['us']:.2f} us/launch, {g['gbs']:.0f} GB/s")
 
@@ -241,7 +308,7 @@ def run_decode(args) -> None:
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         t0 = time.perf_counter()
-        cpu = cpu_baseline(cfg, w, args.cpu_tokens, threads)
+        cpu = cpu_baseline(cfg, w, args.cpu_tokens, threads, pos0)
         log(f"bench: cpu baseline {cpu['value']:.3f} tok/s ({time.perf_counter() - t0:.1f}s)")
 
     out = {
@@ -269,16 +336,21 @@ def run_decode(args) -> None:
             "device": dev_name,
             "prefill": pf,
             "sampled_decode": sampled,
+            "exact_path_decode": exact,
+            "stages": stages,
+            "op_gemv_q4_k_14336x4096": {"kernel": "gemv_q4_k_plain_one", "us": round(g["us"], 3), "bytes": g["bytes"],
+                                        "gbs": round(g["gbs"], 1), "frac": round(g["gbs"] / HBM_PEAK_GBS, 4)},
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_q4_k_plain_one 14336x4096 (Q4_K, 33,103,872 algorithmic bytes per launch)",
-            "achieved": round(g["gbs"], 1),
+            "kernel": (f"{dom['kernel']} (the decode step's FFN gate/up GEMV, 2 x {cfg.ffn} x {cfg.hidden} Q4_K; "
+                       f"{dom['bytes']:,} algorithmic bytes per launch)"),
+            "achieved": dom["gbs"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
-            "avg_launch_us": round(g["us"], 3),
+            "frac": dom["frac"],
+            "traffic": measured_traffic(dom["kernel"]),
+            "avg_launch_us": dom["us"],
         },
         "cpu_baseline": cpu,
     }
@@ -308,8 +380,9 @@ def run_pmc_sample(args) -> None:
     """Workload for the rocprofv3 --pmc passes behind roofline.traffic: the
     element-wise add kernel (add_k) over 64 Mi floats, whose HBM traffic is
     known (reads 2 x 256 MiB, writes 256 MiB), calibrates FETCH_SIZE and
-    WRITE_SIZE; then the roofline kernel (gemv_q4_k_plain_one 14336x4096) on
-    weight copies rotated past the Infinity Cache."""
+    WRITE_SIZE; then the op-level GEMV (gemv_q4_k_plain_one 14336x4096) on
+    weight copies rotated past the Infinity Cache; then each stage of the
+    8B decode step at position 4100, twice over the 32 layers."""
     ctx = I.LlmContext(0, args.code_object)
     n = 64 << 20
     a, b = ctx.alloc(n * 4), ctx.alloc(n * 4)
@@ -322,6 +395,35 @@ def run_pmc_sample(args) -> None:
     b.free()
     g = time_gemv(ctx, I.Q4_K, 14336, 4096, iters=args.gemv_iters)
     log(f"pmc sample: add_k {3} x {n} floats; gemv_q4_k_plain_one 14336x4096 {g['us']:.2f} us")
+    cfg = I.Llama2Config(max_pos=4608, kv_dtype=I.F16, **CFG_8B)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=args.seed)
+    s = I.Llama2State(ctx, cfg)
+    s.reset(np.zeros(4102, np.uint32), 4100)
+    for st in STAGES:
+        us = I.Llama2.time_stage(ctx, s, w, st, 1)
+        log(f"pmc sample: stage {st} ({STAGE_KERNELS[st]}) {us:.2f} us/layer")
+    s.close()
+    w.close()
+    ctx.close()
+
+
+def run_pf_sample(args) -> None:
+    """Workload for the rocprofv3 --pmc passes on the prefill kernels: the
+    8B model's 4095-token prompt through ifr_llama2_prefill, twice."""
+    ctx = I.LlmContext(0, args.code_object)
+    cfg = I.Llama2Config(max_pos=args.prompt + 8, kv_dtype=I.F16, **CFG_8B)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=args.seed)
+    s = I.Llama2State(ctx, cfg)
+    prompt = np.random.default_rng(8).integers(0, cfg.vocab, args.prompt).astype(np.uint32)
+    for _ in range(2):
+        s.reset(prompt, 0)
+        ctx.sync()
+        ctx.event_record(4)
+        I.Llama2.prefill(ctx, s, w, args.prompt - 1)
+        ctx.event_record(5)
+        log(f"pf sample: prefill {args.prompt - 1} tokens in {ctx.event_elapsed(4, 5):.2f} ms")
+    s.close()
+    w.close()
     ctx.close()
 
 
@@ -383,13 +485,16 @@ def main() -> None:
     ap.add_argument("--gemv-iters", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch the decode step's kernels directly")
-    ap.add_argument("--cpu-tokens", type=int, default=32)
+    ap.add_argument("--cpu-tokens", type=int, default=8)
     ap.add_argument("--sample-steps", type=int, default=64,
                     help="decode steps timed with the reference chat loop's sampler (T 0.7, top-p 0.95)")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--exact-steps", type=int, default=32, help="decode steps timed on the exact GEMV path")
+    ap.add_argument("--stage-iters", type=int, default=10, help="passes over the layers per stage timing")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--attn", action="store_true")
     ap.add_argument("--pmc-sample", action="store_true", help="workload for the rocprofv3 --pmc traffic passes")
+    ap.add_argument("--pf-sample", action="store_true", help="workload for the rocprofv3 --pmc prefill passes")
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
@@ -400,6 +505,8 @@ def main() -> None:
         sys.exit(2)
     if args.pmc_sample:
         run_pmc_sample(args)
+    elif args.pf_sample:
+        run_pf_sample(args)
     elif args.sweep:
         run_sweep(args)
     elif args.attn:

@@ -336,6 +336,16 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const 
  * ifr_gemm_quant takes; both RoPE variants and QKV biases are handled. */
 IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,
                                       uint32_t n_tokens);
+/* Measurement hook (no reference counterpart): enqueues one stage of the
+ * fused decode step ("qkv", "attention" = split + merge, "attn_output",
+ * "ffn_gate_up", "ffn_down") for every layer in turn, `iters` times, on the
+ * context's stream between two HIP events, and returns the average time of
+ * one layer's stage in microseconds.  The launches are the decode step's
+ * own; they overwrite the state's activations and this position's KV rows,
+ * so reset the state before decoding on.  Blocks until done. */
+IFR_API ifr_status ifr_llama2_time_stage(ifr_ctx *ctx, ifr_llama2_state *state, const ifr_llama2_weights *weights,
+                                         const char *stage, uint32_t iters, float *us_per_launch);
+
 /* Sampling at the end of each decode step, as sample_next_token does
  * (crates/inferi-chat/src/sampler.rs:91-111, with Sampler::new(vocab, 0.7,
  * 0.95)): with temperature != 0 the step chooses token[p+1] by ifr_sample's

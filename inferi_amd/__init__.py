@@ -102,6 +102,7 @@ SIGNATURES = {
     "ifr_llama2_launch": (_i32, [_vp, _vp, _vp, _i32]),
     "ifr_llama2_generate": (_i32, [_vp, _vp, _vp, _u32, _i32]),
     "ifr_llama2_prefill": (_i32, [_vp, _vp, _vp, _u32]),
+    "ifr_llama2_time_stage": (_i32, [_vp, _vp, _vp, C.c_char_p, _u32, C.POINTER(C.c_float)]),
     "ifr_llama2_set_sampler": (_i32, [_vp, _f, _f, _u64]),
     "ifr_llama2_read_tokens": (_i32, [_vp, _vp, _u32, _u32]),
     "ifr_llama2_state_buffer": (_i32, [_vp, _cp, _i32, C.POINTER(_vp), C.POINTER(_sz)]),
@@ -539,6 +540,15 @@ class Llama2:
     def generate(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, n_steps: int,
                  use_graph: bool = True) -> None:
         ctxt._check(lib().ifr_llama2_generate(ctxt.h, state.h, weights.h, n_steps, int(use_graph)))
+
+    @staticmethod
+    def time_stage(ctxt: LlmContext, state: Llama2State, weights: Llama2Weights, stage: str, iters: int) -> float:
+        """Microseconds per layer of one fused decode stage ("qkv", "attention",
+        "attn_output", "ffn_gate_up", "ffn_down"), every layer in turn, `iters`
+        times (ifr_llama2_time_stage; overwrites the state's activations)."""
+        us = C.c_float()
+        ctxt._check(lib().ifr_llama2_time_stage(ctxt.h, state.h, weights.h, stage.encode(), iters, C.byref(us)))
+        return float(us.value)
 
 
 # ------------------------------------------------------------------- GGUF

@@ -161,17 +161,19 @@ __device__ void attn_split_body(const AttnArgs &a) {
         q[j][4] = w.x * qs; q[j][5] = w.y * qs; q[j][6] = w.z * qs; q[j][7] = w.w * qs;
     }
 
-    // When S batches cover the whole cache (S * Qb >= seq_cap) every chunk is
-    // one batch of Qb positions at s * Qb, known before the device position
-    // arrives: the first batch's K and V loads go out together with the
-    // position load (rows clamped into the cache, masked below).
-    const bool fixed = S * Qb >= a.seq_cap;
+    // When S batches cover the host's bound on the positions (S * Qb >=
+    // spec_rows), every chunk is one batch of Qb positions at s * Qb as long
+    // as pos + 1 <= spec_rows: the first batch's K and V loads go out together
+    // with the position load (rows clamped below spec_rows, masked below).  A
+    // position past the bound falls back to chunks computed from it (the
+    // early loads are then discarded).
+    const bool early = S * Qb >= a.spec_rows;
     KV8<F16> kr[ATTN_BATCH], vr[ATTN_BATCH];
     auto load_batch = [&](uint32_t t0, uint32_t base, uint32_t n) {
 #pragma unroll
         for (int u = 0; u < ATTN_BATCH; u++) {
             const uint32_t tt = base + pg + PPP * u;
-            const uint32_t row = n ? t0 + (tt < n ? tt : 0) : min(t0 + tt, a.seq_cap - 1);
+            const uint32_t row = n ? t0 + (tt < n ? tt : 0) : min(t0 + tt, min(a.spec_rows, a.seq_cap) - 1);
             const size_t off = (size_t)row * a.kv_dim + head_off;
             if (dim_ok) {
                 kv8_load<F16>(a.k_cache, off, kr[u]);
@@ -182,9 +184,10 @@ __device__ void attn_split_body(const AttnArgs &a) {
             }
         }
     };
-    if (fixed) load_batch(s * Qb, 0, 0);
+    if (early) load_batch(s * Qb, 0, 0);
     __builtin_amdgcn_sched_barrier(0); // the batch's loads stay together
     const uint32_t T = min((uint32_t)__builtin_amdgcn_readfirstlane(pos_dev) + 1u, a.seq_cap);
+    const bool fixed = early && T <= a.spec_rows;
     const uint32_t C = fixed ? Qb : attn_chunk<HSP>(T, S);
     const uint32_t t0 = s * C;
     if (t0 >= T && (uint32_t)tid < nj) {

@@ -366,6 +366,15 @@ static void attn_groups(uint32_t kv_mul, uint32_t &n_sub, uint32_t &gt) {
     gt = (kv_mul + n_sub - 1) / n_sub;
 }
 
+// Positions come in buckets of ATTN_BUCKET: steps at positions p of bucket
+// b = p / ATTN_BUCKET assume pos + 1 <= (b + 1) * ATTN_BUCKET (capped at
+// max_pos), so the attention splits cover the positions in use, not the
+// whole cache.
+constexpr uint32_t ATTN_BUCKET = 256;
+static uint32_t attn_spec_for(uint32_t pos, uint32_t max_pos) {
+    return (uint32_t)std::min<uint64_t>(max_pos, ((uint64_t)pos / ATTN_BUCKET + 1) * ATTN_BUCKET);
+}
+
 // Split pass over the KV sequence, then the merge of the partials.  `a`
 // carries head_size, kv_mul, n_splits and n_out; n_sub is set here.
 static ifr_status launch_attn(ifr_ctx *c, int32_t kv_dtype, AttnArgs &a, uint32_t n_kv_heads) {
@@ -407,6 +416,10 @@ struct ifr_llama2_state {
     ifr_ctx *ctx;
     ifr_llama2_config cfg;
     uint32_t kv_dim, head_size, kv_mul, n_splits;
+    // the device position as the host knows it (every step advances it by
+    // one, up to max_pos - 1), and the bound on pos + 1 the steps being
+    // enqueued assume (the attention splits are sized for it)
+    uint32_t host_pos = 0, step_spec = 0;
     std::vector<void *> allocs;
     float *x, *xb, *xb2, *q, *ktmp, *vtmp, *hb, *hb2, *att, *logits, *probs;
     uint8_t *smp_work;
@@ -440,6 +453,10 @@ struct ifr_llama2_state {
     hipGraphExec_t graph = nullptr;
     int graph_grp = -1;
     uint32_t graph_sampler = 0;
+    uint32_t graph_spec = 0; // step_spec the graph was captured with
+    // graphs replaced while their launches may still run: destroyed once the
+    // event recorded after their last launch has completed
+    std::vector<std::pair<hipGraphExec_t, hipEvent_t>> retired;
     uint64_t graph_wid = 0, graph_wgen = 0; // weights id and generation the graph was captured with
     int graph_fused = -1;
     int graph_exact = -1;
@@ -494,43 +511,31 @@ static ifr_status launch_keys_of_y(ifr_ctx *c, const float *logits, uint32_t n, 
 
 static ifr_status enqueue_head(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused, uint32_t n_ss_a);
 
-static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
+// Decode stages of one layer, in order (a mask selects which run: the step
+// runs them all; ifr_llama2_time_stage repeats one).  n_ss_a: partial sums of
+// x^2 in ss_a, read by the fused QKV and set by the fused down GEMV.
+enum : uint32_t { ST_QKV = 1, ST_ATTN = 2, ST_O = 4, ST_GATEUP = 8, ST_DOWN = 16, ST_LAYER = 31 };
+
+static ifr_status enqueue_layer(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused, uint32_t l,
+                                uint32_t stages, uint32_t &n_ss_a) {
     const ifr_llama2_config &cfg = s->cfg;
     const uint32_t hidden = cfg.hidden, kv_dim = s->kv_dim, ffn = cfg.ffn, L = cfg.n_layers;
     const uint32_t n_ss_res = hidden / 16; // partial sums written by a RESID GEMV (one per 16-row tile)
     ifr_status st;
+    const LayerW &Lw = w->layers[l];
+    uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
+    uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
+    const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype;
+    const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
+    // gate/up as one item per wave with h in f32, quantized by the down
+    // GEMV itself (Q4_K, rows of one K step; option gemv_grp bit 5)
+    const bool h32 = fuse_ffn && (c->gemv_grp & 32) && !c->gemv_exact && !c->gemv_waves && !c->gemv_max_grid &&
+                     Lw.ffn_gate.dtype == IFR_Q4_K && Lw.ffn_down.dtype == IFR_Q4_K && hidden <= 4096 &&
+                     hidden % 256 == 0 && c->fn("gemv_q4_k_gateup_one") && c->fn("gemv_q4_k_resid_xf");
+    const float *next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
+    GemvPlan p;
 
-    uint32_t n_ss_a;
-    {   // x <- token_embd[tokens[pos]], and x * attn_norm(0) quantized
-        EmbedArgs e{};
-        e.x = s->x;
-        e.table = w->token_embd.data;
-        e.tokens = s->tokens;
-        e.ctl = s->ctl;
-        e.xq_out = s->xq_a;
-        e.ss_out = s->ss_a;
-        e.gamma = (const float *)w->layers[0].attn_norm.data;
-        e.hidden = hidden;
-        e.row_bytes = hidden / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
-        e.fmt = w->token_embd.dtype;
-        n_ss_a = (hidden + 255) / 256;
-        if ((st = c->launch("embed_k", dim3(n_ss_a), dim3(256), 0, e))) return st;
-    }
-
-    for (uint32_t l = 0; l < L; l++) {
-        const LayerW &Lw = w->layers[l];
-        uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
-        uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
-        const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype;
-        const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
-        // gate/up as one item per wave with h in f32, quantized by the down
-        // GEMV itself (Q4_K, rows of one K step; option gemv_grp bit 5)
-        const bool h32 = fuse_ffn && (c->gemv_grp & 32) && !c->gemv_exact && !c->gemv_waves && !c->gemv_max_grid &&
-                         Lw.ffn_gate.dtype == IFR_Q4_K && Lw.ffn_down.dtype == IFR_Q4_K && hidden <= 4096 &&
-                         hidden % 256 == 0 && c->fn("gemv_q4_k_gateup_one") && c->fn("gemv_q4_k_resid_xf");
-        const float *next_norm = (const float *)(l + 1 < L ? w->layers[l + 1].attn_norm.data : w->output_norm.data);
-        GemvPlan p;
-
+    if (stages & ST_QKV) {
         // ---- attention block
         if (fuse_qkv) {
             if ((st = check_gemv(c, Lw.attn_q.dtype, hidden, Lw.attn_q.data, p))) return st;
@@ -605,6 +610,8 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             kv.kv_f16 = cfg.kv_dtype == IFR_F16;
             if ((st = c->launch("kv_store_k", dim3((kv_dim + 255) / 256), dim3(256), 0, kv))) return st;
         }
+    }
+    if (stages & ST_ATTN) {
         {
             AttnArgs a{};
             a.q = s->q;
@@ -616,13 +623,16 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             a.part_ml = s->part_ml;
             a.pos = &s->ctl->pos;
             a.kv_dim = kv_dim;
-            a.n_splits = s->n_splits;
+            a.n_splits = attn_splits_for(s->step_spec, s->head_size);
             a.seq_cap = cfg.max_pos;
+            a.spec_rows = s->step_spec;
             a.n_out = hidden;
             a.head_size = s->head_size;
             a.kv_mul = s->kv_mul;
             if ((st = launch_attn(c, cfg.kv_dtype, a, cfg.n_kv_heads))) return st;
         }
+    }
+    if (stages & ST_O) {
         if (fused) {   // x += Wo att; x * ffn_norm quantized for gate/up
             if ((st = check_gemv(c, Lw.attn_output.dtype, hidden, Lw.attn_output.data, p))) return st;
             GemvArgs a{};
@@ -647,7 +657,9 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             e.n = hidden;
             if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
         }
+    }
 
+    if (stages & ST_GATEUP) {
         // ---- feed-forward block
         if (fuse_ffn) {
             if ((st = check_gemv(c, Lw.ffn_gate.dtype, hidden, Lw.ffn_gate.data, p))) return st;
@@ -696,6 +708,8 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             if ((st = c->launch("silu_k", dim3((ffn + 255) / 256), dim3(256), 0, e))) return st;
             if (fused && (st = launch_quant_act(c, s->hb, nullptr, ffn, s->xq_h, nullptr))) return st;
         }
+    }
+    if (stages & ST_DOWN) {
         if (fused) {   // x += Wdown h; x * next norm quantized for the next QKV / the head
             if ((st = check_gemv(c, Lw.ffn_down.dtype, ffn, Lw.ffn_down.data, p))) return st;
             GemvArgs a{};
@@ -730,7 +744,33 @@ static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2
             if ((st = c->launch("add_k", dim3((hidden + 255) / 256), dim3(256), 0, e))) return st;
         }
     }
+    return IFR_OK;
+}
 
+static ifr_status enqueue_step(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int fused) {
+    const ifr_llama2_config &cfg = s->cfg;
+    const uint32_t hidden = cfg.hidden, L = cfg.n_layers;
+    ifr_status st;
+
+    uint32_t n_ss_a;
+    {   // x <- token_embd[tokens[pos]], and x * attn_norm(0) quantized
+        EmbedArgs e{};
+        e.x = s->x;
+        e.table = w->token_embd.data;
+        e.tokens = s->tokens;
+        e.ctl = s->ctl;
+        e.xq_out = s->xq_a;
+        e.ss_out = s->ss_a;
+        e.gamma = (const float *)w->layers[0].attn_norm.data;
+        e.hidden = hidden;
+        e.row_bytes = hidden / (uint32_t)qk_of(w->token_embd.dtype) * (uint32_t)bytes_of(w->token_embd.dtype);
+        e.fmt = w->token_embd.dtype;
+        n_ss_a = (hidden + 255) / 256;
+        if ((st = c->launch("embed_k", dim3(n_ss_a), dim3(256), 0, e))) return st;
+    }
+
+    for (uint32_t l = 0; l < L; l++)
+        if ((st = enqueue_layer(c, s, w, fused, l, ST_LAYER, n_ss_a))) return st;
     return enqueue_head(c, s, w, fused, n_ss_a);
 }
 
@@ -1130,6 +1170,7 @@ IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr
     a.kv_dim = p->kv_dim;
     a.n_splits = S;
     a.seq_cap = T;
+    a.spec_rows = T;
     a.n_out = p->n_heads * p->head_size;
     a.head_size = p->head_size;
     a.kv_mul = g;
@@ -1408,6 +1449,10 @@ static void state_free(ifr_llama2_state *s) {
     if (!s) return;
     hipStreamSynchronize(s->ctx->stream);
     if (s->graph) hipGraphExecDestroy(s->graph);
+    for (auto &r : s->retired) {
+        hipGraphExecDestroy(r.first);
+        hipEventDestroy(r.second);
+    }
     for (void *p : s->allocs) hipFree(p);
     delete s;
 }
@@ -1480,6 +1525,7 @@ IFR_API ifr_status ifr_llama2_state_reset(ifr_llama2_state *s, const uint32_t *p
     if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
     if (n && (st = c->hip(hipMemcpy(s->tokens, prompt, n * 4, hipMemcpyHostToDevice), "hipMemcpy(tokens)"))) return st;
     StepCtl ctl{pos, n, cfg.max_pos, 0};
+    s->host_pos = pos;
     ifr_rope_config rope{s->head_size, s->kv_dim, pos, cfg.rope_theta};
     ifr_attn_params ap{cfg.max_pos, s->kv_dim, s->kv_mul, cfg.n_heads, s->head_size, pos};
     if ((st = c->hip(hipMemcpy(s->ctl, &ctl, sizeof ctl, hipMemcpyHostToDevice), "hipMemcpy(ctl)"))) return st;
@@ -1654,6 +1700,7 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     const uint32_t pos = pos0 + n;
     if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
     ctl.pos = pos;
+    s->host_pos = pos;
     ifr_rope_config rope{hs, kvd, pos, cfg.rope_theta};
     ifr_attn_params ap{cfg.max_pos, kvd, G, cfg.n_heads, hs, pos};
     if ((st = c->hip(hipMemcpy(s->ctl, &ctl, sizeof ctl, hipMemcpyHostToDevice), "hipMemcpy(ctl)"))) return st;
@@ -1661,11 +1708,18 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     return c->hip(hipMemcpy(s->attn_params, &ap, sizeof ap, hipMemcpyHostToDevice), "hipMemcpy(attn)");
 }
 
+static void host_advance(ifr_llama2_state *s, uint32_t steps) {
+    s->host_pos = (uint32_t)std::min<uint64_t>((uint64_t)s->host_pos + steps, s->cfg.max_pos - 1);
+}
+
 IFR_API ifr_status ifr_llama2_launch(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, int32_t fused) {
     if (!c || !s) return IFR_EINVAL;
     ifr_status st = check_weights(c, s, w);
     if (st) return st;
-    return enqueue_step(c, s, w, fused);
+    s->step_spec = attn_spec_for(s->host_pos, s->cfg.max_pos);
+    if ((st = enqueue_step(c, s, w, fused))) return st;
+    host_advance(s, 1);
+    return IFR_OK;
 }
 
 IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, uint32_t n_steps,
@@ -1674,40 +1728,114 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
     ifr_status st = check_weights(c, s, w);
     if (st) return st;
     if (!use_graph) {
-        for (uint32_t i = 0; i < n_steps; i++)
+        for (uint32_t i = 0; i < n_steps; i++) {
+            s->step_spec = attn_spec_for(s->host_pos, s->cfg.max_pos);
             if ((st = enqueue_step(c, s, w, 1))) return st;
+            host_advance(s, 1);
+        }
         return IFR_OK;
     }
-    if (!s->graph || s->graph_wid != w->id || s->graph_wgen != w->gen || s->graph_fused != 1 || s->graph_exact != c->gemv_exact ||
-        s->graph_sampler != s->sampler_gen || s->graph_grp != c->gemv_grp) {
-        if (s->graph) {
-            hipStreamSynchronize(c->stream);
-            hipGraphExecDestroy(s->graph);
-            s->graph = nullptr;
+    // one captured step per position bucket: replayed for the steps of the
+    // bucket, captured again (after the stream drains) when the position
+    // leaves it, or when the weights, options or sampler changed
+    for (size_t i = 0; i < s->retired.size();) {
+        if (hipEventQuery(s->retired[i].second) == hipSuccess) {
+            hipGraphExecDestroy(s->retired[i].first);
+            hipEventDestroy(s->retired[i].second);
+            s->retired[i] = s->retired.back();
+            s->retired.pop_back();
+        } else {
+            i++;
         }
-        if ((st = c->hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture")))
-            return st;
-        ifr_status est = enqueue_step(c, s, w, 1);
-        hipGraph_t g = nullptr;
-        st = c->hip(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
-        if (est) {
-            if (g) hipGraphDestroy(g);
-            return est;
-        }
-        if (st) return st;
-        st = c->hip(hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0), "hipGraphInstantiate");
-        hipGraphDestroy(g);
-        if (st) return st;
-        s->graph_wid = w->id;
-        s->graph_wgen = w->gen;
-        s->graph_fused = 1;
-        s->graph_exact = c->gemv_exact;
-        s->graph_sampler = s->sampler_gen;
-        s->graph_grp = c->gemv_grp;
     }
-    for (uint32_t i = 0; i < n_steps; i++)
-        if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;
+    uint32_t done = 0;
+    while (done < n_steps) {
+        const uint32_t spec = attn_spec_for(s->host_pos, s->cfg.max_pos);
+        if (!s->graph || s->graph_wid != w->id || s->graph_wgen != w->gen || s->graph_fused != 1 ||
+            s->graph_exact != c->gemv_exact || s->graph_sampler != s->sampler_gen || s->graph_grp != c->gemv_grp ||
+            s->graph_spec != spec) {
+            if (s->graph) {
+                hipEvent_t ev = nullptr;
+                if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess &&
+                    hipEventRecord(ev, c->stream) == hipSuccess) {
+                    s->retired.emplace_back(s->graph, ev);
+                } else {
+                    if (ev) hipEventDestroy(ev);
+                    hipStreamSynchronize(c->stream);
+                    hipGraphExecDestroy(s->graph);
+                }
+                s->graph = nullptr;
+            }
+            s->step_spec = spec;
+            if ((st = c->hip(hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture")))
+                return st;
+            ifr_status est = enqueue_step(c, s, w, 1);
+            hipGraph_t g = nullptr;
+            st = c->hip(hipStreamEndCapture(c->stream, &g), "hipStreamEndCapture");
+            if (est) {
+                if (g) hipGraphDestroy(g);
+                return est;
+            }
+            if (st) return st;
+            st = c->hip(hipGraphInstantiate(&s->graph, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+            hipGraphDestroy(g);
+            if (st) return st;
+            s->graph_wid = w->id;
+            s->graph_wgen = w->gen;
+            s->graph_fused = 1;
+            s->graph_exact = c->gemv_exact;
+            s->graph_sampler = s->sampler_gen;
+            s->graph_grp = c->gemv_grp;
+            s->graph_spec = spec;
+        }
+        // steps left in this bucket (the last position, max_pos - 1, repeats)
+        const uint32_t left = s->host_pos + 1 >= s->cfg.max_pos ? n_steps - done
+                            : std::min(n_steps - done, spec - s->host_pos);
+        for (uint32_t i = 0; i < left; i++)
+            if ((st = c->hip(hipGraphLaunch(s->graph, c->stream), "hipGraphLaunch"))) return st;
+        host_advance(s, left);
+        done += left;
+    }
     return IFR_OK;
+}
+
+IFR_API ifr_status ifr_llama2_time_stage(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, const char *stage,
+                                         uint32_t iters, float *us_per_launch) {
+    if (!c || !s || !stage || !us_per_launch) return IFR_EINVAL;
+    if (!iters) return c->fail(IFR_EINVAL, "time_stage: zero iterations");
+    ifr_status st = check_weights(c, s, w);
+    if (st) return st;
+    const std::string n = stage;
+    const uint32_t mask = n == "qkv" ? ST_QKV : n == "attention" ? ST_ATTN : n == "attn_output" ? ST_O
+                        : n == "ffn_gate_up" ? ST_GATEUP : n == "ffn_down" ? ST_DOWN : 0u;
+    if (!mask) return c->fail(IFR_EINVAL, "time_stage: unknown stage '%s'", stage);
+    const uint32_t L = s->cfg.n_layers;
+    s->step_spec = attn_spec_for(s->host_pos, s->cfg.max_pos);
+    auto pass = [&]() -> ifr_status {
+        for (uint32_t l = 0; l < L; l++) {
+            uint32_t n_ss = s->cfg.hidden / 16; // the partial sums a previous step's down GEMV left in ss_a
+            ifr_status e = enqueue_layer(c, s, w, 1, l, mask, n_ss);
+            if (e) return e;
+        }
+        return IFR_OK;
+    };
+    if ((st = pass())) return st; // warm-up
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if ((st = c->hip(hipEventCreate(&e0), "hipEventCreate"))) return st;
+    if ((st = c->hip(hipEventCreate(&e1), "hipEventCreate"))) {
+        hipEventDestroy(e0);
+        return st;
+    }
+    st = c->hip(hipEventRecord(e0, c->stream), "hipEventRecord");
+    for (uint32_t i = 0; i < iters && !st; i++) st = pass();
+    if (!st) st = c->hip(hipEventRecord(e1, c->stream), "hipEventRecord");
+    if (!st) st = c->hip(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.0f;
+    if (!st) st = c->hip(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (!st) *us_per_launch = ms * 1000.0f / (float)((uint64_t)iters * L);
+    return st;
 }
 
 IFR_API ifr_status ifr_llama2_set_sampler(ifr_llama2_state *s, float temperature, float topp, uint64_t seed) {

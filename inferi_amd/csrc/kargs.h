@@ -99,6 +99,8 @@ struct AttnArgs {
     uint32_t kv_dim;
     uint32_t n_splits;        // gridDim.y
     uint32_t seq_cap;         // positions attended never exceed this (cache rows)
+    uint32_t spec_rows;       // the host's bound on pos + 1: the first batch is loaded before pos is read
+                              // when n_splits batches cover it (any pos stays correct, a larger one is slower)
     uint32_t n_out;           // n_heads * head_size (length of out and xq_out)
     uint32_t head_size;       // a multiple of 8, at most 128
     uint32_t kv_mul;          // query heads per KV head

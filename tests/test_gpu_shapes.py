@@ -231,3 +231,63 @@ def test_prefill_model_shapes(ctx, oracle_lib, name):
     finally:
         s.close()
         w.close()
+
+
+@pytest.mark.timeout(300)
+def test_decode_position_buckets(ctx, oracle_lib):
+    """The attention launch is sized for the bucket of 256 positions the host
+    expects (the graph is captured again when the position leaves it).  A
+    20,000-position cache decoded from position 240 across the 256 and 512
+    bucket edges, with the graph and without; then the device position moved
+    past the host's bucket behind its back (the kernel's fallback to chunks
+    computed from the position it reads).  Logits against the oracle over
+    the same planted cache rows."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=256, ffn=512, n_heads=4, n_kv_heads=1, vocab=1000, max_pos=20000,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=91, std=0.05)
+    try:
+        m = oracle_model(cfg, w)
+        rng = np.random.default_rng(92)
+        planted = {}
+        for layer in range(cfg.n_layers):
+            for which in ("k", "v"):
+                planted[layer, which] = O.encode_f16(rng.standard_normal((cfg.max_pos, cfg.kv_dim), np.float32))
+
+        def plant(s):
+            for (layer, which), rows in planted.items():
+                m.set_kv_rows(layer, which, rows)
+                ptr, n = s.buffer("key_cache" if which == "k" else "value_cache", layer)
+                ctx._check(I.lib().ifr_upload(ctx.h, ptr, rows.ctypes.data, rows.nbytes))
+
+        p0, n = 240, 300
+        toks = rng.integers(0, cfg.vocab, p0 + n + 1).astype(np.uint32)
+        for use_graph in (True, False):
+            s = I.Llama2State(ctx, cfg)
+            try:
+                plant(s)
+                s.reset(toks, p0)
+                got = []
+                for _ in range(n):
+                    I.Llama2.generate(ctx, s, w, 1, use_graph=use_graph)
+                    got.append(s.read("logits").copy())
+                for i, pos in enumerate(range(p0, p0 + n)):
+                    ref = m.forward(int(toks[pos]), pos)
+                    if i % 25 == 0 or pos in (255, 256, 511, 512):
+                        assert_close(got[i], ref, what=f"graph={use_graph} pos {pos}")
+                # a position the host does not know: 5000 (its bucket ends at 768)
+                s.reset(toks, p0 + n)
+                ptr, _ = s.buffer("pos")
+                jump = np.array([5000], np.uint32)
+                ctx._check(I.lib().ifr_upload(ctx.h, ptr, jump.ctypes.data, 4))
+                big = np.zeros(5002, np.uint32)
+                big[5000] = 77
+                tok_ptr, _ = s.buffer("tokens")
+                ctx._check(I.lib().ifr_upload(ctx.h, tok_ptr, big.ctypes.data, big.nbytes))
+                I.Llama2.generate(ctx, s, w, 1, use_graph=use_graph)
+                assert_close(s.read("logits"), m.forward(77, 5000), what=f"graph={use_graph} pos 5000 (fallback)")
+            finally:
+                s.close()
+    finally:
+        w.close()
