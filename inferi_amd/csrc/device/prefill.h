@@ -330,6 +330,29 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
         }
 }
 
+// W -> f16 [N][K] with the GEMM tiles' dequant arithmetic (so the f16
+// weights are the ones the fused GEMM multiplies): thread t takes row
+// t / (K/32), elements [k0 + 32 hs, +32) of it (k0 a multiple of 64).
+template <int FMT>
+__device__ void pf_deq_f16_body(const PfDeqArgs &a) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t segs = a.K / 32;
+    const uint32_t r = t / segs, sg = t % segs;
+    if (r >= a.N) return;
+    const uint32_t k0 = (sg >> 1) * 64, hs = sg & 1u;
+    PfTile<FMT> wt;
+    wt.load(a.w + (size_t)r * a.row_bytes, k0, hs);
+    _Float16 h[32];
+    wt.deq(k0, hs, h);
+    uint4 *dst = (uint4 *)(a.out + (size_t)r * a.K + k0 + 32 * hs);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint4 u;
+        __builtin_memcpy(&u, &h[8 * i], 16);
+        dst[i] = u;
+    }
+}
+
 // ------------------------------------------------------------ pointwise --
 
 // X[m] = dequant(table)[tok[p0 + m]]

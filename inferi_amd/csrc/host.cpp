@@ -11,8 +11,10 @@
 // argmax all on the device.
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -133,6 +135,21 @@ struct ifr_ctx {
     uint32_t pf_chunk = 0;
     // this device's fixed scratch of ifr_matmul_quant_noalloc (noalloc.hip)
     void *noalloc_scratch = nullptr;
+    // prefill GEMMs of at least PF_BLAS_MIN_M rows: the weights dequantized
+    // to f16 (wh), then a hipBLASLt f16 x f16 -> f32 product (option pf_blas)
+    int pf_blas = 1;
+    hipblasLtHandle_t blaslt = nullptr;
+    bool blaslt_failed = false;
+    void *blas_ws = nullptr, *wh = nullptr;
+    size_t blas_ws_bytes = 0, wh_bytes = 0;
+    struct BlasPlan {
+        bool ok = false;
+        hipblasLtMatmulDesc_t desc = nullptr;
+        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+        hipblasLtMatmulAlgo_t algo{};
+        size_t ws = 0;
+    };
+    std::map<std::array<uint32_t, 6>, BlasPlan> blas_plans; // (M, N, K, ldx, ldy, accumulate)
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -912,6 +929,16 @@ IFR_API void ifr_destroy(ifr_ctx *c) {
     hipStreamSynchronize(c->stream);
     if (c->scratch) hipFree(c->scratch);
     if (c->xq_scratch) hipFree(c->xq_scratch);
+    for (auto &kv : c->blas_plans) {
+        ifr_ctx::BlasPlan &b = kv.second;
+        if (b.la) hipblasLtMatrixLayoutDestroy(b.la);
+        if (b.lb) hipblasLtMatrixLayoutDestroy(b.lb);
+        if (b.lc) hipblasLtMatrixLayoutDestroy(b.lc);
+        if (b.desc) hipblasLtMatmulDescDestroy(b.desc);
+    }
+    if (c->blaslt) hipblasLtDestroy(c->blaslt);
+    if (c->blas_ws) hipFree(c->blas_ws);
+    if (c->wh) hipFree(c->wh);
     for (auto &e : c->events)
         if (e) hipEventDestroy(e);
     if (c->module) hipModuleUnload(c->module);
@@ -941,6 +968,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
     if (!strcmp(key, "pf_chunk")) {
         if (value < 0 || value > 16384 || value % 64) return c->fail(IFR_EINVAL, "pf_chunk must be a multiple of 64 in [0, 16384]");
         c->pf_chunk = (uint32_t)value;
+        return IFR_OK;
+    }
+    if (!strcmp(key, "pf_blas")) {
+        c->pf_blas = value ? 1 : 0;
         return IFR_OK;
     }
     if (!strcmp(key, "gemv_grp")) {
@@ -1555,8 +1586,101 @@ static ifr_status check_weights(ifr_ctx *c, const ifr_llama2_state *s, const ifr
 // ---------------------------------------------------------------- prefill --
 
 // Y[m][n] (+)= sum_k Xh[m][k] * deq(W)[n][k] on the matrix cores.
+// The hipBLASLt plan for Y[M][N] (+)= X[M][K] W^T (X f16 row-major, W f16
+// [N][K], Y f32 row-major), cached per shape.  In hipBLASLt's column-major
+// terms: D (N x M, ld ldy) = op(A) B + beta C with A = W as a K x N matrix
+// (ld K) transposed, B = X as K x M (ld ldx), C = D.  Null when hipBLASLt
+// has no algorithm for it (the caller then uses the fused kernel).
+static const ifr_ctx::BlasPlan *blas_plan(ifr_ctx *c, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldy,
+                                          bool accumulate) {
+    if (c->blaslt_failed) return nullptr;
+    if (!c->blaslt && hipblasLtCreate(&c->blaslt) != HIPBLAS_STATUS_SUCCESS) {
+        c->blaslt = nullptr;
+        c->blaslt_failed = true;
+        return nullptr;
+    }
+    const std::array<uint32_t, 6> key{M, N, K, ldx, ldy, accumulate ? 1u : 0u};
+    auto it = c->blas_plans.find(key);
+    if (it != c->blas_plans.end()) return it->second.ok ? &it->second : nullptr;
+    ifr_ctx::BlasPlan &b = c->blas_plans[key];
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&b.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(b.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(b.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&b.la, HIP_R_16F, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&b.lb, HIP_R_16F, K, M, ldx) == HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatrixLayoutCreate(&b.lc, HIP_R_32F, N, M, ldy) == HIPBLAS_STATUS_SUCCESS;
+    if (ok) {
+        hipblasLtMatmulPreference_t pref = nullptr;
+        const uint64_t max_ws = 64ull << 20;
+        hipblasLtMatmulHeuristicResult_t heur[1];
+        int n = 0;
+        ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+             hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws, sizeof max_ws) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             hipblasLtMatmulAlgoGetHeuristic(c->blaslt, b.desc, b.la, b.lb, b.lc, b.lc, pref, 1, heur, &n) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             n > 0 && heur[0].state == HIPBLAS_STATUS_SUCCESS;
+        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        if (ok) {
+            b.algo = heur[0].algo;
+            b.ws = heur[0].workspaceSize;
+        }
+    }
+    b.ok = ok;
+    return ok ? &b : nullptr;
+}
+
+// Y[M][N] (+)= X[M][K] . deq(W)^T for a prefill chunk: with at least
+// PF_BLAS_MIN_M rows (option pf_blas) the weights are dequantized once into
+// f16 and hipBLASLt multiplies them; otherwise, or without a hipBLASLt
+// algorithm for the shape, the fused kernel dequantizes each 128 x 64 tile
+// into LDS.  The f16 weights are the same either way.
+constexpr uint32_t PF_BLAS_MIN_M = 256;
 static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const Tens &w, float *y, uint32_t ldy,
                                  uint32_t M, bool accumulate) {
+    const uint32_t row_bytes = (w.cols / (uint32_t)qk_of(w.dtype)) * (uint32_t)bytes_of(w.dtype);
+    const ifr_ctx::BlasPlan *bp =
+        c->pf_blas && M >= PF_BLAS_MIN_M ? blas_plan(c, M, w.rows, w.cols, ldx, ldy, accumulate) : nullptr;
+    if (bp) {
+        ifr_status st;
+        const size_t wh = (size_t)w.rows * w.cols * 2;
+        if (wh > c->wh_bytes) {
+            if (c->wh) {
+                if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
+                hipFree(c->wh);
+                c->wh = nullptr;
+                c->wh_bytes = 0;
+            }
+            if ((st = c->hip(hipMalloc(&c->wh, wh), "hipMalloc(f16 weights)"))) return st;
+            c->wh_bytes = wh;
+        }
+        if (bp->ws > c->blas_ws_bytes) {
+            if (c->blas_ws) {
+                if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
+                hipFree(c->blas_ws);
+                c->blas_ws = nullptr;
+                c->blas_ws_bytes = 0;
+            }
+            if ((st = c->hip(hipMalloc(&c->blas_ws, bp->ws), "hipMalloc(GEMM workspace)"))) return st;
+            c->blas_ws_bytes = bp->ws;
+        }
+        PfDeqArgs d{};
+        d.w = w.data;
+        d.out = (uint16_t *)c->wh;
+        d.N = w.rows;
+        d.K = w.cols;
+        d.row_bytes = row_bytes;
+        const uint64_t threads = (uint64_t)w.rows * (w.cols / 32);
+        if ((st = c->launch(std::string("deq_f16_") + gemv_fmt_name(w.dtype), dim3((uint32_t)((threads + 255) / 256)),
+                            dim3(256), 0, d)))
+            return st;
+        const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
+        const hipblasStatus_t bs = hipblasLtMatmul(c->blaslt, bp->desc, &alpha, c->wh, bp->la, xh, bp->lb, &beta, y, bp->lc,
+                                                   y, bp->lc, &bp->algo, c->blas_ws, bp->ws, c->stream);
+        if (bs != HIPBLAS_STATUS_SUCCESS) return c->fail(IFR_EHIP, "hipblasLtMatmul: status %d", (int)bs);
+        return IFR_OK;
+    }
     PfGemmArgs g{};
     g.x = xh;
     g.w = w.data;
@@ -1566,7 +1690,7 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
     g.K = w.cols;
     g.ldx = ldx;
     g.ldy = ldy;
-    g.row_bytes = (w.cols / (uint32_t)qk_of(w.dtype)) * (uint32_t)bytes_of(w.dtype);
+    g.row_bytes = row_bytes;
     const dim3 grid((w.rows + PF_GEMM_TILE - 1) / PF_GEMM_TILE, (M + PF_GEMM_TILE - 1) / PF_GEMM_TILE);
     return c->launch(std::string("gemm_") + gemv_fmt_name(w.dtype) + (accumulate ? "_f16_add" : "_f16_store"), grid,
                      dim3(256), 0, g);

@@ -233,6 +233,14 @@ struct PfGemmArgs {
     uint32_t M, N, K, ldx, ldy, row_bytes;
 };
 
+// A weight matrix dequantized to f16 (the prefill GEMM's operand when a
+// library GEMM multiplies it): out[n][k] for n < N, k < K.
+struct PfDeqArgs {
+    const uint8_t *w;    // rows of K/QK GGUF blocks
+    uint16_t *out;       // f16 [N][K]
+    uint32_t N, K, row_bytes;
+};
+
 // Prefill pointwise and attention kernels (one chunk of M prompt tokens at
 // positions p0 .. p0+M-1).
 struct PfArgs {

@@ -120,7 +120,8 @@ extern "C" __global__ void __launch_bounds__(256) fill_normal_k(FillArgs a) { fi
 // prompt (prefill) path
 #define GEMM_KERNELS(FMTNAME, FMT)                                                                          \
     extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_store(PfGemmArgs a) { gemm_f16_body<FMT, 0>(a); } \
-    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_add(PfGemmArgs a) { gemm_f16_body<FMT, 1>(a); }
+    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_add(PfGemmArgs a) { gemm_f16_body<FMT, 1>(a); } \
+    extern "C" __global__ void __launch_bounds__(256) deq_f16_##FMTNAME(PfDeqArgs a) { pf_deq_f16_body<FMT>(a); }
 GEMM_KERNELS(q4_k, Q4_K)
 GEMM_KERNELS(q5_k, Q5_K)
 GEMM_KERNELS(q6_k, Q6_K)

@@ -178,8 +178,11 @@ def test_c5_prefill_4095_tokens(ctx, oracle_lib):
     against the exact arithmetic within the f16 rounding bound; every layer's
     rows (2e-2 normwise) and the next step's logits (5e-2 scaled: 32 layers of
     f16-operand products) against sequential decode of the same prompt on the
-    device; and passes of 512 tokens give the same rows and logits bit for
-    bit."""
+    device; and passes of 512 tokens give rows and logits within the same
+    bars (both pass lengths multiply on hipBLASLt, whose algorithm, and so
+    summation order, depends on the number of rows; on the fused kernel,
+    option pf_blas 0, pass lengths agree bit for bit:
+    test_prefill_pass_length_gives_same_results)."""
     import inferi_amd as I
 
     P = 4096
@@ -193,18 +196,21 @@ def test_c5_prefill_4095_tokens(ctx, oracle_lib):
         I.Llama2.generate(ctx, sa, w, 1, use_graph=True)
         la = sa.read("logits").copy()
         bound_use = check_layer0_bound(sa, cfg, w, prompt[: P - 1])
-        # passes of 512 tokens: identical bits
+        # passes of 512 tokens
         ctx.set_option("pf_chunk", 512)
         sc = I.Llama2State(ctx, cfg)
         try:
             sc.reset(prompt, 0)
             I.Llama2.prefill(ctx, sc, w, P - 1)
             I.Llama2.generate(ctx, sc, w, 1, use_graph=True)
-            assert np.array_equal(sc.read("logits").view(np.uint32), la.view(np.uint32)), "logits, passes of 512"
+            e512 = float(scaled(sc.read("logits"), la).max())
+            kv512 = 0.0
             for layer in range(cfg.n_layers):
                 for which in ("key_cache", "value_cache"):
-                    assert np.array_equal(sc.read(which, np.uint16, layer), sa.read(which, np.uint16, layer)), \
-                        f"{which} layer {layer}, passes of 512"
+                    ga, gc = kv_rows(sa, cfg, layer, which, P), kv_rows(sc, cfg, layer, which, P)
+                    kv512 = max(kv512, float(np.abs(gc - ga).max() / np.abs(ga).max()))
+            assert kv512 <= 2e-2, f"KV rows, passes of 512: normwise {kv512:.3e}"
+            assert e512 <= 5e-2, f"logits, passes of 512: {e512:.3e}"
         finally:
             ctx.set_option("pf_chunk", 0)
             sc.close()
@@ -226,7 +232,8 @@ def test_c5_prefill_4095_tokens(ctx, oracle_lib):
             same_id = O.argmax(la) == O.argmax(lb)
             print(f"c5 prefill of {P - 1} tokens: layer-0 K/V at {bound_use:.2f} of the f16 bound; all layers' rows "
                   f"within {worst:.2e} (normwise) of sequential decode; next logits within {el:.2e} (scaled); greedy "
-                  f"id {'equal' if same_id else 'differs'} (margin {top2[1] - top2[0]:.3e}); passes of 512 identical",
+                  f"id {'equal' if same_id else 'differs'} (margin {top2[1] - top2[0]:.3e}); passes of 512: rows within "
+                  f"{kv512:.2e}, logits within {e512:.2e}",
                   flush=True)
             # 32 layers of f16-operand products: the KV rows stay within 2e-2
             # normwise; the logits that read all of them within 5e-2
