@@ -453,151 +453,201 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
 // ------------------------------------------------------------ attention --
 // Causal attention of the chunk's queries (positions p0 .. p0+M-1) over the
 // cache rows [0, position], on the matrix cores (flash attention).
-// Workgroup (h, qt): KV head h, its G = kv_mul query heads and QT = 64 / G
-// queries, i.e. QT * G <= 64 rows r = qi * G + j (rows past QT * G hold
-// nothing).  Head dims run to HSP (the head size rounded up to 64 or 128;
-// dims past the head size are zeros).  Per key tile of 64 cache rows:
-//   S = Q K^T     (f16 operands from LDS, 4 waves x one 32x32 MFMA tile)
-//   running softmax per row in base-2 units (q pre-scaled by
-//   log2(e)/sqrt(hs)); P = 2^(S - m) as f16
-//   O = alpha O + P V   (4 waves x 32 rows x HSP/2 dims)
-// and out = O / l is written as f16 for the O GEMM.
-constexpr int PF_ROWS = 64, PF_KT = 64;
+// Workgroup (h, t): KV head h and a tile of QT = 128 / G queries, i.e. the
+// 128 rows r = qi * G + j (query qi, query head j of the G = kv_mul heads of
+// KV head h; rows past QT * G hold nothing).  Wave w owns rows 32w .. 32w+31,
+// one per lane pair (lanes l and l + 32 share row l % 32).  Head dims run to
+// HSP (the head size rounded up to 64 or 128; the padding is zeros).  Per
+// tile of 64 cache rows (K and V^T staged in LDS, double-buffered, loaded
+// from memory one tile ahead):
+//   S^T = K Q^T      (Q^T, scaled by log2(e)/sqrt(hs), stays in registers as
+//                     the B operand; 2 x HSP/16 v_mfma_f32_32x32x16_f16)
+//   running softmax per row in base-2 units, in registers: each lane holds
+//   16 of its row's 32 scores per 32-key block (its half of the keys);
+//   P^T (f16) is then the B operand of
+//   O^T = V^T P^T    (HSP/32 x 4 MFMAs), the k index of both operands
+//                     running over the keys in the order the score
+//                     accumulator holds them (4 keys of this lane half, 4 of
+//                     the other, ...), so P^T needs no shuffle;
+// and out = O / l is written as f16 for the O GEMM.  The last query tiles,
+// which see the most keys, are dispatched first.
+constexpr int PFA_WAVES = 4, PFA_ROWS = 32 * PFA_WAVES, PFA_KT = 64;
 
 template <int HSP, bool F16>
 __device__ void pf_attn_body(const PfArgs &a) {
-    constexpr int R = PF_ROWS, NT = 256;
-    constexpr int HSL = HSP + 8, KTP = PF_KT + 8; // padded LDS rows (halves)
-    constexpr int DT = HSP / 64;                  // 32x32 O tiles per wave along the dims
-    __shared__ __attribute__((aligned(16))) _Float16 qh[R][HSL];
-    __shared__ __attribute__((aligned(16))) _Float16 kh[PF_KT][HSL];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[HSP][KTP];
-    __shared__ __attribute__((aligned(16))) _Float16 ph[R][KTP];
-    __shared__ float sf[R][PF_KT + 1];
-    __shared__ float alpha_s[R], l_s[R];
-    __shared__ int32_t qpos_s[R]; // position of row r's query, -1 for an unused row
+    constexpr int KC = HSP / 16;          // k-chunks of the scores (head dims)
+    constexpr int DT = HSP / 32;          // O^T tiles along the head dims
+    constexpr int KP = HSP + 8;           // K tile row pitch (halves)
+    constexpr int VP = PFA_KT + 8;        // V^T row pitch (halves)
+    constexpr int CPK = HSP / 8;          // 8-dim chunks per key row
+    constexpr int NLD = PFA_KT * CPK / 256; // chunks of K (and of V) each thread stages per tile
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][PFA_KT][KP];
+    __shared__ __attribute__((aligned(16))) _Float16 vts[2][HSP][VP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t G = a.kv_mul, hs = a.head_size, QT = (uint32_t)PF_ROWS / G;
-    const uint32_t kvh = blockIdx.x, qt0 = blockIdx.y * QT;
-    const uint32_t nq = min(QT, a.M - qt0);
-    const float qscale = 1.44269504088896341f / sqrtf((float)hs);
-    const float *qbase = (const float *)a.qkv;
-    for (uint32_t i = tid; i < (uint32_t)R * HSP; i += NT) {
-        const uint32_t rr = i / HSP, d = i % HSP, qi = rr / G, j = rr % G;
-        const float v = (qi < nq && d < hs) ? qbase[(size_t)(qt0 + qi) * a.ld_qkv + (kvh * G + j) * hs + d] : 0.0f;
-        qh[rr][d] = (_Float16)(v * qscale);
-    }
-    if (tid < R) {
-        const uint32_t qi = (uint32_t)tid / G;
-        qpos_s[tid] = qi < nq ? (int32_t)(a.p0 + qt0 + qi) : -1;
-    }
-    // softmax ownership: row sr, keys [16 * sq, 16 * sq + 16)
-    const uint32_t sr = (uint32_t)tid >> 2, sq = (uint32_t)tid & 3u;
-    float m_run = -INFINITY, l_run = 0.0f;
-    // MFMA roles
-    const uint32_t li = (uint32_t)lane & 31u, lk = 8 * ((uint32_t)lane >> 5);
-    const uint32_t srow = 32 * (uint32_t)(wave >> 1), skey = 32 * (uint32_t)(wave & 1); // S tile of this wave
-    const uint32_t orow = 32 * (uint32_t)(wave >> 1), odim = (HSP / 2) * (uint32_t)(wave & 1); // O block
-    float16v oacc[DT];
-#pragma unroll
-    for (int t = 0; t < DT; t++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) oacc[t][e] = 0.0f;
+    const uint32_t G = a.kv_mul, hs = a.head_size, QT = (uint32_t)PFA_ROWS / G;
+    const uint32_t ntiles = (a.M + QT - 1) / QT;
+    const uint32_t kvh = blockIdx.x, q0 = (ntiles - 1 - blockIdx.y) * QT;
+    const uint32_t nq = min(QT, a.M - q0);
+    const uint32_t li = (uint32_t)lane & 31u, hl = (uint32_t)lane >> 5;
+    const uint32_t r = (uint32_t)wave * 32 + li, qi = r / G, j = r % G;
+    const bool row_ok = qi < nq;
+    const int32_t qpos = row_ok ? (int32_t)(a.p0 + q0 + qi) : -1;
+    const uint32_t qlast = a.p0 + q0 + nq - 1;  // largest query position of the tile
+    const uint32_t ntk = qlast / PFA_KT + 1;    // key tiles
 
-    const uint32_t last = a.p0 + qt0 + nq - 1; // largest query position of the tile
-    for (uint32_t k0 = 0; k0 <= last; k0 += PF_KT) {
-        __syncthreads(); // previous tile's operands are consumed
-        for (uint32_t i = tid; i < (uint32_t)PF_KT * HSP; i += NT) {
-            const uint32_t kr = i / HSP, d = i % HSP, kp = k0 + kr;
-            _Float16 kk = (_Float16)0.0f, vv = (_Float16)0.0f;
-            if (kp <= last && d < hs) {
-                const size_t off = (size_t)kp * a.kv_dim + (size_t)kvh * hs + d;
-                if constexpr (F16) {
-                    const uint16_t kb = ((const uint16_t *)a.k_cache)[off], vb = ((const uint16_t *)a.v_cache)[off];
-                    __builtin_memcpy(&kk, &kb, 2);
-                    __builtin_memcpy(&vv, &vb, 2);
+    // this thread's staging chunks: key kk = tid % 64, dims 8 * dc .. +8 for
+    // dc = tid / 64 + 4 i
+    const uint32_t kk = (uint32_t)tid & 63u;
+    uint4 kraw[NLD][F16 ? 1 : 2], vraw[NLD][F16 ? 1 : 2];
+    auto gload = [&](uint32_t t) {
+        const uint32_t kp = t * PFA_KT + kk;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const uint32_t dc = (uint32_t)tid / 64 + 4 * (uint32_t)i;
+            const bool ok = kp <= qlast && dc * 8 < hs;
+            const size_t off = (size_t)(ok ? kp : 0) * a.kv_dim + (size_t)kvh * hs + (ok ? dc * 8 : 0);
+#pragma unroll
+            for (int h = 0; h < (F16 ? 1 : 2); h++) {
+                if (F16) {
+                    kraw[i][h] = ok ? *(const uint4 *)((const uint16_t *)a.k_cache + off) : make_uint4(0, 0, 0, 0);
+                    vraw[i][h] = ok ? *(const uint4 *)((const uint16_t *)a.v_cache + off) : make_uint4(0, 0, 0, 0);
                 } else {
-                    kk = (_Float16)((const float *)a.k_cache)[off];
-                    vv = (_Float16)((const float *)a.v_cache)[off];
+                    kraw[i][h] = ok ? *(const uint4 *)((const float *)a.k_cache + off + 4 * h) : make_uint4(0, 0, 0, 0);
+                    vraw[i][h] = ok ? *(const uint4 *)((const float *)a.v_cache + off + 4 * h) : make_uint4(0, 0, 0, 0);
                 }
             }
-            kh[kr][d] = kk;
-            vt[d][kr] = vv;
         }
-        __syncthreads();
-        // S tile: rows srow.., keys skey..
-        {
-            float16v sacc;
+    };
+    auto lstore = [&](uint32_t b) {
 #pragma unroll
-            for (int e = 0; e < 16; e++) sacc[e] = 0.0f;
+        for (int i = 0; i < NLD; i++) {
+            const uint32_t dc = (uint32_t)tid / 64 + 4 * (uint32_t)i;
+            _Float16 kh[8], vh[8];
+            if constexpr (F16) {
+                __builtin_memcpy(kh, &kraw[i][0], 16);
+                __builtin_memcpy(vh, &vraw[i][0], 16);
+            } else {
+                float kf[8], vf[8];
+                __builtin_memcpy(kf, &kraw[i][0], 32);
+                __builtin_memcpy(vf, &vraw[i][0], 32);
 #pragma unroll
-            for (int kk = 0; kk < HSP; kk += 16) {
-                const half8v av = *(const half8v *)&qh[srow + li][kk + lk];
-                const half8v bv = *(const half8v *)&kh[skey + li][kk + lk];
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, sacc, 0, 0, 0);
+                for (int e = 0; e < 8; e++) {
+                    kh[e] = (_Float16)kf[e];
+                    vh[e] = (_Float16)vf[e];
+                }
             }
+            uint4 u;
+            __builtin_memcpy(&u, kh, 16);
+            *(uint4 *)&ks[b][kk][8 * dc] = u;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t row = srow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
-                const uint32_t key = skey + li;
-                sf[row][key] = ((int32_t)(k0 + key) <= qpos_s[row]) ? sacc[e] : -INFINITY;
-            }
+            for (int e = 0; e < 8; e++) vts[b][8 * dc + e][kk] = vh[e];
         }
-        __syncthreads();
-        // running softmax: 4 threads per row, 16 keys each
-        {
-            float mt = -INFINITY;
+    };
+
+    // Q^T operand: dims 16c + 8 hl .. +8 of this lane's row
+    const float qscale = 1.44269504088896341f / sqrtf((float)hs);
+    half8v qb[KC];
+    {
+        const float *qrow = (const float *)a.qkv + (size_t)(q0 + (row_ok ? qi : 0)) * a.ld_qkv + (size_t)(kvh * G + j) * hs;
 #pragma unroll
-            for (int k = 0; k < 16; k++) mt = fmaxf(mt, sf[sr][16 * sq + k]);
-            mt = fmaxf(mt, __shfl_xor(mt, 1, 64));
-            mt = fmaxf(mt, __shfl_xor(mt, 2, 64));
-            const float mn = fmaxf(m_run, mt);
-            // a row with no key yet (mn = -inf) keeps alpha 1 and p 0
-            const float al = (mn == -INFINITY) ? 1.0f : exp2f(m_run - mn);
-            float ls = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float p = (mn == -INFINITY) ? 0.0f : exp2f(sf[sr][16 * sq + k] - mn);
-                ls += p;
-                ph[sr][16 * sq + k] = (_Float16)p;
+        for (int c = 0; c < KC; c++) {
+            const uint32_t d = 16 * (uint32_t)c + 8 * hl;
+            float4 x0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), x1 = x0;
+            if (row_ok && d < hs) {
+                x0 = *(const float4 *)(qrow + d);
+                x1 = *(const float4 *)(qrow + d + 4);
             }
-            ls += __shfl_xor(ls, 1, 64);
-            ls += __shfl_xor(ls, 2, 64);
-            l_run = l_run * al + ls;
-            m_run = mn;
-            if (sq == 0) alpha_s[sr] = al;
-        }
-        __syncthreads();
-        // O = alpha O + P V
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-        for (int t = 0; t < DT; t++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t row = orow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
-                oacc[t][e] *= alpha_s[row];
-            }
-#pragma unroll
-        for (int kk = 0; kk < PF_KT; kk += 16) {
-            const half8v av = *(const half8v *)&ph[orow + li][kk + lk];
-#pragma unroll
-            for (int t = 0; t < DT; t++) {
-                const half8v bv = *(const half8v *)&vt[odim + 32 * t + li][kk + lk];
-                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, oacc[t], 0, 0, 0);
-            }
+            for (int e = 0; e < 8; e++) qb[c][e] = (_Float16)(xv[e] * qscale);
         }
     }
-    if (sq == 0) l_s[sr] = l_run;
-    __syncthreads();
+
+    float16v o[DT];
 #pragma unroll
     for (int t = 0; t < DT; t++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const uint32_t row = orow + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
-            const uint32_t qi = row / G, dim = odim + 32 * t + li;
-            if (qpos_s[row] >= 0 && dim < hs)
-                ((_Float16 *)a.xh)[(size_t)(qt0 + qi) * a.ldh + (kvh * G + row % G) * hs + dim] =
-                    (_Float16)(oacc[t][e] / l_s[row]);
+        for (int e = 0; e < 16; e++) o[t][e] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (uint32_t t = 0; t < ntk; t++) {
+        const uint32_t b = t & 1u, k0 = t * PFA_KT;
+        if (t + 1 < ntk) gload(t + 1);
+        // S^T for keys k0 + 32 u + (8 (e / 4) + 4 hl + e % 4), this lane's row
+        float16v sacc[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; c++) {
+                const half8v av = *(const half8v *)&ks[b][32 * u + li][16 * c + 8 * hl];
+                sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[c], sacc[u], 0, 0, 0);
+            }
         }
+        // causal mask and the running softmax of this lane's row
+        float mt = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int32_t kp = (int32_t)(k0 + 32 * u + 8 * (e / 4) + 4 * hl + (e % 4));
+                sacc[u][e] = kp <= qpos ? sacc[u][e] : -INFINITY;
+                mt = fmaxf(mt, sacc[u][e]);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(m_run, mt);
+        const float al = mn == -INFINITY ? 1.0f : exp2f(m_run - mn); // a row with no key yet keeps 1
+        float ls = 0.0f;
+        half8v pb[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float pv = mn == -INFINITY ? 0.0f : exp2f(sacc[u][e] - mn);
+                ls += pv;
+                pb[u][e / 8][e % 8] = (_Float16)pv;
+            }
+        l_run = l_run * al + ls;
+        m_run = mn;
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) o[d][e] *= al;
+        // O^T += V^T P^T over the tile's 4 chunks of 16 keys
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int cc = 0; cc < 2; cc++) {
+                const uint32_t kb = 32 * u + 16 * cc + 4 * hl;
+#pragma unroll
+                for (int d = 0; d < DT; d++) {
+                    const _Float16 *vrow = &vts[b][32 * d + li][0];
+                    half8v av;
+                    const uint2 lo = *(const uint2 *)(vrow + kb), hi = *(const uint2 *)(vrow + kb + 8);
+                    __builtin_memcpy(&av, &lo, 8);
+                    __builtin_memcpy((char *)&av + 8, &hi, 8);
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[u][cc], o[d], 0, 0, 0);
+                }
+            }
+        if (t + 1 < ntk) lstore(b ^ 1u);
+        __syncthreads();
+    }
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    if (row_ok) {
+        _Float16 *orow = (_Float16 *)a.xh + (size_t)(q0 + qi) * a.ldh + (size_t)(kvh * G + j) * hs;
+        const float inv = 1.0f / l_tot;
+#pragma unroll
+        for (int d = 0; d < DT; d++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t dim = 32 * d + 8 * (e / 4) + 4 * hl + (e % 4);
+                if (dim < hs) orow[dim] = (_Float16)(o[d][e] * inv);
+            }
+    }
 }
 
 } // namespace ifr

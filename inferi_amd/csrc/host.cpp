@@ -1770,7 +1770,7 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     const uint32_t G = s->kv_mul, ldq = qd + 2 * kvd, ldh = s->pf_ldh;
     char attn_name[64];
     snprintf(attn_name, sizeof attn_name, "pf_attn_%s_h%u", cfg.kv_dtype == IFR_F16 ? "f16" : "f32", attn_hsp(hs));
-    const uint32_t attn_qt = 64 / G; // device/prefill.h: PF_ROWS / kv_mul queries per workgroup
+    const uint32_t attn_qt = 128 / G; // device/prefill.h: PFA_ROWS / kv_mul queries per workgroup
     for (uint32_t c0 = 0; c0 < n; c0 += s->pf_chunk) {
         const uint32_t M = std::min(s->pf_chunk, n - c0), p0 = pos0 + c0;
         PfArgs a{};
