@@ -98,8 +98,12 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * the FFN down GEMV quantizing h itself; bit 6, a default, the Q6_K output
  * head in 4-wave workgroups of up to 256 VGPRs, two per CU).  Default 97.  "pf_chunk"
  * sets the prompt tokens per ifr_llama2_prefill pass (a multiple of 64, at
- * most 16384; 0 = 4096), read at a state's first prefill: the results do
- * not depend on it. */
+ * most 16384; 0 = 4096), read at a state's first prefill.  "pf_blas" = 1
+ * (the default) multiplies prefill passes of 256 or more tokens (and
+ * ifr_gemm_quant calls of m >= 256) on hipBLASLt after dequantizing each
+ * matrix once to f16; 0 keeps them on the fused kernel, whose results do not
+ * depend on the pass length (hipBLASLt's summation order depends on the
+ * number of rows). */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */
@@ -240,12 +244,13 @@ IFR_API ifr_status ifr_sample(ifr_ctx *ctx, const float *logits, float *probs, u
  * crates/inferi/src/ops/gemv_quant.rs:183-340):
  * y[m][rows] (+)= x[m][cols] . dequant(W)[rows x cols]^T, x f16 (IEEE
  * binary16, row-major, 16-byte aligned), W rows of any quantized GGUF type
- * (Q4_0 .. Q8_K) as a GGUF file stores them (16-byte aligned for Q4_K and
- * Q5_K, 4 otherwise; cols a multiple of 64 and of the block size), y f32
- * row-major with leading dimension `rows`.  The weights are dequantized with
- * the reference's arithmetic into f16 tiles and multiplied on the matrix
- * cores (v_mfma_f32_32x32x16_f16, f32 accumulation); accumulate != 0 adds
- * to y. */
+ * (Q4_0 .. Q8_K) or F16/F32 as a GGUF file stores them (16-byte aligned for
+ * Q4_K, Q5_K, F16 and F32, 4 otherwise; cols a multiple of 64 and of the
+ * block size), y f32 row-major with leading dimension `rows`.  The weights
+ * are dequantized with the reference's arithmetic to f16 and multiplied on
+ * the matrix cores with f32 accumulation: for m >= 256 (option pf_blas) the
+ * whole matrix once into a context scratch, then hipBLASLt; otherwise tile
+ * by tile inside one kernel.  accumulate != 0 adds to y. */
 IFR_API ifr_status ifr_gemm_quant(ifr_ctx *ctx, float *y, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
                                   const void *x_f16, uint32_t m, int32_t accumulate);
 
