@@ -136,12 +136,15 @@ _lib = None
 
 
 def lib() -> C.CDLL:
-    """Loads libinferi_hip.so (raises if it was not built)."""
+    """Loads libinferi_hip.so (raises if it was not built).  IFR_LIB names
+    another build of it (the AddressSanitizer build of inferi_amd/build.py
+    build_host_asan)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"{LIB_PATH} is missing: run `python -c 'import __graft_entry__ as g; g.build()'`")
-        L = C.CDLL(LIB_PATH)
+        path = os.environ.get("IFR_LIB") or LIB_PATH
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = C.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             f = getattr(L, name)
             f.restype = res

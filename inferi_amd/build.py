@@ -70,6 +70,34 @@ def build_host(out: str = LIB) -> str:
     return out
 
 
+ASAN_LIB = os.path.join(ROOT, "_build", "libinferi_hip_asan.so")
+
+
+def asan_runtime() -> str:
+    """Path of the compiler's AddressSanitizer runtime (to preload into an
+    uninstrumented interpreter)."""
+    cxx = shutil.which("g++") or "g++"
+    r = subprocess.run([cxx, "-print-file-name=libasan.so"], stdout=subprocess.PIPE, text=True, check=True)
+    return r.stdout.strip()
+
+
+def build_host_asan(out: str = ASAN_LIB) -> str:
+    """The host library (C ABI, GGUF reader, launches) built by g++ with
+    AddressSanitizer for CPU-side checks; the device code is the ordinary
+    code object.  Load it with IFR_LIB=<out> and the runtime preloaded."""
+    cxx = shutil.which("g++") or "g++"
+    obj_dir = os.path.join(ROOT, "_build")
+    os.makedirs(obj_dir, exist_ok=True)
+    noalloc_o = os.path.join(obj_dir, "noalloc.o")
+    if not os.path.exists(noalloc_o):
+        build_host()
+    _run([cxx, "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer", "-std=c++17", "-shared", "-fPIC",
+          "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
+          os.path.join(CSRC, "host.cpp"), os.path.join(CSRC, "gguf.cpp"), noalloc_o,
+          f"-L{ROCM}/lib", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib", "-o", out])
+    return out
+
+
 def build() -> None:
     build_kernels()
     build_host()
