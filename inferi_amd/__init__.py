@@ -452,11 +452,15 @@ class Llama2Weights:
     @classmethod
     def synthetic(cls, ctxt: LlmContext, config: Llama2Config, seed: int, mat_dtype: int = Q4_K,
                   head_dtype: int = Q6_K, embd_dtype: int = Q4_K, std: float = 0.02, norm_mean: float = 1.0,
-                  norm_std: float = 0.1, qkv_bias: bool = False, bias_std: float = 0.5) -> "Llama2Weights":
+                  norm_std: float = 0.1, qkv_bias: bool = False, bias_std: float = 0.5,
+                  overrides: dict | None = None) -> "Llama2Weights":
         """Random-init model made on the device: every matrix ~ N(0, std)
         quantized with the GGUF quantizer, norms ~ N(norm_mean, norm_std) in
         F32, and with qkv_bias Qwen2's QKV biases ~ N(0, bias_std) in F32.
-        Tensor i (in ``config.shapes(qkv_bias)`` order) uses generator stream i."""
+        ``overrides`` maps a tensor name ("blk.3.attn_v.weight") or a matrix
+        kind ("attn_v", "ffn_down") to another GGUF type, as mixed files
+        (Q4_K_M) store some matrices.  Tensor i (in
+        ``config.shapes(qkv_bias)`` order) uses generator stream i."""
         w = cls(ctxt, config)
         shapes = config.shapes(qkv_bias)
         biggest = max(r * c for r, c in shapes.values())
@@ -471,6 +475,10 @@ class Llama2Weights:
                     w.set(name, F32, buf, rows, cols)
                     continue
                 dt = head_dtype if name == "output.weight" else embd_dtype if name == "token_embd.weight" else mat_dtype
+                if overrides:
+                    parts = name.split(".")
+                    kind = parts[2] if len(parts) == 4 and parts[0] == "blk" else None
+                    dt = overrides.get(name, overrides.get(kind, dt))
                 ctxt.fill_normal(tmp, n, seed, i, 0.0, std)
                 buf = ctxt.alloc(rows * row_bytes(dt, cols))
                 ctxt.quantize(buf, tmp, dt, n)

@@ -542,7 +542,7 @@ static ifr_status enqueue_layer(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama
     const LayerW &Lw = w->layers[l];
     uint8_t *kc = s->kcache + (size_t)l * s->layer_kv_bytes;
     uint8_t *vc = s->vcache + (size_t)l * s->layer_kv_bytes;
-    const bool fuse_qkv = fused && Lw.attn_q.dtype == Lw.attn_k.dtype && Lw.attn_q.dtype == Lw.attn_v.dtype;
+    const bool fuse_qkv = fused != 0;
     const bool fuse_ffn = fused && Lw.ffn_gate.dtype == Lw.ffn_up.dtype;
     // gate/up as one item per wave with h in f32, quantized by the down
     // GEMV itself (Q4_K, rows of one K step; option gemv_grp bit 5)
@@ -555,37 +555,48 @@ static ifr_status enqueue_layer(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama
     if (stages & ST_QKV) {
         // ---- attention block
         if (fuse_qkv) {
-            if ((st = check_gemv(c, Lw.attn_q.dtype, hidden, Lw.attn_q.data, p))) return st;
-            GemvArgs a{};
-            a.w0 = Lw.attn_q.data;
-            a.w1 = Lw.attn_k.data;
-            a.w2 = Lw.attn_v.data;
-            a.rows0 = hidden;
-            a.rows1 = kv_dim;
-            a.rows2 = kv_dim;
-            a.total_rows = hidden + 2 * kv_dim;
-            a.cols = hidden;
-            a.nb = p.nb;
-            a.row_bytes = p.row_bytes;
-            a.x = s->x;
-            a.gamma = (const float *)Lw.attn_norm.data;
-            a.xq = s->xq_a;
-            a.ss_part = s->ss_a;
-            a.n_ss = n_ss_a;
-            a.eps = cfg.rms_eps;
-            a.rope_tab = s->rope_tab;
-            a.y = s->q;
-            a.k_cache = kc;
-            a.v_cache = vc;
-            a.ctl = s->ctl;
-            a.kv_dim = kv_dim;
-            a.head_size = s->head_size;
-            a.kv_f16 = cfg.kv_dtype == IFR_F16;
-            a.q_bias = (const float *)Lw.q_bias.data;
-            a.k_bias = (const float *)Lw.k_bias.data;
-            a.v_bias = (const float *)Lw.v_bias.data;
-            a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
-            if ((st = launch_gemv(c, p, "qkv", a))) return st;
+            // one launch per run of consecutive matrices of one GGUF type
+            // (q, k, v in that order; a Q4_K_M file keeps v in Q6_K on some
+            // layers): the launch's rows are those matrices' rows, the others
+            // counted as zero rows so the epilogue still tells q, k and v apart
+            const Tens *m3[3] = {&Lw.attn_q, &Lw.attn_k, &Lw.attn_v};
+            const uint32_t r3[3] = {hidden, kv_dim, kv_dim};
+            for (uint32_t g0 = 0; g0 < 3;) {
+                uint32_t g1 = g0 + 1;
+                while (g1 < 3 && m3[g1]->dtype == m3[g0]->dtype) g1++;
+                if ((st = check_gemv(c, m3[g0]->dtype, hidden, m3[g0]->data, p))) return st;
+                GemvArgs a{};
+                a.w0 = Lw.attn_q.data;
+                a.w1 = Lw.attn_k.data;
+                a.w2 = Lw.attn_v.data;
+                a.rows0 = g0 <= 0 && 0 < g1 ? r3[0] : 0;
+                a.rows1 = g0 <= 1 && 1 < g1 ? r3[1] : 0;
+                a.rows2 = g0 <= 2 && 2 < g1 ? r3[2] : 0;
+                a.total_rows = a.rows0 + a.rows1 + a.rows2;
+                a.cols = hidden;
+                a.nb = p.nb;
+                a.row_bytes = p.row_bytes;
+                a.x = s->x;
+                a.gamma = (const float *)Lw.attn_norm.data;
+                a.xq = s->xq_a;
+                a.ss_part = s->ss_a;
+                a.n_ss = n_ss_a;
+                a.eps = cfg.rms_eps;
+                a.rope_tab = s->rope_tab;
+                a.y = s->q;
+                a.k_cache = kc;
+                a.v_cache = vc;
+                a.ctl = s->ctl;
+                a.kv_dim = kv_dim;
+                a.head_size = s->head_size;
+                a.kv_f16 = cfg.kv_dtype == IFR_F16;
+                a.q_bias = (const float *)Lw.q_bias.data;
+                a.k_bias = (const float *)Lw.k_bias.data;
+                a.v_bias = (const float *)Lw.v_bias.data;
+                a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
+                if ((st = launch_gemv(c, p, "qkv", a))) return st;
+                g0 = g1;
+            }
         } else {
             EltArgs n{};
             n.a = s->xb;

@@ -101,6 +101,26 @@ def test_qwen2_style_step_by_step(ctx, oracle_lib, mode):
         w.close()
 
 
+@pytest.mark.parametrize("mode", ["fused", "unfused", "graph"])
+@pytest.mark.parametrize("exact", [False, True], ids=["int", "exact"])
+def test_mixed_type_layers(ctx, oracle_lib, mode, exact):
+    """A Q4_K_M-style model: Q4_K matrices, with attn_v and ffn_down in Q6_K
+    on layer 0, only ffn_down on layer 1, and attn_k in Q8_0 on layer 2 (the
+    fused QKV then takes one launch per run of one type)."""
+    import inferi_amd as I
+
+    cfg = tiny_cfg(n_layers=3)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=17, std=0.05, overrides={
+        "blk.0.attn_v.weight": I.Q6_K, "blk.0.ffn_down.weight": I.Q6_K, "blk.1.ffn_down.weight": I.Q6_K,
+        "blk.2.attn_k.weight": I.Q8_0})
+    ctx.set_option("gemv_exact", int(exact))
+    try:
+        check_steps_vs_oracle(ctx, cfg, w, mode)
+    finally:
+        ctx.set_option("gemv_exact", 0)
+        w.close()
+
+
 def check_steps_vs_oracle(ctx, cfg, w, mode):
     """20 steps (a 5-token prompt, then greedy): every step's logits and the
     KV-cache rows against the oracle, the generated ids identical."""
