@@ -34,6 +34,14 @@ namespace ifr {
 constexpr int ATTN_THREADS = 256;
 constexpr int ATTN_BATCH = 4;  // positions per thread whose K and V are loaded together
 constexpr int ATTN_GT_MAX = 8; // query heads one workgroup serves
+// Start of a running maximum: finite, so that no max minus max is inf - inf
+// (NaN) before the first valid score and no branch has to guard it; any real
+// score is far above it, and 2^(it - score) is 0.
+constexpr float ATTN_M0 = -1.0e30f;
+
+// 2^x for softmax weights and rescales: the hardware v_exp_f32 (results
+// below 2^-126 flush to 0, weights too small to change any sum; 2^-inf = 0).
+IFR_DEV float softmax_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Eight consecutive cache elements of one row, kept raw until used (f16:
 // u; f32: u and w), so a batch's loads are issued back to back and the
@@ -201,7 +209,7 @@ __device__ void attn_split_body(const AttnArgs &a) {
     float m[GT], l[GT], o[GT][8];
 #pragma unroll
     for (int j = 0; j < GT; j++) {
-        m[j] = -INFINITY;
+        m[j] = ATTN_M0;
         l[j] = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) o[j][e] = 0.0f;
@@ -210,12 +218,14 @@ __device__ void attn_split_body(const AttnArgs &a) {
     for (uint32_t base = 0; base < n; base += PPP * U) {
         if (!fixed || base) load_batch(t0, base, n);
         __builtin_amdgcn_sched_barrier(0);
+        if (base + PPP * U > n) { // (uniform) the batch runs past the split's positions
 #pragma unroll
-        for (int u = 0; u < U; u++)
-            if (base + pg + PPP * u >= n) {
-                // a masked row (possibly never written): its values must not reach the sums
-                kv8_zero<F16>(vr[u]);
-            }
+            for (int u = 0; u < U; u++)
+                if (base + pg + PPP * u >= n) {
+                    // a masked row (possibly never written): its values must not reach the sums
+                    kv8_zero<F16>(vr[u]);
+                }
+        }
 #pragma unroll
         for (int j = 0; j < GT; j++) {
             float sc[U];
@@ -229,15 +239,16 @@ __device__ void attn_split_body(const AttnArgs &a) {
                 sc[u] = (base + pg + PPP * u < n) ? d : -INFINITY;
                 mb = fmaxf(mb, sc[u]);
             }
-            if (mb == -INFINITY) continue; // no position of this batch for this thread
+            // mb is -inf when none of this thread's positions is valid: then
+            // mn = m[j], al = 1 and every p = 0
             const float mn = fmaxf(m[j], mb);
-            const float al = exp2f(m[j] - mn); // 0 while m[j] is still -inf
+            const float al = softmax_exp2(m[j] - mn); // 0 on the first valid batch
             float lsum = l[j] * al, ov[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) ov[e] = o[j][e] * al;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const float p = exp2f(sc[u] - mn); // 0 for a masked position
+                const float p = softmax_exp2(sc[u] - mn); // 0 for a masked position
                 lsum += p;
 #pragma unroll
                 for (int e = 0; e < 8; e++) ov[e] = fmaf(p, kv8_at<F16>(vr[u], e), ov[e]);
@@ -272,7 +283,7 @@ __device__ void attn_split_body(const AttnArgs &a) {
     if (live)
         for (int i = tid; i < NPG * GT; i += ATTN_THREADS) {
             const int g = i / GT, j = i % GT;
-            wg[g][j] = exp2f(mg[g][j] - Mh[j]); // 0 for a group that saw no position
+            wg[g][j] = softmax_exp2(mg[g][j] - Mh[j]); // 0 for a group that saw no position (m = ATTN_M0)
         }
     __syncthreads();
 
@@ -309,7 +320,7 @@ constexpr uint32_t ATTN_MERGE_CHUNK = 24; // splits of a subset whose loads are 
 IFR_DEV void merge_fold(float &M, float &L, float &O, float m, float l, float o) {
     if (m == -INFINITY) return; // an empty split (its o was never written)
     const float Mn = fmaxf(M, m);
-    const float a = exp2f(M - Mn), b = exp2f(m - Mn); // a = 0 while M is -inf
+    const float a = softmax_exp2(M - Mn), b = softmax_exp2(m - Mn); // a = 0 while M is -inf
     L = fmaf(l, b, L * a);
     O = fmaf(o, b, O * a);
     M = Mn;
@@ -343,7 +354,7 @@ __device__ inline void attn_merge_body(const AttnArgs &a) {
     for (int off = 16; off < 64; off <<= 1) {
         const float Mo = __shfl_xor(M, off, 64), Lo = __shfl_xor(L, off, 64), Oo = __shfl_xor(O, off, 64);
         const float Mn = fmaxf(M, Mo);
-        const float wa = M == -INFINITY ? 0.0f : exp2f(M - Mn), wb = Mo == -INFINITY ? 0.0f : exp2f(Mo - Mn);
+        const float wa = M == -INFINITY ? 0.0f : softmax_exp2(M - Mn), wb = Mo == -INFINITY ? 0.0f : softmax_exp2(Mo - Mn);
         L = fmaf(Lo, wb, L * wa);
         O = fmaf(Oo, wb, O * wa);
         M = Mn;

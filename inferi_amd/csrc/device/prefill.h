@@ -568,7 +568,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
     for (int t = 0; t < DT; t++)
 #pragma unroll
         for (int e = 0; e < 16; e++) o[t][e] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = ATTN_M0, l_run = 0.0f;
 
     gload(0);
     lstore(0);
@@ -599,15 +599,16 @@ __device__ void pf_attn_body(const PfArgs &a) {
                 mt = fmaxf(mt, sacc[u][e]);
             }
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        // a row with no valid key yet keeps mn = ATTN_M0: al = 1, every p = 0
         const float mn = fmaxf(m_run, mt);
-        const float al = mn == -INFINITY ? 1.0f : exp2f(m_run - mn); // a row with no key yet keeps 1
+        const float al = softmax_exp2(m_run - mn);
         float ls = 0.0f;
         half8v pb[2][2];
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const float pv = mn == -INFINITY ? 0.0f : exp2f(sacc[u][e] - mn);
+                const float pv = softmax_exp2(sacc[u][e] - mn);
                 ls += pv;
                 pb[u][e / 8][e % 8] = (_Float16)pv;
             }
