@@ -317,12 +317,14 @@ __device__ void attn_split_body(const AttnArgs &a) {
 constexpr uint32_t ATTN_MERGE_SUBSETS = 4;
 constexpr uint32_t ATTN_MERGE_CHUNK = 24; // splits of a subset whose loads are in flight together
 
+// M starts at ATTN_M0 (finite), so Mn is finite and no weight is NaN; an
+// empty split carries m = -inf and l = 0: weight 0, and its o (never
+// written) is replaced by 0 rather than read into the sum.
 IFR_DEV void merge_fold(float &M, float &L, float &O, float m, float l, float o) {
-    if (m == -INFINITY) return; // an empty split (its o was never written)
     const float Mn = fmaxf(M, m);
-    const float a = softmax_exp2(M - Mn), b = softmax_exp2(m - Mn); // a = 0 while M is -inf
+    const float a = softmax_exp2(M - Mn), b = softmax_exp2(m - Mn);
     L = fmaf(l, b, L * a);
-    O = fmaf(o, b, O * a);
+    O = fmaf(m == -INFINITY ? 0.0f : o, b, O * a);
     M = Mn;
 }
 
@@ -335,16 +337,19 @@ __device__ inline void attn_merge_body(const AttnArgs &a) {
     const uint32_t h = in ? oi / hs : 0, d = in ? oi % hs : 0;
     const float *po = a.part_o + (size_t)h * S * hs + d; // split t at po[t * hs]
     const float *pml = a.part_ml + (size_t)h * S * 2;    // split t at pml[t * 2]
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    float M = ATTN_M0, L = 0.0f, O = 0.0f;
     for (uint32_t t0 = r; t0 < S; t0 += NR * CH) {
         float mv[CH], lv[CH], ov[CH];
 #pragma unroll
         for (uint32_t u = 0; u < CH; u++) {
-            const uint32_t t = t0 + NR * u;
+            // loads from a split in range (a past-the-end slot rereads the
+            // last split, then counts as empty), so no load sits behind a branch
+            const uint32_t t = t0 + NR * u, tc = min(t, S - 1);
             const bool ok = t < S;
-            mv[u] = ok ? pml[(size_t)t * 2] : -INFINITY;
-            lv[u] = ok ? pml[(size_t)t * 2 + 1] : 0.0f;
-            ov[u] = ok ? po[(size_t)t * hs] : 0.0f;
+            const float mm = pml[(size_t)tc * 2], ll = pml[(size_t)tc * 2 + 1], oo = po[(size_t)tc * hs];
+            mv[u] = ok ? mm : -INFINITY;
+            lv[u] = ok ? ll : 0.0f;
+            ov[u] = oo;
         }
 #pragma unroll
         for (uint32_t u = 0; u < CH; u++) merge_fold(M, L, O, mv[u], lv[u], ov[u]);
@@ -353,8 +358,8 @@ __device__ inline void attn_merge_body(const AttnArgs &a) {
 #pragma unroll
     for (int off = 16; off < 64; off <<= 1) {
         const float Mo = __shfl_xor(M, off, 64), Lo = __shfl_xor(L, off, 64), Oo = __shfl_xor(O, off, 64);
-        const float Mn = fmaxf(M, Mo);
-        const float wa = M == -INFINITY ? 0.0f : softmax_exp2(M - Mn), wb = Mo == -INFINITY ? 0.0f : softmax_exp2(Mo - Mn);
+        const float Mn = fmaxf(M, Mo); // both at least ATTN_M0
+        const float wa = softmax_exp2(M - Mn), wb = softmax_exp2(Mo - Mn);
         L = fmaf(Lo, wb, L * wa);
         O = fmaf(Oo, wb, O * wa);
         M = Mn;
