@@ -444,6 +444,9 @@ struct XQ {
 
 
 constexpr float XQ_MAXCODE = 2097151.0f; // 2^21 - 1
+// clamp to the code range in one v_med3_f32 (v * inv only overshoots it by
+// rounding; the same value as a compare-and-select clamp for any non-NaN)
+IFR_DEV float xq_clamp(float v) { return __builtin_amdgcn_fmed3f(v, -XQ_MAXCODE, XQ_MAXCODE); }
 
 // Quantizes one value per lane into XQ at element i; the 16 lanes of a DPP
 // row form one group (i % 16 == lane % 16).  Every lane of the wave must call
@@ -453,7 +456,7 @@ IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int 
     const float am = max16(fabsf(v));
     const float sc = am / XQ_MAXCODE;
     const float inv = am > 0.0f ? XQ_MAXCODE / am : 0.0f;
-    const int q = (int)rintf(clampf(v * inv, -XQ_MAXCODE, XQ_MAXCODE));
+    const int q = (int)rintf(xq_clamp(v * inv));
     // balanced base-256 digits: dc, db in [-128, 127], da in [-32, 32]
     const int dc = ((q + 128) & 0xFF) - 128;
     const int q1 = (q - dc) >> 8;
@@ -488,7 +491,7 @@ IFR_DEV void quant4x4(float4 v, bool ok, uint8_t *xq, uint32_t K, uint32_t c) {
     float qf[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-        const int q = (int)rintf(clampf(vals[e] * inv, -XQ_MAXCODE, XQ_MAXCODE));
+        const int q = (int)rintf(xq_clamp(vals[e] * inv));
         const int dc = ((q + 128) & 0xFF) - 128;
         const int q1 = (q - dc) >> 8;
         const int db = ((q1 + 128) & 0xFF) - 128;
