@@ -133,9 +133,10 @@ def prefill_flops(cfg: I.Llama2Config, n: int) -> float:
 
 
 STAGES = ("qkv", "attention", "attn_output", "ffn_gate_up", "ffn_down")
-# the decode step's kernel behind each stage (Q4_K matrices, f16 cache, head size 128, 4 query heads per KV head)
+# the decode step's kernel behind each stage (Q4_K matrices, f16 cache, head size 128, 4 query heads per KV
+# head; the library's default GEMV forms)
 STAGE_KERNELS = {"qkv": "gemv_q4_k_qkv_one", "attention": "attn_f16_h128_g4 + attn_merge",
-                 "attn_output": "gemv_q4_k_resid_r2w8k1", "ffn_gate_up": "gemv_q4_k_gateup_one",
+                 "attn_output": "gemv_q4_k_resid_r2w8k1", "ffn_gate_up": "gemv_q4_k_gateup_one4",
                  "ffn_down": "gemv_q4_k_resid_xf"}
 ROOFLINE_STAGE = "ffn_gate_up"  # the decode step's dominant kernel
 
@@ -209,6 +210,8 @@ def run_decode(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
+    if args.gemv_grp >= 0:
+        ctx.set_option("gemv_grp", args.gemv_grp)
     dev_name, n_cu = ctx.device_info()
     base = CFG_8B if args.model == "8b" else CFG_C4
     prompt_len = args.prompt
@@ -364,6 +367,8 @@ def run_sweep(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
+    if args.gemv_grp >= 0:
+        ctx.set_option("gemv_grp", args.gemv_grp)
     rows_out = []
     for name, dt in (("Q4_K", I.Q4_K), ("Q5_K", I.Q5_K), ("Q6_K", I.Q6_K), ("Q8_0", I.Q8_0)):
         for rows, cols in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
@@ -431,6 +436,8 @@ def run_attn(args) -> None:
     ctx = I.LlmContext(0, args.code_object)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
+    if args.gemv_grp >= 0:
+        ctx.set_option("gemv_grp", args.gemv_grp)
     out = []
     nh, nkv, hs = 32, 8, 128
     kv_dim = nkv * hs
@@ -498,6 +505,7 @@ def main() -> None:
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
+    ap.add_argument("--gemv-grp", type=int, default=-1, help="GEMV form mask (option gemv_grp; -1: the library default, whose kernels the stage lines name)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU; the multi-GPU sharding of the decode path is designed "

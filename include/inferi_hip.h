@@ -96,7 +96,10 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * a default; bit 1 FFN down; bit 2 gate/up, bit 3 with 16 waves of two
  * rows; bit 4 the output head; bit 5, a default, gate/up with h in f32 and
  * the FFN down GEMV quantizing h itself; bit 6, a default, the Q6_K output
- * head in 4-wave workgroups of up to 256 VGPRs, two per CU).  Default 97.  "pf_chunk"
+ * head in 4-wave workgroups of up to 256 VGPRs, two per CU; bit 7, a
+ * default, four rows per wave in the Q4_K one-item gate/up form; bit 8 four
+ * rows per wave in the Q4_K one-item plain and QKV forms).  Default 225.
+ * "pf_chunk"
  * sets the prompt tokens per ifr_llama2_prefill pass (a multiple of 64, at
  * most 16384; 0 = 4096), read at a state's first prefill.  "pf_blas" = 1
  * (the default) multiplies prefill passes of 256 or more tokens (and

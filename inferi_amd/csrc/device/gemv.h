@@ -1155,6 +1155,19 @@ __device__ void gemv_f32_body(const GemvArgs &a) {
     }
 }
 
+// Epilogue arithmetic of the integer path's fused norms and activations, on
+// the hardware's reciprocal, reciprocal square root and exp2 (each within
+// about 1 ulp) instead of the correctly rounded library sequences (about 35
+// instructions each, issued by every wave for its one or two outputs).
+// RMSNorm scale 1 / sqrt(t / n + eps) (rms_norm.rs:115):
+IFR_DEV float rms_scale(float t, uint32_t n, float eps) {
+    return __builtin_amdgcn_rsqf(fmaf(t, __builtin_amdgcn_rcpf((float)n), eps));
+}
+// silu(g) = g / (1 + e^-g) (silu.rs:59): e^-g as 2^(-g log2 e); a large
+// negative g gives 2^+inf = inf and g * 0 = -0, the function's limit.
+IFR_DEV float silu_fast(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
 
 // ------------------------------------------------------------------------
 // Integer path.  A workgroup of W waves (W = blockDim.x / 64) copies the
@@ -1329,7 +1342,7 @@ __device__ void gemv_int_body(const GemvArgs &a) {
         for (uint32_t j = 0; j < SC; j++) t += (uint32_t)lane + 64 * j < a.n_ss ? sv[j] : 0.0f;
         for (uint32_t i = (uint32_t)lane + 64 * SC; i < a.n_ss; i += 64) t += a.ss_part[i];
         t = wave_sum(t);
-        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+        rs = rms_scale(t, a.cols, a.eps);
     }
     if constexpr (MODE == GEMV_QKV)
         if (tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = th;
@@ -1385,7 +1398,7 @@ __device__ void gemv_int_body(const GemvArgs &a) {
             float h = 0.0f;
             if (ok) {
                 const float gt = val(2 * l), up = val(2 * l + 1);
-                h = up * (gt / (1.0f + expf(-gt)));
+                h = up * silu_fast(gt);
                 a.y[v] = h;
             }
             if (a.xq_out) quant16(h, ok, a.xq_out, K, v, lane);
@@ -1499,14 +1512,17 @@ __device__ void gemv_int_body(const GemvArgs &a) {
 
 // ------------------------------------------------------------------------
 // One-item form of the integer path for the modes whose waves finish their
-// own rows (PLAIN, QKV) when a row is one 64-lane step (K <= 64/LPB blocks):
-// workgroups of GEMV_ONE_WAVES waves of two rows each, one workgroup per
-// 2*GEMV_ONE_WAVES rows, launched all at once.  Each wave requests x, then
-// its rows' weights, then stages x and computes: no item loop, no buffers
-// carried between items.  Same arithmetic and order as gemv_int_body.
-template <int FMT, int MODE>
+// own rows (PLAIN, QKV, HEAD, GATEUP) when a row is one 64-lane step (K <=
+// 64/LPB blocks): workgroups of GEMV_ONE_WAVES waves of R rows each (R = 2
+// or 4), one workgroup per R*GEMV_ONE_WAVES rows, launched all at once.
+// Each wave requests x, then its rows' weights, then stages x and computes:
+// no item loop, no buffers carried between items.  With R = 4 a wave's fixed
+// work (staging, the RMSNorm scale, the reductions, the epilogue, which
+// lanes 0 and 1 run side by side for two outputs) serves twice the rows.
+// Same arithmetic and order as gemv_int_body for every R.
+template <int FMT, int MODE, int R = 2>
 __device__ void gemv_one_body(const GemvArgs &a) {
-    constexpr int R = 2;
+    static_assert(R == 2 || R == 4, "two or four rows per wave");
     using CH = ChunkI<FMT, R>;
     constexpr int LPB = CH::LPB;
     constexpr bool NORM = MODE == GEMV_QKV || MODE == GEMV_HEAD || MODE == GEMV_GATEUP;
@@ -1563,24 +1579,38 @@ __device__ void gemv_one_body(const GemvArgs &a) {
         for (uint32_t j = 0; j < 4; j++) t += (uint32_t)lane + 64 * j < a.n_ss ? sv[j] : 0.0f;
         for (uint32_t i = (uint32_t)lane + 256; i < a.n_ss; i += 64) t += a.ss_part[i];
         t = wave_sum(t);
-        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+        rs = rms_scale(t, a.cols, a.eps);
         if (MODE == GEMV_QKV && tid < 64 && (uint32_t)tid < a.head_size / 2) theta_lds[tid] = th;
     }
     __syncthreads();
     const XQ xq(lds, a.cols);
-    float acc[R] = {0.0f, 0.0f};
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
     chunk_step<FMT, R>(w, xq, min(bsub, a.nb - 1), c, bsub < a.nb, acc);
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    // lane p < R/2 takes the row pair (v0 + 2p, v0 + 2p + 1); with R = 2 the
+    // pair index is the constant 0, so its row arithmetic stays scalar
+    const uint32_t p = R == 2 ? 0u : (uint32_t)lane;
+    const bool pl = R == 2 ? lane == 0 : (uint32_t)lane < R / 2;
+    float pr0 = acc[0], pr1 = acc[1];
+#pragma unroll
+    for (int k = 1; k < R / 2; k++)
+        if (p == (uint32_t)k) {
+            pr0 = acc[2 * k];
+            pr1 = acc[2 * k + 1];
+        }
     if constexpr (MODE == GEMV_GATEUP) {
-        // virtual rows v0 (gate j), v0 + 1 (up j): h[j] = up * silu(gate), in
-        // f32 (the down GEMV quantizes it)
-        if (lane == 0 && v0 + 1 < a.total_rows) {
-            const float gt = acc[0] * rs, up = acc[1] * rs;
-            a.y[v0 >> 1] = up * (gt / (1.0f + expf(-gt)));
+        // virtual rows v0 + 2p (gate j), v0 + 2p + 1 (up j): h[j] = up *
+        // silu(gate), in f32 (the down GEMV quantizes it)
+        if (pl && v0 + 2 * p + 1 < a.total_rows) {
+            const float gt = pr0 * rs, up = pr1 * rs;
+            a.y[(v0 >> 1) + p] = up * silu_fast(gt);
         }
     } else if constexpr (MODE == GEMV_QKV) {
-        if (lane == 0 && v0 + 1 < a.total_rows) qkv_store_pair(a, v0, acc[0] * rs, acc[1] * rs, pos, theta_lds);
+        if (pl && v0 + 2 * p + 1 < a.total_rows)
+            qkv_store_pair(a, v0 + 2 * p, pr0 * rs, pr1 * rs, pos, theta_lds);
     } else {
         uint64_t best = 0;
 #pragma unroll
@@ -1677,7 +1707,7 @@ __device__ void gemv_grp_body(const GemvArgs &a) {
         for (uint32_t j = 0; j < 4; j++) t += (uint32_t)lane + 64 * j < a.n_ss ? sv[j] : 0.0f;
         for (uint32_t i = (uint32_t)lane + 256; i < a.n_ss; i += 64) t += a.ss_part[i];
         t = wave_sum(t);
-        rs = 1.0f / sqrtf(t / (float)a.cols + a.eps); // rms_norm.rs:115
+        rs = rms_scale(t, a.cols, a.eps);
     }
     __syncthreads();
     const XQ xq(lds, a.cols);
@@ -1721,7 +1751,7 @@ __device__ void gemv_grp_body(const GemvArgs &a) {
         float h = 0.0f;
         if (ok) {
             const float gt = val(2 * l), up = val(2 * l + 1);
-            h = up * (gt / (1.0f + expf(-gt)));
+            h = up * silu_fast(gt);
             a.y[v] = h;
         }
         if (a.xq_out) quant16(h, ok, a.xq_out, K, v, lane);

@@ -130,7 +130,7 @@ struct ifr_ctx {
     // resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16 waves of
     // two rows (else 8 waves of four), bit 4 the output head, bit 5 gateup
     // with h in f32 and the down GEMV quantizing it (default: bits 0 and 5)
-    int gemv_grp = 97;
+    int gemv_grp = 225;
     // prompt tokens per prefill pass (0: PF_CHUNK), read at a state's first prefill
     uint32_t pf_chunk = 0;
     // this device's fixed scratch of ifr_matmul_quant_noalloc (noalloc.hip)
@@ -292,11 +292,15 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
     // workgroup launched at once
     const bool one_mode = !strcmp(mode, "plain") || !strcmp(mode, "qkv");
     if (one_mode && a.nb <= p.bpi && !c->gemv_waves && !c->gemv_max_grid && a.total_rows) {
-        const uint32_t rows_per = GEMV_ONE_WAVES * 2, g = (a.total_rows + rows_per - 1) / rows_per;
+        // four rows per wave where the code object has that form (bit 8;
+        // slower for the QKV launch's 6144 rows, whose 384 workgroups of
+        // four-row waves do not fill the chip)
+        const bool four = (c->gemv_grp & 256) && c->fn(name + "_one4");
+        const uint32_t rows_per = GEMV_ONE_WAVES * (four ? 4 : 2), g = (a.total_rows + rows_per - 1) / rows_per;
         a.ks = 1;
         a.nwaves = GEMV_ONE_WAVES;
         if (grid_out) *grid_out = g;
-        return c->launch(name + "_one", dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a);
+        return c->launch(name + (four ? "_one4" : "_one"), dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a);
     }
     // resid and gateup: one output group per workgroup, one item per wave,
     // where the code object has the form for this format and K
@@ -710,9 +714,10 @@ static ifr_status enqueue_layer(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama
                 a.xq_out = nullptr;
                 a.ks = 1;
                 a.nwaves = GEMV_ONE_WAVES;
-                const uint32_t g = (a.total_rows + GEMV_ONE_WAVES * 2 - 1) / (GEMV_ONE_WAVES * 2);
-                if ((st = c->launch("gemv_q4_k_gateup_one", dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols),
-                                    a)))
+                const bool four = (c->gemv_grp & 128) && c->fn("gemv_q4_k_gateup_one4");
+                const uint32_t rows_per = GEMV_ONE_WAVES * (four ? 4 : 2), g = (a.total_rows + rows_per - 1) / rows_per;
+                if ((st = c->launch(four ? "gemv_q4_k_gateup_one4" : "gemv_q4_k_gateup_one", dim3(g),
+                                    dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a)))
                     return st;
             } else if ((st = launch_gemv(c, p, "gateup", a))) {
                 return st;

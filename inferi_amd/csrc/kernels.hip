@@ -48,6 +48,16 @@ using namespace ifr;
 extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) gemv_q4_k_gateup_one(GemvArgs a) {
     gemv_one_body<Q4_K, GEMV_GATEUP>(a);
 }
+// one-item forms with four rows per wave (option gemv_grp bits 7 and 8)
+extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) gemv_q4_k_gateup_one4(GemvArgs a) {
+    gemv_one_body<Q4_K, GEMV_GATEUP, 4>(a);
+}
+extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) gemv_q4_k_qkv_one4(GemvArgs a) {
+    gemv_one_body<Q4_K, GEMV_QKV, 4>(a);
+}
+extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) gemv_q4_k_plain_one4(GemvArgs a) {
+    gemv_one_body<Q4_K, GEMV_PLAIN, 4>(a);
+}
 extern "C" __global__ void __launch_bounds__(GEMV_INT_MAX_WAVES * 64)
     __attribute__((amdgpu_waves_per_eu(GEMV_INT_WPE, 8))) gemv_q4_k_resid_xf(GemvArgs a) {
     gemv_int_body<Q4_K, GEMV_RESID, GEMV_INT_PIPE, GEMV_INT_NI, true>(a);

@@ -34,10 +34,11 @@ def assert_same(a, b, what):
         raise AssertionError(f"{what}: not bit-identical (max |diff| {d.max():.3e} at {np.unravel_index(d.argmax(), d.shape)})")
 
 
-@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31, 33, 63, 64, 97])
+@pytest.mark.parametrize("grp", [0, 2, 4, 12, 16, 31, 33, 63, 64, 97, 128, 160, 225])
 def test_gemv_forms_same_results(ctx, grp):
     """The looping body, the one-item forms of O, down, gate/up and the
-    head, and the head's 256-VGPR form, on the C4 shape."""
+    head, the head's 256-VGPR form, and the four-row one-item forms (bit 7),
+    on the C4 shape."""
     import inferi_amd as I
 
     cfg = I.Llama2Config(n_layers=4, hidden=2048, ffn=5632, n_heads=32, n_kv_heads=4, vocab=32000, max_pos=32,
@@ -50,7 +51,7 @@ def test_gemv_forms_same_results(ctx, grp):
         try:
             got = decode(ctx, cfg, w, prompt, 12)
         finally:
-            ctx.set_option("gemv_grp", 97)
+            ctx.set_option("gemv_grp", 225)
         assert_same(got[0], ref[0], "logits")
         assert np.array_equal(got[1], ref[1]), "tokens"
         for k in ref[2]:
