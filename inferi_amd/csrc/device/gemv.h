@@ -474,44 +474,51 @@ IFR_DEV void quant16(float v, bool ok, uint8_t *xq, uint32_t K, uint32_t i, int 
     }
 }
 
-// The same quantization with four consecutive values per lane: a quad of
-// lanes holds one 16-value group (lane & 3 = which four).  The maximum, the
-// scale and every digit are quant16's; the sum of codes is formed as
-// quant16's is (exact 8-value halves, one final rounding), so the bytes are
-// identical.  Writes through a generic pointer (LDS or global memory); the
-// caller's quad holds elements 4c .. 4c+15 with c % 4 == 0 at lane & 3 == 0.
-IFR_DEV void quant4x4(float4 v, bool ok, uint8_t *xq, uint32_t K, uint32_t c) {
-    float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    am = fmaxf(am, dpp_f<DPP_QUAD_XOR1>(am));
-    am = fmaxf(am, dpp_f<DPP_QUAD_XOR2>(am));
+// The same quantization with one whole 16-value group per lane (elements
+// 16g .. 16g+15, as the bits of four uint4): the maximum, the two divisions
+// and the sum of codes are issued once per 16 values instead of once per 4.
+// Bytes are quant16's: the same scale, codes and digits, and the sum of
+// codes formed from two exact 8-value halves with one final rounding.  The
+// maximum uses the NaN-propagating v_maximum3 (no canonicalising moves);
+// it equals quant16's for every non-NaN input.  Writes 16 bytes of each
+// digit plane and the group's two floats through a generic pointer.
+IFR_DEV void quant1x16(const uint4 (&u)[4], bool ok, uint8_t *xq, uint32_t K, uint32_t g) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        v[4 * k] = __uint_as_float(u[k].x);
+        v[4 * k + 1] = __uint_as_float(u[k].y);
+        v[4 * k + 2] = __uint_as_float(u[k].z);
+        v[4 * k + 3] = __uint_as_float(u[k].w);
+    }
+    float am = fabsf(v[0]);
+#pragma unroll
+    for (int e = 1; e < 16; e++) am = __builtin_elementwise_maximum(am, fabsf(v[e]));
     const float sc = am / XQ_MAXCODE;
     const float inv = am > 0.0f ? XQ_MAXCODE / am : 0.0f;
-    const float vals[4] = {v.x, v.y, v.z, v.w};
-    uint32_t wa = 0, wb = 0, wc = 0;
-    float qf[4];
+    uint32_t wa[4] = {0, 0, 0, 0}, wb[4] = {0, 0, 0, 0}, wc[4] = {0, 0, 0, 0};
+    float s0 = 0.0f, s1 = 0.0f; // exact: |code| <= 2^21, eight of them
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int q = (int)rintf(xq_clamp(vals[e] * inv));
+    for (int e = 0; e < 16; e++) {
+        const float qf = rintf(xq_clamp(v[e] * inv));
+        const int q = (int)qf;
         const int dc = ((q + 128) & 0xFF) - 128;
         const int q1 = (q - dc) >> 8;
         const int db = ((q1 + 128) & 0xFF) - 128;
         const int da = (q1 - db) >> 8;
-        wa |= ((uint32_t)da & 0xFFu) << (8 * e);
-        wb |= ((uint32_t)db & 0xFFu) << (8 * e);
-        wc |= ((uint32_t)dc & 0xFFu) << (8 * e);
-        qf[e] = (float)q;
+        wa[e / 4] |= ((uint32_t)da & 0xFFu) << (8 * (e % 4));
+        wb[e / 4] |= ((uint32_t)db & 0xFFu) << (8 * (e % 4));
+        wc[e / 4] |= ((uint32_t)dc & 0xFFu) << (8 * (e % 4));
+        if (e < 8) s0 += qf;
+        else s1 += qf;
     }
-    const float s4 = (qf[0] + qf[1]) + (qf[2] + qf[3]);
-    const float s8 = s4 + dpp_f<DPP_QUAD_XOR1>(s4);
-    const float sq = s8 + dpp_f<DPP_QUAD_XOR2>(s8);
+    const float sq = s0 + s1;
     if (ok) {
-        *(uint32_t *)(xq + 4 * c) = wa;
-        *(uint32_t *)(xq + K + 4 * c) = wb;
-        *(uint32_t *)(xq + 2 * K + 4 * c) = wc;
-        if ((c & 3u) == 0) {
-            ((float *)(xq + 3 * K))[c / 4] = sc;
-            ((float *)(xq + 3 * K + K / 4))[c / 4] = sc * sq;
-        }
+        *(uint4 *)(xq + 16 * g) = make_uint4(wa[0], wa[1], wa[2], wa[3]);
+        *(uint4 *)(xq + K + 16 * g) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+        *(uint4 *)(xq + 2 * K + 16 * g) = make_uint4(wc[0], wc[1], wc[2], wc[3]);
+        ((float *)(xq + 3 * K))[g] = sc;
+        ((float *)(xq + 3 * K + K / 4))[g] = sc * sq;
     }
 }
 
@@ -1264,14 +1271,18 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     // The first XC chunks per thread and SC partial sums per lane are
     // straight-line loads of clamped (valid) addresses; loops cover larger
     // inputs.
-    // XF: x arrives in f32 (four values per thread and chunk) and this
-    // kernel quantizes it into LDS itself (quant4x4, quant16's bytes)
+    // XF: x arrives in f32 and this kernel quantizes it into LDS itself,
+    // one 16-value group per thread (quant1x16, quant16's bytes): the four
+    // chunks are the four 16-byte quarters of the thread's first group
     constexpr uint32_t XC = 4, SC = 4;
     const uint32_t n16 = XF ? a.cols / 4 : xq_bytes(a.cols) / 16;
+    const uint32_t ngrp = a.cols / 16, gq = min((uint32_t)tid, ngrp - 1);
     const uint4 *xsrc = XF ? (const uint4 *)a.x : (const uint4 *)a.xq;
     static_assert(XC == 4, "four named chunks");
-    const uint32_t xi0 = min((uint32_t)tid, n16 - 1), xi1 = min((uint32_t)tid + NT, n16 - 1);
-    const uint32_t xi2 = min((uint32_t)tid + 2 * NT, n16 - 1), xi3 = min((uint32_t)tid + 3 * NT, n16 - 1);
+    const uint32_t xi0 = XF ? gq * 4 : min((uint32_t)tid, n16 - 1);
+    const uint32_t xi1 = XF ? gq * 4 + 1 : min((uint32_t)tid + NT, n16 - 1);
+    const uint32_t xi2 = XF ? gq * 4 + 2 : min((uint32_t)tid + 2 * NT, n16 - 1);
+    const uint32_t xi3 = XF ? gq * 4 + 3 : min((uint32_t)tid + 3 * NT, n16 - 1);
     const uint4 xv0 = xsrc[xi0], xv1 = xsrc[xi1], xv2 = xsrc[xi2], xv3 = xsrc[xi3];
     float sv[SC];
     if constexpr (NORM) {
@@ -1311,19 +1322,15 @@ __device__ void gemv_int_body(const GemvArgs &a) {
     if constexpr (NI >= 2) load(B, c2.g < ngroups ? c2 : cur);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (XF) {
-        // every quad of lanes quantizes one 16-value group per chunk; a
-        // thread past the end quantizes the last chunk again (stores off)
-        auto qc = [&](uint4 u, uint32_t i, uint32_t c) {
-            quant4x4(make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)),
-                     i < n16, lds, a.cols, c);
-        };
-        qc(xv0, (uint32_t)tid, xi0);
-        qc(xv1, (uint32_t)tid + NT, xi1);
-        qc(xv2, (uint32_t)tid + 2 * NT, xi2);
-        qc(xv3, (uint32_t)tid + 3 * NT, xi3);
-        for (uint32_t base = XC * NT; base < n16; base += NT) {
-            const uint32_t i = base + (uint32_t)tid;
-            qc(xsrc[min(i, n16 - 1)], i, min(i, n16 - 1));
+        // a wave with no group skips (uniform); in a wave that has some, a
+        // thread past the last group quantizes it again with the stores off
+        if ((uint32_t)wave * 64 < ngrp) {
+            const uint4 u[4] = {xv0, xv1, xv2, xv3};
+            quant1x16(u, (uint32_t)tid < ngrp, lds, a.cols, gq);
+        }
+        for (uint32_t g = (uint32_t)tid + NT; g < ngrp; g += NT) {
+            const uint4 u[4] = {xsrc[4 * g], xsrc[4 * g + 1], xsrc[4 * g + 2], xsrc[4 * g + 3]};
+            quant1x16(u, true, lds, a.cols, g);
         }
     } else {
         uint4 *dst = (uint4 *)lds;
