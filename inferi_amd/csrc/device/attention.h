@@ -105,10 +105,21 @@ IFR_DEV uint32_t attn_chunk(uint32_t T, uint32_t S) {
 template <int HSP, int GT>
 struct AttnLds {
     static constexpr int NPG = ATTN_THREADS / 64 * (64 / (HSP / 8)); // position groups
-    float og[NPG][GT][HSP]; // per position group: unnormalised o
+    // per position group: unnormalised o, in a lane-half order: the thread
+    // with dims 8c .. 8c+7 writes 8c..8c+3 at word 4c and 8c+4..8c+7 at
+    // word HSP/2 + 4c, so the TPP threads of a group fill one contiguous row
+    // per store (no bank conflicts); attn_og_dim maps a word back to its dim
+    float og[NPG][GT][HSP];
     float mg[NPG][GT], lg[NPG][GT];
     float wg[NPG][GT], Mh[GT];
 };
+
+// Dim of word w of an og row (its lane-half order, see AttnLds).
+template <int HSP>
+IFR_DEV uint32_t attn_og_dim(uint32_t w) {
+    constexpr uint32_t HH = HSP / 2;
+    return (w % HH) / 4 * 8 + (w / HH) * 4 + w % 4;
+}
 
 // Positions of the split [t0, t0 + C) below T.  Written without a select
 // on t0 < T: hipcc (ROCm 7.2) folds `t0 < T ? min(C, T - t0) : 0`, when the
@@ -266,7 +277,10 @@ __device__ void attn_split_body(const AttnArgs &a) {
 #pragma unroll
         for (int j = 0; j < GT; j++) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) og[pg][j][dc * 8 + e] = o[j][e];
+            for (int e = 0; e < 4; e++) {
+                og[pg][j][dc * 4 + e] = o[j][e];
+                og[pg][j][HSP / 2 + dc * 4 + e] = o[j][4 + e];
+            }
             if (dc == 0) {
                 mg[pg][j] = m[j];
                 lg[pg][j] = l[j];
@@ -289,11 +303,12 @@ __device__ void attn_split_body(const AttnArgs &a) {
 
     if (live)
         for (int i = tid; i < GT * HSP; i += ATTN_THREADS) {
-            const uint32_t j = (uint32_t)i / HSP, d = (uint32_t)i % HSP;
+            // consecutive threads read consecutive og words (word w, dim d)
+            const uint32_t j = (uint32_t)i / HSP, w = (uint32_t)i % HSP, d = attn_og_dim<HSP>(w);
             if (j >= nj || d >= hs) continue;
             float v = 0.0f;
 #pragma unroll
-            for (int g = 0; g < NPG; g++) v = fmaf(wg[g][j], og[g][j][d], v);
+            for (int g = 0; g < NPG; g++) v = fmaf(wg[g][j], og[g][j][w], v);
             const size_t ph = (size_t)(h0 + j) * S + s;
             a.part_o[ph * hs + d] = v;
             if (d == 0) {
