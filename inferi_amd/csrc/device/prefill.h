@@ -472,6 +472,14 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
 // and out = O / l is written as f16 for the O GEMM.  The last query tiles,
 // which see the most keys, are dispatched first.
 constexpr int PFA_WAVES = 4, PFA_ROWS = 32 * PFA_WAVES, PFA_KT = 64;
+// A row's softmax reference maximum moves only when a tile's maximum passes
+// it by more than this (base-2 units): the weights 2^(s - m) then stay below
+// 2^PFA_LAZY (f16 holds them at the same relative precision as weights
+// below 1), and O and l, both taken against the same reference, keep their
+// ratio.  The rescale of O (its accumulators live in AGPRs: a read, a
+// multiply and a write per value) is skipped for a wave none of whose rows
+// moved.
+constexpr float PFA_LAZY = 8.0f;
 
 template <int HSP, bool F16>
 __device__ void pf_attn_body(const PfArgs &a) {
@@ -569,6 +577,11 @@ __device__ void pf_attn_body(const PfArgs &a) {
 #pragma unroll
         for (int e = 0; e < 16; e++) o[t][e] = 0.0f;
     float m_run = ATTN_M0, l_run = 0.0f;
+    // (uniform) every row of the wave holds a query of the chunk, and the
+    // wave's smallest query position: a key tile at or below it needs no
+    // causal mask
+    const bool wave_rows_ok = ((uint32_t)wave * 32 + 31) / G < nq;
+    const int32_t wave_qmin = (int32_t)(a.p0 + q0 + ((uint32_t)wave * 32) / G);
 
     gload(0);
     lstore(0);
@@ -588,36 +601,48 @@ __device__ void pf_attn_body(const PfArgs &a) {
                 sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qb[c], sacc[u], 0, 0, 0);
             }
         }
-        // causal mask and the running softmax of this lane's row
+        // causal mask (a tile reaching past the wave's first query, or a
+        // wave with rows past the chunk) and the running softmax of this
+        // lane's row
+        if (!wave_rows_ok || (int32_t)(k0 + PFA_KT - 1) > wave_qmin) {
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int32_t kp = (int32_t)(k0 + 32 * u + 8 * (e / 4) + 4 * hl + (e % 4));
+                    sacc[u][e] = kp <= qpos ? sacc[u][e] : -INFINITY;
+                }
+        }
         float mt = -INFINITY;
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int32_t kp = (int32_t)(k0 + 32 * u + 8 * (e / 4) + 4 * hl + (e % 4));
-                sacc[u][e] = kp <= qpos ? sacc[u][e] : -INFINITY;
-                mt = fmaxf(mt, sacc[u][e]);
-            }
+            for (int e = 0; e < 16; e++) mt = fmaxf(mt, sacc[u][e]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        // a row with no valid key yet keeps mn = ATTN_M0: al = 1, every p = 0
-        const float mn = fmaxf(m_run, mt);
-        const float al = softmax_exp2(m_run - mn);
+        // the reference maximum moves (and O, l are rescaled) only where a
+        // row's tile maximum passes it by more than PFA_LAZY; a row with no
+        // valid key yet keeps m_run = ATTN_M0 and every p = 0
+        if (__ballot(mt > m_run + PFA_LAZY)) {
+            const float mn = fmaxf(m_run, mt);
+            const float al = softmax_exp2(m_run - mn);
+            l_run *= al;
+            m_run = mn;
+#pragma unroll
+            for (int d = 0; d < DT; d++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) o[d][e] *= al;
+        }
         float ls = 0.0f;
         half8v pb[2][2];
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const float pv = softmax_exp2(sacc[u][e] - mn);
+                const float pv = softmax_exp2(sacc[u][e] - m_run);
                 ls += pv;
                 pb[u][e / 8][e % 8] = (_Float16)pv;
             }
-        l_run = l_run * al + ls;
-        m_run = mn;
-#pragma unroll
-        for (int d = 0; d < DT; d++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) o[d][e] *= al;
+        l_run += ls;
         // O^T += V^T P^T over the tile's 4 chunks of 16 keys
 #pragma unroll
         for (int u = 0; u < 2; u++)
