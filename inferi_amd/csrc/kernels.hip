@@ -149,11 +149,16 @@ extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_ro
 extern "C" __global__ void __launch_bounds__(256) pf_silu_k(PfArgs a) { pf_silu_body(a); }
 
 #define PF_ATTN_KERNEL(HSP)                                                                     \
-    extern "C" __global__ void __launch_bounds__(256) pf_attn_f16_h##HSP(PfArgs a) {             \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF_ATTN_WPE, 8)))  \
+    pf_attn_f16_h##HSP(PfArgs a) {                                                                   \
         pf_attn_body<HSP, true>(a);                                                              \
     }                                                                                            \
-    extern "C" __global__ void __launch_bounds__(256) pf_attn_f32_h##HSP(PfArgs a) {             \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(PF_ATTN_WPE, 8)))  \
+    pf_attn_f32_h##HSP(PfArgs a) {                                                                   \
         pf_attn_body<HSP, false>(a);                                                             \
     }
+#ifndef PF_ATTN_WPE
+#define PF_ATTN_WPE 2
+#endif
 PF_ATTN_KERNEL(64)
 PF_ATTN_KERNEL(128)
