@@ -471,7 +471,11 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
 //                     the other, ...), so P^T needs no shuffle;
 // and out = O / l is written as f16 for the O GEMM.  The last query tiles,
 // which see the most keys, are dispatched first.
-constexpr int PFA_WAVES = 4, PFA_ROWS = 32 * PFA_WAVES, PFA_KT = 64;
+#ifndef PFA_KEYS
+#define PFA_KEYS 64
+#endif
+constexpr int PFA_WAVES = 4, PFA_ROWS = 32 * PFA_WAVES, PFA_KT = PFA_KEYS; // keys per tile: 32 or 64
+constexpr int PFA_KB = PFA_KT / 32;                                      // 32-key blocks per tile
 // A row's softmax reference maximum moves only when a tile's maximum passes
 // it by more than this (base-2 units): the weights 2^(s - m) then stay below
 // 2^PFA_LAZY (f16 holds them at the same relative precision as weights
@@ -503,15 +507,15 @@ __device__ void pf_attn_body(const PfArgs &a) {
     const uint32_t qlast = a.p0 + q0 + nq - 1;  // largest query position of the tile
     const uint32_t ntk = qlast / PFA_KT + 1;    // key tiles
 
-    // this thread's staging chunks: key kk = tid % 64, dims 8 * dc .. +8 for
-    // dc = tid / 64 + 4 i
-    const uint32_t kk = (uint32_t)tid & 63u;
+    // this thread's staging chunks: key kk = tid % KT, dims 8 * dc .. +8 for
+    // dc = tid / KT + (256 / KT) i
+    const uint32_t kk = (uint32_t)tid % PFA_KT;
     uint4 kraw[NLD][F16 ? 1 : 2], vraw[NLD][F16 ? 1 : 2];
     auto gload = [&](uint32_t t) {
         const uint32_t kp = t * PFA_KT + kk;
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
-            const uint32_t dc = (uint32_t)tid / 64 + 4 * (uint32_t)i;
+            const uint32_t dc = (uint32_t)tid / PFA_KT + (256 / PFA_KT) * (uint32_t)i;
             const bool ok = kp <= qlast && dc * 8 < hs;
             const size_t off = (size_t)(ok ? kp : 0) * a.kv_dim + (size_t)kvh * hs + (ok ? dc * 8 : 0);
 #pragma unroll
@@ -529,7 +533,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
     auto lstore = [&](uint32_t b) {
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
-            const uint32_t dc = (uint32_t)tid / 64 + 4 * (uint32_t)i;
+            const uint32_t dc = (uint32_t)tid / PFA_KT + (256 / PFA_KT) * (uint32_t)i;
             _Float16 kh[8], vh[8];
             if constexpr (F16) {
                 __builtin_memcpy(kh, &kraw[i][0], 16);
@@ -590,9 +594,9 @@ __device__ void pf_attn_body(const PfArgs &a) {
         const uint32_t b = t & 1u, k0 = t * PFA_KT;
         if (t + 1 < ntk) gload(t + 1);
         // S^T for keys k0 + 32 u + (8 (e / 4) + 4 hl + e % 4), this lane's row
-        float16v sacc[2];
+        float16v sacc[PFA_KB];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
+        for (int u = 0; u < PFA_KB; u++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) sacc[u][e] = 0.0f;
 #pragma unroll
@@ -606,7 +610,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
         // lane's row
         if (!wave_rows_ok || (int32_t)(k0 + PFA_KT - 1) > wave_qmin) {
 #pragma unroll
-            for (int u = 0; u < 2; u++)
+            for (int u = 0; u < PFA_KB; u++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int32_t kp = (int32_t)(k0 + 32 * u + 8 * (e / 4) + 4 * hl + (e % 4));
@@ -615,7 +619,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
         }
         float mt = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < 2; u++)
+        for (int u = 0; u < PFA_KB; u++)
 #pragma unroll
             for (int e = 0; e < 16; e++) mt = fmaxf(mt, sacc[u][e]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
@@ -633,9 +637,9 @@ __device__ void pf_attn_body(const PfArgs &a) {
                 for (int e = 0; e < 16; e++) o[d][e] *= al;
         }
         float ls = 0.0f;
-        half8v pb[2][2];
+        half8v pb[PFA_KB][2];
 #pragma unroll
-        for (int u = 0; u < 2; u++)
+        for (int u = 0; u < PFA_KB; u++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const float pv = softmax_exp2(sacc[u][e] - m_run);
@@ -645,7 +649,7 @@ __device__ void pf_attn_body(const PfArgs &a) {
         l_run += ls;
         // O^T += V^T P^T over the tile's 4 chunks of 16 keys
 #pragma unroll
-        for (int u = 0; u < 2; u++)
+        for (int u = 0; u < PFA_KB; u++)
 #pragma unroll
             for (int cc = 0; cc < 2; cc++) {
                 const uint32_t kb = 32 * u + 16 * cc + 4 * hl;
