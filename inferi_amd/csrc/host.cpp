@@ -129,7 +129,9 @@ struct ifr_ctx {
     // one-item GEMV forms in use: bit 0 resid with one K step (O), bit 1
     // resid with K-slices (down), bit 2 gateup, bit 3 gateup as 16 waves of
     // two rows (else 8 waves of four), bit 4 the output head, bit 5 gateup
-    // with h in f32 and the down GEMV quantizing it (default: bits 0 and 5)
+    // with h in f32 and the down GEMV quantizing it, bit 6 the Q6_K head in
+    // 256-VGPR workgroups, bit 7 gateup with four rows per wave, bit 8 plain
+    // and qkv with four rows per wave (default: bits 0, 5, 6 and 7)
     int gemv_grp = 225;
     // prompt tokens per prefill pass (0: PF_CHUNK), read at a state's first prefill
     uint32_t pf_chunk = 0;
@@ -1789,6 +1791,11 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     const uint32_t attn_qt = 128 / G; // device/prefill.h: PFA_ROWS / kv_mul queries per workgroup
     for (uint32_t c0 = 0; c0 < n; c0 += s->pf_chunk) {
         const uint32_t M = std::min(s->pf_chunk, n - c0), p0 = pos0 + c0;
+        // passes of at least 256 rows run their products on M rounded up to
+        // 256 where the scratch holds them (a 4095-token pass as 4096): rows
+        // are independent, and the rows past M are never read (rope,
+        // attention, SiLU and RMSNorm take M)
+        const uint32_t Mg = M >= 256 ? std::min((M + 255) / 256 * 256, s->pf_chunk) : M;
         PfArgs a{};
         a.x = s->pf_x;
         a.xh = s->pf_xh;
@@ -1822,18 +1829,18 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
             a.k_bias = (const float *)L.k_bias.data;
             a.v_bias = (const float *)L.v_bias.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, M, false))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, M, false))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, M, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, Mg, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, Mg, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, Mg, false))) return st;
             if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
             if ((st = c->launch(attn_name, dim3(cfg.n_kv_heads, (M + attn_qt - 1) / attn_qt), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, M, true))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, Mg, true))) return st;
             a.gamma = (const float *)L.ffn_norm.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, M, false))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, M, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, Mg, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, Mg, false))) return st;
             if ((st = c->launch("pf_silu_k", dim3((F + 255) / 256, M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, M, true))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, Mg, true))) return st;
         }
     }
     // advance the device position (and the unfused path's op parameters)
