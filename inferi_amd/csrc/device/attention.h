@@ -323,25 +323,17 @@ __device__ void attn_split_body(const AttnArgs &a) {
 
 // Merge of the split partials, one wave per 16 consecutive output values
 // (element i of the n_heads * hs output is dim i % hs of query head i / hs):
-// lane = (subset r = lane / 16, output 16c + lane % 16); subset r folds
-// splits r, r + 4, ... into a running (M, L, O) with base-2 weights, then the
-// four subsets combine through lane shuffles:
+// lane = (subset r = lane / 16, output 16c + lane % 16); subset r takes
+// splits r, r + 4, ... in chunks of ATTN_MERGE_CHUNK whose loads are in
+// flight together: the chunk's maximum first, then its weighted sums in four
+// independent accumulators, folded into a running (M, L, O) with base-2
+// weights (no chain of rescales through the chunk); then the four subsets
+// combine through lane shuffles:
 // out = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s.  No LDS and no barrier.
 // Every split of the launch is read (an empty one carries m = -inf and is
 // skipped), so no load waits for the position.
 constexpr uint32_t ATTN_MERGE_SUBSETS = 4;
 constexpr uint32_t ATTN_MERGE_CHUNK = 24; // splits of a subset whose loads are in flight together
-
-// M starts at ATTN_M0 (finite), so Mn is finite and no weight is NaN; an
-// empty split carries m = -inf and l = 0: weight 0, and its o (never
-// written) is replaced by 0 rather than read into the sum.
-IFR_DEV void merge_fold(float &M, float &L, float &O, float m, float l, float o) {
-    const float Mn = fmaxf(M, m);
-    const float a = softmax_exp2(M - Mn), b = softmax_exp2(m - Mn);
-    L = fmaf(l, b, L * a);
-    O = fmaf(m == -INFINITY ? 0.0f : o, b, O * a);
-    M = Mn;
-}
 
 __device__ inline void attn_merge_body(const AttnArgs &a) {
     constexpr uint32_t NR = ATTN_MERGE_SUBSETS, CH = ATTN_MERGE_CHUNK;
@@ -366,8 +358,27 @@ __device__ inline void attn_merge_body(const AttnArgs &a) {
             lv[u] = ok ? ll : 0.0f;
             ov[u] = oo;
         }
+        // the chunk's maximum (a pairwise tree), then its sums at that base
+        float mx[CH];
 #pragma unroll
-        for (uint32_t u = 0; u < CH; u++) merge_fold(M, L, O, mv[u], lv[u], ov[u]);
+        for (uint32_t u = 0; u < CH; u++) mx[u] = mv[u];
+#pragma unroll
+        for (uint32_t w = 1; w < CH; w <<= 1)
+#pragma unroll
+            for (uint32_t u = 0; u + w < CH; u += 2 * w) mx[u] = fmaxf(mx[u], mx[u + w]);
+        const float Mn = fmaxf(M, mx[0]); // at least ATTN_M0: finite
+        float Ls[4] = {0.0f, 0.0f, 0.0f, 0.0f}, Os[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t u = 0; u < CH; u++) {
+            // an empty split (m = -inf) weighs 0 and its o, never written, is not read into the sum
+            const float b = softmax_exp2(mv[u] - Mn);
+            Ls[u % 4] = fmaf(lv[u], b, Ls[u % 4]);
+            Os[u % 4] = fmaf(mv[u] == -INFINITY ? 0.0f : ov[u], b, Os[u % 4]);
+        }
+        const float sc = softmax_exp2(M - Mn);
+        L = fmaf(L, sc, (Ls[0] + Ls[1]) + (Ls[2] + Ls[3]));
+        O = fmaf(O, sc, (Os[0] + Os[1]) + (Os[2] + Os[3]));
+        M = Mn;
     }
     // the four subsets of each output: lanes i, i + 16, i + 32, i + 48
 #pragma unroll
