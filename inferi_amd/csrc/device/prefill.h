@@ -490,7 +490,9 @@ __device__ void pf_attn_body(const PfArgs &a) {
     constexpr int KC = HSP / 16;          // k-chunks of the scores (head dims)
     constexpr int DT = HSP / 32;          // O^T tiles along the head dims
     constexpr int KP = HSP + 8;           // K tile row pitch (halves)
-    constexpr int VP = PFA_KT + 8;        // V^T row pitch (halves)
+    // V^T row pitch (halves): 2 x an odd number of dwords, so the 32 lanes of
+    // an 8-byte operand read (rows li, dwords kb/2 + {0,1}) hit 64 distinct banks
+    constexpr int VP = PFA_KT + 4;
     constexpr int CPK = HSP / 8;          // 8-dim chunks per key row
     constexpr int NLD = PFA_KT * CPK / 256; // chunks of K (and of V) each thread stages per tile
     __shared__ __attribute__((aligned(16))) _Float16 ks[2][PFA_KT][KP];
@@ -508,7 +510,13 @@ __device__ void pf_attn_body(const PfArgs &a) {
     const uint32_t ntk = qlast / PFA_KT + 1;    // key tiles
 
     // this thread's staging chunks: key kk = tid % KT, dims 8 * dc .. +8 for
-    // dc = tid / KT + (256 / KT) i
+    // dc = tid / KT + (256 / KT) i.  The loads are unconditional (a load
+    // behind a branch is drained at the branch's join, which would make the
+    // next tile's loads wait before this tile's products): a key past the
+    // tile's last query reads that query's row instead, a finite cache row
+    // whose weight the causal mask makes exactly 0, and a chunk past the
+    // head size reads the last chunk, which meets Q's zero padding in the
+    // scores and feeds only output dims that are never written.
     const uint32_t kk = (uint32_t)tid % PFA_KT;
     uint4 kraw[NLD][F16 ? 1 : 2], vraw[NLD][F16 ? 1 : 2];
     auto gload = [&](uint32_t t) {
@@ -516,16 +524,15 @@ __device__ void pf_attn_body(const PfArgs &a) {
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
             const uint32_t dc = (uint32_t)tid / PFA_KT + (256 / PFA_KT) * (uint32_t)i;
-            const bool ok = kp <= qlast && dc * 8 < hs;
-            const size_t off = (size_t)(ok ? kp : 0) * a.kv_dim + (size_t)kvh * hs + (ok ? dc * 8 : 0);
+            const size_t off = (size_t)min(kp, qlast) * a.kv_dim + (size_t)kvh * hs + min(dc, hs / 8 - 1) * 8;
 #pragma unroll
             for (int h = 0; h < (F16 ? 1 : 2); h++) {
                 if (F16) {
-                    kraw[i][h] = ok ? *(const uint4 *)((const uint16_t *)a.k_cache + off) : make_uint4(0, 0, 0, 0);
-                    vraw[i][h] = ok ? *(const uint4 *)((const uint16_t *)a.v_cache + off) : make_uint4(0, 0, 0, 0);
+                    kraw[i][h] = *(const uint4 *)((const uint16_t *)a.k_cache + off);
+                    vraw[i][h] = *(const uint4 *)((const uint16_t *)a.v_cache + off);
                 } else {
-                    kraw[i][h] = ok ? *(const uint4 *)((const float *)a.k_cache + off + 4 * h) : make_uint4(0, 0, 0, 0);
-                    vraw[i][h] = ok ? *(const uint4 *)((const float *)a.v_cache + off + 4 * h) : make_uint4(0, 0, 0, 0);
+                    kraw[i][h] = *(const uint4 *)((const float *)a.k_cache + off + 4 * h);
+                    vraw[i][h] = *(const uint4 *)((const float *)a.v_cache + off + 4 * h);
                 }
             }
         }
@@ -592,7 +599,9 @@ __device__ void pf_attn_body(const PfArgs &a) {
     __syncthreads();
     for (uint32_t t = 0; t < ntk; t++) {
         const uint32_t b = t & 1u, k0 = t * PFA_KT;
-        if (t + 1 < ntk) gload(t + 1);
+        // the next tile's loads (the last tile reloads itself, unused), not
+        // behind a branch
+        gload(min(t + 1, ntk - 1));
         // S^T for keys k0 + 32 u + (8 (e / 4) + 4 hl + e % 4), this lane's row
         float16v sacc[PFA_KB];
 #pragma unroll
