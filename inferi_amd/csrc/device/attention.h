@@ -163,21 +163,20 @@ __device__ void attn_split_body(const AttnArgs &a) {
     const int dc = lane % TPP;
     const bool dim_ok = (uint32_t)dc * 8 < hs;
     const uint32_t pg = (uint32_t)(wave * PPW + lane / TPP);
-    const size_t head_off = (size_t)kvh * hs + (size_t)dc * 8;
     const uint32_t h0 = kvh * G + j0; // first query head of the workgroup
 
-    // this thread's 8 query dims of every head, pre-scaled
-    const float qs = 1.44269504088896341f / sqrtf((float)hs);
-    float q[GT][8];
+    // this thread's 8 query dims of every head, loaded here without a
+    // branch (a head past the workgroup's and a lane past the head size read
+    // a valid head's last dims) and scaled, or zeroed, once the K and V loads
+    // are out
+    const uint32_t nq_heads = gridDim.x / a.n_sub * G;
+    const uint32_t dq = min((uint32_t)dc, hs / 8 - 1) * 8;
+    float4 qu[GT], qw[GT];
 #pragma unroll
     for (int j = 0; j < GT; j++) {
-        float4 u = make_float4(0.0f, 0.0f, 0.0f, 0.0f), w = u;
-        if ((uint32_t)j < nj && dim_ok) {
-            u = *(const float4 *)(a.q + (size_t)(h0 + j) * hs + dc * 8);
-            w = *(const float4 *)(a.q + (size_t)(h0 + j) * hs + dc * 8 + 4);
-        }
-        q[j][0] = u.x * qs; q[j][1] = u.y * qs; q[j][2] = u.z * qs; q[j][3] = u.w * qs;
-        q[j][4] = w.x * qs; q[j][5] = w.y * qs; q[j][6] = w.z * qs; q[j][7] = w.w * qs;
+        const float *qp = a.q + (size_t)min(h0 + (uint32_t)j, nq_heads - 1) * hs + dq;
+        qu[j] = *(const float4 *)qp;
+        qw[j] = *(const float4 *)(qp + 4);
     }
 
     // When S batches cover the host's bound on the positions (S * Qb >=
@@ -185,26 +184,36 @@ __device__ void attn_split_body(const AttnArgs &a) {
     // as pos + 1 <= spec_rows: the first batch's K and V loads go out together
     // with the position load (rows clamped below spec_rows, masked below).  A
     // position past the bound falls back to chunks computed from it (the
-    // early loads are then discarded).
+    // early loads are then discarded).  The loads sit behind no branch (the
+    // early batch is requested whatever the bound, and a lane past the head
+    // size reads the head's last 8 dims, which meet its zero q and feed only
+    // dims that are never stored): the compiler drains loads behind a branch
+    // where the branches join, and the position could then be read only
+    // after every K and V row had arrived.
     const bool early = S * Qb >= a.spec_rows;
+    const size_t head_ld = (size_t)kvh * hs + (size_t)min((uint32_t)dc, hs / 8 - 1) * 8;
     KV8<F16> kr[ATTN_BATCH], vr[ATTN_BATCH];
     auto load_batch = [&](uint32_t t0, uint32_t base, uint32_t n) {
 #pragma unroll
         for (int u = 0; u < ATTN_BATCH; u++) {
             const uint32_t tt = base + pg + PPP * u;
             const uint32_t row = n ? t0 + (tt < n ? tt : 0) : min(t0 + tt, min(a.spec_rows, a.seq_cap) - 1);
-            const size_t off = (size_t)row * a.kv_dim + head_off;
-            if (dim_ok) {
-                kv8_load<F16>(a.k_cache, off, kr[u]);
-                kv8_load<F16>(a.v_cache, off, vr[u]);
-            } else {
-                kv8_zero<F16>(kr[u]);
-                kv8_zero<F16>(vr[u]);
-            }
+            const size_t off = (size_t)row * a.kv_dim + head_ld;
+            kv8_load<F16>(a.k_cache, off, kr[u]);
+            kv8_load<F16>(a.v_cache, off, vr[u]);
         }
     };
-    if (early) load_batch(s * Qb, 0, 0);
+    load_batch(s * Qb, 0, 0);
     __builtin_amdgcn_sched_barrier(0); // the batch's loads stay together
+    const float qs = 1.44269504088896341f / sqrtf((float)hs);
+    float q[GT][8];
+#pragma unroll
+    for (int j = 0; j < GT; j++) {
+        const float sj = (uint32_t)j < nj && dim_ok ? qs : 0.0f; // q is finite: 0 * q = 0
+        const float4 u = qu[j], w = qw[j];
+        q[j][0] = u.x * sj; q[j][1] = u.y * sj; q[j][2] = u.z * sj; q[j][3] = u.w * sj;
+        q[j][4] = w.x * sj; q[j][5] = w.y * sj; q[j][6] = w.z * sj; q[j][7] = w.w * sj;
+    }
     const uint32_t T = min((uint32_t)__builtin_amdgcn_readfirstlane(pos_dev) + 1u, a.seq_cap);
     const bool fixed = early && T <= a.spec_rows;
     const uint32_t C = fixed ? Qb : attn_chunk<HSP>(T, S);
