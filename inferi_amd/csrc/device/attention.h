@@ -346,6 +346,12 @@ constexpr uint32_t ATTN_MERGE_CHUNK = 24; // splits of a subset whose loads are 
 
 __device__ inline void attn_merge_body(const AttnArgs &a) {
     constexpr uint32_t NR = ATTN_MERGE_SUBSETS, CH = ATTN_MERGE_CHUNK;
+    // the arguments in one batch of scalar loads (left to itself the compiler
+    // reads the sizes, divides, and only then fetches the partials' addresses
+    // from the other half of the argument block: two round trips before the
+    // first load); an empty asm that emits nothing
+    asm volatile("" ::"s"(a.part_o), "s"(a.part_ml), "s"(a.out), "s"(a.xq_out), "s"(a.n_splits), "s"(a.head_size),
+                 "s"(a.n_out));
     const int lane = (int)threadIdx.x;
     const uint32_t hs = a.head_size, S = a.n_splits;
     const uint32_t r = (uint32_t)lane / 16, oi = blockIdx.x * 16 + (uint32_t)lane % 16;

@@ -138,10 +138,15 @@ __device__ void argmax_final_body(const ArgmaxArgs &a) {
 // sums of x^2 (one element per thread: launch ceil(hidden/256) x 256).
 __device__ void embed_body(const EmbedArgs &a) {
     __shared__ float red[4];
+    // the arguments in one batch of scalar loads, so the position's load
+    // (then the token's, then the row's) starts after one round trip; an
+    // empty asm that emits nothing
+    asm volatile("" ::"s"(a.x), "s"(a.table), "s"(a.tokens), "s"(a.ctl), "s"(a.xq_out), "s"(a.ss_out), "s"(a.gamma),
+                 "s"(a.hidden), "s"(a.row_bytes), "s"(a.fmt));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t tok = a.tokens[a.ctl->pos];
     const uint8_t *row = a.table + (size_t)tok * a.row_bytes;
-    const uint32_t i = blockIdx.x * blockDim.x + (uint32_t)tid;
+    const uint32_t i = blockIdx.x * 256u + (uint32_t)tid; // launched with 256 threads (red[] holds 4 waves)
     const bool ok = i < a.hidden;
     const float v = ok ? deq_elem(a.fmt, row, i) : 0.0f;
     if (ok) a.x[i] = v;
