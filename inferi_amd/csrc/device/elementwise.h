@@ -112,11 +112,18 @@ IFR_DEV void step_advance(StepCtl *ctl, uint32_t *tokens, uint32_t *rope_pos, ui
 // One workgroup: reduce the partial keys to the winning index; optionally
 // finish a decode step (store the next token unless it is forced, advance
 // the device position and the position fields of the op configs).
+// Launched as one workgroup of ARGMAX_FINAL_THREADS threads (a constant:
+// blockDim.x would be one more scalar round trip, to the hidden arguments).
+constexpr uint32_t ARGMAX_FINAL_THREADS = 1024;
 __device__ void argmax_final_body(const ArgmaxArgs &a) {
-    __shared__ uint64_t red[16];
+    __shared__ uint64_t red[ARGMAX_FINAL_THREADS / 64];
+    // the arguments in one batch of scalar loads; an empty asm that emits nothing
+    asm volatile("" ::"s"(a.n_parts), "s"(a.part_keys), "s"(a.out_index), "s"(a.ctl), "s"(a.tokens), "s"(a.rope_pos),
+                 "s"(a.attn_pos));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t best = 0;
-    for (uint32_t i = tid; i < a.n_parts; i += blockDim.x) best = a.part_keys[i] > best ? a.part_keys[i] : best;
+    for (uint32_t i = tid; i < a.n_parts; i += ARGMAX_FINAL_THREADS)
+        best = a.part_keys[i] > best ? a.part_keys[i] : best;
     for (int sh = 1; sh < 64; sh <<= 1) {
         const uint64_t o = __shfl_xor(best, sh, 64);
         best = o > best ? o : best;
@@ -125,7 +132,7 @@ __device__ void argmax_final_body(const ArgmaxArgs &a) {
     __syncthreads();
     if (tid == 0) {
         uint64_t b = red[0];
-        for (uint32_t w = 1; w < (blockDim.x >> 6); w++) b = red[w] > b ? red[w] : b;
+        for (uint32_t w = 1; w < ARGMAX_FINAL_THREADS / 64; w++) b = red[w] > b ? red[w] : b;
         const uint32_t idx = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu);
         if (a.out_index) *a.out_index = idx;
         if (a.ctl) step_advance(a.ctl, a.tokens, a.rope_pos, a.attn_pos, a.ctl->pos, idx);
