@@ -50,13 +50,23 @@ template <bool F16>
 struct KV8 {
     uint4 u, w;
 };
+// The loads are non-temporal: a step reads each cache row once, and the
+// streaming hint keeps them from displacing lines the step reuses (8B
+// shape at 4.1 K positions: attention 11.81 -> 11.36 us per layer, -5
+// us/token, alternated on one box).  The same hint on the GEMVs' weight
+// loads measured far slower (gate/up 15.0 -> 18.8 us per layer), and on
+// the partials' stores slower (+5 us/token).
+IFR_DEV uint4 ld16_stream(const void *p) {
+    const u32x4_a16 v = __builtin_nontemporal_load((const u32x4_a16 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 template <bool F16>
 IFR_DEV void kv8_load(const void *cache, size_t off, KV8<F16> &r) {
     if constexpr (F16) {
-        r.u = *(const uint4 *)((const uint16_t *)cache + off);
+        r.u = ld16_stream((const uint16_t *)cache + off);
     } else {
-        r.u = *(const uint4 *)((const float *)cache + off);
-        r.w = *(const uint4 *)((const float *)cache + off + 4);
+        r.u = ld16_stream((const float *)cache + off);
+        r.w = ld16_stream((const float *)cache + off + 4);
     }
 }
 template <bool F16>
