@@ -106,7 +106,14 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * ifr_gemm_quant calls of m >= 256) on hipBLASLt after dequantizing each
  * matrix once to f16; 0 keeps them on the fused kernel, whose results do not
  * depend on the pass length (hipBLASLt's summation order depends on the
- * number of rows). */
+ * number of rows).  "pf_keep_f16" = 1 (the default) keeps those f16
+ * matrices on the device with the weights object after the first prefill
+ * that reaches hipBLASLt (every layer matrix: 2 bytes per weight, 14 GB at
+ * the 8B shape), so later prefills skip the dequantization; the copies are
+ * rebuilt after an ifr_llama2_weights_set call, freed by
+ * ifr_llama2_weights_destroy or by the next prefill once the option is 0,
+ * and skipped (per-pass dequantization) when they cannot be allocated.
+ * Results are the same bit for bit either way. */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */

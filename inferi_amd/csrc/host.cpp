@@ -140,6 +140,9 @@ struct ifr_ctx {
     // prefill GEMMs of at least PF_BLAS_MIN_M rows: the weights dequantized
     // to f16 (wh), then a hipBLASLt f16 x f16 -> f32 product (option pf_blas)
     int pf_blas = 1;
+    // keep every layer matrix resident in f16 for those products, per
+    // weights object (option pf_keep_f16)
+    int pf_keep_f16 = 1;
     hipblasLtHandle_t blaslt = nullptr;
     bool blaslt_failed = false;
     void *blas_ws = nullptr, *wh = nullptr;
@@ -433,6 +436,16 @@ struct ifr_llama2_weights {
     Tens token_embd, output_norm, output;
     std::vector<LayerW> layers;
     std::vector<void *> owned; // device copies made by ifr_llama2_weights_from_gguf
+    // the layer matrices dequantized to f16 for the prefill products (option
+    // pf_keep_f16): one allocation, matrix m of layer l at w16 + w16_off[7 l
+    // + m] (q, k, v, output, gate, up, down), holding generation w16_gen
+    // when w16_ok.  Built by the first prefill that needs it; prefill only
+    // reads the tensor table, so these are the one part it updates.
+    mutable uint8_t *w16 = nullptr;
+    mutable size_t w16_bytes = 0;
+    mutable std::vector<size_t> w16_off;
+    mutable uint64_t w16_gen = 0;
+    mutable bool w16_ok = false;
 };
 
 struct ifr_llama2_state {
@@ -992,6 +1005,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->pf_blas = value ? 1 : 0;
         return IFR_OK;
     }
+    if (!strcmp(key, "pf_keep_f16")) {
+        c->pf_keep_f16 = value ? 1 : 0;
+        return IFR_OK;
+    }
     if (!strcmp(key, "gemv_grp")) {
         c->gemv_grp = (int)value;
         return IFR_OK;
@@ -1386,9 +1403,10 @@ IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *nam
 
 IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w) {
     if (!w) return;
-    if (!w->owned.empty()) {
+    if (!w->owned.empty() || w->w16) {
         hipStreamSynchronize(w->ctx->stream);
         for (void *p : w->owned) hipFree(p);
+        if (w->w16) hipFree(w->w16);
     }
     delete w;
 }
@@ -1655,15 +1673,34 @@ static const ifr_ctx::BlasPlan *blas_plan(ifr_ctx *c, uint32_t M, uint32_t N, ui
 // algorithm for the shape, the fused kernel dequantizes each 128 x 64 tile
 // into LDS.  The f16 weights are the same either way.
 constexpr uint32_t PF_BLAS_MIN_M = 256;
+static uint32_t pf_row_bytes(const Tens &w) {
+    return (w.cols / (uint32_t)qk_of(w.dtype)) * (uint32_t)bytes_of(w.dtype);
+}
+
+// out[rows][cols] = f16(deq(W)): one thread per 32 elements.
+static ifr_status launch_deq_f16(ifr_ctx *c, const Tens &w, void *out) {
+    PfDeqArgs d{};
+    d.w = w.data;
+    d.out = (uint16_t *)out;
+    d.N = w.rows;
+    d.K = w.cols;
+    d.row_bytes = pf_row_bytes(w);
+    const uint64_t threads = (uint64_t)w.rows * (w.cols / 32);
+    return c->launch(std::string("deq_f16_") + gemv_fmt_name(w.dtype), dim3((uint32_t)((threads + 255) / 256)),
+                     dim3(256), 0, d);
+}
+
+// w16: the matrix already dequantized to f16 (a resident copy), or null to
+// dequantize it here into the context's scratch.
 static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const Tens &w, float *y, uint32_t ldy,
-                                 uint32_t M, bool accumulate) {
-    const uint32_t row_bytes = (w.cols / (uint32_t)qk_of(w.dtype)) * (uint32_t)bytes_of(w.dtype);
+                                 uint32_t M, bool accumulate, const void *w16 = nullptr) {
+    const uint32_t row_bytes = pf_row_bytes(w);
     const ifr_ctx::BlasPlan *bp =
         c->pf_blas && M >= PF_BLAS_MIN_M ? blas_plan(c, M, w.rows, w.cols, ldx, ldy, accumulate) : nullptr;
     if (bp) {
         ifr_status st;
         const size_t wh = (size_t)w.rows * w.cols * 2;
-        if (wh > c->wh_bytes) {
+        if (!w16 && wh > c->wh_bytes) {
             if (c->wh) {
                 if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
                 hipFree(c->wh);
@@ -1683,18 +1720,12 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
             if ((st = c->hip(hipMalloc(&c->blas_ws, bp->ws), "hipMalloc(GEMM workspace)"))) return st;
             c->blas_ws_bytes = bp->ws;
         }
-        PfDeqArgs d{};
-        d.w = w.data;
-        d.out = (uint16_t *)c->wh;
-        d.N = w.rows;
-        d.K = w.cols;
-        d.row_bytes = row_bytes;
-        const uint64_t threads = (uint64_t)w.rows * (w.cols / 32);
-        if ((st = c->launch(std::string("deq_f16_") + gemv_fmt_name(w.dtype), dim3((uint32_t)((threads + 255) / 256)),
-                            dim3(256), 0, d)))
-            return st;
+        if (!w16) {
+            if ((st = launch_deq_f16(c, w, c->wh))) return st;
+            w16 = c->wh;
+        }
         const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
-        const hipblasStatus_t bs = hipblasLtMatmul(c->blaslt, bp->desc, &alpha, c->wh, bp->la, xh, bp->lb, &beta, y, bp->lc,
+        const hipblasStatus_t bs = hipblasLtMatmul(c->blaslt, bp->desc, &alpha, w16, bp->la, xh, bp->lb, &beta, y, bp->lc,
                                                    y, bp->lc, &bp->algo, c->blas_ws, bp->ws, c->stream);
         if (bs != HIPBLAS_STATUS_SUCCESS) return c->fail(IFR_EHIP, "hipblasLtMatmul: status %d", (int)bs);
         return IFR_OK;
@@ -1741,6 +1772,76 @@ IFR_API ifr_status ifr_gemm_quant(ifr_ctx *c, float *y, const void *w, int32_t d
     return launch_pf_gemm(c, x_f16, cols, t, y, rows, m, accumulate != 0);
 }
 
+// The layer matrices in the prefill products' order.
+static void pf_mats(const LayerW &L, const Tens *m[7]) {
+    m[0] = &L.attn_q;
+    m[1] = &L.attn_k;
+    m[2] = &L.attn_v;
+    m[3] = &L.attn_output;
+    m[4] = &L.ffn_gate;
+    m[5] = &L.ffn_up;
+    m[6] = &L.ffn_down;
+}
+
+// Every layer matrix dequantized to f16 and kept on the device with the
+// weights (option pf_keep_f16), so a prompt's hipBLASLt passes skip the
+// per-pass dequantization (8B shape: 14 GB of f16 matrices, ~5.5 ms of a
+// 4095-token prefill).  Built once per weights generation: an
+// ifr_llama2_weights_set call makes the copies stale, and the next prefill
+// dequantizes into the same allocation again.  `have` is false when the
+// option (or pf_blas) is off or the allocation fails; the passes then
+// dequantize per call, with the same f16 values.
+static ifr_status pf_resident_f16(ifr_ctx *c, const ifr_llama2_weights *w, bool &have) {
+    have = false;
+    ifr_status st;
+    auto release = [&]() -> ifr_status {
+        if (!w->w16) return IFR_OK;
+        ifr_status e = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        hipFree(w->w16);
+        w->w16 = nullptr;
+        w->w16_bytes = 0;
+        w->w16_ok = false;
+        return e;
+    };
+    if (!c->pf_keep_f16 || !c->pf_blas) return release();
+    std::vector<size_t> off;
+    size_t total = 0;
+    for (const LayerW &L : w->layers) {
+        const Tens *m[7];
+        pf_mats(L, m);
+        for (const Tens *t : m) {
+            off.push_back(total);
+            total += ((size_t)t->rows * t->cols * 2 + 255) / 256 * 256;
+        }
+    }
+    if (w->w16 && w->w16_bytes != total && (st = release())) return st;
+    if (w->w16 && w->w16_ok && w->w16_gen == w->gen) {
+        have = true;
+        return IFR_OK;
+    }
+    if (!w->w16) {
+        void *p = nullptr;
+        if (hipMalloc(&p, total) != hipSuccess) {
+            (void)hipGetLastError(); // not enough memory: dequantize per pass
+            return IFR_OK;
+        }
+        w->w16 = (uint8_t *)p;
+        w->w16_bytes = total;
+    }
+    w->w16_off = off;
+    w->w16_ok = false;
+    for (size_t l = 0; l < w->layers.size(); l++) {
+        const Tens *m[7];
+        pf_mats(w->layers[l], m);
+        for (int i = 0; i < 7; i++)
+            if ((st = launch_deq_f16(c, *m[i], w->w16 + off[l * 7 + i]))) return st;
+    }
+    w->w16_gen = w->gen;
+    w->w16_ok = true;
+    have = true;
+    return IFR_OK;
+}
+
 static ifr_status pf_ensure_scratch(ifr_llama2_state *s) {
     if (s->pf_x) return IFR_OK;
     ifr_ctx *c = s->ctx;
@@ -1770,12 +1871,16 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     if (st) return st;
     const ifr_llama2_config &cfg = s->cfg;
     for (const LayerW &L : w->layers) {
-        const Tens *mats[] = {&L.attn_q, &L.attn_k, &L.attn_v, &L.attn_output, &L.ffn_gate, &L.ffn_up, &L.ffn_down};
+        const Tens *mats[7];
+        pf_mats(L, mats);
         for (const Tens *t : mats)
             if ((st = check_pf_matrix(c, t->dtype, t->cols, t->data))) return st;
     }
     if (!n) return IFR_OK;
     if ((st = pf_ensure_scratch(s))) return st;
+    // resident f16 matrices, when a pass reaches the hipBLASLt products
+    bool w16 = false;
+    if (std::min(s->pf_chunk, n) >= PF_BLAS_MIN_M && (st = pf_resident_f16(c, w, w16))) return st;
     // the position lives on the device: read it once
     StepCtl ctl;
     if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
@@ -1822,6 +1927,8 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
         if ((st = c->launch("pf_embed_k", dim3(M), dim3(256), 0, a))) return st;
         for (uint32_t l = 0; l < cfg.n_layers; l++) {
             const LayerW &L = w->layers[l];
+            // the resident f16 copy of this layer's matrix i, or null
+            auto r16 = [&](int i) -> const void * { return w16 ? w->w16 + w->w16_off[(size_t)l * 7 + i] : nullptr; };
             a.k_cache = s->kcache + (size_t)l * s->layer_kv_bytes;
             a.v_cache = s->vcache + (size_t)l * s->layer_kv_bytes;
             a.gamma = (const float *)L.attn_norm.data;
@@ -1829,18 +1936,18 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
             a.k_bias = (const float *)L.k_bias.data;
             a.v_bias = (const float *)L.v_bias.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, Mg, false))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, Mg, false))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, Mg, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, Mg, false, r16(0)))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, Mg, false, r16(1)))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, Mg, false, r16(2)))) return st;
             if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
             if ((st = c->launch(attn_name, dim3(cfg.n_kv_heads, (M + attn_qt - 1) / attn_qt), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, Mg, true))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, Mg, true, r16(3)))) return st;
             a.gamma = (const float *)L.ffn_norm.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, Mg, false))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, Mg, false))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, Mg, false, r16(4)))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, Mg, false, r16(5)))) return st;
             if ((st = c->launch("pf_silu_k", dim3((F + 255) / 256, M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, Mg, true))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, Mg, true, r16(6)))) return st;
         }
     }
     // advance the device position (and the unfused path's op parameters)

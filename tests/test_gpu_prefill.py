@@ -238,6 +238,64 @@ def test_prefill_pass_length_gives_same_results(ctx, blas):
             assert nw <= 2e-3, f"KV cache, passes of {chunk}: normwise {nw:.3e}"
 
 
+def test_prefill_resident_f16_matrices(ctx):
+    """Option pf_keep_f16 (the default) keeps every layer matrix dequantized
+    to f16 with the weights after the first prefill that reaches hipBLASLt;
+    later prefills multiply those copies.  The copies hold the same f16
+    values the per-pass dequantization writes, so prefills with the copies
+    (the one that builds them, then one that reuses them) and without them
+    (option 0) leave the same KV cache rows, logits and tokens bit for bit.
+    Replacing a matrix (ifr_llama2_weights_set) makes the copies stale: the
+    next prefill dequantizes again and still matches the per-pass path."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, vocab=700, max_pos=400,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=47, std=0.05)
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab, 300).astype(np.uint32)
+
+    def run(keep):
+        ctx.set_option("pf_keep_f16", keep)
+        s = I.Llama2State(ctx, cfg)
+        try:
+            s.reset(prompt, 0)
+            I.Llama2.prefill(ctx, s, w, 299)  # one pass of 299 rows: hipBLASLt products
+            I.Llama2.generate(ctx, s, w, 4, use_graph=True)
+            kv = [s.read(n, np.uint16, layer).copy() for layer in range(cfg.n_layers)
+                  for n in ("key_cache", "value_cache")]
+            return s.read("logits").view(np.uint32).copy(), s.tokens(0, 304), kv
+        finally:
+            s.close()
+
+    def same(a, b, what):
+        assert np.array_equal(a[0], b[0]), f"logits: {what}"
+        assert np.array_equal(a[1], b[1]), f"tokens: {what}"
+        for x, y in zip(a[2], b[2]):
+            assert np.array_equal(x, y), f"KV cache: {what}"
+
+    try:
+        build, reuse, per_pass = run(1), run(1), run(0)
+        same(build, per_pass, "copies built in this prefill vs per-pass dequantization")
+        same(reuse, per_pass, "resident copies vs per-pass dequantization")
+        # a new ffn_down for layer 0 (another draw, quantized on the device):
+        # layer 1's KV rows depend on it
+        rows, cols = cfg.hidden, cfg.ffn
+        tmp = ctx.alloc(rows * cols * 4)
+        ctx.fill_normal(tmp, rows * cols, 1234, 0, 0.0, 0.05)
+        down = ctx.alloc(rows * I.row_bytes(I.Q4_K, cols))
+        ctx.quantize(down, tmp, I.Q4_K, rows * cols)
+        tmp.free()
+        run(1)  # copies of the old tensor table resident again
+        w.buffers["blk.0.ffn_down.weight"][1].free()
+        w.set("blk.0.ffn_down.weight", I.Q4_K, down, rows, cols)
+        after, after_per_pass = run(1), run(0)
+        same(after, after_per_pass, "after a matrix was replaced (a stale f16 copy would differ)")
+        assert not np.array_equal(after[2][2], per_pass[2][2]), "layer 1's K rows ignore the new matrix"
+    finally:
+        ctx.set_option("pf_keep_f16", 1)
+        w.close()
+
+
 def test_prefill_qwen2_style(ctx, oracle_lib):
     """NeoX RoPE pairs and QKV biases (Qwen2) in the prefill's RoPE/KV kernel."""
     import inferi_amd as I
