@@ -112,7 +112,8 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * the 8B shape), so later prefills skip the dequantization; the copies are
  * rebuilt after an ifr_llama2_weights_set call, freed by
  * ifr_llama2_weights_destroy or by the next prefill once the option is 0,
- * and skipped (per-pass dequantization) when they cannot be allocated.
+ * and skipped (per-pass dequantization) when they cannot be allocated or
+ * when the prefill runs on another context than the weights'.
  * Results are the same bit for bit either way. */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 

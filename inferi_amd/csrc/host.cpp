@@ -1793,6 +1793,9 @@ static void pf_mats(const LayerW &L, const Tens *m[7]) {
 // dequantize per call, with the same f16 values.
 static ifr_status pf_resident_f16(ifr_ctx *c, const ifr_llama2_weights *w, bool &have) {
     have = false;
+    // the copies are written and read on the weights' own context, whose
+    // stream orders them; a prefill on another context dequantizes per pass
+    if (c != w->ctx) return IFR_OK;
     ifr_status st;
     auto release = [&]() -> ifr_status {
         if (!w->w16) return IFR_OK;
