@@ -306,7 +306,12 @@ IFR_API ifr_status ifr_llama2_weights_create(ifr_ctx *ctx, const ifr_llama2_conf
  * "blk.N.attn_{q,k,v}.bias") already in device memory.
  * rows/cols follow gguf.rs:591-593 (dims reversed: rows = ne1, cols = ne0);
  * norms and biases are F32 vectors with rows = 1.  A layer with biases adds
- * them to q, k and v before RoPE (transformer.rs:434-442). */
+ * them to q, k and v before RoPE (transformer.rs:434-442).  Every call
+ * starts a new generation of the table: captured decode graphs and the
+ * resident f16 prefill matrices (option "pf_keep_f16") made before it are
+ * rebuilt.  A caller that rewrites a bound tensor's bytes in place (new
+ * weights in the same buffer) binds it again with this call before the next
+ * prefill; the decode kernels read the buffers directly and need no call. */
 IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *gguf_name, int32_t dtype,
                                           const void *dev_data, uint32_t rows, uint32_t cols);
 IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w);
