@@ -113,8 +113,14 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * rebuilt after an ifr_llama2_weights_set call, freed by
  * ifr_llama2_weights_destroy or by the next prefill once the option is 0,
  * and skipped (per-pass dequantization) when they cannot be allocated or
- * when the prefill runs on another context than the weights'.
- * Results are the same bit for bit either way. */
+ * when the prefill runs on another context than the weights'.  "pf_stack"
+ * (bit 0, the default: Q, K and V; bit 1: gate and up) multiplies those
+ * resident matrices as one stacked product per group (one hipBLASLt call
+ * over the adjacent f16 copies; -0.6 ms per 8B 4095-token prefill for Q, K
+ * and V, none measured for gate and up).  With pf_stack 0 the resident
+ * copies give the same results as per-pass dequantization bit for bit; a
+ * stacked product may run another hipBLASLt kernel, whose summation order
+ * can differ in the last bits (at the 8B shape the results were identical). */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */

@@ -143,6 +143,10 @@ struct ifr_ctx {
     // keep every layer matrix resident in f16 for those products, per
     // weights object (option pf_keep_f16)
     int pf_keep_f16 = 1;
+    // products over the resident copies of consecutive matrices stacked into
+    // one hipBLASLt call: bit 0 Q, K and V (the default); bit 1 gate and up
+    // (option pf_stack)
+    int pf_stack = 1;
     hipblasLtHandle_t blaslt = nullptr;
     bool blaslt_failed = false;
     void *blas_ws = nullptr, *wh = nullptr;
@@ -1005,6 +1009,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->pf_blas = value ? 1 : 0;
         return IFR_OK;
     }
+    if (!strcmp(key, "pf_stack")) {
+        c->pf_stack = (int)value & 3;
+        return IFR_OK;
+    }
     if (!strcmp(key, "pf_keep_f16")) {
         c->pf_keep_f16 = value ? 1 : 0;
         return IFR_OK;
@@ -1772,6 +1780,34 @@ IFR_API ifr_status ifr_gemm_quant(ifr_ctx *c, float *y, const void *w, int32_t d
     return launch_pf_gemm(c, x_f16, cols, t, y, rows, m, accumulate != 0);
 }
 
+// Y[M][N] = X[M][K] . W16^T for N rows of resident f16 matrices stored one
+// after another (stacked products), on hipBLASLt; done stays false (and
+// nothing is launched) when the pass is short or hipBLASLt has no plan.
+static ifr_status pf_gemm_stacked(ifr_ctx *c, const void *xh, uint32_t ldx, const void *w16, uint32_t N, uint32_t K,
+                                  float *y, uint32_t ldy, uint32_t M, bool &done) {
+    done = false;
+    if (!c->pf_blas || M < PF_BLAS_MIN_M) return IFR_OK;
+    const ifr_ctx::BlasPlan *bp = blas_plan(c, M, N, K, ldx, ldy, false);
+    if (!bp) return IFR_OK;
+    ifr_status st;
+    if (bp->ws > c->blas_ws_bytes) {
+        if (c->blas_ws) {
+            if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
+            hipFree(c->blas_ws);
+            c->blas_ws = nullptr;
+            c->blas_ws_bytes = 0;
+        }
+        if ((st = c->hip(hipMalloc(&c->blas_ws, bp->ws), "hipMalloc(GEMM workspace)"))) return st;
+        c->blas_ws_bytes = bp->ws;
+    }
+    const float alpha = 1.0f, beta = 0.0f;
+    const hipblasStatus_t bs = hipblasLtMatmul(c->blaslt, bp->desc, &alpha, w16, bp->la, xh, bp->lb, &beta, y, bp->lc, y,
+                                               bp->lc, &bp->algo, c->blas_ws, bp->ws, c->stream);
+    if (bs != HIPBLAS_STATUS_SUCCESS) return c->fail(IFR_EHIP, "hipblasLtMatmul: status %d", (int)bs);
+    done = true;
+    return IFR_OK;
+}
+
 // The layer matrices in the prefill products' order.
 static void pf_mats(const LayerW &L, const Tens *m[7]) {
     m[0] = &L.attn_q;
@@ -1939,16 +1975,38 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
             a.k_bias = (const float *)L.k_bias.data;
             a.v_bias = (const float *)L.v_bias.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, Mg, false, r16(0)))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, Mg, false, r16(1)))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, Mg, false, r16(2)))) return st;
+            // the resident copies of matrices i .. j lie one after another
+            const Tens *mats[7];
+            pf_mats(L, mats);
+            auto adjacent = [&](int i, int j) {
+                for (int m = i; m < j; m++)
+                    if (w->w16_off[(size_t)l * 7 + m + 1] !=
+                        w->w16_off[(size_t)l * 7 + m] + (size_t)mats[m]->rows * mats[m]->cols * 2)
+                        return false;
+                return true;
+            };
+            bool stacked = false;
+            if (w16 && (c->pf_stack & 1) && adjacent(0, 2) &&
+                (st = pf_gemm_stacked(c, s->pf_xh, ldh, r16(0), qd + 2 * kvd, H, s->pf_qkv, ldq, Mg, stacked)))
+                return st;
+            if (!stacked) {
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, Mg, false, r16(0)))) return st;
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, Mg, false, r16(1)))) return st;
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, Mg, false, r16(2)))) return st;
+            }
             if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
             if ((st = c->launch(attn_name, dim3(cfg.n_kv_heads, (M + attn_qt - 1) / attn_qt), dim3(256), 0, a))) return st;
             if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, Mg, true, r16(3)))) return st;
             a.gamma = (const float *)L.ffn_norm.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, Mg, false, r16(4)))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, Mg, false, r16(5)))) return st;
+            stacked = false;
+            if (w16 && (c->pf_stack & 2) && adjacent(4, 5) &&
+                (st = pf_gemm_stacked(c, s->pf_xh, ldh, r16(4), 2 * F, H, s->pf_gu, 2 * F, Mg, stacked)))
+                return st;
+            if (!stacked) {
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, Mg, false, r16(4)))) return st;
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, Mg, false, r16(5)))) return st;
+            }
             if ((st = c->launch("pf_silu_k", dim3((F + 255) / 256, M), dim3(256), 0, a))) return st;
             if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, Mg, true, r16(6)))) return st;
         }

@@ -244,7 +244,9 @@ def test_prefill_resident_f16_matrices(ctx):
     later prefills multiply those copies.  The copies hold the same f16
     values the per-pass dequantization writes, so prefills with the copies
     (the one that builds them, then one that reuses them) and without them
-    (option 0) leave the same KV cache rows, logits and tokens bit for bit.
+    (option 0) leave the same KV cache rows, logits and tokens bit for bit
+    with unstacked products (option pf_stack 0), and within hipBLASLt's
+    summation-order tolerance with stacked ones.
     Replacing a matrix (ifr_llama2_weights_set) makes the copies stale: the
     next prefill dequantizes again and still matches the per-pass path."""
     import inferi_amd as I
@@ -254,8 +256,9 @@ def test_prefill_resident_f16_matrices(ctx):
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=47, std=0.05)
     prompt = np.random.default_rng(9).integers(0, cfg.vocab, 300).astype(np.uint32)
 
-    def run(keep):
+    def run(keep, stack=0):
         ctx.set_option("pf_keep_f16", keep)
+        ctx.set_option("pf_stack", stack)
         s = I.Llama2State(ctx, cfg)
         try:
             s.reset(prompt, 0)
@@ -277,6 +280,18 @@ def test_prefill_resident_f16_matrices(ctx):
         build, reuse, per_pass = run(1), run(1), run(0)
         same(build, per_pass, "copies built in this prefill vs per-pass dequantization")
         same(reuse, per_pass, "resident copies vs per-pass dequantization")
+        # stacked products (option pf_stack: Q, K, V as one; gate, up as one)
+        # over the same f16 copies: hipBLASLt may choose another kernel for
+        # the stacked shape, so within its summation-order tolerance
+        for stack in (1, 2, 3):
+            got = run(1, stack)
+            lg, ref = got[0].view(np.float32).astype(np.float64), per_pass[0].view(np.float32)
+            e = np.abs(lg - ref) / np.maximum(np.abs(ref), 1.0)
+            assert e.max() <= 1e-3, f"logits, pf_stack {stack}: {e.max():.3e}"
+            for a, b in zip(got[2], per_pass[2]):
+                fa, fb = O.decode_f16(a).astype(np.float64), O.decode_f16(b).astype(np.float64)
+                nw = float(np.abs(fa - fb).max() / np.abs(fb).max())
+                assert nw <= 2e-3, f"KV cache, pf_stack {stack}: normwise {nw:.3e}"
         # a new ffn_down for layer 0 (another draw, quantized on the device):
         # layer 1's KV rows depend on it
         rows, cols = cfg.hidden, cfg.ffn
@@ -293,6 +308,7 @@ def test_prefill_resident_f16_matrices(ctx):
         assert not np.array_equal(after[2][2], per_pass[2][2]), "layer 1's K rows ignore the new matrix"
     finally:
         ctx.set_option("pf_keep_f16", 1)
+        ctx.set_option("pf_stack", 1)
         w.close()
 
 
