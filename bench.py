@@ -8,9 +8,9 @@ weights resident in HBM and the 4096-token prompt already in the KV cache:
 its first 4095 tokens go through ifr_llama2_prefill (MFMA GEMMs and causal
 attention, in passes of up to 4096 tokens), which is timed on its own and
 reported as config.prefill, the last through the first decode step.  The
-timed prefill runs with the layer matrices resident in f16 (built by a
-warm-up prefill); config.prefill.ms_dequant_per_pass times the same prompt
-with every matrix dequantized inside each pass.
+prefill GEMMs dequantize the GGUF weight tiles inside the kernel (no f16
+copy of the weights); config.prefill.ms_tile128 times the same prompt with
+every product forced onto the 128 x 128-tile kernel.
 
 Prints one JSON line.  Besides the decode rate it carries each decode
 stage's time and HBM rate (config.stages), the exact-GEMV-path decode rate,
@@ -243,19 +243,19 @@ def run_decode(args) -> None:
         pf = {"tokens": n_pf, "ms": round(pf_ms, 3), "tok_s": round(n_pf / pf_ms * 1000.0, 1),
               "tflops": round(flops / (pf_ms * 1e-3) / 1e12, 2), "flops": int(flops),
               "mfma_frac": round(flops / (pf_ms * 1e-3) / MFMA_F16_PEAK, 4),
-              "f16_matrices": "resident (option pf_keep_f16, built by the warm-up prefill)"}
+              "weights": "GGUF blocks dequantized to f16 inside the GEMM tiles (no f16 copy)"}
         log(f"bench: prefill {n_pf} tokens in {pf_ms:.2f} ms ({pf['tok_s']:.0f} tok/s, {pf['tflops']:.1f} TFLOP/s, "
             f"{pf['mfma_frac'] * 100:.1f}% of the f16 dense peak)")
-        # the same prompt with each matrix dequantized to f16 inside every pass
-        ctx.set_option("pf_keep_f16", 0)
+        # the same prompt on 128 x 128 GEMM tiles (the same results bit for bit)
+        ctx.set_option("pf_tile", 128)
         s.reset(prompt, 0)
         ctx.sync()
         ctx.event_record(4)
         I.Llama2.prefill(ctx, s, w, n_pf)
         ctx.event_record(5)
-        pf["ms_dequant_per_pass"] = round(ctx.event_elapsed(4, 5), 3)
-        ctx.set_option("pf_keep_f16", 1)
-        log(f"bench: prefill with the dequantization in every pass {pf['ms_dequant_per_pass']:.2f} ms")
+        pf["ms_tile128"] = round(ctx.event_elapsed(4, 5), 3)
+        ctx.set_option("pf_tile", 0)
+        log(f"bench: prefill on 128 x 128 GEMM tiles {pf['ms_tile128']:.2f} ms")
     I.Llama2.generate(ctx, s, w, args.warmup, use_graph=not args.no_graph)
     ctx.sync()
     pos0 = int(s.read("pos", np.uint32)[0])

@@ -101,26 +101,11 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * rows per wave in the Q4_K one-item plain and QKV forms).  Default 225.
  * "pf_chunk"
  * sets the prompt tokens per ifr_llama2_prefill pass (a multiple of 64, at
- * most 16384; 0 = 4096), read at a state's first prefill.  "pf_blas" = 1
- * (the default) multiplies prefill passes of 256 or more tokens (and
- * ifr_gemm_quant calls of m >= 256) on hipBLASLt after dequantizing each
- * matrix once to f16; 0 keeps them on the fused kernel, whose results do not
- * depend on the pass length (hipBLASLt's summation order depends on the
- * number of rows).  "pf_keep_f16" = 1 (the default) keeps those f16
- * matrices on the device with the weights object after the first prefill
- * that reaches hipBLASLt (every layer matrix: 2 bytes per weight, 14 GB at
- * the 8B shape), so later prefills skip the dequantization; the copies are
- * rebuilt after an ifr_llama2_weights_set call, freed by
- * ifr_llama2_weights_destroy or by the next prefill once the option is 0,
- * and skipped (per-pass dequantization) when they cannot be allocated or
- * when the prefill runs on another context than the weights'.  "pf_stack"
- * (bit 0, the default: Q, K and V; bit 1: gate and up) multiplies those
- * resident matrices as one stacked product per group (one hipBLASLt call
- * over the adjacent f16 copies; -0.6 ms per 8B 4095-token prefill for Q, K
- * and V, none measured for gate and up).  With pf_stack 0 the resident
- * copies give the same results as per-pass dequantization bit for bit; a
- * stacked product may run another hipBLASLt kernel, whose summation order
- * can differ in the last bits (at the 8B shape the results were identical). */
+ * most 16384; 0 = 4096), read at a state's first prefill.  "pf_tile"
+ * selects the prefill GEMM's tiles: 0 (the default) 256 x 256 tiles where a
+ * product has at least 128 of them, else 128 x 128 tiles; 128 or 256 forces
+ * one form.  Both forms sum each output element's products in the same
+ * order, so the results do not depend on the tile or the pass length. */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 
 /* ----------------------------------------------------------------- memory */
@@ -264,10 +249,10 @@ IFR_API ifr_status ifr_sample(ifr_ctx *ctx, const float *logits, float *probs, u
  * (Q4_0 .. Q8_K) or F16/F32 as a GGUF file stores them (16-byte aligned for
  * Q4_K, Q5_K, F16 and F32, 4 otherwise; cols a multiple of 64 and of the
  * block size), y f32 row-major with leading dimension `rows`.  The weights
- * are dequantized with the reference's arithmetic to f16 and multiplied on
- * the matrix cores with f32 accumulation: for m >= 256 (option pf_blas) the
- * whole matrix once into a context scratch, then hipBLASLt; otherwise tile
- * by tile inside one kernel.  accumulate != 0 adds to y. */
+ * are dequantized tile by tile with the reference's arithmetic to f16 inside
+ * the kernel (nothing is allocated) and multiplied on the matrix cores with
+ * f32 accumulation (option pf_tile picks the tile size).  accumulate != 0
+ * adds to y. */
 IFR_API ifr_status ifr_gemm_quant(ifr_ctx *ctx, float *y, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
                                   const void *x_f16, uint32_t m, int32_t accumulate);
 
@@ -313,11 +298,9 @@ IFR_API ifr_status ifr_llama2_weights_create(ifr_ctx *ctx, const ifr_llama2_conf
  * rows/cols follow gguf.rs:591-593 (dims reversed: rows = ne1, cols = ne0);
  * norms and biases are F32 vectors with rows = 1.  A layer with biases adds
  * them to q, k and v before RoPE (transformer.rs:434-442).  Every call
- * starts a new generation of the table: captured decode graphs and the
- * resident f16 prefill matrices (option "pf_keep_f16") made before it are
- * rebuilt.  A caller that rewrites a bound tensor's bytes in place (new
- * weights in the same buffer) binds it again with this call before the next
- * prefill; the decode kernels read the buffers directly and need no call. */
+ * starts a new generation of the table: captured decode graphs made before
+ * it are rebuilt.  The decode and prefill kernels read the bound buffers
+ * directly, so bytes rewritten in place are used by the next call. */
 IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *gguf_name, int32_t dtype,
                                           const void *dev_data, uint32_t rows, uint32_t cols);
 IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w);

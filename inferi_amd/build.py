@@ -65,7 +65,7 @@ def build_host(out: str = LIB) -> str:
     _run([cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-result",
           "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
           os.path.join(CSRC, "host.cpp"), os.path.join(CSRC, "gguf.cpp"), noalloc_o,
-          f"-L{ROCM}/lib", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", tmp])
     os.replace(tmp, out)
     return out
 
@@ -94,7 +94,7 @@ def build_host_asan(out: str = ASAN_LIB) -> str:
     _run([cxx, "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer", "-std=c++17", "-shared", "-fPIC",
           "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include",
           os.path.join(CSRC, "host.cpp"), os.path.join(CSRC, "gguf.cpp"), noalloc_o,
-          f"-L{ROCM}/lib", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib", "-o", out])
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", out])
     return out
 
 

@@ -1,0 +1,345 @@
+// Prefill GEMM on the matrix cores with the weights dequantized in the tile
+// staging: Y[m][n] = sum_k X[m][k] * deq(W)[n][k] for a pass of M prompt
+// tokens (X f16 [M][ldx], W rows of GGUF blocks, Y f32 [M][ldy]).
+//
+// The reference has no batched prompt path: it feeds the prompt through its
+// decode step one token at a time (crates/inferi-chat/src/chat_llama2.rs:
+// 137-160), i.e. every product is a GEMV over the same GGUF rows
+// (crates/inferi-shaders/src/gemv_quant_q4_k.rs:97-182).  Here a pass's
+// products are GEMMs: each 256 (n) x 64 (k) weight tile is read as GGUF
+// blocks, dequantized with the reference's f32 arithmetic
+// (crates/inferi/src/quantization.rs:47-392), rounded to f16 and staged in
+// LDS, where the 256 token rows of the workgroup's X tile share it.
+//
+// Workgroup: 4 waves (one per SIMD), a 256 (m) x 256 (n) tile of Y.  Wave w
+// owns the 128 x 128 sub-tile m in [128 (w & 1), +128), n in [128 (w >> 1),
+// +128): 4 x 4 blocks of v_mfma_f32_32x32x16_f16 (256 f32 accumulators per
+// lane), so each operand fragment read from LDS feeds four products.  K runs
+// in steps of 64 through two LDS buffers: while the matrix cores work on
+// step s, the global loads of step s + 1 are in flight; their tiles are then
+// dequantized into the other buffer, so one barrier per step suffices.
+//
+// Rows of the virtual n range come from up to three matrices of one GGUF
+// type stacked one after another (n < n1: w0, n < n2: w1, else w2), so Q, K
+// and V run as one product writing adjacent columns.  In the SwiGLU form
+// (EPI 2) the tile's n rows alternate in runs of 32 between the gate (w0)
+// and up (w1) rows of the same 32 FFN indices, so each lane holds gate and up
+// of the same (m, j) and the epilogue writes h[m][j] = f16(u * silu(g))
+// straight into the down product's input (the reference's silu, silu.rs:
+// 24-53, on the two products).
+#pragma once
+#include "pf_tiles.h"
+
+namespace ifr {
+
+constexpr int PG_BM = 256, PG_BN = 256, PG_BK = 64;
+constexpr int PG_THREADS = 256;
+
+// epilogues
+constexpr int PG_STORE = 0;  // Y = X W^T
+constexpr int PG_ADD = 1;    // Y += X W^T (the residual stream)
+constexpr int PG_SWIGLU = 2; // h = f16(up * silu(gate)), gate/up interleaved by 32 rows
+
+// LDS tiles: 256 rows of 64 halves (128 B) without padding; the 16-byte
+// chunk c of row r sits at chunk c ^ ((r / 2) % 8), so the sixteen
+// consecutive rows whose 16-byte chunks one LDS pass serves (64 banks of 4
+// bytes, two rows per bank line) fall on distinct banks, for the operand
+// reads (rows of one chunk) and the dequantized row stores alike.
+IFR_DEV uint32_t pg_swz_of(uint32_t r) { return (r >> 1) & 7u; }
+IFR_DEV uint32_t pg_swz(uint32_t r, uint32_t c) { return r * PG_BK + 8 * (c ^ pg_swz_of(r)); }
+
+typedef __attribute__((address_space(3))) char lds_char_t;
+
+// LDS byte address of a pointer into a __shared__ array.
+IFR_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const lds_char_t *)p; }
+
+// 16 bytes per lane from global memory straight into LDS: lane i writes
+// LDS bytes [lds + 16 i, +16) (global_load_lds_dwordx4, LDS base in M0).
+// Issued as assembly so the compiler's wait-count tracking leaves these
+// loads to the kernel's own waits; the caller waits with vmcnt before the
+// LDS is read.
+// The address is a wave-uniform base plus this lane's 32-bit byte offset.
+IFR_DEV void lds_dma16(const void *base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds));
+}
+
+// 16-byte global load issued as assembly (not counted by the compiler's
+// wait tracking): the caller waits with pg_wait before reading r.
+IFR_DEV void ld16_asm(u32x4_a16 &r, const uint8_t *p) { asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p)); }
+
+// Weight staging of one thread: the 64 elements of one tile row in a K
+// step, stored as eight swizzled 16-byte chunks.  Generic: two PfTile
+// loads, elements [0, 32) and [32, 64).
+template <int FMT>
+struct PgStage {
+    static constexpr bool MANUAL = false; // compiler-tracked loads
+    PfTile<FMT> t0, t1;
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0) {
+        t0.load(wrow, k0, 0);
+        t1.load(wrow, k0, 1);
+    }
+    template <int N>
+    IFR_DEV void wait() {}
+    IFR_DEV void store(uint32_t k0, _Float16 *tile, uint32_t r) const {
+        _Float16 h[64];
+        t0.deq(k0, 0, h);
+        t1.deq(k0, 1, h + 32);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            uint4 u;
+            __builtin_memcpy(&u, &h[8 * c], 16);
+            *(uint4 *)(tile + pg_swz(r, (uint32_t)c)) = u;
+        }
+    }
+};
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+// f16 pair of two f32 values, each rounded to nearest from its f32 value
+// (v_cvt_pk_f16_f32 written out, so the compiler cannot fuse the producing
+// FMA into one rounding straight to f16, v_fma_mix)
+IFR_DEV uint32_t pack_f16x2(float a, float b) {
+    uint32_t u;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
+    return u;
+}
+
+// Q4_K (quantization.rs:358-392): the step's 64 elements are group g =
+// (k0 % 256) / 64 of the block, qs bytes [32 g, +32): low nibbles are
+// elements 0..31 (sub-block 2g), high nibbles 32..63 (sub-block 2g + 1).
+// y = d1 * q - m1 with d1 = d * sc and m1 = dmin * m: d1 * q is exact in f32
+// (at most 11 + 6 + 4 significant bits), so the fused multiply-add rounds
+// once, exactly as the reference's multiply then subtract does.
+template <>
+struct PgStage<Q4_K> {
+    static constexpr bool MANUAL = true; // loads issued as assembly, waited for with wait<N>
+    u32x4_a16 hv, q0, q1;
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0) {
+        const uint8_t *b = wrow + (size_t)(k0 / 256) * 144;
+        ld16_asm(hv, b);
+        ld16_asm(q0, b + 16 + 32 * ((k0 % 256) / 64));
+        ld16_asm(q1, b + 32 + 32 * ((k0 % 256) / 64));
+    }
+    // until at most N vector-memory loads issued after these are outstanding
+    template <int N>
+    IFR_DEV void wait() {
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(hv), "+v"(q0), "+v"(q1) : "n"(N));
+    }
+    IFR_DEV void store(uint32_t k0, _Float16 *tile, uint32_t r) const {
+#pragma clang fp contract(off)
+        uint32_t sc0, m0s, sc1, m1s;
+        scale_min_pair((k0 % 256) / 64, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
+        const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
+        const float d1 = d * (float)sc0, n1 = -(dm * (float)m0s), d2 = d * (float)sc1, n2 = -(dm * (float)m1s);
+        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        uint32_t lo[16], hi[16];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t l = q[i] & 0x0F0F0F0Fu, h = (q[i] >> 4) & 0x0F0F0F0Fu;
+            lo[2 * i] = pack_f16x2(fmaf(d1, ub<0>(l), n1), fmaf(d1, ub<1>(l), n1));
+            lo[2 * i + 1] = pack_f16x2(fmaf(d1, ub<2>(l), n1), fmaf(d1, ub<3>(l), n1));
+            hi[2 * i] = pack_f16x2(fmaf(d2, ub<0>(h), n2), fmaf(d2, ub<1>(h), n2));
+            hi[2 * i + 1] = pack_f16x2(fmaf(d2, ub<2>(h), n2), fmaf(d2, ub<3>(h), n2));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            *(uint4 *)(tile + pg_swz(r, (uint32_t)c)) = make_uint4(lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]);
+            *(uint4 *)(tile + pg_swz(r, (uint32_t)(4 + c))) =
+                make_uint4(hi[4 * c], hi[4 * c + 1], hi[4 * c + 2], hi[4 * c + 3]);
+        }
+    }
+};
+
+// The step's end: this wave's LDS stores are done, its direct X loads have
+// landed (the weight loads issued after them may still be in flight), then
+// the workgroup barrier.
+template <int NW>
+IFR_DEV void pg_step_barrier() {
+    if constexpr (NW == 3)
+        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The order of a step's instructions: each of the 64 products followed by
+// 4 VALU instructions (the dequantization of the next step's weights), so
+// the vector ALU works while the matrix core runs instead of before it
+// (measured 2.5x faster than the compiler's own order, which put every
+// dequantization instruction before the first product).
+IFR_DEV void pg_interleave() {
+#pragma unroll
+    for (int m = 0; m < 64; m++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); // VALU
+    }
+}
+
+// One workgroup's state over the K loop.
+template <int FMT>
+struct PgCtx {
+    _Float16 *xs[2], *ws[2];     // LDS tiles [PG_BM * PG_BK], [PG_BN * PG_BK], two buffers each
+    const _Float16 *x;           // X (wave-uniform)
+    uint32_t xoff[8];            // byte offsets of this lane's X rows of the direct loads, at its chunk
+    const uint8_t *wrow;         // this thread's weight row
+    uint32_t r, nk, lane, wave, wm, wn;
+    PgStage<FMT> st0, st1;       // weights of the next two steps
+    float16v acc[4][4];
+
+    // X of step k into LDS buffer B: eight 1 KB direct loads per wave (lane
+    // l of load j fills row 64 w + 8 j + l / 8 at physical chunk l % 8)
+    template <int B>
+    IFR_DEV void load_x(uint32_t k) {
+        const uint32_t dst = lds_addr(xs[B] + (64 * wave) * PG_BK);
+#pragma unroll
+        for (int j = 0; j < 8; j++) lds_dma16(x + k * PG_BK, xoff[j], __builtin_amdgcn_readfirstlane(dst + 1024 * j));
+    }
+    // the products of one K step from LDS buffer B
+    template <int B>
+    IFR_DEV void mfma_step() {
+        const _Float16 *xb = xs[B], *wb = ws[B];
+        const uint32_t li = lane & 31u, hi = lane >> 5;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            half8v av[4], bv[4];
+            const uint32_t c = 2 * (uint32_t)kk + hi;
+#pragma unroll
+            for (int i = 0; i < 4; i++) av[i] = *(const half8v *)(xb + pg_swz(wm + 32 * i + li, c));
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = *(const half8v *)(wb + pg_swz(wn + 32 * j + li, c));
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    // step s on buffer B: X of step s + 1 and the weights of step s + 2 are
+    // requested, the products of step s run while the weights of step s + 1
+    // (register set B ^ 1) are dequantized into the other buffer.  Steps past
+    // the end load step nk - 1 again into buffers nobody reads.  Loads in
+    // flight at the wait: the 3 weight loads of step s + 1, then 8 X loads
+    // and 3 weight loads of this step.
+    template <int B>
+    IFR_DEV void step(uint32_t s) {
+        PgStage<FMT> &ld = B ? st1 : st0, &dq = B ? st0 : st1;
+        load_x<B ^ 1>(min(s + 1, nk - 1));
+        ld.load(wrow, min(s + 2, nk - 1) * PG_BK);
+        dq.template wait<11>();
+        dq.store(min(s + 1, nk - 1) * PG_BK, ws[B ^ 1], r);
+        mfma_step<B>();
+        pg_interleave();
+        pg_step_barrier<PgStage<FMT>::MANUAL ? 3 : 0>();
+    }
+};
+
+template <int FMT, int EPI>
+__device__ void pf_gemm_body(const PfGemmArgs &a) {
+    // four LDS objects, so the compiler sees that the direct loads into one
+    // buffer do not alias the operand reads of the other
+    __shared__ __attribute__((aligned(1024))) _Float16 xs0[PG_BM * PG_BK], xs1[PG_BM * PG_BK];
+    __shared__ __attribute__((aligned(1024))) _Float16 ws0[PG_BN * PG_BK], ws1[PG_BN * PG_BK];
+    PgCtx<FMT> g;
+    const uint32_t tid = threadIdx.x;
+    g.xs[0] = xs0;
+    g.xs[1] = xs1;
+    g.ws[0] = ws0;
+    g.ws[1] = ws1;
+    g.lane = tid & 63u;
+    g.wave = tid >> 6;
+    g.r = tid;
+    g.wm = 128 * (g.wave & 1u);
+    g.wn = 128 * (g.wave >> 1);
+    g.nk = a.K / PG_BK;
+    g.x = (const _Float16 *)a.x;
+
+    // tiles in n-fastest order: consecutive workgroups share an X tile.
+    // Workgroup b runs on XCD b % 8; tile t = (b % 8) * per + b / 8 gives
+    // each XCD a contiguous run of tiles (per = tiles / 8 when it divides).
+    const uint32_t tn = a.tiles_n, tiles = tn * a.tiles_m;
+    const uint32_t b = blockIdx.x;
+    const uint32_t t = (tiles & 7u) == 0 ? (b & 7u) * (tiles >> 3) + (b >> 3) : b;
+    const uint32_t m0 = (t / tn) * PG_BM, n0 = (t % tn) * PG_BN;
+
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t row = 64 * g.wave + 8 * (uint32_t)j + (g.lane >> 3);
+        const uint32_t c = (g.lane & 7u) ^ pg_swz_of(row);
+        g.xoff[j] = 2 * (min(m0 + row, a.M - 1) * a.ldx + 8 * c);
+    }
+    const uint32_t r = tid;
+    if constexpr (EPI == PG_SWIGLU) {
+        // wave column c = r / 128 holds FFN rows j in [n0 / 2 + 64 c, +64):
+        // tile rows 128 c + 32 b + i are gate (b even) or up (b odd) row
+        // j = n0 / 2 + 64 c + 32 (b / 2) + i
+        const uint32_t bk = (r >> 5) & 3u;
+        const uint32_t j = min(n0 / 2 + 64 * (r >> 7) + 32 * (bk >> 1) + (r & 31u), a.n1 - 1);
+        g.wrow = (bk & 1u ? a.w1 : a.w0) + (size_t)j * a.row_bytes;
+    } else {
+        const uint32_t n = min(n0 + r, a.N - 1);
+        const uint8_t *base = n < a.n1 ? a.w0 : n < a.n2 ? a.w1 : a.w2;
+        const uint32_t nr = n < a.n1 ? n : n < a.n2 ? n - a.n1 : n - a.n2;
+        g.wrow = base + (size_t)nr * a.row_bytes;
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) g.acc[i][j][e] = 0.0f;
+
+    // prologue: X and weights of step 0 into buffer 0, weights of step 1 in
+    // flight
+    g.template load_x<0>(0);
+    g.st0.load(g.wrow, 0);
+    g.st1.load(g.wrow, min(1u, g.nk - 1) * PG_BK);
+    g.st0.template wait<3>();
+    g.st0.store(0, ws0, r);
+    pg_step_barrier<PgStage<FMT>::MANUAL ? 3 : 0>();
+    for (uint32_t s = 0; s < g.nk; s += 2) {
+        g.template step<0>(s);
+        if (s + 1 < g.nk) g.template step<1>(s + 1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the clamped loads past the end
+
+    // D[row][col] of block (i, j): col = lane % 32 (n), row = 8 (e / 4) +
+    // 4 (lane / 32) + e % 4 (m)
+    const uint32_t lane = g.lane, li = lane & 31u, wm = g.wm, wn = g.wn;
+    if constexpr (EPI == PG_SWIGLU) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint32_t jn = n0 / 2 + wn / 2 + 32 * q + li;
+            if (jn >= a.n1) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                    if (m < a.M) {
+                        const float gg = g.acc[i][2 * q][e], u = g.acc[i][2 * q + 1][e];
+                        ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = (_Float16)(u * (gg / (1.0f + expf(-gg))));
+                    }
+                }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t n = n0 + wn + 32 * j + li;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                    if (m < a.M) {
+                        float *yp = (float *)a.y + (size_t)m * a.ldy + n;
+                        if constexpr (EPI == PG_ADD)
+                            *yp += g.acc[i][j][e];
+                        else
+                            *yp = g.acc[i][j][e];
+                    }
+                }
+        }
+    }
+}
+
+} // namespace ifr

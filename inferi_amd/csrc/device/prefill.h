@@ -11,236 +11,24 @@
 // which produces the logits and the next token.
 #pragma once
 #include "attention.h"
+#include "pf_gemm.h"
+#include "pf_tiles.h"
 
 namespace ifr {
 
 
 // ------------------------------------------------------------------ GEMM --
-// Y[m][n] = sum_k X[m][k] * deq(W)[n][k]   (EPI 0: Y =, EPI 1: Y +=)
-// X: f16, row m at x + m * ldx; W: rows of K/QK GGUF blocks; Y: f32, row m
-// at y + m * ldy.  Tile 128 (m) x 128 (n), K steps of 64; four waves, each a
+// The small-tile form of the prefill GEMM (device/pf_gemm.h has the
+// 256 x 256 form and the argument conventions): Y[m][n] = sum_k X[m][k] *
+// deq(W)[n][k] with the same epilogues (EPI: PG_STORE, PG_ADD, PG_SWIGLU)
+// and stacked matrices, for products with too few 256 x 256 tiles to fill
+// the chip.  Tile 128 (m) x 128 (n), K steps of 64; four waves, each a
 // 64 x 64 quadrant as 2 x 2 MFMA 32x32x16 tiles.  The next K step's global
-// loads are issued before the current step's MFMAs.
+// loads are issued before the current step's MFMAs.  Each output element
+// sums its k in the same order as the large form (steps of 64, products of
+// 16), so both forms give the same results bit for bit.
 constexpr int PF_BM = 128, PF_BN = 128, PF_BK = 64;
 constexpr int PF_LDS = PF_BK + 8; // halves per LDS row: 144 B, so the 32 rows an MFMA operand read touches spread over the banks
-
-// Weight tiles by format: row r's elements [k0 + 32*hs, +32) (k0 a multiple
-// of 64, hs 0 or 1), loaded as raw bytes (load) and dequantized with the
-// reference's f32 arithmetic, contraction off, then rounded to f16 (deq).
-// Runtime offsets select among loaded registers; nothing is indexed by a
-// runtime value, so the staging stays in registers.
-IFR_DEV uint32_t pick4(const uint4 &v, uint32_t i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-// byte l (0..31) of two 16-byte registers, l known at compile time after unrolling
-IFR_DEV uint32_t byte32(const uint4 &a, const uint4 &b, int l) {
-    const uint32_t w = l < 16 ? pick4(a, (uint32_t)(l >> 2)) : pick4(b, (uint32_t)((l - 16) >> 2));
-    return (w >> (8 * (l & 3))) & 0xFFu;
-}
-
-template <int FMT>
-struct PfTile;
-
-// Q4_K (quantization.rs:358-392): sub-block 2g + hs of block k0/256.
-template <>
-struct PfTile<Q4_K> {
-    static constexpr int QK = 256, BB = 144;
-    uint4 hv, q0, q1;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t) {
-        const uint32_t kb = k0 / 256, g = (k0 % 256) / 64;
-        const uint8_t *b = wrow + (size_t)kb * 144;
-        hv = ld16(b);
-        q0 = ld16(b + 16 + 32 * g);
-        q1 = ld16(b + 32 + 32 * g);
-    }
-    IFR_DEV void deq(uint32_t k0, uint32_t hs, _Float16 *h) const {
-#pragma clang fp contract(off)
-        const uint32_t g = (k0 % 256) / 64;
-        uint32_t sc0, m0s, sc1, m1s;
-        scale_min_pair(g, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
-        const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
-        const float d1 = d * (float)(hs ? sc1 : sc0), mm = dm * (float)(hs ? m1s : m0s);
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const uint32_t b = byte32(q0, q1, l);
-            const float q = (float)(hs ? (b >> 4) : (b & 15u));
-            h[l] = (_Float16)(d1 * q - mm);
-        }
-    }
-};
-
-// Q5_K (quantization.rs:287-330): as Q4_K plus qh[l] bit 2g + hs.
-template <>
-struct PfTile<Q5_K> {
-    static constexpr int QK = 256, BB = 176;
-    uint4 hv, e0, e1, q0, q1;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t) {
-        const uint32_t kb = k0 / 256, g = (k0 % 256) / 64;
-        const uint8_t *b = wrow + (size_t)kb * 176;
-        hv = ld16(b);
-        e0 = ld16(b + 16);
-        e1 = ld16(b + 32);
-        q0 = ld16(b + 48 + 32 * g);
-        q1 = ld16(b + 64 + 32 * g);
-    }
-    IFR_DEV void deq(uint32_t k0, uint32_t hs, _Float16 *h) const {
-#pragma clang fp contract(off)
-        const uint32_t g = (k0 % 256) / 64, sh = 2 * g + hs;
-        uint32_t sc0, m0s, sc1, m1s;
-        scale_min_pair(g, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
-        const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
-        const float d1 = d * (float)(hs ? sc1 : sc0), mm = dm * (float)(hs ? m1s : m0s);
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const uint32_t b = byte32(q0, q1, l);
-            const uint32_t q = (hs ? (b >> 4) : (b & 15u)) + (((byte32(e0, e1, l) >> sh) & 1u) ? 16u : 0u);
-            h[l] = (_Float16)(d1 * (float)q - mm);
-        }
-    }
-};
-
-// Q6_K (quantization.rs:224-257): run j = 2*((k0%256)/64) + hs of 32
-// elements 128i + 32k + l (i = j/4, k = j%4): ql[64i + 32(k&1) + l] (low
-// nibble for k < 2), qh[32i + l] bits 2k..2k+1, scale[8i + 2k + l/16].
-template <>
-struct PfTile<Q6_K> {
-    static constexpr int QK = 256, BB = 210;
-    uint4 l0, l1, h0, h1;
-    uint32_t sc, dd;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
-        const uint32_t kb = k0 / 256, j = 2 * ((k0 % 256) / 64) + hs, i = j >> 2, k = j & 3u;
-        const uint8_t *b = wrow + (size_t)kb * 210;
-        l0 = ld16_a2(b + 64 * i + 32 * (k & 1u));
-        l1 = ld16_a2(b + 64 * i + 32 * (k & 1u) + 16);
-        h0 = ld16_a2(b + 128 + 32 * i);
-        h1 = ld16_a2(b + 144 + 32 * i);
-        sc = ld_u16(b + 192 + 8 * i + 2 * k);
-        dd = ld_u16(b + 208);
-    }
-    IFR_DEV void deq(uint32_t k0, uint32_t hs, _Float16 *h) const {
-#pragma clang fp contract(off)
-        const uint32_t k = (2 * ((k0 % 256) / 64) + hs) & 3u;
-        const float d = f16_to_f32(dd);
-        const float s_lo = (float)(int)(int8_t)(sc & 0xFFu), s_hi = (float)(int)(int8_t)(sc >> 8);
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const uint32_t qlb = byte32(l0, l1, l);
-            const uint32_t nib = k < 2 ? (qlb & 15u) : (qlb >> 4);
-            const uint32_t hb = (byte32(h0, h1, l) >> (2 * k)) & 3u;
-            const int q = (int)(nib | (hb << 4)) - 32;
-            h[l] = (_Float16)(d * (l < 16 ? s_lo : s_hi) * (float)q);
-        }
-    }
-};
-
-// Q8_K (quantization.rs:204-212): d:f32, qs[(k0%256) + 32hs, +32).
-template <>
-struct PfTile<Q8_K> {
-    static constexpr int QK = 256, BB = 292;
-    uint4 q0, q1;
-    uint32_t db;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
-        const uint8_t *b = wrow + (size_t)(k0 / 256) * 292;
-        db = *(const uint32_t *)b;
-        q0 = ld16_a4(b + 4 + (k0 % 256) + 32 * hs);
-        q1 = ld16_a4(b + 20 + (k0 % 256) + 32 * hs);
-    }
-    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
-#pragma clang fp contract(off)
-        const float d = __uint_as_float(db);
-#pragma unroll
-        for (int l = 0; l < 32; l++) h[l] = (_Float16)(d * (float)(int)(int8_t)byte32(q0, q1, l));
-    }
-};
-
-// Unquantized rows (GpuQuantTensor::F32, and F16 which the reference
-// converts to F32 at load, gguf.rs:113-128): elements k0 + 32hs .. +32 taken
-// as they are (F16) or rounded to f16 (F32) for the matrix cores.
-template <>
-struct PfTile<F16> {
-    static constexpr int QK = 1, BB = 2;
-    uint4 v[4];
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
-        const uint8_t *b = wrow + 2 * (size_t)(k0 + 32 * hs);
-#pragma unroll
-        for (int k = 0; k < 4; k++) v[k] = ld16(b + 16 * k);
-    }
-    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const uint32_t w = pick4(v[l >> 3], (uint32_t)((l >> 1) & 3));
-            const uint16_t b = (uint16_t)((l & 1) ? (w >> 16) : (w & 0xFFFFu));
-            __builtin_memcpy(&h[l], &b, 2);
-        }
-    }
-};
-template <>
-struct PfTile<F32> {
-    static constexpr int QK = 1, BB = 4;
-    uint4 v[8];
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
-        const uint8_t *b = wrow + 4 * (size_t)(k0 + 32 * hs);
-#pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = ld16(b + 16 * k);
-    }
-    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
-#pragma unroll
-        for (int l = 0; l < 32; l++) h[l] = (_Float16)__uint_as_float(pick4(v[l >> 2], (uint32_t)(l & 3)));
-    }
-};
-
-// The 32-element formats: the run is exactly block (k0 + 32hs)/32.
-// Q8_0 (quantization.rs:47-55): d@0 qs:i8[32]@2, y = q * d.
-template <>
-struct PfTile<Q8_0> {
-    static constexpr int QK = 32, BB = 34;
-    uint4 q0, q1;
-    uint32_t dd;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
-        const uint8_t *b = wrow + (size_t)((k0 + 32 * hs) / 32) * 34;
-        dd = ld_u16(b);
-        q0 = ld16_a2(b + 2);
-        q1 = ld16_a2(b + 18);
-    }
-    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
-#pragma clang fp contract(off)
-        const float d = f16_to_f32(dd);
-#pragma unroll
-        for (int l = 0; l < 32; l++) h[l] = (_Float16)((float)(int)(int8_t)byte32(q0, q1, l) * d);
-    }
-};
-
-// Q4_0/Q4_1/Q5_0/Q5_1 (quantization.rs:66-177) through Blk32 (device/gemv.h):
-// element l < 16 is the low nibble of qs byte l, element l >= 16 the high
-// nibble of byte l - 16; the fifth bit is bit l of qh.
-template <int FMT>
-struct PfTile32 {
-    static constexpr int QK = 32, BB = QFmt<FMT>::BB;
-    Blk32<FMT> blk;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t hs) {
-        blk.load(wrow + (size_t)((k0 + 32 * hs) / 32) * BB);
-    }
-    IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
-#pragma clang fp contract(off)
-        const float d = blk.d(), m = Blk32<FMT>::AFF ? blk.m() : 0.0f;
-#pragma unroll
-        for (int l = 0; l < 32; l++) {
-            const uint32_t b = byte32(blk.qs, blk.qs, l & 15);
-            uint32_t q = l < 16 ? (b & 15u) : (b >> 4);
-            if constexpr (Blk32<FMT>::FIVE) q |= ((blk.qh >> l) & 1u) << 4;
-            float y;
-            if constexpr (Blk32<FMT>::AFF) y = (float)q * d + m;
-            else y = (float)((int)q - (int)Blk32<FMT>::H) * d;
-            h[l] = (_Float16)y;
-        }
-    }
-};
-template <>
-struct PfTile<Q4_0> : PfTile32<Q4_0> {};
-template <>
-struct PfTile<Q4_1> : PfTile32<Q4_1> {};
-template <>
-struct PfTile<Q5_0> : PfTile32<Q5_0> {};
-template <>
-struct PfTile<Q5_1> : PfTile32<Q5_1> {};
 
 template <int FMT, int EPI>
 __device__ void gemm_f16_body(const PfGemmArgs &a) {
@@ -249,25 +37,35 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t m0 = blockIdx.y * PF_BM, n0 = blockIdx.x * PF_BN;
 
-    // global -> register staging: thread t owns tile row t/2, halves [32*(t%2), +32)
+    // global -> register staging: thread t owns tile row t/2, halves
+    // [32*(t%2), +32); rows past M or N repeat the last row (their outputs
+    // are not stored)
     const uint32_t r = (uint32_t)tid >> 1, hseg = (uint32_t)tid & 1u;
-    const bool xrow_ok = m0 + r < a.M, wrow_ok = n0 + r < a.N;
     const _Float16 *xrow = (const _Float16 *)a.x + (size_t)min(m0 + r, a.M - 1) * a.ldx;
-    const uint8_t *wrow = a.w + (size_t)min(n0 + r, a.N - 1) * a.row_bytes;
+    const uint8_t *wrow;
+    if constexpr (EPI == PG_SWIGLU) {
+        // wave column c = r / 64 holds FFN rows j in [n0 / 2 + 32 c, +32):
+        // tile rows 64 c + i are gate row j, 64 c + 32 + i up row j
+        const uint32_t j = min(n0 / 2 + 32 * (r >> 6) + (r & 31u), a.n1 - 1);
+        wrow = ((r >> 5) & 1u ? a.w1 : a.w0) + (size_t)j * a.row_bytes;
+    } else {
+        const uint32_t n = min(n0 + r, a.N - 1);
+        const uint8_t *base = n < a.n1 ? a.w0 : n < a.n2 ? a.w1 : a.w2;
+        const uint32_t nr = n < a.n1 ? n : n < a.n2 ? n - a.n1 : n - a.n2;
+        wrow = base + (size_t)nr * a.row_bytes;
+    }
     uint4 xv[4];
     PfTile<FMT> wt;
     auto gload = [&](uint32_t k0) {
         const uint4 *xp = (const uint4 *)(xrow + k0 + 32 * hseg);
 #pragma unroll
-        for (int i = 0; i < 4; i++) xv[i] = xrow_ok ? xp[i] : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < 4; i++) xv[i] = xp[i];
         wt.load(wrow, k0, hseg);
     };
-    // this thread's 32 weights into LDS as f16 (a row past N as zeros)
+    // this thread's 32 weights into LDS as f16
     auto lstore = [&](uint32_t k0) {
         _Float16 h[32];
         wt.deq(k0, hseg, h);
-#pragma unroll
-        for (int i = 0; i < 32; i++) h[i] = wrow_ok ? h[i] : (_Float16)0.0f;
         uint4 *wd = (uint4 *)&ws[r][32 * hseg];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -311,45 +109,37 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
         }
     }
     // D[row][col]: col = lane % 32, row = 8*(e/4) + 4*(lane/32) + e%4
+    if constexpr (EPI == PG_SWIGLU) {
+        const uint32_t jn = n0 / 2 + wn / 2 + li;
+        if (jn >= a.n1) return;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint32_t n = n0 + wn + 32 * j + li;
+        for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
-                if (m < a.M && n < a.N) {
-                    float *yp = a.y + (size_t)m * a.ldy + n;
-                    if constexpr (EPI == 1)
-                        *yp += acc[i][j][e];
-                    else
-                        *yp = acc[i][j][e];
+                if (m < a.M) {
+                    const float g = acc[i][0][e], u = acc[i][1][e];
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = (_Float16)(u * (g / (1.0f + expf(-g))));
                 }
             }
-        }
-}
-
-// W -> f16 [N][K] with the GEMM tiles' dequant arithmetic (so the f16
-// weights are the ones the fused GEMM multiplies): thread t takes row
-// t / (K/32), elements [k0 + 32 hs, +32) of it (k0 a multiple of 64).
-template <int FMT>
-__device__ void pf_deq_f16_body(const PfDeqArgs &a) {
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t segs = a.K / 32;
-    const uint32_t r = t / segs, sg = t % segs;
-    if (r >= a.N) return;
-    const uint32_t k0 = (sg >> 1) * 64, hs = sg & 1u;
-    PfTile<FMT> wt;
-    wt.load(a.w + (size_t)r * a.row_bytes, k0, hs);
-    _Float16 h[32];
-    wt.deq(k0, hs, h);
-    uint4 *dst = (uint4 *)(a.out + (size_t)r * a.K + k0 + 32 * hs);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        uint4 u;
-        __builtin_memcpy(&u, &h[8 * i], 16);
-        dst[i] = u;
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t n = n0 + wn + 32 * j + li;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+                    if (m < a.M && n < a.N) {
+                        float *yp = (float *)a.y + (size_t)m * a.ldy + n;
+                        if constexpr (EPI == PG_ADD)
+                            *yp += acc[i][j][e];
+                        else
+                            *yp = acc[i][j][e];
+                    }
+                }
+            }
     }
 }
 
@@ -440,14 +230,16 @@ IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
     }
 }
 
-// h[m][j] = f16(u * (g / (1 + exp(-g)))), g = gu[m][j], u = gu[m][F + j] (silu.rs:24-53)
+// h[m][j] = f16(u * (g / (1 + exp(-g)))), g = gu[m][j], u = gu[m][F + j]
+// (silu.rs:24-53), for layers whose gate and up matrices differ in type (the
+// others take the GEMM's SwiGLU epilogue, the same arithmetic)
 IFR_DEV void pf_silu_body(const PfArgs &a) {
     const uint32_t m = blockIdx.y, F = a.ffn;
     const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= F) return;
     const float *gu = (const float *)a.gu;
     const float g = gu[(size_t)m * 2 * F + j], u = gu[(size_t)m * 2 * F + F + j];
-    ((_Float16 *)a.xh)[(size_t)m * a.ldh + j] = (_Float16)(u * (g / (1.0f + expf(-g))));
+    ((_Float16 *)a.h)[(size_t)m * F + j] = (_Float16)(u * (g / (1.0f + expf(-g))));
 }
 
 // ------------------------------------------------------------ attention --

@@ -11,7 +11,6 @@
 // argmax all on the device.
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <array>
@@ -48,6 +47,7 @@ constexpr uint32_t ATTN_SPLITS_MAX = 256; // attention splits per KV head (at mo
 constexpr uint32_t ATTN_GT_MAX = 8;       // device/attention.h: query heads per workgroup
 constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
 constexpr uint32_t PF_GEMM_TILE = 128;    // device/prefill.h: PF_BM = PF_BN
+constexpr uint32_t PF_BIG_TILE = 256;     // device/pf_gemm.h: PG_BM = PG_BN (and PG_THREADS threads)
 constexpr uint32_t PF_CHUNK = 4096;       // prompt tokens per prefill pass (at most)
 
 int qk_of(int32_t dt) {
@@ -137,28 +137,10 @@ struct ifr_ctx {
     uint32_t pf_chunk = 0;
     // this device's fixed scratch of ifr_matmul_quant_noalloc (noalloc.hip)
     void *noalloc_scratch = nullptr;
-    // prefill GEMMs of at least PF_BLAS_MIN_M rows: the weights dequantized
-    // to f16 (wh), then a hipBLASLt f16 x f16 -> f32 product (option pf_blas)
-    int pf_blas = 1;
-    // keep every layer matrix resident in f16 for those products, per
-    // weights object (option pf_keep_f16)
-    int pf_keep_f16 = 1;
-    // products over the resident copies of consecutive matrices stacked into
-    // one hipBLASLt call: bit 0 Q, K and V (the default); bit 1 gate and up
-    // (option pf_stack)
-    int pf_stack = 1;
-    hipblasLtHandle_t blaslt = nullptr;
-    bool blaslt_failed = false;
-    void *blas_ws = nullptr, *wh = nullptr;
-    size_t blas_ws_bytes = 0, wh_bytes = 0;
-    struct BlasPlan {
-        bool ok = false;
-        hipblasLtMatmulDesc_t desc = nullptr;
-        hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-        hipblasLtMatmulAlgo_t algo{};
-        size_t ws = 0;
-    };
-    std::map<std::array<uint32_t, 6>, BlasPlan> blas_plans; // (M, N, K, ldx, ldy, accumulate)
+    // prefill GEMM tiles: 0 = by shape (256 x 256 tiles where the product
+    // has enough of them, else 128 x 128), 128 or 256 to force one (option
+    // pf_tile)
+    uint32_t pf_tile = 0;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -440,16 +422,6 @@ struct ifr_llama2_weights {
     Tens token_embd, output_norm, output;
     std::vector<LayerW> layers;
     std::vector<void *> owned; // device copies made by ifr_llama2_weights_from_gguf
-    // the layer matrices dequantized to f16 for the prefill products (option
-    // pf_keep_f16): one allocation, matrix m of layer l at w16 + w16_off[7 l
-    // + m] (q, k, v, output, gate, up, down), holding generation w16_gen
-    // when w16_ok.  Built by the first prefill that needs it; prefill only
-    // reads the tensor table, so these are the one part it updates.
-    mutable uint8_t *w16 = nullptr;
-    mutable size_t w16_bytes = 0;
-    mutable std::vector<size_t> w16_off;
-    mutable uint64_t w16_gen = 0;
-    mutable bool w16_ok = false;
 };
 
 struct ifr_llama2_state {
@@ -484,7 +456,7 @@ struct ifr_llama2_state {
     // prefill scratch (allocated at the first prefill): a chunk of pf_chunk tokens
     uint32_t pf_chunk = 0, pf_ldh = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_gu = nullptr;
-    uint16_t *pf_xh = nullptr;
+    uint16_t *pf_xh = nullptr, *pf_h = nullptr;
     // sampler of the step end: temperature 0 takes the argmax
     float temperature = 0.0f, topp = 0.0f;
     uint64_t seed = 0;
@@ -964,16 +936,6 @@ IFR_API void ifr_destroy(ifr_ctx *c) {
     hipStreamSynchronize(c->stream);
     if (c->scratch) hipFree(c->scratch);
     if (c->xq_scratch) hipFree(c->xq_scratch);
-    for (auto &kv : c->blas_plans) {
-        ifr_ctx::BlasPlan &b = kv.second;
-        if (b.la) hipblasLtMatrixLayoutDestroy(b.la);
-        if (b.lb) hipblasLtMatrixLayoutDestroy(b.lb);
-        if (b.lc) hipblasLtMatrixLayoutDestroy(b.lc);
-        if (b.desc) hipblasLtMatmulDescDestroy(b.desc);
-    }
-    if (c->blaslt) hipblasLtDestroy(c->blaslt);
-    if (c->blas_ws) hipFree(c->blas_ws);
-    if (c->wh) hipFree(c->wh);
     for (auto &e : c->events)
         if (e) hipEventDestroy(e);
     if (c->module) hipModuleUnload(c->module);
@@ -1005,16 +967,9 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->pf_chunk = (uint32_t)value;
         return IFR_OK;
     }
-    if (!strcmp(key, "pf_blas")) {
-        c->pf_blas = value ? 1 : 0;
-        return IFR_OK;
-    }
-    if (!strcmp(key, "pf_stack")) {
-        c->pf_stack = (int)value & 3;
-        return IFR_OK;
-    }
-    if (!strcmp(key, "pf_keep_f16")) {
-        c->pf_keep_f16 = value ? 1 : 0;
+    if (!strcmp(key, "pf_tile")) {
+        if (value != 0 && value != 128 && value != 256) return c->fail(IFR_EINVAL, "pf_tile must be 0, 128 or 256");
+        c->pf_tile = (uint32_t)value;
         return IFR_OK;
     }
     if (!strcmp(key, "gemv_grp")) {
@@ -1411,10 +1366,9 @@ IFR_API ifr_status ifr_llama2_weights_set(ifr_llama2_weights *w, const char *nam
 
 IFR_API void ifr_llama2_weights_destroy(ifr_llama2_weights *w) {
     if (!w) return;
-    if (!w->owned.empty() || w->w16) {
+    if (!w->owned.empty()) {
         hipStreamSynchronize(w->ctx->stream);
         for (void *p : w->owned) hipFree(p);
-        if (w->w16) hipFree(w->w16);
     }
     delete w;
 }
@@ -1629,128 +1583,56 @@ static ifr_status check_weights(ifr_ctx *c, const ifr_llama2_state *s, const ifr
 
 // ---------------------------------------------------------------- prefill --
 
-// Y[m][n] (+)= sum_k Xh[m][k] * deq(W)[n][k] on the matrix cores.
-// The hipBLASLt plan for Y[M][N] (+)= X[M][K] W^T (X f16 row-major, W f16
-// [N][K], Y f32 row-major), cached per shape.  In hipBLASLt's column-major
-// terms: D (N x M, ld ldy) = op(A) B + beta C with A = W as a K x N matrix
-// (ld K) transposed, B = X as K x M (ld ldx), C = D.  Null when hipBLASLt
-// has no algorithm for it (the caller then uses the fused kernel).
-static const ifr_ctx::BlasPlan *blas_plan(ifr_ctx *c, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldy,
-                                          bool accumulate) {
-    if (c->blaslt_failed) return nullptr;
-    if (!c->blaslt && hipblasLtCreate(&c->blaslt) != HIPBLAS_STATUS_SUCCESS) {
-        c->blaslt = nullptr;
-        c->blaslt_failed = true;
-        return nullptr;
-    }
-    const std::array<uint32_t, 6> key{M, N, K, ldx, ldy, accumulate ? 1u : 0u};
-    auto it = c->blas_plans.find(key);
-    if (it != c->blas_plans.end()) return it->second.ok ? &it->second : nullptr;
-    ifr_ctx::BlasPlan &b = c->blas_plans[key];
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    bool ok = hipblasLtMatmulDescCreate(&b.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(b.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulDescSetAttribute(b.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&b.la, HIP_R_16F, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&b.lb, HIP_R_16F, K, M, ldx) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatrixLayoutCreate(&b.lc, HIP_R_32F, N, M, ldy) == HIPBLAS_STATUS_SUCCESS;
-    if (ok) {
-        hipblasLtMatmulPreference_t pref = nullptr;
-        const uint64_t max_ws = 64ull << 20;
-        hipblasLtMatmulHeuristicResult_t heur[1];
-        int n = 0;
-        ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
-             hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws, sizeof max_ws) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-             hipblasLtMatmulAlgoGetHeuristic(c->blaslt, b.desc, b.la, b.lb, b.lc, b.lc, pref, 1, heur, &n) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-             n > 0 && heur[0].state == HIPBLAS_STATUS_SUCCESS;
-        if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-        if (ok) {
-            b.algo = heur[0].algo;
-            b.ws = heur[0].workspaceSize;
-        }
-    }
-    b.ok = ok;
-    return ok ? &b : nullptr;
-}
-
-// Y[M][N] (+)= X[M][K] . deq(W)^T for a prefill chunk: with at least
-// PF_BLAS_MIN_M rows (option pf_blas) the weights are dequantized once into
-// f16 and hipBLASLt multiplies them; otherwise, or without a hipBLASLt
-// algorithm for the shape, the fused kernel dequantizes each 128 x 64 tile
-// into LDS.  The f16 weights are the same either way.
-constexpr uint32_t PF_BLAS_MIN_M = 256;
+// Y[m][n] (+)= sum_k Xh[m][k] * deq(W)[n][k] on the matrix cores, the weight
+// tiles dequantized to f16 inside the kernels (device/pf_gemm.h: 256 x 256
+// tiles; device/prefill.h gemm_f16_body: 128 x 128 tiles, the same results
+// bit for bit).
 static uint32_t pf_row_bytes(const Tens &w) {
     return (w.cols / (uint32_t)qk_of(w.dtype)) * (uint32_t)bytes_of(w.dtype);
 }
 
-// out[rows][cols] = f16(deq(W)): one thread per 32 elements.
-static ifr_status launch_deq_f16(ifr_ctx *c, const Tens &w, void *out) {
-    PfDeqArgs d{};
-    d.w = w.data;
-    d.out = (uint16_t *)out;
-    d.N = w.rows;
-    d.K = w.cols;
-    d.row_bytes = pf_row_bytes(w);
-    const uint64_t threads = (uint64_t)w.rows * (w.cols / 32);
-    return c->launch(std::string("deq_f16_") + gemv_fmt_name(w.dtype), dim3((uint32_t)((threads + 255) / 256)),
-                     dim3(256), 0, d);
-}
+enum PfEpi { PF_EPI_STORE = 0, PF_EPI_ADD = 1, PF_EPI_SWIGLU = 2 };
+// Products with at least this many 256 x 256 tiles take that form (every
+// product of a 4096-token pass at the 8B shape: 256 to 1792 tiles); smaller
+// ones run 128 x 128 tiles, four times the workgroups.
+constexpr uint32_t PF_BIG_TILES_MIN = 128;
 
-// w16: the matrix already dequantized to f16 (a resident copy), or null to
-// dequantize it here into the context's scratch.
-static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const Tens &w, float *y, uint32_t ldy,
-                                 uint32_t M, bool accumulate, const void *w16 = nullptr) {
-    const uint32_t row_bytes = pf_row_bytes(w);
-    const ifr_ctx::BlasPlan *bp =
-        c->pf_blas && M >= PF_BLAS_MIN_M ? blas_plan(c, M, w.rows, w.cols, ldx, ldy, accumulate) : nullptr;
-    if (bp) {
-        ifr_status st;
-        const size_t wh = (size_t)w.rows * w.cols * 2;
-        if (!w16 && wh > c->wh_bytes) {
-            if (c->wh) {
-                if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
-                hipFree(c->wh);
-                c->wh = nullptr;
-                c->wh_bytes = 0;
-            }
-            if ((st = c->hip(hipMalloc(&c->wh, wh), "hipMalloc(f16 weights)"))) return st;
-            c->wh_bytes = wh;
-        }
-        if (bp->ws > c->blas_ws_bytes) {
-            if (c->blas_ws) {
-                if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
-                hipFree(c->blas_ws);
-                c->blas_ws = nullptr;
-                c->blas_ws_bytes = 0;
-            }
-            if ((st = c->hip(hipMalloc(&c->blas_ws, bp->ws), "hipMalloc(GEMM workspace)"))) return st;
-            c->blas_ws_bytes = bp->ws;
-        }
-        if (!w16) {
-            if ((st = launch_deq_f16(c, w, c->wh))) return st;
-            w16 = c->wh;
-        }
-        const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
-        const hipblasStatus_t bs = hipblasLtMatmul(c->blaslt, bp->desc, &alpha, w16, bp->la, xh, bp->lb, &beta, y, bp->lc,
-                                                   y, bp->lc, &bp->algo, c->blas_ws, bp->ws, c->stream);
-        if (bs != HIPBLAS_STATUS_SUCCESS) return c->fail(IFR_EHIP, "hipblasLtMatmul: status %d", (int)bs);
-        return IFR_OK;
-    }
+// One product of a pass: nm (1 to 3) matrices of one type stacked by rows
+// into Y[M][ldy] f32 (stored or added), or (SwiGLU) gate m[0] and up m[1]
+// into h[M][ldy] = f16(up * silu(gate)).  X rows (pitch ldx halves) must be
+// 16-byte aligned.
+static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const Tens *const *m, int nm, void *y,
+                                 uint32_t ldy, uint32_t M, PfEpi epi) {
     PfGemmArgs g{};
     g.x = xh;
-    g.w = w.data;
+    g.w0 = m[0]->data;
+    g.w1 = nm > 1 ? m[1]->data : m[0]->data;
+    g.w2 = nm > 2 ? m[2]->data : g.w1;
     g.y = y;
     g.M = M;
-    g.N = w.rows;
-    g.K = w.cols;
+    g.K = m[0]->cols;
     g.ldx = ldx;
     g.ldy = ldy;
-    g.row_bytes = row_bytes;
-    const dim3 grid((w.rows + PF_GEMM_TILE - 1) / PF_GEMM_TILE, (M + PF_GEMM_TILE - 1) / PF_GEMM_TILE);
-    return c->launch(std::string("gemm_") + gemv_fmt_name(w.dtype) + (accumulate ? "_f16_add" : "_f16_store"), grid,
-                     dim3(256), 0, g);
+    g.row_bytes = pf_row_bytes(*m[0]);
+    if (epi == PF_EPI_SWIGLU) {
+        g.n1 = g.n2 = m[0]->rows;
+        g.N = 2 * m[0]->rows;
+    } else {
+        g.n1 = m[0]->rows;
+        g.n2 = g.n1 + (nm > 1 ? m[1]->rows : 0);
+        g.N = g.n2 + (nm > 2 ? m[2]->rows : 0);
+    }
+    g.tiles_n = (g.N + PF_BIG_TILE - 1) / PF_BIG_TILE;
+    g.tiles_m = (M + PF_BIG_TILE - 1) / PF_BIG_TILE;
+    static const char *epi_name[3] = {"store", "add", "swiglu"};
+    // the large form addresses X rows with 32-bit byte offsets
+    const bool big_ok = (uint64_t)M * ldx * 2 < (1ull << 32);
+    const bool big = big_ok && (c->pf_tile == 256 || (c->pf_tile == 0 && g.tiles_n * g.tiles_m >= PF_BIG_TILES_MIN));
+    if (big)
+        return c->launch(std::string("pf_gemm_") + gemv_fmt_name(m[0]->dtype) + "_" + epi_name[epi],
+                         dim3(g.tiles_n * g.tiles_m), dim3(PF_BIG_TILE), 0, g);
+    const dim3 grid((g.N + PF_GEMM_TILE - 1) / PF_GEMM_TILE, (M + PF_GEMM_TILE - 1) / PF_GEMM_TILE);
+    return c->launch(std::string("gemm_") + gemv_fmt_name(m[0]->dtype) + "_f16_" + epi_name[epi], grid, dim3(256), 0, g);
 }
 
 // A matrix the prefill GEMM takes: a quantized GGUF type, K a whole number
@@ -1777,35 +1659,8 @@ IFR_API ifr_status ifr_gemm_quant(ifr_ctx *c, float *y, const void *w, int32_t d
     t.data = (const uint8_t *)w;
     t.rows = rows;
     t.cols = cols;
-    return launch_pf_gemm(c, x_f16, cols, t, y, rows, m, accumulate != 0);
-}
-
-// Y[M][N] = X[M][K] . W16^T for N rows of resident f16 matrices stored one
-// after another (stacked products), on hipBLASLt; done stays false (and
-// nothing is launched) when the pass is short or hipBLASLt has no plan.
-static ifr_status pf_gemm_stacked(ifr_ctx *c, const void *xh, uint32_t ldx, const void *w16, uint32_t N, uint32_t K,
-                                  float *y, uint32_t ldy, uint32_t M, bool &done) {
-    done = false;
-    if (!c->pf_blas || M < PF_BLAS_MIN_M) return IFR_OK;
-    const ifr_ctx::BlasPlan *bp = blas_plan(c, M, N, K, ldx, ldy, false);
-    if (!bp) return IFR_OK;
-    ifr_status st;
-    if (bp->ws > c->blas_ws_bytes) {
-        if (c->blas_ws) {
-            if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
-            hipFree(c->blas_ws);
-            c->blas_ws = nullptr;
-            c->blas_ws_bytes = 0;
-        }
-        if ((st = c->hip(hipMalloc(&c->blas_ws, bp->ws), "hipMalloc(GEMM workspace)"))) return st;
-        c->blas_ws_bytes = bp->ws;
-    }
-    const float alpha = 1.0f, beta = 0.0f;
-    const hipblasStatus_t bs = hipblasLtMatmul(c->blaslt, bp->desc, &alpha, w16, bp->la, xh, bp->lb, &beta, y, bp->lc, y,
-                                               bp->lc, &bp->algo, c->blas_ws, bp->ws, c->stream);
-    if (bs != HIPBLAS_STATUS_SUCCESS) return c->fail(IFR_EHIP, "hipblasLtMatmul: status %d", (int)bs);
-    done = true;
-    return IFR_OK;
+    const Tens *mats[1] = {&t};
+    return launch_pf_gemm(c, x_f16, cols, mats, 1, y, rows, m, accumulate ? PF_EPI_ADD : PF_EPI_STORE);
 }
 
 // The layer matrices in the prefill products' order.
@@ -1819,68 +1674,6 @@ static void pf_mats(const LayerW &L, const Tens *m[7]) {
     m[6] = &L.ffn_down;
 }
 
-// Every layer matrix dequantized to f16 and kept on the device with the
-// weights (option pf_keep_f16), so a prompt's hipBLASLt passes skip the
-// per-pass dequantization (8B shape: 14 GB of f16 matrices, ~5.5 ms of a
-// 4095-token prefill).  Built once per weights generation: an
-// ifr_llama2_weights_set call makes the copies stale, and the next prefill
-// dequantizes into the same allocation again.  `have` is false when the
-// option (or pf_blas) is off or the allocation fails; the passes then
-// dequantize per call, with the same f16 values.
-static ifr_status pf_resident_f16(ifr_ctx *c, const ifr_llama2_weights *w, bool &have) {
-    have = false;
-    // the copies are written and read on the weights' own context, whose
-    // stream orders them; a prefill on another context dequantizes per pass
-    if (c != w->ctx) return IFR_OK;
-    ifr_status st;
-    auto release = [&]() -> ifr_status {
-        if (!w->w16) return IFR_OK;
-        ifr_status e = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-        hipFree(w->w16);
-        w->w16 = nullptr;
-        w->w16_bytes = 0;
-        w->w16_ok = false;
-        return e;
-    };
-    if (!c->pf_keep_f16 || !c->pf_blas) return release();
-    std::vector<size_t> off;
-    size_t total = 0;
-    for (const LayerW &L : w->layers) {
-        const Tens *m[7];
-        pf_mats(L, m);
-        for (const Tens *t : m) {
-            off.push_back(total);
-            total += ((size_t)t->rows * t->cols * 2 + 255) / 256 * 256;
-        }
-    }
-    if (w->w16 && w->w16_bytes != total && (st = release())) return st;
-    if (w->w16 && w->w16_ok && w->w16_gen == w->gen) {
-        have = true;
-        return IFR_OK;
-    }
-    if (!w->w16) {
-        void *p = nullptr;
-        if (hipMalloc(&p, total) != hipSuccess) {
-            (void)hipGetLastError(); // not enough memory: dequantize per pass
-            return IFR_OK;
-        }
-        w->w16 = (uint8_t *)p;
-        w->w16_bytes = total;
-    }
-    w->w16_off = off;
-    w->w16_ok = false;
-    for (size_t l = 0; l < w->layers.size(); l++) {
-        const Tens *m[7];
-        pf_mats(w->layers[l], m);
-        for (int i = 0; i < 7; i++)
-            if ((st = launch_deq_f16(c, *m[i], w->w16 + off[l * 7 + i]))) return st;
-    }
-    w->w16_gen = w->gen;
-    w->w16_ok = true;
-    have = true;
-    return IFR_OK;
-}
-
 static ifr_status pf_ensure_scratch(ifr_llama2_state *s) {
     if (s->pf_x) return IFR_OK;
     ifr_ctx *c = s->ctx;
@@ -1891,7 +1684,7 @@ static ifr_status pf_ensure_scratch(ifr_llama2_state *s) {
     const uint32_t C = std::min(c->pf_chunk ? c->pf_chunk : PF_CHUNK, (cfg.max_pos + 63) / 64 * 64);
     const uint32_t H = cfg.hidden, F = cfg.ffn, qd = cfg.n_heads * s->head_size;
     s->pf_chunk = C;
-    s->pf_ldh = std::max(std::max(H, F), qd);
+    s->pf_ldh = std::max(H, qd);
     auto A = [&](size_t bytes, void **p) -> ifr_status {
         ifr_status e = c->hip(hipMalloc(p, bytes), "hipMalloc(prefill)");
         if (!e) s->allocs.push_back(*p);
@@ -1901,7 +1694,7 @@ static ifr_status pf_ensure_scratch(ifr_llama2_state *s) {
     if ((st = A((size_t)C * H * 4, (void **)&s->pf_x))) return st;
     if ((st = A((size_t)C * s->pf_ldh * 2, (void **)&s->pf_xh))) return st;
     if ((st = A((size_t)C * (qd + 2 * s->kv_dim) * 4, (void **)&s->pf_qkv))) return st;
-    return A((size_t)C * 2 * F * 4, (void **)&s->pf_gu);
+    return A((size_t)C * F * 2, (void **)&s->pf_h);
 }
 
 IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr_llama2_weights *w, uint32_t n) {
@@ -1909,17 +1702,16 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     ifr_status st = check_weights(c, s, w);
     if (st) return st;
     const ifr_llama2_config &cfg = s->cfg;
+    bool mixed_ffn = false; // a layer whose gate and up types differ
     for (const LayerW &L : w->layers) {
         const Tens *mats[7];
         pf_mats(L, mats);
         for (const Tens *t : mats)
             if ((st = check_pf_matrix(c, t->dtype, t->cols, t->data))) return st;
+        mixed_ffn |= L.ffn_gate.dtype != L.ffn_up.dtype;
     }
     if (!n) return IFR_OK;
     if ((st = pf_ensure_scratch(s))) return st;
-    // resident f16 matrices, when a pass reaches the hipBLASLt products
-    bool w16 = false;
-    if (std::min(s->pf_chunk, n) >= PF_BLAS_MIN_M && (st = pf_resident_f16(c, w, w16))) return st;
     // the position lives on the device: read it once
     StepCtl ctl;
     if ((st = c->hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize"))) return st;
@@ -1927,6 +1719,12 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     const uint32_t pos0 = ctl.pos;
     if ((uint64_t)pos0 + n > cfg.max_pos) return c->fail(IFR_EINVAL, "prefill: %u tokens from position %u exceed max_pos", n, pos0);
     if (pos0 + n > ctl.n_forced) return c->fail(IFR_EINVAL, "prefill: positions up to %u hold no prompt token", pos0 + n);
+    if (mixed_ffn && !s->pf_gu) {
+        // separate gate and up products into f32, then the SiLU pass
+        const size_t bytes = (size_t)s->pf_chunk * 2 * cfg.ffn * 4;
+        if ((st = c->hip(hipMalloc((void **)&s->pf_gu, bytes), "hipMalloc(prefill gate/up)"))) return st;
+        s->allocs.push_back(s->pf_gu);
+    }
 
     const uint32_t H = cfg.hidden, F = cfg.ffn, hs = s->head_size, kvd = s->kv_dim, qd = cfg.n_heads * hs;
     const uint32_t G = s->kv_mul, ldq = qd + 2 * kvd, ldh = s->pf_ldh;
@@ -1935,11 +1733,6 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
     const uint32_t attn_qt = 128 / G; // device/prefill.h: PFA_ROWS / kv_mul queries per workgroup
     for (uint32_t c0 = 0; c0 < n; c0 += s->pf_chunk) {
         const uint32_t M = std::min(s->pf_chunk, n - c0), p0 = pos0 + c0;
-        // passes of at least 256 rows run their products on M rounded up to
-        // 256 where the scratch holds them (a 4095-token pass as 4096): rows
-        // are independent, and the rows past M are never read (rope,
-        // attention, SiLU and RMSNorm take M)
-        const uint32_t Mg = M >= 256 ? std::min((M + 255) / 256 * 256, s->pf_chunk) : M;
         PfArgs a{};
         a.x = s->pf_x;
         a.xh = s->pf_xh;
@@ -1961,13 +1754,14 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
         a.kv_f16 = cfg.kv_dtype == IFR_F16;
         a.ffn = F;
         a.gu = s->pf_gu;
+        a.h = s->pf_h;
         a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
         a.kv_mul = G;
         if ((st = c->launch("pf_embed_k", dim3(M), dim3(256), 0, a))) return st;
         for (uint32_t l = 0; l < cfg.n_layers; l++) {
             const LayerW &L = w->layers[l];
-            // the resident f16 copy of this layer's matrix i, or null
-            auto r16 = [&](int i) -> const void * { return w16 ? w->w16 + w->w16_off[(size_t)l * 7 + i] : nullptr; };
+            const Tens *mats[7];
+            pf_mats(L, mats);
             a.k_cache = s->kcache + (size_t)l * s->layer_kv_bytes;
             a.v_cache = s->vcache + (size_t)l * s->layer_kv_bytes;
             a.gamma = (const float *)L.attn_norm.data;
@@ -1975,40 +1769,30 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
             a.k_bias = (const float *)L.k_bias.data;
             a.v_bias = (const float *)L.v_bias.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            // the resident copies of matrices i .. j lie one after another
-            const Tens *mats[7];
-            pf_mats(L, mats);
-            auto adjacent = [&](int i, int j) {
-                for (int m = i; m < j; m++)
-                    if (w->w16_off[(size_t)l * 7 + m + 1] !=
-                        w->w16_off[(size_t)l * 7 + m] + (size_t)mats[m]->rows * mats[m]->cols * 2)
-                        return false;
-                return true;
-            };
-            bool stacked = false;
-            if (w16 && (c->pf_stack & 1) && adjacent(0, 2) &&
-                (st = pf_gemm_stacked(c, s->pf_xh, ldh, r16(0), qd + 2 * kvd, H, s->pf_qkv, ldq, Mg, stacked)))
-                return st;
-            if (!stacked) {
-                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_q, s->pf_qkv, ldq, Mg, false, r16(0)))) return st;
-                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_k, s->pf_qkv + qd, ldq, Mg, false, r16(1)))) return st;
-                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_v, s->pf_qkv + qd + kvd, ldq, Mg, false, r16(2)))) return st;
+            // Q, K and V into adjacent columns of qkv: each run of matrices of
+            // one type as one stacked product
+            for (int i = 0, col = 0; i < 3;) {
+                int j = i + 1;
+                while (j < 3 && mats[j]->dtype == mats[i]->dtype) j++;
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + i, j - i, s->pf_qkv + col, ldq, M, PF_EPI_STORE)))
+                    return st;
+                for (int k = i; k < j; k++) col += (int)mats[k]->rows;
+                i = j;
             }
             if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
             if ((st = c->launch(attn_name, dim3(cfg.n_kv_heads, (M + attn_qt - 1) / attn_qt), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.attn_output, s->pf_x, H, Mg, true, r16(3)))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + 3, 1, s->pf_x, H, M, PF_EPI_ADD))) return st;
             a.gamma = (const float *)L.ffn_norm.data;
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
-            stacked = false;
-            if (w16 && (c->pf_stack & 2) && adjacent(4, 5) &&
-                (st = pf_gemm_stacked(c, s->pf_xh, ldh, r16(4), 2 * F, H, s->pf_gu, 2 * F, Mg, stacked)))
-                return st;
-            if (!stacked) {
-                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_gate, s->pf_gu, 2 * F, Mg, false, r16(4)))) return st;
-                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_up, s->pf_gu + F, 2 * F, Mg, false, r16(5)))) return st;
+            if (L.ffn_gate.dtype == L.ffn_up.dtype) {
+                // h = up * silu(gate) in the product's epilogue
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + 4, 2, s->pf_h, F, M, PF_EPI_SWIGLU))) return st;
+            } else {
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + 4, 1, s->pf_gu, 2 * F, M, PF_EPI_STORE))) return st;
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + 5, 1, s->pf_gu + F, 2 * F, M, PF_EPI_STORE))) return st;
+                if ((st = c->launch("pf_silu_k", dim3((F + 255) / 256, M), dim3(256), 0, a))) return st;
             }
-            if ((st = c->launch("pf_silu_k", dim3((F + 255) / 256, M), dim3(256), 0, a))) return st;
-            if ((st = launch_pf_gemm(c, s->pf_xh, ldh, L.ffn_down, s->pf_x, H, Mg, true, r16(6)))) return st;
+            if ((st = launch_pf_gemm(c, s->pf_h, F, mats + 6, 1, s->pf_x, H, M, PF_EPI_ADD))) return st;
         }
     }
     // advance the device position (and the unfused path's op parameters)

@@ -225,20 +225,17 @@ struct KvStoreArgs {
 };
 
 // Prefill GEMM: Y[m][n] (+)= sum_k X[m][k] * deq(W)[n][k]; X f16 (as raw
-// halves), W Q4_K rows, Y f32.
+// halves), W rows of GGUF blocks, Y f32 (or f16 h for the SwiGLU form).
+// The n rows are those of up to three matrices of one type stacked one after
+// another: n < n1 from w0, n1 <= n < n2 from w1, the rest from w2.  SwiGLU:
+// w0 gate and w1 up, n1 = their row count, N = 2 n1.
 struct PfGemmArgs {
-    const void *x;       // f16 [M][ldx]
-    const uint8_t *w;    // rows of K/QK GGUF blocks
-    float *y;            // f32 [M][ldy]
+    const void *x;       // f16 [M][ldx], rows 16-byte aligned
+    const uint8_t *w0, *w1, *w2; // rows of K/QK GGUF blocks
+    void *y;             // f32 [M][ldy] (f16 for SwiGLU)
     uint32_t M, N, K, ldx, ldy, row_bytes;
-};
-
-// A weight matrix dequantized to f16 (the prefill GEMM's operand when a
-// library GEMM multiplies it): out[n][k] for n < N, k < K.
-struct PfDeqArgs {
-    const uint8_t *w;    // rows of K/QK GGUF blocks
-    uint16_t *out;       // f16 [N][K]
-    uint32_t N, K, row_bytes;
+    uint32_t n1, n2;     // stacked matrix boundaries
+    uint32_t tiles_n, tiles_m; // tile grid (pf_gemm: 256 x 256 tiles)
 };
 
 // Prefill pointwise and attention kernels (one chunk of M prompt tokens at
@@ -260,7 +257,8 @@ struct PfArgs {
     void *k_cache, *v_cache; // this layer's cache base
     int32_t kv_f16;
     uint32_t ffn;
-    void *gu;            // f32 [M][2*ffn]: gate | up
+    void *gu;            // f32 [M][2*ffn]: gate | up (layers whose gate and up types differ)
+    void *h;             // f16 [M][ffn]: silu(gate) * up, the down product's input
     const float *q_bias, *k_bias, *v_bias; // QKV biases (may be null)
     int32_t neox;        // RoPE pairs (j, j + hs/2) instead of (2j, 2j+1)
     uint32_t kv_mul;     // attention: query heads per KV head

@@ -127,22 +127,42 @@ extern "C" __global__ void __launch_bounds__(256) dequant_k(DequantArgs a) { deq
 extern "C" __global__ void __launch_bounds__(64) quantize_k(QuantArgs a) { quantize_body(a); }
 extern "C" __global__ void __launch_bounds__(256) fill_normal_k(FillArgs a) { fill_normal_body(a); }
 
-// prompt (prefill) path
-#define GEMM_KERNELS(FMTNAME, FMT)                                                                          \
-    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_store(PfGemmArgs a) { gemm_f16_body<FMT, 0>(a); } \
-    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_add(PfGemmArgs a) { gemm_f16_body<FMT, 1>(a); } \
-    extern "C" __global__ void __launch_bounds__(256) deq_f16_##FMTNAME(PfDeqArgs a) { pf_deq_f16_body<FMT>(a); }
-GEMM_KERNELS(q4_k, Q4_K)
-GEMM_KERNELS(q5_k, Q5_K)
-GEMM_KERNELS(q6_k, Q6_K)
-GEMM_KERNELS(q8_k, Q8_K)
-GEMM_KERNELS(q8_0, Q8_0)
-GEMM_KERNELS(q4_0, Q4_0)
-GEMM_KERNELS(q4_1, Q4_1)
-GEMM_KERNELS(q5_0, Q5_0)
-GEMM_KERNELS(q5_1, Q5_1)
-GEMM_KERNELS(f16, F16)
-GEMM_KERNELS(f32, F32)
+// prompt (prefill) path: the GEMM in 256 x 256 tiles (four waves, one per
+// SIMD, with the accumulators in AGPRs) and in 128 x 128 tiles, each with
+// the store, accumulate and SwiGLU epilogues
+#define PF_GEMM_KERNELS(FMTNAME, FMT)                                                                             \
+    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))           \
+    pf_gemm_##FMTNAME##_store(PfGemmArgs a) {                                                                     \
+        pf_gemm_body<FMT, PG_STORE>(a);                                                                           \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))           \
+    pf_gemm_##FMTNAME##_add(PfGemmArgs a) {                                                                       \
+        pf_gemm_body<FMT, PG_ADD>(a);                                                                             \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))           \
+    pf_gemm_##FMTNAME##_swiglu(PfGemmArgs a) {                                                                    \
+        pf_gemm_body<FMT, PG_SWIGLU>(a);                                                                          \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_store(PfGemmArgs a) {                  \
+        gemm_f16_body<FMT, PG_STORE>(a);                                                                          \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_add(PfGemmArgs a) {                    \
+        gemm_f16_body<FMT, PG_ADD>(a);                                                                            \
+    }                                                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) gemm_##FMTNAME##_f16_swiglu(PfGemmArgs a) {                 \
+        gemm_f16_body<FMT, PG_SWIGLU>(a);                                                                         \
+    }
+PF_GEMM_KERNELS(q4_k, Q4_K)
+PF_GEMM_KERNELS(q5_k, Q5_K)
+PF_GEMM_KERNELS(q6_k, Q6_K)
+PF_GEMM_KERNELS(q8_k, Q8_K)
+PF_GEMM_KERNELS(q8_0, Q8_0)
+PF_GEMM_KERNELS(q4_0, Q4_0)
+PF_GEMM_KERNELS(q4_1, Q4_1)
+PF_GEMM_KERNELS(q5_0, Q5_0)
+PF_GEMM_KERNELS(q5_1, Q5_1)
+PF_GEMM_KERNELS(f16, F16)
+PF_GEMM_KERNELS(f32, F32)
 extern "C" __global__ void __launch_bounds__(256) pf_embed_k(PfArgs a) { pf_embed_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { pf_rmsnorm_f16_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }

@@ -1,9 +1,10 @@
 """GPU parity of the prompt (prefill) path.
 
 ifr_gemm_quant multiplies f16 activations by weights of any quantized GGUF
-type dequantized to f16 tiles on the matrix cores: it is checked against an
-f64 product of the same f16-rounded operands (only the f32 accumulation
-order may differ).
+type dequantized to f16 tiles on the matrix cores, in 256 x 256 or 128 x 128
+tiles (option pf_tile): both forms are checked against an f64 product of the
+same f16-rounded operands (only the f32 accumulation order may differ) and
+against each other (bit for bit).
 
 ifr_llama2_prefill runs a prompt through every layer in chunks; the state it
 leaves (KV-cache rows, position) must continue exactly like a state that
@@ -34,9 +35,24 @@ def synthetic_q(ctx, rows, cols, seed, dtype):
     return w
 
 
-def _gemm_case(ctx, dtype, rows, cols, m, w, rng):
-    """y = x . deq(W)^T against the f64 product of the same f16-rounded
-    operands (bound 2e-5 * sum |x w|), then the accumulating form."""
+def _gemm_case(ctx, dtype, rows, cols, m, w, rng, tiles=(128, 256)):
+    """y = x . deq(W)^T in each tile form against the f64 product of the same
+    f16-rounded operands (bound 2e-5 * sum |x w|), then the accumulating form;
+    the tile forms agree bit for bit."""
+    import inferi_amd as I
+
+    outs = []
+    for tile in tiles:
+        ctx.set_option("pf_tile", tile)
+        try:
+            outs.append(_gemm_case1(ctx, dtype, rows, cols, m, w, np.random.default_rng(rows + cols + m)))
+        finally:
+            ctx.set_option("pf_tile", 0)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), "tile forms differ"
+
+
+def _gemm_case1(ctx, dtype, rows, cols, m, w, rng):
     import inferi_amd as I
 
     rb = I.row_bytes(dtype, cols)
@@ -56,11 +72,11 @@ def _gemm_case(ctx, dtype, rows, cols, m, w, rng):
     assert np.all(np.abs(got2 - 2 * ref) <= 2 * bound)
     for b in (dx, y):
         b.free()
+    return got.astype(np.float32)
 
 
-# m >= 256 runs the dequant + hipBLASLt path, smaller m the fused kernel
 @pytest.mark.parametrize("rows,cols,m", [(128, 256, 128), (300, 512, 70), (1000, 1024, 257), (4096, 4096, 128),
-                                         (64, 14336, 33), (4096, 4096, 512), (512, 14336, 300)])
+                                         (64, 14336, 33), (4096, 4096, 512), (512, 14336, 300), (1024, 4096, 4095)])
 def test_gemm_quant_matches_f64(ctx, oracle_lib, rows, cols, m):
     import inferi_amd as I
 
@@ -76,9 +92,8 @@ FMTS = ["Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q4_K", "Q5_K", "Q6_K", "Q8_K", 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("rows,cols,m", [(300, 512, 70), (130, 2048, 129), (300, 512, 300), (130, 2048, 260)])
 def test_gemm_quant_every_format(ctx, oracle_lib, fmt, rows, cols, m):
-    """Each GGUF type's tile loader (m < 256: the fused kernel) and its f16
-    dequant kernel (m >= 256: then hipBLASLt): quantized synthetic weights
-    and raw random blocks with a quarter of the scales subnormal (the
+    """Each GGUF type's tile loader in both tile forms: quantized synthetic
+    weights and raw random blocks with a quarter of the scales subnormal (the
     reference's GEMV test generator, gemv_quant.rs:354-430)."""
     import inferi_amd as I
     from tests import kquant as K
@@ -188,14 +203,34 @@ def test_prefill_chunks_and_gqa4_hs128(ctx, oracle_lib, chunk):
         w.close()
 
 
-@pytest.mark.parametrize("blas", [0, 1], ids=["fused", "hipblaslt"])
-def test_prefill_pass_length_gives_same_results(ctx, blas):
-    """The prompt in passes of 64, 192 or all its 299 tokens at once.  On the
-    fused GEMM (option pf_blas 0) the same KV cache rows, logits and tokens
-    bit for bit: each output row's GEMM sum and each query's attention are
-    computed the same way in any pass.  With pf_blas 1 the 299-token pass
-    multiplies on hipBLASLt (passes of 256 rows or more do), whose summation
-    order differs: rows within 2e-3 normwise, logits within 1e-3 scaled."""
+def _prefill_run(ctx, cfg, w, prompt, n_prefill, n_gen):
+    """Prefill then n_gen graph steps on a fresh state: (logits bits, tokens, KV rows)."""
+    import inferi_amd as I
+
+    s = I.Llama2State(ctx, cfg)
+    try:
+        s.reset(prompt, 0)
+        I.Llama2.prefill(ctx, s, w, n_prefill)
+        I.Llama2.generate(ctx, s, w, n_gen, use_graph=True)
+        kv = [s.read(n, np.uint16, layer).copy() for layer in range(cfg.n_layers) for n in ("key_cache", "value_cache")]
+        return s.read("logits").view(np.uint32).copy(), s.tokens(0, n_prefill + n_gen + 1), kv
+    finally:
+        s.close()
+
+
+def _same(a, b, what):
+    assert np.array_equal(a[0], b[0]), f"logits: {what}"
+    assert np.array_equal(a[1], b[1]), f"tokens: {what}"
+    for x, y in zip(a[2], b[2]):
+        assert np.array_equal(x, y), f"KV cache: {what}"
+
+
+def test_prefill_pass_length_and_tile_give_same_results(ctx):
+    """The prompt in passes of 64, 192 or all its 299 tokens at once, with the
+    GEMMs in 128 x 128 or 256 x 256 tiles: the same KV cache rows, logits and
+    tokens bit for bit, since each output row's GEMM sum (k in the same order
+    in both tile forms) and each query's attention are computed the same way
+    in any pass."""
     import inferi_amd as I
 
     cfg = I.Llama2Config(n_layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, vocab=700, max_pos=400,
@@ -203,112 +238,69 @@ def test_prefill_pass_length_gives_same_results(ctx, blas):
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=43, std=0.05)
     prompt = np.random.default_rng(5).integers(0, cfg.vocab, 300).astype(np.uint32)
     out = {}
-    ctx.set_option("pf_blas", blas)
     try:
-        for chunk in (64, 192, 0):
-            ctx.set_option("pf_chunk", chunk)
-            s = I.Llama2State(ctx, cfg)
-            try:
-                s.reset(prompt, 0)
-                I.Llama2.prefill(ctx, s, w, 299)
-                I.Llama2.generate(ctx, s, w, 6, use_graph=True)
-                kv = [s.read(n, np.uint16, layer).copy() for layer in range(cfg.n_layers)
-                      for n in ("key_cache", "value_cache")]
-                out[chunk] = (s.read("logits"), s.tokens(0, 306), kv)
-            finally:
-                s.close()
+        for tile in (128, 256):
+            ctx.set_option("pf_tile", tile)
+            for chunk in (64, 192, 0):
+                ctx.set_option("pf_chunk", chunk)
+                out[tile, chunk] = _prefill_run(ctx, cfg, w, prompt, 299, 6)
     finally:
         ctx.set_option("pf_chunk", 0)
-        ctx.set_option("pf_blas", 1)
+        ctx.set_option("pf_tile", 0)
         w.close()
-    ref = out[0]
-    for chunk in (64, 192):
-        got = out[chunk]
-        if not blas:
-            assert np.array_equal(got[0].view(np.uint32), ref[0].view(np.uint32)), f"logits, passes of {chunk}"
-            assert np.array_equal(got[1], ref[1]), f"tokens, passes of {chunk}"
-            for a, b in zip(got[2], ref[2]):
-                assert np.array_equal(a, b), f"KV cache, passes of {chunk}"
-            continue
-        e = np.abs(got[0].astype(np.float64) - ref[0]) / np.maximum(np.abs(ref[0]), 1.0)
-        assert e.max() <= 1e-3, f"logits, passes of {chunk}: {e.max():.3e}"
-        for a, b in zip(got[2], ref[2]):
-            fa, fb = O.decode_f16(a).astype(np.float64), O.decode_f16(b).astype(np.float64)
-            nw = float(np.abs(fa - fb).max() / np.abs(fb).max())
-            assert nw <= 2e-3, f"KV cache, passes of {chunk}: normwise {nw:.3e}"
+    ref = out[256, 0]
+    for key, got in out.items():
+        _same(got, ref, f"tile {key[0]}, passes of {key[1] or 299}")
 
 
-def test_prefill_resident_f16_matrices(ctx):
-    """Option pf_keep_f16 (the default) keeps every layer matrix dequantized
-    to f16 with the weights after the first prefill that reaches hipBLASLt;
-    later prefills multiply those copies.  The copies hold the same f16
-    values the per-pass dequantization writes, so prefills with the copies
-    (the one that builds them, then one that reuses them) and without them
-    (option 0) leave the same KV cache rows, logits and tokens bit for bit
-    with unstacked products (option pf_stack 0), and within hipBLASLt's
-    summation-order tolerance with stacked ones.
-    Replacing a matrix (ifr_llama2_weights_set) makes the copies stale: the
-    next prefill dequantizes again and still matches the per-pass path."""
+def test_prefill_uses_weights_rewritten_in_place(ctx):
+    """The prefill kernels read the bound GGUF blocks themselves: new bytes
+    written into a bound tensor's buffer (no ifr_llama2_weights_set call) are
+    what the next prefill multiplies, the same as binding a fresh buffer that
+    holds them."""
     import inferi_amd as I
 
     cfg = I.Llama2Config(n_layers=2, hidden=512, ffn=1024, n_heads=8, n_kv_heads=2, vocab=700, max_pos=400,
                          rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=47, std=0.05)
     prompt = np.random.default_rng(9).integers(0, cfg.vocab, 300).astype(np.uint32)
-
-    def run(keep, stack=0):
-        ctx.set_option("pf_keep_f16", keep)
-        ctx.set_option("pf_stack", stack)
-        s = I.Llama2State(ctx, cfg)
-        try:
-            s.reset(prompt, 0)
-            I.Llama2.prefill(ctx, s, w, 299)  # one pass of 299 rows: hipBLASLt products
-            I.Llama2.generate(ctx, s, w, 4, use_graph=True)
-            kv = [s.read(n, np.uint16, layer).copy() for layer in range(cfg.n_layers)
-                  for n in ("key_cache", "value_cache")]
-            return s.read("logits").view(np.uint32).copy(), s.tokens(0, 304), kv
-        finally:
-            s.close()
-
-    def same(a, b, what):
-        assert np.array_equal(a[0], b[0]), f"logits: {what}"
-        assert np.array_equal(a[1], b[1]), f"tokens: {what}"
-        for x, y in zip(a[2], b[2]):
-            assert np.array_equal(x, y), f"KV cache: {what}"
-
+    rows, cols = cfg.hidden, cfg.ffn
+    nbytes = rows * I.row_bytes(I.Q4_K, cols)
+    tmp = ctx.alloc(rows * cols * 4)
+    down = ctx.alloc(nbytes)
     try:
-        build, reuse, per_pass = run(1), run(1), run(0)
-        same(build, per_pass, "copies built in this prefill vs per-pass dequantization")
-        same(reuse, per_pass, "resident copies vs per-pass dequantization")
-        # stacked products (option pf_stack: Q, K, V as one; gate, up as one)
-        # over the same f16 copies: hipBLASLt may choose another kernel for
-        # the stacked shape, so within its summation-order tolerance
-        for stack in (1, 2, 3):
-            got = run(1, stack)
-            lg, ref = got[0].view(np.float32).astype(np.float64), per_pass[0].view(np.float32)
-            e = np.abs(lg - ref) / np.maximum(np.abs(ref), 1.0)
-            assert e.max() <= 1e-3, f"logits, pf_stack {stack}: {e.max():.3e}"
-            for a, b in zip(got[2], per_pass[2]):
-                fa, fb = O.decode_f16(a).astype(np.float64), O.decode_f16(b).astype(np.float64)
-                nw = float(np.abs(fa - fb).max() / np.abs(fb).max())
-                assert nw <= 2e-3, f"KV cache, pf_stack {stack}: normwise {nw:.3e}"
-        # a new ffn_down for layer 0 (another draw, quantized on the device):
-        # layer 1's KV rows depend on it
-        rows, cols = cfg.hidden, cfg.ffn
-        tmp = ctx.alloc(rows * cols * 4)
+        before = _prefill_run(ctx, cfg, w, prompt, 299, 4)
+        # another ffn_down for layer 0, quantized on the device
         ctx.fill_normal(tmp, rows * cols, 1234, 0, 0.0, 0.05)
-        down = ctx.alloc(rows * I.row_bytes(I.Q4_K, cols))
         ctx.quantize(down, tmp, I.Q4_K, rows * cols)
-        tmp.free()
-        run(1)  # copies of the old tensor table resident again
-        w.buffers["blk.0.ffn_down.weight"][1].free()
+        new_bytes = down.download(np.uint8, nbytes)
+        bound = w.buffers["blk.0.ffn_down.weight"][1]
+        ctx._check(I.lib().ifr_upload(ctx.h, bound.ptr, new_bytes.ctypes.data, nbytes))
+        in_place = _prefill_run(ctx, cfg, w, prompt, 299, 4)
         w.set("blk.0.ffn_down.weight", I.Q4_K, down, rows, cols)
-        after, after_per_pass = run(1), run(0)
-        same(after, after_per_pass, "after a matrix was replaced (a stale f16 copy would differ)")
-        assert not np.array_equal(after[2][2], per_pass[2][2]), "layer 1's K rows ignore the new matrix"
+        bound.free()
+        rebound = _prefill_run(ctx, cfg, w, prompt, 299, 4)
+        _same(in_place, rebound, "bytes rewritten in place vs the same bytes bound anew")
+        assert not np.array_equal(in_place[2][2], before[2][2]), "layer 1's K rows ignore the new matrix"
     finally:
-        ctx.set_option("pf_keep_f16", 1)
-        ctx.set_option("pf_stack", 1)
+        tmp.free()
+        w.close()
+
+
+def test_prefill_gate_up_of_different_types(ctx, oracle_lib):
+    """A layer whose gate and up matrices differ in GGUF type takes separate
+    gate and up products and the SiLU pass instead of the SwiGLU epilogue
+    (the other layers keep it); against sequential decode."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=256, ffn=512, n_heads=4, n_kv_heads=2, vocab=700, max_pos=160,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=53, std=0.05, overrides={"blk.1.ffn_up.weight": I.Q6_K,
+                                                                           "attn_v": I.Q8_0})
+    try:
+        prompt = np.random.default_rng(12).integers(0, cfg.vocab, 120).tolist()
+        assert _prefill_vs_decode(ctx, cfg, w, prompt, 8) > 0
+    finally:
         w.close()
 
 

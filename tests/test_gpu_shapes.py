@@ -191,16 +191,20 @@ def test_decode_model_shapes(ctx, oracle_lib, name, mode):
 
 
 @pytest.mark.timeout(300)
+@pytest.mark.parametrize("tile", [0, 256])
 @pytest.mark.parametrize("name", list(MODELS))
-def test_prefill_model_shapes(ctx, oracle_lib, name):
+def test_prefill_model_shapes(ctx, oracle_lib, name, tile):
     """A 150-token prompt: 149 tokens through ifr_llama2_prefill, then 12
     decode steps, every step's logits and every layer's KV rows against the
-    oracle over the same sequence."""
+    oracle over the same sequence; with the GEMM tiles chosen by shape (128 x
+    128 here) and forced to 256 x 256 (stacked QKV products with biases and
+    NeoX pairs, odd query groups, rows and tokens past the matrix edges)."""
     import inferi_amd as I
 
     P, N = 150, 12
     cfg, w = model(ctx, name, P + N + 4)
     s = I.Llama2State(ctx, cfg)
+    ctx.set_option("pf_tile", tile)
     try:
         prompt = np.random.default_rng(11).integers(0, cfg.vocab, P).tolist()
         s.reset(prompt, 0)
@@ -229,6 +233,7 @@ def test_prefill_model_shapes(ctx, oracle_lib, name):
         print(f"{name}: prefill {P - 1} + {N} steps, logits within {worst:.2e}, layer-0 K/V at "
               f"{bound if bound is None else round(bound, 3)} of the f16 bound", flush=True)
     finally:
+        ctx.set_option("pf_tile", 0)
         s.close()
         w.close()
 
