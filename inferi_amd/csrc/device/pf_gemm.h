@@ -11,13 +11,15 @@
 // (crates/inferi/src/quantization.rs:47-392), rounded to f16 and staged in
 // LDS, where the 256 token rows of the workgroup's X tile share it.
 //
-// Workgroup: 4 waves (one per SIMD), a 256 (m) x 256 (n) tile of Y.  Wave w
-// owns the 128 x 128 sub-tile m in [128 (w & 1), +128), n in [128 (w >> 1),
-// +128): 4 x 4 blocks of v_mfma_f32_32x32x16_f16 (256 f32 accumulators per
-// lane), so each operand fragment read from LDS feeds four products.  K runs
-// in steps of 64 through two LDS buffers: while the matrix cores work on
-// step s, the global loads of step s + 1 are in flight; their tiles are then
-// dequantized into the other buffer, so one barrier per step suffices.
+// Workgroup: 8 waves (two per SIMD, so one wave's stalls are the other's
+// issue slots), a 256 (m) x 256 (n) tile of Y.  Wave w owns the 128 x 64
+// sub-tile m in [128 (w & 1), +128), n in [64 (w >> 1), +64): 4 x 2 blocks
+// of v_mfma_f32_32x32x16_f16 (128 f32 accumulators per lane).  K runs in
+// steps of 64 through two LDS buffers: X arrives by direct global-to-LDS
+// loads, issued a step ahead; W's GGUF bytes arrive in registers two steps
+// ahead and are dequantized into the other buffer while the matrix cores
+// work on the current one, so one barrier per step suffices.  (Four waves
+// of 128 x 128, one per SIMD, measured 10-20% slower.)
 //
 // Rows of the virtual n range come from up to three matrices of one GGUF
 // type stacked one after another (n < n1: w0, n < n2: w1, else w2), so Q, K
@@ -33,7 +35,7 @@
 namespace ifr {
 
 constexpr int PG_BM = 256, PG_BN = 256, PG_BK = 64;
-constexpr int PG_THREADS = 256;
+constexpr int PG_THREADS = 512;
 
 // epilogues
 constexpr int PG_STORE = 0;  // Y = X W^T
@@ -67,32 +69,6 @@ IFR_DEV void lds_dma16(const void *base, uint32_t off, uint32_t lds) {
 // wait tracking): the caller waits with pg_wait before reading r.
 IFR_DEV void ld16_asm(u32x4_a16 &r, const uint8_t *p) { asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p)); }
 
-// Weight staging of one thread: the 64 elements of one tile row in a K
-// step, stored as eight swizzled 16-byte chunks.  Generic: two PfTile
-// loads, elements [0, 32) and [32, 64).
-template <int FMT>
-struct PgStage {
-    static constexpr bool MANUAL = false; // compiler-tracked loads
-    PfTile<FMT> t0, t1;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0) {
-        t0.load(wrow, k0, 0);
-        t1.load(wrow, k0, 1);
-    }
-    template <int N>
-    IFR_DEV void wait() {}
-    IFR_DEV void store(uint32_t k0, _Float16 *tile, uint32_t r) const {
-        _Float16 h[64];
-        t0.deq(k0, 0, h);
-        t1.deq(k0, 1, h + 32);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            uint4 u;
-            __builtin_memcpy(&u, &h[8 * c], 16);
-            *(uint4 *)(tile + pg_swz(r, (uint32_t)c)) = u;
-        }
-    }
-};
-
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 // f16 pair of two f32 values, each rounded to nearest from its f32 value
 // (v_cvt_pk_f16_f32 written out, so the compiler cannot fuse the producing
@@ -103,37 +79,60 @@ IFR_DEV uint32_t pack_f16x2(float a, float b) {
     return u;
 }
 
-// Q4_K (quantization.rs:358-392): the step's 64 elements are group g =
-// (k0 % 256) / 64 of the block, qs bytes [32 g, +32): low nibbles are
-// elements 0..31 (sub-block 2g), high nibbles 32..63 (sub-block 2g + 1).
-// y = d1 * q - m1 with d1 = d * sc and m1 = dmin * m: d1 * q is exact in f32
-// (at most 11 + 6 + 4 significant bits), so the fused multiply-add rounds
-// once, exactly as the reference's multiply then subtract does.
+// Weight staging of one thread: half (part p) of one tile row's 64 elements
+// in a K step, stored as four swizzled 16-byte chunks.  Generic: the PfTile
+// loader's elements [32 p, +32) (chunks 4p .. 4p + 3), with compiler-tracked
+// loads.
+template <int FMT>
+struct PgHalf {
+    static constexpr bool MANUAL = false;
+    PfTile<FMT> t;
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t p) { t.load(wrow, k0, p); }
+    template <int N>
+    IFR_DEV void wait() {}
+    IFR_DEV void store(uint32_t k0, uint32_t p, _Float16 *tile, uint32_t r) const {
+        _Float16 h[32];
+        t.deq(k0, p, h);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint4 u;
+            __builtin_memcpy(&u, &h[8 * c], 16);
+            *(uint4 *)(tile + pg_swz(r, 4 * p + (uint32_t)c)) = u;
+        }
+    }
+};
+// Q4_K (quantization.rs:358-392): part p takes qs bytes [32 g + 16 p, +16)
+// of the step's group g = (k0 % 256) / 64: their low nibbles are elements
+// 16 p .. 16 p + 15 (sub-block 2g; chunks 2p, 2p + 1), their high nibbles
+// 32 + 16 p .. (sub-block 2g + 1; chunks 4 + 2p, 5 + 2p).  y = d1 * q - m1
+// with d1 = d * sc and m1 = dmin * m: d1 * q is exact in f32 (at most 11 +
+// 6 + 4 significant bits), so the fused multiply-add rounds once, exactly as
+// the reference's multiply then subtract does.  The loads are issued as
+// assembly and waited for with wait<N> (N = loads issued after them that may
+// stay in flight).
 template <>
-struct PgStage<Q4_K> {
-    static constexpr bool MANUAL = true; // loads issued as assembly, waited for with wait<N>
-    u32x4_a16 hv, q0, q1;
-    IFR_DEV void load(const uint8_t *wrow, uint32_t k0) {
+struct PgHalf<Q4_K> {
+    static constexpr bool MANUAL = true;
+    u32x4_a16 hv, qv;
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0, uint32_t p) {
         const uint8_t *b = wrow + (size_t)(k0 / 256) * 144;
         ld16_asm(hv, b);
-        ld16_asm(q0, b + 16 + 32 * ((k0 % 256) / 64));
-        ld16_asm(q1, b + 32 + 32 * ((k0 % 256) / 64));
+        ld16_asm(qv, b + 16 + 32 * ((k0 % 256) / 64) + 16 * p);
     }
-    // until at most N vector-memory loads issued after these are outstanding
     template <int N>
     IFR_DEV void wait() {
-        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(hv), "+v"(q0), "+v"(q1) : "n"(N));
+        asm volatile("s_waitcnt vmcnt(%2)" : "+v"(hv), "+v"(qv) : "n"(N));
     }
-    IFR_DEV void store(uint32_t k0, _Float16 *tile, uint32_t r) const {
+    IFR_DEV void store(uint32_t k0, uint32_t p, _Float16 *tile, uint32_t r) const {
 #pragma clang fp contract(off)
         uint32_t sc0, m0s, sc1, m1s;
         scale_min_pair((k0 % 256) / 64, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
         const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
         const float d1 = d * (float)sc0, n1 = -(dm * (float)m0s), d2 = d * (float)sc1, n2 = -(dm * (float)m1s);
-        const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        uint32_t lo[16], hi[16];
+        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+        uint32_t lo[8], hi[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < 4; i++) {
             const uint32_t l = q[i] & 0x0F0F0F0Fu, h = (q[i] >> 4) & 0x0F0F0F0Fu;
             lo[2 * i] = pack_f16x2(fmaf(d1, ub<0>(l), n1), fmaf(d1, ub<1>(l), n1));
             lo[2 * i + 1] = pack_f16x2(fmaf(d1, ub<2>(l), n1), fmaf(d1, ub<3>(l), n1));
@@ -141,93 +140,72 @@ struct PgStage<Q4_K> {
             hi[2 * i + 1] = pack_f16x2(fmaf(d2, ub<2>(h), n2), fmaf(d2, ub<3>(h), n2));
         }
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            *(uint4 *)(tile + pg_swz(r, (uint32_t)c)) = make_uint4(lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]);
-            *(uint4 *)(tile + pg_swz(r, (uint32_t)(4 + c))) =
+        for (int c = 0; c < 2; c++) {
+            *(uint4 *)(tile + pg_swz(r, 2 * p + (uint32_t)c)) = make_uint4(lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]);
+            *(uint4 *)(tile + pg_swz(r, 4 + 2 * p + (uint32_t)c)) =
                 make_uint4(hi[4 * c], hi[4 * c + 1], hi[4 * c + 2], hi[4 * c + 3]);
         }
     }
 };
 
-// The step's end: this wave's LDS stores are done, its direct X loads have
-// landed (the weight loads issued after them may still be in flight), then
-// the workgroup barrier.
-template <int NW>
-IFR_DEV void pg_step_barrier() {
-    if constexpr (NW == 3)
-        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// The order of a step's instructions: each of the 64 products followed by
-// 4 VALU instructions (the dequantization of the next step's weights), so
-// the vector ALU works while the matrix core runs instead of before it
-// (measured 2.5x faster than the compiler's own order, which put every
-// dequantization instruction before the first product).
-IFR_DEV void pg_interleave() {
-#pragma unroll
-    for (int m = 0; m < 64; m++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0); // VALU
-    }
-}
-
 // One workgroup's state over the K loop.
 template <int FMT>
 struct PgCtx {
-    _Float16 *xs[2], *ws[2];     // LDS tiles [PG_BM * PG_BK], [PG_BN * PG_BK], two buffers each
-    const _Float16 *x;           // X (wave-uniform)
-    uint32_t xoff[8];            // byte offsets of this lane's X rows of the direct loads, at its chunk
-    const uint8_t *wrow;         // this thread's weight row
-    uint32_t r, nk, lane, wave, wm, wn;
-    PgStage<FMT> st0, st1;       // weights of the next two steps
-    float16v acc[4][4];
+    _Float16 *xs[2], *ws[2];
+    const _Float16 *x;
+    uint32_t xoff[4];            // this lane's X rows of its four direct loads
+    const uint8_t *wrow;
+    uint32_t r, p, nk, lane, wave, wm, wn;
+    PgHalf<FMT> st0, st1;
+    float16v acc[4][2];
 
-    // X of step k into LDS buffer B: eight 1 KB direct loads per wave (lane
-    // l of load j fills row 64 w + 8 j + l / 8 at physical chunk l % 8)
+    // X of step k into buffer B: four 1 KB direct loads per wave (lane l of
+    // load j fills row 32 w + 8 j + l / 8 at physical chunk l % 8)
     template <int B>
     IFR_DEV void load_x(uint32_t k) {
-        const uint32_t dst = lds_addr(xs[B] + (64 * wave) * PG_BK);
+        const uint32_t dst = lds_addr(xs[B] + (32 * wave) * PG_BK);
 #pragma unroll
-        for (int j = 0; j < 8; j++) lds_dma16(x + k * PG_BK, xoff[j], __builtin_amdgcn_readfirstlane(dst + 1024 * j));
+        for (int j = 0; j < 4; j++) lds_dma16(x + k * PG_BK, xoff[j], __builtin_amdgcn_readfirstlane(dst + 1024 * j));
     }
-    // the products of one K step from LDS buffer B
     template <int B>
     IFR_DEV void mfma_step() {
         const _Float16 *xb = xs[B], *wb = ws[B];
         const uint32_t li = lane & 31u, hi = lane >> 5;
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
-            half8v av[4], bv[4];
+            half8v av[4], bv[2];
             const uint32_t c = 2 * (uint32_t)kk + hi;
 #pragma unroll
             for (int i = 0; i < 4; i++) av[i] = *(const half8v *)(xb + pg_swz(wm + 32 * i + li, c));
 #pragma unroll
-            for (int j = 0; j < 4; j++) bv[j] = *(const half8v *)(wb + pg_swz(wn + 32 * j + li, c));
+            for (int j = 0; j < 2; j++) bv[j] = *(const half8v *)(wb + pg_swz(wn + 32 * j + li, c));
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
     }
     // step s on buffer B: X of step s + 1 and the weights of step s + 2 are
     // requested, the products of step s run while the weights of step s + 1
-    // (register set B ^ 1) are dequantized into the other buffer.  Steps past
-    // the end load step nk - 1 again into buffers nobody reads.  Loads in
-    // flight at the wait: the 3 weight loads of step s + 1, then 8 X loads
-    // and 3 weight loads of this step.
+    // (register set B ^ 1) are dequantized into the other buffer; at the end
+    // this wave's LDS stores are done and its X loads have landed (the weight
+    // loads issued after them may stay in flight), then the barrier.  Steps
+    // past the end load step nk - 1 again into buffers nobody reads.  Loads in
+    // flight at the wait: the 2 weight loads of step s + 1, then 4 X loads and
+    // 2 weight loads of this step.
     template <int B>
     IFR_DEV void step(uint32_t s) {
-        PgStage<FMT> &ld = B ? st1 : st0, &dq = B ? st0 : st1;
+        PgHalf<FMT> &ld = B ? st1 : st0, &dq = B ? st0 : st1;
         load_x<B ^ 1>(min(s + 1, nk - 1));
-        ld.load(wrow, min(s + 2, nk - 1) * PG_BK);
-        dq.template wait<11>();
-        dq.store(min(s + 1, nk - 1) * PG_BK, ws[B ^ 1], r);
+        ld.load(wrow, min(s + 2, nk - 1) * PG_BK, p);
+        dq.template wait<6>();
+        dq.store(min(s + 1, nk - 1) * PG_BK, p, ws[B ^ 1], r);
         mfma_step<B>();
-        pg_interleave();
-        pg_step_barrier<PgStage<FMT>::MANUAL ? 3 : 0>();
+        if constexpr (PgHalf<FMT>::MANUAL)
+            asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
 };
 
@@ -245,9 +223,14 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
     g.ws[1] = ws1;
     g.lane = tid & 63u;
     g.wave = tid >> 6;
-    g.r = tid;
+    // weight staging: thread t takes part t % 2 of tile row t / 2 (mapping
+    // the 16 lanes of an LDS pass to 16 consecutive rows of one chunk, which
+    // removes the store bank conflicts, measured 0.4 ms slower per 8B
+    // prefill: the conflicts are not on the critical path)
+    g.r = tid >> 1;
+    g.p = tid & 1u;
     g.wm = 128 * (g.wave & 1u);
-    g.wn = 128 * (g.wave >> 1);
+    g.wn = 64 * (g.wave >> 1);
     g.nk = a.K / PG_BK;
     g.x = (const _Float16 *)a.x;
 
@@ -260,41 +243,41 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
     const uint32_t m0 = (t / tn) * PG_BM, n0 = (t % tn) * PG_BN;
 
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t row = 64 * g.wave + 8 * (uint32_t)j + (g.lane >> 3);
+    for (int j = 0; j < 4; j++) {
+        const uint32_t row = 32 * g.wave + 8 * (uint32_t)j + (g.lane >> 3);
         const uint32_t c = (g.lane & 7u) ^ pg_swz_of(row);
         g.xoff[j] = 2 * (min(m0 + row, a.M - 1) * a.ldx + 8 * c);
     }
-    const uint32_t r = tid;
+    const uint32_t r = g.r;
     if constexpr (EPI == PG_SWIGLU) {
-        // wave column c = r / 128 holds FFN rows j in [n0 / 2 + 64 c, +64):
-        // tile rows 128 c + 32 b + i are gate (b even) or up (b odd) row
-        // j = n0 / 2 + 64 c + 32 (b / 2) + i
-        const uint32_t bk = (r >> 5) & 3u;
-        const uint32_t j = min(n0 / 2 + 64 * (r >> 7) + 32 * (bk >> 1) + (r & 31u), a.n1 - 1);
-        g.wrow = (bk & 1u ? a.w1 : a.w0) + (size_t)j * a.row_bytes;
+        // wave column c = r / 64 holds FFN rows j in [n0 / 2 + 32 c, +32):
+        // tile rows 64 c + i are gate row j, 64 c + 32 + i up row j
+        const uint32_t j = min(n0 / 2 + 32 * (r >> 6) + (r & 31u), a.n1 - 1);
+        g.wrow = ((r >> 5) & 1u ? a.w1 : a.w0) + (size_t)j * a.row_bytes;
     } else {
         const uint32_t n = min(n0 + r, a.N - 1);
         const uint8_t *base = n < a.n1 ? a.w0 : n < a.n2 ? a.w1 : a.w2;
         const uint32_t nr = n < a.n1 ? n : n < a.n2 ? n - a.n1 : n - a.n2;
         g.wrow = base + (size_t)nr * a.row_bytes;
     }
-
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) g.acc[i][j][e] = 0.0f;
 
     // prologue: X and weights of step 0 into buffer 0, weights of step 1 in
     // flight
     g.template load_x<0>(0);
-    g.st0.load(g.wrow, 0);
-    g.st1.load(g.wrow, min(1u, g.nk - 1) * PG_BK);
-    g.st0.template wait<3>();
-    g.st0.store(0, ws0, r);
-    pg_step_barrier<PgStage<FMT>::MANUAL ? 3 : 0>();
+    g.st0.load(g.wrow, 0, g.p);
+    g.st1.load(g.wrow, min(1u, g.nk - 1) * PG_BK, g.p);
+    g.st0.template wait<2>();
+    g.st0.store(0, g.p, ws0, r);
+    if constexpr (PgHalf<FMT>::MANUAL)
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     for (uint32_t s = 0; s < g.nk; s += 2) {
         g.template step<0>(s);
         if (s + 1 < g.nk) g.template step<1>(s + 1);
@@ -305,24 +288,21 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
     // 4 (lane / 32) + e % 4 (m)
     const uint32_t lane = g.lane, li = lane & 31u, wm = g.wm, wn = g.wn;
     if constexpr (EPI == PG_SWIGLU) {
+        const uint32_t jn = n0 / 2 + wn / 2 + li;
+        if (jn >= a.n1) return;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const uint32_t jn = n0 / 2 + wn / 2 + 32 * q + li;
-            if (jn >= a.n1) continue;
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                    if (m < a.M) {
-                        const float gg = g.acc[i][2 * q][e], u = g.acc[i][2 * q + 1][e];
-                        ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = (_Float16)(u * (gg / (1.0f + expf(-gg))));
-                    }
+            for (int e = 0; e < 16; e++) {
+                const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                if (m < a.M) {
+                    const float gg = g.acc[i][0][e], u = g.acc[i][1][e];
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = (_Float16)(u * (gg / (1.0f + expf(-gg))));
                 }
-        }
+            }
     } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < 2; j++) {
             const uint32_t n = n0 + wn + 32 * j + li;
             if (n >= a.N) continue;
 #pragma unroll

@@ -54,30 +54,8 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
         const uint32_t nr = n < a.n1 ? n : n < a.n2 ? n - a.n1 : n - a.n2;
         wrow = base + (size_t)nr * a.row_bytes;
     }
-    uint4 xv[4];
+    u32x4_a16 x0, x1, x2, x3; // the next K step's X segment
     PfTile<FMT> wt;
-    auto gload = [&](uint32_t k0) {
-        const uint4 *xp = (const uint4 *)(xrow + k0 + 32 * hseg);
-#pragma unroll
-        for (int i = 0; i < 4; i++) xv[i] = xp[i];
-        wt.load(wrow, k0, hseg);
-    };
-    // this thread's 32 weights into LDS as f16
-    auto lstore = [&](uint32_t k0) {
-        _Float16 h[32];
-        wt.deq(k0, hseg, h);
-        uint4 *wd = (uint4 *)&ws[r][32 * hseg];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint4 u;
-            __builtin_memcpy(&u, &h[8 * i], 16);
-            wd[i] = u;
-        }
-        uint4 *xd = (uint4 *)&xs[r][32 * hseg];
-#pragma unroll
-        for (int i = 0; i < 4; i++) xd[i] = xv[i];
-    };
-
     float16v acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; i++)
@@ -88,11 +66,30 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
 
     const uint32_t wm = 64 * (uint32_t)(wave >> 1), wn = 64 * (uint32_t)(wave & 1);
     const uint32_t li = (uint32_t)lane & 31u, lk = 8 * ((uint32_t)lane >> 5);
-    gload(0);
+    const u32x4_a16 *xp = (const u32x4_a16 *)(xrow + 32 * hseg);
+    x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+    wt.load(wrow, 0, hseg);
     for (uint32_t k0 = 0; k0 < a.K; k0 += PF_BK) {
         __syncthreads(); // the previous step's operand reads are done
-        lstore(k0);
-        if (k0 + PF_BK < a.K) gload(k0 + PF_BK);
+        {
+            // this thread's 32 weights into LDS as f16, then its X segment
+            _Float16 h[32];
+            wt.deq(k0, hseg, h);
+            uint4 *wd = (uint4 *)&ws[r][32 * hseg];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint4 u;
+                __builtin_memcpy(&u, &h[8 * i], 16);
+                wd[i] = u;
+            }
+            u32x4_a16 *xd = (u32x4_a16 *)&xs[r][32 * hseg];
+            xd[0] = x0, xd[1] = x1, xd[2] = x2, xd[3] = x3;
+        }
+        if (k0 + PF_BK < a.K) {
+            const u32x4_a16 *xn = xp + (k0 + PF_BK) / 8;
+            x0 = xn[0], x1 = xn[1], x2 = xn[2], x3 = xn[3];
+            wt.load(wrow, k0 + PF_BK, hseg);
+        }
         __syncthreads();
 #pragma unroll
         for (int kk = 0; kk < PF_BK; kk += 16) {

@@ -47,7 +47,8 @@ constexpr uint32_t ATTN_SPLITS_MAX = 256; // attention splits per KV head (at mo
 constexpr uint32_t ATTN_GT_MAX = 8;       // device/attention.h: query heads per workgroup
 constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
 constexpr uint32_t PF_GEMM_TILE = 128;    // device/prefill.h: PF_BM = PF_BN
-constexpr uint32_t PF_BIG_TILE = 256;     // device/pf_gemm.h: PG_BM = PG_BN (and PG_THREADS threads)
+constexpr uint32_t PF_BIG_TILE = 256;     // device/pf_gemm.h: PG_BM = PG_BN
+constexpr uint32_t PF_BIG_THREADS = 512;  // device/pf_gemm.h: PG_THREADS
 constexpr uint32_t PF_CHUNK = 4096;       // prompt tokens per prefill pass (at most)
 
 int qk_of(int32_t dt) {
@@ -1630,7 +1631,7 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
     const bool big = big_ok && (c->pf_tile == 256 || (c->pf_tile == 0 && g.tiles_n * g.tiles_m >= PF_BIG_TILES_MIN));
     if (big)
         return c->launch(std::string("pf_gemm_") + gemv_fmt_name(m[0]->dtype) + "_" + epi_name[epi],
-                         dim3(g.tiles_n * g.tiles_m), dim3(PF_BIG_TILE), 0, g);
+                         dim3(g.tiles_n * g.tiles_m), dim3(PF_BIG_THREADS), 0, g);
     const dim3 grid((g.N + PF_GEMM_TILE - 1) / PF_GEMM_TILE, (M + PF_GEMM_TILE - 1) / PF_GEMM_TILE);
     return c->launch(std::string("gemm_") + gemv_fmt_name(m[0]->dtype) + "_f16_" + epi_name[epi], grid, dim3(256), 0, g);
 }

@@ -127,19 +127,19 @@ extern "C" __global__ void __launch_bounds__(256) dequant_k(DequantArgs a) { deq
 extern "C" __global__ void __launch_bounds__(64) quantize_k(QuantArgs a) { quantize_body(a); }
 extern "C" __global__ void __launch_bounds__(256) fill_normal_k(FillArgs a) { fill_normal_body(a); }
 
-// prompt (prefill) path: the GEMM in 256 x 256 tiles (four waves, one per
-// SIMD, with the accumulators in AGPRs) and in 128 x 128 tiles, each with
-// the store, accumulate and SwiGLU epilogues
+// prompt (prefill) path: the GEMM in 256 x 256 tiles (eight waves, two per
+// SIMD) and in 128 x 128 tiles, each with the store, accumulate and SwiGLU
+// epilogues
 #define PF_GEMM_KERNELS(FMTNAME, FMT)                                                                             \
-    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))           \
+    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))           \
     pf_gemm_##FMTNAME##_store(PfGemmArgs a) {                                                                     \
         pf_gemm_body<FMT, PG_STORE>(a);                                                                           \
     }                                                                                                             \
-    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))           \
+    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))           \
     pf_gemm_##FMTNAME##_add(PfGemmArgs a) {                                                                       \
         pf_gemm_body<FMT, PG_ADD>(a);                                                                             \
     }                                                                                                             \
-    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))           \
+    extern "C" __global__ void __launch_bounds__(PG_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))           \
     pf_gemm_##FMTNAME##_swiglu(PfGemmArgs a) {                                                                    \
         pf_gemm_body<FMT, PG_SWIGLU>(a);                                                                          \
     }                                                                                                             \
