@@ -62,10 +62,14 @@ def decode_token_bytes(cfg: I.Llama2Config, ctx_len: float, mat=I.Q4_K, head=I.Q
     return weights + kv_bytes
 
 
-def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, seed: int = 0) -> dict:
+def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, seed: int = 0,
+              keep_host: bool = False) -> dict:
     """Average launch time of the GEMV kernel the decode step uses
     (ifr_matmul_quant_xq on a pre-quantized x) over `iters` back-to-back
-    launches, rotating through enough weight copies to defeat the MALL."""
+    launches, rotating through enough weight copies to defeat the MALL; and
+    of ifr_matmul_quant as a caller sees it (x in f32, its quantization
+    inside the call) over the same rotation.  keep_host: also return the
+    first copy's bytes and x on the host (for the CPU baseline)."""
     n = rows * cols
     wbytes = rows * I.row_bytes(dtype, cols)
     copies = max(2, -(-ROT_BYTES // wbytes))
@@ -77,26 +81,54 @@ def time_gemv(ctx: I.LlmContext, dtype: int, rows: int, cols: int, iters: int, s
         ctx.quantize(b, tmp, dtype, n)
         ws.append(b)
     tmp.free()
-    x = ctx.upload(np.random.default_rng(seed).standard_normal(cols).astype(np.float32))
+    xh = np.random.default_rng(seed).standard_normal(cols).astype(np.float32)
+    x = ctx.upload(xh)
     xq = ctx.alloc(I.LlmContext.activation_bytes(cols))
     ctx.quantize_activation(xq, x, cols)  # once: the decode step's GEMVs get x quantized by its producer
     y = ctx.alloc(rows * 4)
     for i in range(copies):  # warm-up
         ctx.matmul_quant_xq(y, ws[i], dtype, rows, cols, xq)
+        ctx.matmul_quant_assign(y, ws[i], dtype, rows, cols, x)
     ctx.sync()
     ctx.event_record(2)
     for i in range(iters):
         ctx.matmul_quant_xq(y, ws[i % copies], dtype, rows, cols, xq)
     ctx.event_record(3)
     ms = ctx.event_elapsed(2, 3)
+    ctx.event_record(2)
+    for i in range(iters):
+        ctx.matmul_quant_assign(y, ws[i % copies], dtype, rows, cols, x)
+    ctx.event_record(3)
+    ms_f32 = ctx.event_elapsed(2, 3)
+    host_w = ws[0].download(np.uint8, wbytes) if keep_host else None
     for b in ws:
         b.free()
     x.free()
     xq.free()
     y.free()
-    us = ms * 1000.0 / iters
+    us, us_f32 = ms * 1000.0 / iters, ms_f32 * 1000.0 / iters
     nbytes = gemv_bytes(dtype, rows, cols)
-    return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
+    return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9, "us_f32x": us_f32,
+            "gbs_f32x": nbytes / (us_f32 * 1e-6) / 1e9, "host_w": host_w, "host_x": xh}
+
+
+def cpu_threads(args) -> int:
+    """Threads of the CPU baselines: --cpu-threads, else the cores this
+    process may run on (at most 16, the GPU box's CPU share)."""
+    if args.cpu_threads:
+        return args.cpu_threads
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_median_ms(fn, runs: int) -> float:
+    """One warm-up, then the median wall time of `runs` calls (ms)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1000.0)
+    return float(np.median(ts))
 
 
 MFMA_F16_PEAK = 2.5e15  # MI355X dense f16 matrix-core FLOP/s
@@ -179,7 +211,9 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
     """The CPU oracle (a C restatement of the reference's forward) timed on
     the host cores on a bounded sample: n_tokens decode steps of the same
     model bytes at the GPU leg's positions pos0.. (the oracle's cache rows
-    below pos0 are zeros, which cost the same attention work)."""
+    below pos0 are zeros, which cost the same attention work), with its
+    matrix products accumulated left to right in f32 as the reference's CPU
+    forward does (crates/inferi/src/models/llama2/cpu.rs:375-381)."""
     import oracle as O
 
     if not os.path.exists(O.LIB_PATH):
@@ -193,11 +227,12 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
              vocab=cfg.vocab, max_pos=pos0 + n_tokens + 1, rope_theta=cfg.rope_theta, rms_eps=cfg.rms_eps,
              kv_f16=1)
     m = O.Model(c, host)
-    m.forward(1, pos0, threads)  # warm the pages
-    t0 = time.perf_counter()
-    for p in range(pos0 + 1, pos0 + n_tokens + 1):
-        m.forward(p % cfg.vocab, p, threads)
-    dt = time.perf_counter() - t0
+    with O.f32_accumulation():
+        m.forward(1, pos0, threads)  # warm the pages
+        t0 = time.perf_counter()
+        for p in range(pos0 + 1, pos0 + n_tokens + 1):
+            m.forward(p % cfg.vocab, p, threads)
+        dt = time.perf_counter() - t0
     try:
         host_cores = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -205,7 +240,8 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
     return {"value": n_tokens / dt, "unit": "tok/s", "cores": threads, "host_cores": host_cores,
             "host_cpu_count": os.cpu_count(), "kind": "port",
             "sample": f"{n_tokens} decode tokens of the same 8B-shape model bytes at positions {pos0 + 1}-"
-                      f"{pos0 + n_tokens} (the GPU leg's context) through oracle/oracle.c ifo_forward, "
+                      f"{pos0 + n_tokens} (the GPU leg's context) through oracle/oracle.c ifo_forward with f32 "
+                      f"left-to-right GEMV accumulation (the reference CPU forward's arithmetic), "
                       f"{threads} threads on {host_cores} available cores"}
 
 
@@ -384,13 +420,26 @@ def run_sweep(args) -> None:
     if args.gemv_grp >= 0:
         ctx.set_option("gemv_grp", args.gemv_grp)
     rows_out = []
+    cpu = not args.no_cpu
+    if cpu:
+        import oracle as O  # the CPU baseline only: the reference shaders' decomposition on host threads
+
+        nthr = cpu_threads(args)
     for name, dt in (("Q4_K", I.Q4_K), ("Q5_K", I.Q5_K), ("Q6_K", I.Q6_K), ("Q8_0", I.Q8_0)):
         for rows, cols in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
-            g = time_gemv(ctx, dt, rows, cols, iters=args.gemv_iters)
+            g = time_gemv(ctx, dt, rows, cols, iters=args.gemv_iters, keep_host=cpu)
             rec = {"format": name, "rows": rows, "cols": cols, "us": round(g["us"], 3), "bytes": g["bytes"],
-                   "gbs": round(g["gbs"], 1), "frac": round(g["gbs"] / HBM_PEAK_GBS, 4)}
+                   "gbs": round(g["gbs"], 1), "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+                   "us_f32x": round(g["us_f32x"], 3), "gbs_f32x": round(g["gbs_f32x"], 1),
+                   "frac_f32x": round(g["gbs_f32x"] / HBM_PEAK_GBS, 4)}
+            if cpu:
+                w, x = g["host_w"], g["host_x"]
+                cms = cpu_median_ms(lambda: O.ref_gemv(dt, w, rows, cols, x, nthr), 5)
+                rec["cpu"] = {"ms": round(cms, 3), "gbs": round(g["bytes"] / (cms * 1e-3) / 1e9, 2), "threads": nthr}
             rows_out.append(rec)
-            log(f"sweep: {name} {rows}x{cols}: {g['us']:.2f} us, {g['gbs']:.0f} GB/s ({rec['frac'] * 100:.1f}%)")
+            log(f"sweep: {name} {rows}x{cols}: {g['us']:.2f} us, {g['gbs']:.0f} GB/s ({rec['frac'] * 100:.1f}%); "
+                f"f32 x {g['us_f32x']:.2f} us ({rec['frac_f32x'] * 100:.1f}%)"
+                + (f"; cpu {rec['cpu']['ms']:.2f} ms, {rec['cpu']['gbs']:.2f} GB/s" if cpu else ""))
     print(json.dumps({"sweep": rows_out}), flush=True)
     ctx.close()
 
@@ -483,8 +532,18 @@ def run_attn(args) -> None:
         us = ctx.event_elapsed(2, 3) * 1000.0 / iters
         nbytes = 2 * L * kv_dim * 2 + 2 * nh * hs * 4
         rec = {"L": L, "us": round(us, 3), "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        if not args.no_cpu:
+            import oracle as O  # the CPU baseline only: the reference shaders' decomposition on host threads
+
+            k16, v16 = caches[0]
+            kh, vh = k16.download(np.uint16, L * kv_dim), v16.download(np.uint16, L * kv_dim)
+            qh = np.random.default_rng(5).standard_normal(nh * hs).astype(np.float32)
+            nthr = cpu_threads(args)
+            cms = cpu_median_ms(lambda: O.ref_attention(qh, kh, vh, nh, nkv, hs, L - 1, nthr), 3)
+            rec["cpu"] = {"ms": round(cms, 3), "gbs": round(nbytes / (cms * 1e-3) / 1e9, 2), "threads": nthr}
         out.append(rec)
-        log(f"attn: L={L}: {us:.2f} us, {rec['gbs']:.0f} GB/s")
+        log(f"attn: L={L}: {us:.2f} us, {rec['gbs']:.0f} GB/s"
+            + (f"; cpu {rec['cpu']['ms']:.2f} ms, {rec['cpu']['gbs']:.2f} GB/s" if "cpu" in rec else ""))
         for k16, v16 in caches:
             k16.free()
             v16.free()

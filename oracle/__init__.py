@@ -56,6 +56,11 @@ def lib() -> C.CDLL:
         L.ifo_gemv_f64.argtypes = [vp, i, i, vp, vp]
         L.ifo_gemv_quant.argtypes = [i, vp, i, i, vp, vp, i]
         L.ifo_gemv_quant.restype = i
+        u32 = C.c_uint32
+        L.ifo_ref_gemv.argtypes = [C.c_int32, u32, u32, vp, vp, vp, i]
+        L.ifo_ref_gemv.restype = i
+        L.ifo_ref_attention.argtypes = [vp, vp, vp, u32, u32, u32, u32, vp, i]
+        L.ifo_ref_attention.restype = i
         L.ifo_rms_norm.argtypes = [vp, vp, vp, i, f]
         L.ifo_rope.argtypes = [i, vp, i, vp, i, i, i, f]
         L.ifo_silu_mul.argtypes = [vp, vp, i]
@@ -184,6 +189,33 @@ def attention(q, k_cache, v_cache, n_heads: int, n_kv_heads: int, head_size: int
     p = AttnParams(k_cache.shape[0], kv_dim, n_heads // n_kv_heads, n_heads, head_size, pos)
     out = np.empty(n_heads * head_size, np.float32)
     lib().ifo_attention(C.byref(p), _p(q), _p(k_cache), _p(v_cache), int(kv_f16), _p(out))
+    return out
+
+
+def ref_gemv(dtype: int, w, rows: int, cols: int, x: np.ndarray, nthreads: int = 1) -> np.ndarray:
+    """The reference GEMV shader's decomposition on host threads
+    (oracle/ref_shaders.c): the CPU baseline of the GEMV configs."""
+    w = np.ascontiguousarray(w).view(np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    assert w.size >= rows * row_bytes(dtype, cols) and x.size == cols
+    y = np.empty(rows, np.float32)
+    if lib().ifo_ref_gemv(dtype, rows, cols, _p(w), _p(x), _p(y), nthreads) != 0:
+        raise ValueError("ref_gemv: a shape the reference shader does not take")
+    return y
+
+
+def ref_attention(q, k_cache, v_cache, n_heads: int, n_kv_heads: int, head_size: int, pos: int,
+                  nthreads: int = 1) -> np.ndarray:
+    """The reference attention shaders' decomposition on host threads over
+    f16 caches (uint16 codes, [>= pos + 1, kv_dim]): fused_attention up to
+    2048 positions, flash_attention beyond."""
+    q = np.ascontiguousarray(q, np.float32)
+    k_cache = np.ascontiguousarray(k_cache, np.uint16)
+    v_cache = np.ascontiguousarray(v_cache, np.uint16)
+    out = np.empty(n_heads * head_size, np.float32)
+    if lib().ifo_ref_attention(_p(q), _p(k_cache), _p(v_cache), n_heads, n_kv_heads, head_size, pos, _p(out),
+                               nthreads) != 0:
+        raise ValueError("ref_attention: bad shape")
     return out
 
 

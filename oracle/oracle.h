@@ -168,6 +168,17 @@ int ifo_forward(const ifo_model *m, ifo_state *s, int token, int pos, float *log
 /* Access to the state for checks: which = 0 x, 1 k_cache layer, 2 v_cache layer. */
 const void *ifo_state_buffer(const ifo_state *s, int which, int layer);
 
+/* CPU baseline (oracle/ref_shaders.c): the reference's GEMV and decode
+ * attention shader decompositions restated on host threads.  ifo_ref_gemv:
+ * y[rows] = W x for Q4_K, Q5_K (cols % 256), Q6_K (block pairs, cols % 512)
+ * or Q8_0 (block pairs, cols % 128), rows % 4 == 0.  ifo_ref_attention:
+ * one query head per workgroup over cache rows 0..pos (f16 caches
+ * [pos + 1][n_kv_heads * head_size]), out[n_heads * head_size].  Return 0,
+ * or -1 for a shape the shaders do not take. */
+int ifo_ref_gemv(int32_t dtype, uint32_t rows, uint32_t cols, const void *w, const float *x, float *y, int nthreads);
+int ifo_ref_attention(const float *q, const uint16_t *k_cache, const uint16_t *v_cache, uint32_t n_heads,
+                      uint32_t n_kv_heads, uint32_t head_size, uint32_t pos, float *out, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif
