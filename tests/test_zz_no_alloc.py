@@ -1,9 +1,23 @@
 """ifr_matmul_quant_noalloc (the entry point that allocates nothing) against
 ifr_matmul_quant, through the C ABI: the same kernels, so the outputs are
-identical; two calls in a row, the second smaller, share the fixed scratch."""
+identical; two calls in a row, the second smaller, share the fixed scratch;
+the device's free memory (hipMemGetInfo) is the same before and after the
+calls."""
+
+import ctypes
 
 import numpy as np
 import pytest
+
+
+def _free_bytes(ctx):
+    """Free device memory as the HIP runtime reports it, after draining the
+    context's stream."""
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime the library is linked against
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    ctx.sync()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
 
 
 @pytest.mark.gpu
@@ -21,7 +35,12 @@ def test_noalloc_matches_matmul_quant(ctx, path):
             dw, dx = ctx.upload(w), ctx.upload(x)
             y1, y2 = ctx.alloc(rows * 4), ctx.alloc(rows * 4)
             ctx.matmul_quant_assign(y1, dw, dtype, rows, cols, dx)
-            ctx.matmul_quant_noalloc(y2, dw, dtype, rows, cols, dx)
+            ctx.matmul_quant_noalloc(y2, dw, dtype, rows, cols, dx)  # warm-up: modules loaded
+            before = _free_bytes(ctx)
+            for _ in range(3):
+                ctx.matmul_quant_noalloc(y2, dw, dtype, rows, cols, dx)
+            after = _free_bytes(ctx)
+            assert after == before, f"device free memory changed by {before - after} bytes across the calls"
             a, b = y1.download(np.float32, rows), y2.download(np.float32, rows)
             print(f"{path} {rows}x{cols} dtype {dtype}: max |diff| {np.abs(a - b).max():.3e}", flush=True)
             assert np.array_equal(a, b), "noalloc output differs from ifr_matmul_quant"
