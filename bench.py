@@ -43,6 +43,15 @@ CFG_C4 = dict(n_layers=22, hidden=2048, ffn=5632, n_heads=32, n_kv_heads=4, voca
               rms_eps=1e-5)
 
 
+def make_ctx(args):
+    """The library context with the options given by --opt KEY=VALUE."""
+    ctx = I.LlmContext(0, args.code_object)
+    for kv in args.opt:
+        k, v = kv.split("=", 1)
+        ctx.set_option(k, int(v))
+    return ctx
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -246,7 +255,7 @@ def cpu_baseline(cfg: I.Llama2Config, weights: I.Llama2Weights, n_tokens: int, t
 
 
 def run_decode(args) -> None:
-    ctx = I.LlmContext(0, args.code_object)
+    ctx = make_ctx(args)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
     if args.gemv_grp >= 0:
@@ -414,7 +423,7 @@ def run_decode(args) -> None:
 
 
 def run_sweep(args) -> None:
-    ctx = I.LlmContext(0, args.code_object)
+    ctx = make_ctx(args)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
     if args.gemv_grp >= 0:
@@ -451,7 +460,7 @@ def run_pmc_sample(args) -> None:
     WRITE_SIZE; then the op-level GEMV (gemv_q4_k_plain_one 14336x4096) on
     weight copies rotated past the Infinity Cache; then each stage of the
     8B decode step at position 4100, twice over the 32 layers."""
-    ctx = I.LlmContext(0, args.code_object)
+    ctx = make_ctx(args)
     n = 64 << 20
     a, b = ctx.alloc(n * 4), ctx.alloc(n * 4)
     ctx.fill_normal(a, n, 1, 0, 0.0, 1.0)
@@ -478,7 +487,7 @@ def run_pmc_sample(args) -> None:
 def run_pf_sample(args) -> None:
     """Workload for the rocprofv3 --pmc passes on the prefill kernels: the
     8B model's 4095-token prompt through ifr_llama2_prefill, twice."""
-    ctx = I.LlmContext(0, args.code_object)
+    ctx = make_ctx(args)
     cfg = I.Llama2Config(max_pos=args.prompt + 8, kv_dtype=I.F16, **CFG_8B)
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=args.seed)
     s = I.Llama2State(ctx, cfg)
@@ -496,7 +505,7 @@ def run_pf_sample(args) -> None:
 
 
 def run_attn(args) -> None:
-    ctx = I.LlmContext(0, args.code_object)
+    ctx = make_ctx(args)
     ctx.set_option("gemv_max_grid", args.gemv_grid)
     ctx.set_option("gemv_waves", args.gemv_waves)
     if args.gemv_grp >= 0:
@@ -576,6 +585,7 @@ def main() -> None:
     ap.add_argument("--pmc-sample", action="store_true", help="workload for the rocprofv3 --pmc traffic passes")
     ap.add_argument("--pf-sample", action="store_true", help="workload for the rocprofv3 --pmc prefill passes")
     ap.add_argument("--code-object", default=None, help="another build of the kernels' code object")
+    ap.add_argument("--opt", action="append", default=[], help="library option KEY=VALUE (repeatable)")
     ap.add_argument("--gemv-grid", type=int, default=0, help="GEMV workgroups (0: chosen by shape)")
     ap.add_argument("--gemv-waves", type=int, default=0, help="waves per GEMV workgroup (0: chosen by shape)")
     ap.add_argument("--gemv-grp", type=int, default=-1, help="GEMV form mask (option gemv_grp; -1: the library default, whose kernels the stage lines name)")

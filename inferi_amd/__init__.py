@@ -69,6 +69,7 @@ SIGNATURES = {
     "ifr_last_error": (_cp, [_vp]),
     "ifr_device_info": (_i32, [_vp, _cp, _sz, C.POINTER(_i32)]),
     "ifr_set_option": (_i32, [_vp, _cp, C.c_int64]),
+    "ifr_get_option": (_i32, [_vp, _cp, C.POINTER(C.c_int64)]),
     "ifr_alloc": (_i32, [_vp, _sz, C.POINTER(_vp)]),
     "ifr_free": (_i32, [_vp, _vp]),
     "ifr_upload": (_i32, [_vp, _vp, _vp, _sz]),
@@ -226,6 +227,11 @@ class LlmContext:
 
     def set_option(self, key: str, value: int) -> None:
         self._check(lib().ifr_set_option(self.h, key.encode(), int(value)))
+
+    def get_option(self, key: str) -> int:
+        v = C.c_int64()
+        self._check(lib().ifr_get_option(self.h, key.encode(), C.byref(v)))
+        return v.value
 
     def alloc(self, nbytes: int) -> DeviceBuffer:
         return DeviceBuffer(self, nbytes)

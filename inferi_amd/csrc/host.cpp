@@ -142,6 +142,9 @@ struct ifr_ctx {
     // has enough of them, else 128 x 128), 128 or 256 to force one (option
     // pf_tile)
     uint32_t pf_tile = 0;
+    // bumped by every option change: a captured decode step is captured
+    // again when it differs
+    uint64_t opt_gen = 0;
 
     ifr_status fail(ifr_status st, const char *fmt, ...) {
         char buf[1024];
@@ -464,7 +467,7 @@ struct ifr_llama2_state {
     uint32_t sampler_gen = 0;
     // captured decode step
     hipGraphExec_t graph = nullptr;
-    int graph_grp = -1;
+    uint64_t graph_opt = ~0ull; // the context's option generation the graph was captured with
     uint32_t graph_sampler = 0;
     uint32_t graph_spec = 0; // step_spec the graph was captured with
     // graphs replaced while their launches may still run: destroyed once the
@@ -472,7 +475,6 @@ struct ifr_llama2_state {
     std::vector<std::pair<hipGraphExec_t, hipEvent_t>> retired;
     uint64_t graph_wid = 0, graph_wgen = 0; // weights id and generation the graph was captured with
     int graph_fused = -1;
-    int graph_exact = -1;
 };
 
 static ifr_status validate_cfg(ifr_ctx *c, const ifr_llama2_config *cfg) {
@@ -955,6 +957,7 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *c, char *name, size_t name_len, int3
 
 IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
     if (!c || !key) return IFR_EINVAL;
+    c->opt_gen++;
     if (!strcmp(key, "gemv_max_grid")) {
         c->gemv_max_grid = (uint32_t)std::max<int64_t>(0, value);
         return IFR_OK;
@@ -985,6 +988,19 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         return IFR_OK;
     }
     return c->fail(IFR_EINVAL, "unknown option %s", key);
+}
+
+IFR_API ifr_status ifr_get_option(ifr_ctx *c, const char *key, int64_t *value) {
+    if (!c || !key || !value) return IFR_EINVAL;
+    const std::string k = key;
+    if (k == "gemv_max_grid") *value = c->gemv_max_grid;
+    else if (k == "gemv_exact") *value = c->gemv_exact;
+    else if (k == "pf_chunk") *value = c->pf_chunk;
+    else if (k == "pf_tile") *value = c->pf_tile;
+    else if (k == "gemv_grp") *value = c->gemv_grp;
+    else if (k == "gemv_waves") *value = c->gemv_waves;
+    else return c->fail(IFR_EINVAL, "unknown option %s", key);
+    return IFR_OK;
 }
 
 IFR_API ifr_status ifr_alloc(ifr_ctx *c, size_t bytes, void **p) {
@@ -1852,8 +1868,7 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
     while (done < n_steps) {
         const uint32_t spec = attn_spec_for(s->host_pos, s->cfg.max_pos);
         if (!s->graph || s->graph_wid != w->id || s->graph_wgen != w->gen || s->graph_fused != 1 ||
-            s->graph_exact != c->gemv_exact || s->graph_sampler != s->sampler_gen || s->graph_grp != c->gemv_grp ||
-            s->graph_spec != spec) {
+            s->graph_opt != c->opt_gen || s->graph_sampler != s->sampler_gen || s->graph_spec != spec) {
             if (s->graph) {
                 hipEvent_t ev = nullptr;
                 if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess &&
@@ -1883,9 +1898,8 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *c, ifr_llama2_state *s, const if
             s->graph_wid = w->id;
             s->graph_wgen = w->gen;
             s->graph_fused = 1;
-            s->graph_exact = c->gemv_exact;
+            s->graph_opt = c->opt_gen;
             s->graph_sampler = s->sampler_gen;
-            s->graph_grp = c->gemv_grp;
             s->graph_spec = spec;
         }
         // steps left in this bucket (the last position, max_pos - 1, repeats)
