@@ -303,6 +303,72 @@ def test_c5_8b_first_steps(ctx, oracle_lib, exact, n_gen):
 
 
 @pytest.mark.timeout(1100)
+def test_c5_8b_prefill_against_oracle(ctx, oracle_lib):
+    """BASELINE config 5 at full size through ifr_llama2_prefill: a 130-token
+    prompt, 129 of its tokens prefilled on the matrix cores, on the 256 x
+    256-tile kernel and on the 128 x 128 one, then 4 greedy graph steps; the
+    oracle runs the same sequence token by token (the reference's prompt
+    path, chat_llama2.rs:137-160).  Bars (f16 operands on the matrix cores):
+    every layer's K/V rows of the prefilled positions normwise within 2e-2 of
+    the oracle's, the decode steps' logits within 5e-2 scaled, and the greedy
+    ids where the oracle's top-2 gap exceeds twice the device's error; the
+    two tile forms bit-identical."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=32, hidden=4096, ffn=14336, n_heads=32, n_kv_heads=8, vocab=128256, max_pos=140,
+                         rope_theta=500000.0, rms_eps=1e-5, kv_dtype=I.F16)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=2000)
+    P, N = 130, 4
+    prompt = np.random.default_rng(130).integers(0, cfg.vocab, P).tolist()
+    runs = {}
+    try:
+        for tile in (256, 128):
+            ctx.set_option("pf_tile", tile)
+            s = I.Llama2State(ctx, cfg)
+            try:
+                s.reset(prompt, 0)
+                I.Llama2.prefill(ctx, s, w, P - 1)
+                logits = []
+                for _ in range(N):
+                    I.Llama2.generate(ctx, s, w, 1, use_graph=True)
+                    logits.append(s.read("logits").copy())
+                kv = [O.decode_f16(s.read(n, np.uint16, layer).reshape(cfg.max_pos, cfg.kv_dim)[: P - 1])
+                      for layer in range(cfg.n_layers) for n in ("key_cache", "value_cache")]
+                runs[tile] = (logits, s.tokens(0, P + N), kv)
+            finally:
+                s.close()
+        ctx.set_option("pf_tile", 0)
+        for a, b in zip(runs[256][0], runs[128][0]):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), "tile forms differ"
+        logits, toks, kv = runs[256]
+        m = oracle_model(cfg, w)
+        refs = [m.forward(int(toks[pos]), pos) for pos in range(P + N - 1)]
+        worst_kv = 0.0
+        for layer in range(cfg.n_layers):
+            for i, key in enumerate(("k", "v")):
+                e = O.decode_f16(m.kv_cache(layer, key)[: P - 1]).astype(np.float64)
+                nw = float(np.abs(kv[2 * layer + i] - e).max() / np.abs(e).max())
+                worst_kv = max(worst_kv, nw)
+                assert nw <= 2e-2, f"layer {layer} {key}: normwise {nw:.3e}"
+        ids, worst = 0, 0.0
+        for i in range(N):
+            pos = P - 1 + i
+            ref = refs[pos]
+            err = scaled_err(logits[i], ref)
+            worst = max(worst, err)
+            assert err <= 5e-2, f"pos {pos}: scaled error {err:.3e}"
+            top = np.sort(ref)[-2:]
+            if top[1] - top[0] > 2 * np.abs(logits[i] - ref).max():
+                assert int(toks[pos + 1]) == O.argmax(ref), f"greedy id at pos {pos + 1}"
+                ids += 1
+        print(f"c5 prefill of {P - 1} tokens vs the oracle: K/V rows within {worst_kv:.2e} (normwise), next "
+              f"{N} steps' logits within {worst:.2e} (scaled), {ids}/{N} greedy ids compared and identical", flush=True)
+    finally:
+        ctx.set_option("pf_tile", 0)
+        w.close()
+
+
+@pytest.mark.timeout(1100)
 def test_c5_8b_at_benchmark_context(ctx, oracle_lib):
     """BASELINE config 5 at the benchmark's own context: the full 8B shape
     with random f16 K/V rows planted at positions 0..4099 of every layer
