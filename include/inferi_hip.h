@@ -208,6 +208,27 @@ IFR_API ifr_status ifr_rope(ifr_ctx *ctx, int32_t variant, const ifr_rope_config
  * (inferi-shaders/src/silu.rs:24-53). */
 IFR_API ifr_status ifr_silu(ifr_ctx *ctx, float *in_out_h1, const float *h2, uint32_t n);
 
+/* Strided views of the same four ops.  The reference's op shaders index
+ * every operand through its tensor layout (shape.it(..): rms_norm.rs:118-119,
+ * rope.rs:81-87 and 129-132, silu.rs:46-47), so an operand may be a view of
+ * a larger buffer.  Here a view is (offset, stride) in elements: element i
+ * of the operand is base[offset + i * stride].  As in the reference, a RoPE
+ * pair's second element lies 1 (Original) or head_size / 2 (NeoX) elements
+ * after its first in memory, whatever the stride.  The caller sizes the
+ * buffers; the library cannot check views against them. */
+typedef struct {
+    int64_t offset;
+    int64_t stride;
+} ifr_view;
+IFR_API ifr_status ifr_rms_norm_view(ifr_ctx *ctx, const ifr_rms_norm_config *dev_cfg, float *out, ifr_view out_v,
+                                     const float *value, ifr_view value_v, const float *weight, ifr_view weight_v,
+                                     uint32_t n);
+IFR_API ifr_status ifr_add_view(ifr_ctx *ctx, float *in_out_a, ifr_view a_v, const float *b, ifr_view b_v, uint32_t n);
+IFR_API ifr_status ifr_rope_view(ifr_ctx *ctx, int32_t variant, const ifr_rope_config *dev_cfg, float *q, ifr_view q_v,
+                                 uint32_t q_len, float *k, ifr_view k_v, uint32_t k_len);
+IFR_API ifr_status ifr_silu_view(ifr_ctx *ctx, float *in_out_h1, ifr_view h1_v, const float *h2, ifr_view h2_v,
+                                 uint32_t n);
+
 /* Decode attention of one token over the KV cache:
  * xb[h] = softmax_t((q[h] . k_t[h/kv_mul]) / sqrt(head_size)) . v_t, t in [0, pos].
  * Caches are [seq_len][kv_dim] row-major, kv_dtype IFR_F32 (the reference's

@@ -61,6 +61,11 @@ class Llama2ConfigC(C.Structure):
         ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("kv_dtype", C.c_int32), ("rope_variant", C.c_int32)]
 
 
+class View(C.Structure):
+    """ifr_view: element i of an operand at base[offset + i * stride]."""
+    _fields_ = [("offset", C.c_int64), ("stride", C.c_int64)]
+
+
 # Every symbol include/inferi_hip.h declares, with its ctypes signature.
 _vp, _i32, _u32, _u64, _sz, _f, _cp = C.c_void_p, C.c_int32, C.c_uint32, C.c_uint64, C.c_size_t, C.c_float, C.c_char_p
 SIGNATURES = {
@@ -89,6 +94,10 @@ SIGNATURES = {
     "ifr_add": (_i32, [_vp, _vp, _vp, _u32]),
     "ifr_rope": (_i32, [_vp, _i32, _vp, _vp, _u32, _vp, _u32]),
     "ifr_silu": (_i32, [_vp, _vp, _vp, _u32]),
+    "ifr_rms_norm_view": (_i32, [_vp, _vp, _vp, View, _vp, View, _vp, View, _u32]),
+    "ifr_add_view": (_i32, [_vp, _vp, View, _vp, View, _u32]),
+    "ifr_rope_view": (_i32, [_vp, _i32, _vp, _vp, View, _u32, _vp, View, _u32]),
+    "ifr_silu_view": (_i32, [_vp, _vp, View, _vp, View, _u32]),
     "ifr_attention": (_i32, [_vp, C.POINTER(AttentionParams), _vp, _vp, _vp, _vp, _i32, _vp]),
     "ifr_argmax": (_i32, [_vp, _vp, _u32, _vp]),
     "ifr_sample": (_i32, [_vp, _vp, _vp, _u32, _f, _f, _vp, _vp]),
@@ -297,6 +306,21 @@ class LlmContext:
 
     def silu(self, in_out_h1, in_h2, n: int) -> None:
         self._check(lib().ifr_silu(self.h, _ptr(in_out_h1), _ptr(in_h2), n))
+
+    # strided views (offset, stride) in elements, as the reference ops take tensor layouts
+    def rms_norm_view(self, config, out, ov, value, vv, weight, wv, n: int) -> None:
+        self._check(lib().ifr_rms_norm_view(self.h, _ptr(config), _ptr(out), View(*ov), _ptr(value), View(*vv),
+                                            _ptr(weight), View(*wv), n))
+
+    def add_view(self, in_out_a, av, b, bv, n: int) -> None:
+        self._check(lib().ifr_add_view(self.h, _ptr(in_out_a), View(*av), _ptr(b), View(*bv), n))
+
+    def rope_view(self, variant: int, config, q, qv, q_len: int, k, kv, k_len: int) -> None:
+        self._check(lib().ifr_rope_view(self.h, variant, _ptr(config), _ptr(q), View(*qv), q_len, _ptr(k), View(*kv),
+                                        k_len))
+
+    def silu_view(self, h1, av, h2, bv, n: int) -> None:
+        self._check(lib().ifr_silu_view(self.h, _ptr(h1), View(*av), _ptr(h2), View(*bv), n))
 
     def argmax(self, v, n: int, out_index) -> None:
         self._check(lib().ifr_argmax(self.h, _ptr(v), n, _ptr(out_index)))

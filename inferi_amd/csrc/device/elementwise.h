@@ -6,6 +6,10 @@
 
 namespace ifr {
 
+// The operands are views: element i of a sits at a.a[i * a.sa] (likewise b,
+// w, k), as the reference shaders index through their tensor layouts
+// (shape.it(..), rms_norm.rs:118-119, rope.rs:81-87, silu.rs:46-47).
+
 // RMSNorm with one 1024-thread workgroup (inferi-shaders/src/rms_norm.rs:81-121):
 // rms = 1 / sqrt(sum(x^2)/n + eps); out = (x * rms) * w.
 __device__ void rms_norm_body(const EltArgs &a) {
@@ -13,7 +17,7 @@ __device__ void rms_norm_body(const EltArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float eps = ((const ifr_rms_cfg_dev *)a.cfg)->nudge_factor;
     float ss = 0.0f;
-    for (uint32_t i = tid; i < a.n; i += blockDim.x) ss = fmaf(a.b[i], a.b[i], ss);
+    for (uint32_t i = tid; i < a.n; i += blockDim.x) ss = fmaf(a.b[i * a.sb], a.b[i * a.sb], ss);
     ss = wave_sum(ss);
     if (lane == 0) red[wave] = ss;
     __syncthreads();
@@ -24,11 +28,14 @@ __device__ void rms_norm_body(const EltArgs &a) {
     }
     __syncthreads();
     const float rms = 1.0f / sqrtf(red[0] / (float)a.n + eps);
-    for (uint32_t i = tid; i < a.n; i += blockDim.x) a.a[i] = (a.b[i] * rms) * a.w[i];
+    for (uint32_t i = tid; i < a.n; i += blockDim.x) a.a[i * a.sa] = (a.b[i * a.sb] * rms) * a.w[i * a.sw];
 }
 
 // RoPE (inferi-shaders/src/rope.rs:51-92 Original, :97-141 NeoX).  Thread i
-// rotates pair i of q and, while 2i < kv_dim, the same pair of k.
+// rotates pair i of q and, while 2i < kv_dim, the same pair of k.  Through a
+// view, the pair's first element is the view's element iq and its second
+// lies `shift` elements after it in memory (rope.rs:81-84, 129-132: the
+// partner is at it(..) + 1, or + head_size / 2).
 __device__ void rope_body(const EltArgs &a) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= a.n / 2) return;
@@ -48,14 +55,16 @@ __device__ void rope_body(const EltArgs &a) {
         shift = 1;
     }
     if (iq + shift >= a.n) return;
-    float x = a.a[iq], y = a.a[iq + shift];
-    a.a[iq] = cs * x - sn * y;
-    a.a[iq + shift] = sn * x + cs * y;
+    float *q0 = a.a + iq * a.sa;
+    float x = q0[0], y = q0[shift];
+    q0[0] = cs * x - sn * y;
+    q0[shift] = sn * x + cs * y;
     if (i * 2 < c.kv_dim && iq + shift < a.n2) {
-        x = a.k[iq];
-        y = a.k[iq + shift];
-        a.k[iq] = cs * x - sn * y;
-        a.k[iq + shift] = sn * x + cs * y;
+        float *k0 = a.k + iq * a.sk;
+        x = k0[0];
+        y = k0[shift];
+        k0[0] = cs * x - sn * y;
+        k0[shift] = sn * x + cs * y;
     }
 }
 
@@ -63,13 +72,13 @@ __device__ void rope_body(const EltArgs &a) {
 __device__ void silu_body(const EltArgs &a) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= a.n) return;
-    const float h = a.a[i];
-    a.a[i] = a.b[i] * (h / (1.0f + expf(-h)));
+    const float h = a.a[i * a.sa];
+    a.a[i * a.sa] = a.b[i * a.sb] * (h / (1.0f + expf(-h)));
 }
 
 __device__ void add_body(const EltArgs &a) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < a.n) a.a[i] = a.a[i] + a.b[i];
+    if (i < a.n) a.a[i * a.sa] = a.a[i * a.sa] + a.b[i * a.sb];
 }
 
 // Per-workgroup best key over a grid-stride range of v.

@@ -1185,6 +1185,71 @@ IFR_API ifr_status ifr_silu(ifr_ctx *c, float *h1, const float *h2, uint32_t n) 
     return c->launch("silu_k", dim3((n + 255) / 256), dim3(256), 0, a);
 }
 
+// ------------------------------------------------- strided operand views
+
+IFR_API ifr_status ifr_rms_norm_view(ifr_ctx *c, const ifr_rms_norm_config *cfg, float *out, ifr_view ov,
+                                     const float *value, ifr_view vv, const float *weight, ifr_view wv, uint32_t n) {
+    if (!c) return IFR_EINVAL;
+    if (!cfg || !out || !value || !weight) return c->fail(IFR_EINVAL, "rms_norm_view: null pointer");
+    if (!n) return IFR_OK;
+    EltArgs a{};
+    a.a = out + ov.offset;
+    a.b = value + vv.offset;
+    a.w = weight + wv.offset;
+    a.sa = ov.stride;
+    a.sb = vv.stride;
+    a.sw = wv.stride;
+    a.cfg = cfg;
+    a.n = n;
+    return c->launch("rms_norm_k", dim3(1), dim3(1024), 0, a);
+}
+
+IFR_API ifr_status ifr_add_view(ifr_ctx *c, float *x, ifr_view xv, const float *b, ifr_view bv, uint32_t n) {
+    if (!c) return IFR_EINVAL;
+    if (!x || !b) return c->fail(IFR_EINVAL, "add_view: null pointer");
+    if (!n) return IFR_OK;
+    EltArgs a{};
+    a.a = x + xv.offset;
+    a.b = b + bv.offset;
+    a.sa = xv.stride;
+    a.sb = bv.stride;
+    a.n = n;
+    return c->launch("add_k", dim3((n + 255) / 256), dim3(256), 0, a);
+}
+
+IFR_API ifr_status ifr_rope_view(ifr_ctx *c, int32_t variant, const ifr_rope_config *cfg, float *q, ifr_view qv,
+                                 uint32_t q_len, float *k, ifr_view kv, uint32_t k_len) {
+    if (!c) return IFR_EINVAL;
+    if (!cfg || !q) return c->fail(IFR_EINVAL, "rope_view: null pointer");
+    if (variant != IFR_ROPE_ORIGINAL && variant != IFR_ROPE_NEOX) return c->fail(IFR_EINVAL, "rope_view: bad variant");
+    if (q_len % 2 || k_len % 2) return c->fail(IFR_EINVAL, "rope_view: q_len and k_len must be even (ops/rope.rs:39-44)");
+    if (k_len && !k) return c->fail(IFR_EINVAL, "rope_view: null k");
+    if (!q_len) return IFR_OK;
+    EltArgs a{};
+    a.a = q + qv.offset;
+    a.k = k ? k + kv.offset : nullptr;
+    a.sa = qv.stride;
+    a.sk = kv.stride;
+    a.cfg = cfg;
+    a.n = q_len;
+    a.n2 = k_len;
+    a.variant = variant;
+    return c->launch("rope_k", dim3((q_len / 2 + 255) / 256), dim3(256), 0, a);
+}
+
+IFR_API ifr_status ifr_silu_view(ifr_ctx *c, float *h1, ifr_view av, const float *h2, ifr_view bv, uint32_t n) {
+    if (!c) return IFR_EINVAL;
+    if (!h1 || !h2) return c->fail(IFR_EINVAL, "silu_view: null pointer");
+    if (!n) return IFR_OK;
+    EltArgs a{};
+    a.a = h1 + av.offset;
+    a.b = h2 + bv.offset;
+    a.sa = av.stride;
+    a.sb = bv.stride;
+    a.n = n;
+    return c->launch("silu_k", dim3((n + 255) / 256), dim3(256), 0, a);
+}
+
 IFR_API ifr_status ifr_attention(ifr_ctx *c, const ifr_attn_params *p, const ifr_attn_params *dev_p, const float *q,
                                  const void *kc, const void *vc, int32_t kv_dtype, float *xb) {
     if (!c) return IFR_EINVAL;

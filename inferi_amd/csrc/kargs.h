@@ -116,6 +116,9 @@ struct EltArgs {
     uint32_t n, n2;
     int32_t variant;
     uint32_t pad;
+    // element strides of the views a, b, w and k (the pointers already at
+    // the views' first elements); 1 for contiguous vectors
+    int64_t sa = 1, sb = 1, sw = 1, sk = 1;
 };
 
 struct DequantArgs {
