@@ -1527,9 +1527,10 @@ __device__ void gemv_int_body(const GemvArgs &a) {
 // work (staging, the RMSNorm scale, the reductions, the epilogue, which
 // lanes 0 and 1 run side by side for two outputs) serves twice the rows.
 // Same arithmetic and order as gemv_int_body for every R.
-template <int FMT, int MODE, int R = 2>
+template <int FMT, int MODE, int R = 2, bool XF = false>
 __device__ void gemv_one_body(const GemvArgs &a) {
     static_assert(R == 2 || R == 4, "two or four rows per wave");
+    static_assert(!XF || MODE == GEMV_PLAIN, "f32 input only for the plain GEMV");
     using CH = ChunkI<FMT, R>;
     constexpr int LPB = CH::LPB;
     constexpr bool NORM = MODE == GEMV_QKV || MODE == GEMV_HEAD || MODE == GEMV_GATEUP;
@@ -1541,13 +1542,20 @@ __device__ void gemv_one_body(const GemvArgs &a) {
     constexpr uint32_t NT = GEMV_ONE_WAVES * 64;
     const uint32_t v0 = (blockIdx.x * GEMV_ONE_WAVES + (uint32_t)wave) * R;
     const uint32_t c = (uint32_t)lane % LPB, bsub = (uint32_t)lane / LPB;
-    // x first (loads complete in issue order: staging waits for these only)
-    const uint32_t n16 = xq_bytes(a.cols) / 16;
-    const uint4 *xsrc = (const uint4 *)a.xq;
+    // x first (loads complete in issue order: staging waits for these only).
+    // XF: x arrives in f32 (ifr_matmul_quant's caller) and is quantized into
+    // LDS here, one 16-value group per thread (quant1x16: quant16's bytes),
+    // instead of by a launch of its own: the four chunks are the four
+    // 16-byte quarters of the thread's first group
+    const uint32_t n16 = XF ? a.cols / 4 : xq_bytes(a.cols) / 16;
+    const uint32_t ngrp = a.cols / 16, gq = min((uint32_t)tid, ngrp - 1);
+    const uint4 *xsrc = XF ? (const uint4 *)a.x : (const uint4 *)a.xq;
     // four named chunks (an array here ends up in scratch memory)
     constexpr uint32_t XC = 4;
-    const uint32_t xi0 = min((uint32_t)tid, n16 - 1), xi1 = min((uint32_t)tid + NT, n16 - 1);
-    const uint32_t xi2 = min((uint32_t)tid + 2 * NT, n16 - 1), xi3 = min((uint32_t)tid + 3 * NT, n16 - 1);
+    const uint32_t xi0 = XF ? 4 * gq : min((uint32_t)tid, n16 - 1);
+    const uint32_t xi1 = XF ? 4 * gq + 1 : min((uint32_t)tid + NT, n16 - 1);
+    const uint32_t xi2 = XF ? 4 * gq + 2 : min((uint32_t)tid + 2 * NT, n16 - 1);
+    const uint32_t xi3 = XF ? 4 * gq + 3 : min((uint32_t)tid + 3 * NT, n16 - 1);
     const uint4 xv0 = xsrc[xi0], xv1 = xsrc[xi1], xv2 = xsrc[xi2], xv3 = xsrc[xi3];
     float sv[4];
     uint32_t pos = 0;
@@ -1571,7 +1579,18 @@ __device__ void gemv_one_body(const GemvArgs &a) {
         w.load(rowp, min(bsub, a.nb - 1), c);
     }
     __builtin_amdgcn_sched_barrier(0);
-    {
+    if constexpr (XF) {
+        // a wave with no group skips (uniform); in a wave that has some, a
+        // thread past the last group quantizes it again with the stores off
+        if ((uint32_t)wave * 64 < ngrp) {
+            const uint4 u[4] = {xv0, xv1, xv2, xv3};
+            quant1x16(u, (uint32_t)tid < ngrp, lds, a.cols, gq);
+        }
+        for (uint32_t g = (uint32_t)tid + NT; g < ngrp; g += NT) {
+            const uint4 u[4] = {xsrc[4 * g], xsrc[4 * g + 1], xsrc[4 * g + 2], xsrc[4 * g + 3]};
+            quant1x16(u, true, lds, a.cols, g);
+        }
+    } else {
         uint4 *dst = (uint4 *)lds;
         dst[xi0] = xv0;
         dst[xi1] = xv1;

@@ -357,6 +357,18 @@ static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtyp
     a.x = v;
     a.y = out;
     if (!c->gemv_exact) {
+        // rows of one 64-lane step: the one-item kernel quantizes the f32 x
+        // into its LDS itself (the same bytes as the quantize launch), one
+        // launch instead of two
+        const std::string xf = std::string("gemv_") + p.fmt + "_plain_one_xf";
+        if (a.nb <= p.bpi && cols % 16 == 0 && !c->gemv_waves && !c->gemv_max_grid && !(c->gemv_grp & 256) &&
+            c->fn(xf)) {
+            const uint32_t rows_per = GEMV_ONE_WAVES * 2;
+            a.ks = 1;
+            a.nwaves = GEMV_ONE_WAVES;
+            return c->launch(xf, dim3((rows + rows_per - 1) / rows_per), dim3(GEMV_ONE_WAVES * 64),
+                             (uint32_t)xq_bytes(cols), a);
+        }
         if ((st = launch_quant_act(c, v, nullptr, cols, xq, nullptr))) return st;
         a.xq = xq;
     }

@@ -73,8 +73,15 @@ GEMV_GRP_KERNEL(gemv_q4_k_resid, Q4_K, GEMV_RESID, 4, 4, 4)
 GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 4, 8, 1)
 GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 2, 16, 1)
 
+// the plain one-item form on an f32 x it quantizes itself (ifr_matmul_quant)
+#define GEMV_ONE_XF_KERNEL(NAME, FMT)                                                                 \
+    extern "C" __global__ void __launch_bounds__(GEMV_ONE_WAVES * 64) NAME##_one_xf(GemvArgs a) {      \
+        gemv_one_body<FMT, GEMV_PLAIN, 2, true>(a);                                                   \
+    }
+
 #define GEMV_ALL_MODES(FMTNAME, FMT)                  \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN) \
+    GEMV_ONE_XF_KERNEL(gemv_##FMTNAME##_plain, FMT)          \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)     \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD)   \
     GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)   \
