@@ -268,8 +268,10 @@ static IntGeom int_geom(const ifr_ctx *c, uint32_t bpi, const char *mode, const 
     return g;
 }
 
+// xf (plain mode only): a.x is f32 and the kernel quantizes it into its LDS
+// itself (the `_xf` forms), instead of reading a.xq.
 static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, GemvArgs &a, uint32_t cap = 0,
-                              uint32_t *grid_out = nullptr) {
+                              uint32_t *grid_out = nullptr, bool xf = false) {
     const bool exact = c->gemv_exact != 0;
     std::string name = std::string("gemv_") + p.fmt + "_" + mode + (exact ? "_f32" : "");
     if (exact) {
@@ -282,7 +284,8 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
         if (grid_out) *grid_out = g;
         return c->launch(name, dim3(g), dim3((uint32_t)ge.W * 64u), a.cols * 4, a);
     }
-    if (!a.xq || (a.total_rows && a.cols % 16)) return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
+    if ((!xf && !a.xq) || (a.total_rows && a.cols % 16))
+        return c->fail(IFR_EINVAL, "gemv: integer path needs a quantized input");
     // plain and qkv rows of one 64-lane step: the one-item kernel, every
     // workgroup launched at once
     const bool one_mode = !strcmp(mode, "plain") || !strcmp(mode, "qkv");
@@ -290,12 +293,13 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
         // four rows per wave where the code object has that form (bit 8;
         // slower for the QKV launch's 6144 rows, whose 384 workgroups of
         // four-row waves do not fill the chip)
-        const bool four = (c->gemv_grp & 256) && c->fn(name + "_one4");
+        const bool four = !xf && (c->gemv_grp & 256) && c->fn(name + "_one4");
         const uint32_t rows_per = GEMV_ONE_WAVES * (four ? 4 : 2), g = (a.total_rows + rows_per - 1) / rows_per;
         a.ks = 1;
         a.nwaves = GEMV_ONE_WAVES;
         if (grid_out) *grid_out = g;
-        return c->launch(name + (four ? "_one4" : "_one"), dim3(g), dim3(GEMV_ONE_WAVES * 64), (uint32_t)xq_bytes(a.cols), a);
+        return c->launch(name + (four ? "_one4" : xf ? "_one_xf" : "_one"), dim3(g), dim3(GEMV_ONE_WAVES * 64),
+                         (uint32_t)xq_bytes(a.cols), a);
     }
     // resid and gateup: one output group per workgroup, one item per wave,
     // where the code object has the form for this format and K
@@ -330,7 +334,7 @@ static ifr_status launch_gemv(ifr_ctx *c, const GemvPlan &p, const char *mode, G
         if (grid_out) *grid_out = gg;
         return c->launch(name + "_w2", dim3(gg), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
     }
-    return c->launch(name, dim3(g.grid), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
+    return c->launch(name + (xf ? "_xf" : ""), dim3(g.grid), dim3(g.waves * 64), (uint32_t)xq_bytes(a.cols), a);
 }
 
 // x (times gamma) -> XQ with per-256 partial sums of x^2.
@@ -357,18 +361,10 @@ static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtyp
     a.x = v;
     a.y = out;
     if (!c->gemv_exact) {
-        // rows of one 64-lane step: the one-item kernel quantizes the f32 x
-        // into its LDS itself (the same bytes as the quantize launch), one
-        // launch instead of two
-        const std::string xf = std::string("gemv_") + p.fmt + "_plain_one_xf";
-        if (a.nb <= p.bpi && cols % 16 == 0 && !c->gemv_waves && !c->gemv_max_grid && !(c->gemv_grp & 256) &&
-            c->fn(xf)) {
-            const uint32_t rows_per = GEMV_ONE_WAVES * 2;
-            a.ks = 1;
-            a.nwaves = GEMV_ONE_WAVES;
-            return c->launch(xf, dim3((rows + rows_per - 1) / rows_per), dim3(GEMV_ONE_WAVES * 64),
-                             (uint32_t)xq_bytes(cols), a);
-        }
+        // the GEMV kernel quantizes the f32 x into its LDS itself (the same
+        // bytes as the quantize launch): one launch instead of two
+        const std::string one = std::string("gemv_") + p.fmt + "_plain_one_xf", loop = std::string("gemv_") + p.fmt + "_plain_xf";
+        if (cols % 16 == 0 && c->fn(one) && c->fn(loop)) return launch_gemv(c, p, "plain", a, 0, nullptr, true);
         if ((st = launch_quant_act(c, v, nullptr, cols, xq, nullptr))) return st;
         a.xq = xq;
     }

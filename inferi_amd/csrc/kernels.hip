@@ -79,9 +79,17 @@ GEMV_GRP_KERNEL(gemv_q4_k_gateup, Q4_K, GEMV_GATEUP, 2, 16, 1)
         gemv_one_body<FMT, GEMV_PLAIN, 2, true>(a);                                                   \
     }
 
+// the looping plain form on an f32 x it quantizes itself (ifr_matmul_quant, K past one step)
+#define GEMV_XF_KERNEL(NAME, FMT)                                                                      \
+    extern "C" __global__ void __launch_bounds__(GEMV_INT_MAX_WAVES * 64)                            \
+        __attribute__((amdgpu_waves_per_eu(GEMV_INT_WPE, 8))) NAME##_xf(GemvArgs a) {                  \
+        gemv_int_body<FMT, GEMV_PLAIN, GEMV_INT_PIPE, GEMV_INT_NI, true>(a);                         \
+    }
+
 #define GEMV_ALL_MODES(FMTNAME, FMT)                  \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN) \
     GEMV_ONE_XF_KERNEL(gemv_##FMTNAME##_plain, FMT)          \
+    GEMV_XF_KERNEL(gemv_##FMTNAME##_plain, FMT)              \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_qkv, FMT, GEMV_QKV)     \
     GEMV_ONE_KERNEL(gemv_##FMTNAME##_head, FMT, GEMV_HEAD)   \
     GEMV_KERNEL(gemv_##FMTNAME##_plain, FMT, GEMV_PLAIN)   \
