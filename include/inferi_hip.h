@@ -147,7 +147,8 @@ IFR_API ifr_status ifr_dequant(ifr_ctx *ctx, float *out, const void *blocks, int
  * (crates/inferi/src/context.rs:441-456) -> GemvQuant::launch
  * (crates/inferi/src/ops/gemv_quant.rs:183-340).
  * The product runs on the integer path (see ifr_quantize_activation) unless
- * the "gemv_exact" option is set.
+ * the "gemv_exact" option is set; on it the GEMV kernel quantizes v into its
+ * LDS itself (one launch, nothing allocated).
  * Requirements: cols % QK == 0; cols <= 18432 (integer path; 16320 with
  * "gemv_exact"), as x is staged in one workgroup's LDS; W 16-byte aligned
  * for Q4_K and Q5_K, 4-byte aligned for the other formats (GGUF data is
@@ -159,10 +160,11 @@ IFR_API ifr_status ifr_matmul_quant(ifr_ctx *ctx, float *out, const void *w, int
 /* ifr_matmul_quant without allocation (no counterpart in the reference): for
  * callers that cannot allocate device memory -- code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
- * arguments, kernels and results as ifr_matmul_quant, but the quantized copy
- * of v lives in a fixed device array of 65536 bytes (one per GPU, held until
- * the process ends) instead of a buffer the library allocates; the call
- * makes no hipMalloc, hipFree or other allocating call.  cols whose
+ * arguments and results as ifr_matmul_quant, computed in two launches (the
+ * activation quantization, then the GEMV on it) whose quantized copy of v
+ * lives in a fixed device array of 65536 bytes (one per GPU, held until the
+ * process ends); the call makes no hipMalloc, hipFree or other allocating
+ * call.  cols whose
  * quantized input would not fit (cols > 18724 on the integer path) return
  * IFR_EINVAL.  Every call on one GPU shares that array: calls that overlap
  * on one GPU (two streams, two contexts) race; calls queued on one context's

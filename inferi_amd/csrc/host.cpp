@@ -348,7 +348,7 @@ static ifr_status launch_quant_act(ifr_ctx *c, const float *x, const float *gamm
 
 // out = W v for a plain f32 v: quantizes v into `xq` first on the integer path.
 static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtype, uint32_t rows, uint32_t cols,
-                             const float *v, uint8_t *xq) {
+                             const float *v, uint8_t *xq, bool allow_xf = true) {
     GemvPlan p;
     ifr_status st = check_gemv(c, dtype, cols, w, p);
     if (st) return st;
@@ -364,7 +364,11 @@ static ifr_status gemv_plain(ifr_ctx *c, float *out, const void *w, int32_t dtyp
         // the GEMV kernel quantizes the f32 x into its LDS itself (the same
         // bytes as the quantize launch): one launch instead of two
         const std::string one = std::string("gemv_") + p.fmt + "_plain_one_xf", loop = std::string("gemv_") + p.fmt + "_plain_xf";
-        if (cols % 16 == 0 && c->fn(one) && c->fn(loop)) return launch_gemv(c, p, "plain", a, 0, nullptr, true);
+        if (allow_xf && cols % 16 == 0 && c->fn(one) && c->fn(loop)) return launch_gemv(c, p, "plain", a, 0, nullptr, true);
+        if (!xq) {
+            if ((st = c->ensure_xq_scratch(xq_bytes(cols)))) return st;
+            xq = (uint8_t *)c->xq_scratch;
+        }
         if ((st = launch_quant_act(c, v, nullptr, cols, xq, nullptr))) return st;
         a.xq = xq;
     }
@@ -1085,9 +1089,9 @@ IFR_API ifr_status ifr_matmul_quant(ifr_ctx *c, float *out, const void *w, int32
     if (!out || !w || !v) return c->fail(IFR_EINVAL, "matmul_quant: null pointer");
     if (!rows) return IFR_OK;
     if ((uintptr_t)v % 16) return c->fail(IFR_EINVAL, "matmul_quant: v not 16-byte aligned");
-    ifr_status st = c->ensure_xq_scratch(xq_bytes(cols));
-    if (st) return st;
-    return gemv_plain(c, out, w, dtype, rows, cols, v, (uint8_t *)c->xq_scratch);
+    // the GEMV quantizes v itself where the code object has that form; the
+    // context's scratch is allocated only for the two-launch form
+    return gemv_plain(c, out, w, dtype, rows, cols, v, nullptr);
 }
 
 IFR_API ifr_status ifr_matmul_quant_noalloc(ifr_ctx *c, float *out, const void *w, int32_t dtype, uint32_t rows,
@@ -1099,9 +1103,11 @@ IFR_API ifr_status ifr_matmul_quant_noalloc(ifr_ctx *c, float *out, const void *
     if (!c->gemv_exact && xq_bytes(cols) > IFR_NOALLOC_SCRATCH_BYTES)
         return c->fail(IFR_EINVAL, "matmul_quant_noalloc: cols %u needs %llu bytes of scratch, above the fixed %u", cols,
                        (unsigned long long)xq_bytes(cols), (unsigned)IFR_NOALLOC_SCRATCH_BYTES);
-    // the same kernels as ifr_matmul_quant, with the quantized input in the
-    // device's fixed array (shared by every call on this device)
-    return gemv_plain(c, out, w, dtype, rows, cols, v, (uint8_t *)c->noalloc_scratch);
+    // ifr_matmul_quant's two-launch form (the activation quantization, then
+    // the GEMV on it), with the quantized input in the device's fixed array
+    // (shared by every call on this device); the same bytes and results as
+    // the form that quantizes inside the GEMV
+    return gemv_plain(c, out, w, dtype, rows, cols, v, (uint8_t *)c->noalloc_scratch, false);
 }
 
 IFR_API uint64_t ifr_activation_bytes(uint32_t n) { return xq_bytes(n); }
