@@ -69,18 +69,8 @@ IFR_DEV void lds_dma16(const void *base, uint32_t off, uint32_t lds) {
 }
 
 // 16-byte global load issued as assembly (not counted by the compiler's
-// wait tracking): the caller waits with pg_wait before reading r.
+// wait tracking): the caller waits with s_waitcnt before reading r.
 IFR_DEV void ld16_asm(u32x4_a16 &r, const uint8_t *p) { asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p)); }
-
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-// f16 pair of two f32 values, each rounded to nearest from its f32 value
-// (v_cvt_pk_f16_f32 written out, so the compiler cannot fuse the producing
-// FMA into one rounding straight to f16, v_fma_mix)
-IFR_DEV uint32_t pack_f16x2(float a, float b) {
-    uint32_t u;
-    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
-    return u;
-}
 
 // Weight staging of one thread: half (part p) of one tile row's 64 elements
 // in a K step, stored as four swizzled 16-byte chunks.  Generic: the PfTile
@@ -285,7 +275,12 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
         g.template step<0>(s);
         if (s + 1 < g.nk) g.template step<1>(s + 1);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the clamped loads past the end
+    // the clamped loads past the end: their destination registers stay
+    // allocated until they have landed
+    if constexpr (PgHalf<FMT>::MANUAL)
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(g.st0.hv), "+v"(g.st0.qv), "+v"(g.st1.hv), "+v"(g.st1.qv)::"memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // D[row][col] of block (i, j): col = lane % 32 (n), row = 8 (e / 4) +
     // 4 (lane / 32) + e % 4 (m)
@@ -300,7 +295,7 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
                 const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
                 if (m < a.M) {
                     const float gg = g.acc[i][0][e], u = g.acc[i][1][e];
-                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = (_Float16)(u * (gg / (1.0f + expf(-gg))));
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * (gg / (1.0f + expf(-gg))));
                 }
             }
     } else {

@@ -8,7 +8,9 @@ namespace ifr {
 
 // Weight tiles by format: row r's elements [k0 + 32*hs, +32) (k0 a multiple
 // of 64, hs 0 or 1), loaded as raw bytes (load) and dequantized with the
-// reference's f32 arithmetic, contraction off, then rounded to f16 (deq).
+// reference's f32 arithmetic, contraction off, then rounded to f16 (deq,
+// through f16_run, whose conversion instruction is fixed so that the
+// rounding is always f32 value -> f16).
 // Runtime offsets select among loaded registers; nothing is indexed by a
 // runtime value, so the staging stays in registers.
 IFR_DEV uint32_t pick4(const uint4 &v, uint32_t i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
@@ -16,6 +18,32 @@ IFR_DEV uint32_t pick4(const uint4 &v, uint32_t i) { return i == 0 ? v.x : i == 
 IFR_DEV uint32_t byte32(const uint4 &a, const uint4 &b, int l) {
     const uint32_t w = l < 16 ? pick4(a, (uint32_t)(l >> 2)) : pick4(b, (uint32_t)((l - 16) >> 2));
     return (w >> (8 * (l & 3))) & 0xFFu;
+}
+
+// f16 pair of two f32 values, each rounded to nearest from its f32 value
+// (v_cvt_pk_f16_f32 written out, so the compiler cannot fuse the producing
+// multiply or FMA into one rounding straight to f16, v_fma_mix)
+IFR_DEV uint32_t pack_f16x2(float a, float b) {
+    uint32_t u;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
+    return u;
+}
+// f16 of one f32 value (v_cvt_f16_f32 written out, for the same reason)
+IFR_DEV _Float16 f16_of(float a) {
+    uint32_t u;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(u) : "v"(a));
+    const uint16_t b = (uint16_t)u;
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return h;
+}
+// h[l] = f16(y[l]) for the 32 values of a run, rounded from f32 by pack_f16x2
+IFR_DEV void f16_run(const float *y, _Float16 *h) {
+#pragma unroll
+    for (int l = 0; l < 32; l += 2) {
+        const uint32_t u = pack_f16x2(y[l], y[l + 1]);
+        __builtin_memcpy(&h[l], &u, 4);
+    }
 }
 
 template <int FMT>
@@ -40,12 +68,14 @@ struct PfTile<Q4_K> {
         scale_min_pair(g, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
         const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
         const float d1 = d * (float)(hs ? sc1 : sc0), mm = dm * (float)(hs ? m1s : m0s);
+        float y[32];
 #pragma unroll
         for (int l = 0; l < 32; l++) {
             const uint32_t b = byte32(q0, q1, l);
             const float q = (float)(hs ? (b >> 4) : (b & 15u));
-            h[l] = (_Float16)(d1 * q - mm);
+            y[l] = d1 * q - mm;
         }
+        f16_run(y, h);
     }
 };
 
@@ -70,12 +100,14 @@ struct PfTile<Q5_K> {
         scale_min_pair(g, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
         const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
         const float d1 = d * (float)(hs ? sc1 : sc0), mm = dm * (float)(hs ? m1s : m0s);
+        float y[32];
 #pragma unroll
         for (int l = 0; l < 32; l++) {
             const uint32_t b = byte32(q0, q1, l);
             const uint32_t q = (hs ? (b >> 4) : (b & 15u)) + (((byte32(e0, e1, l) >> sh) & 1u) ? 16u : 0u);
-            h[l] = (_Float16)(d1 * (float)q - mm);
+            y[l] = d1 * (float)q - mm;
         }
+        f16_run(y, h);
     }
 };
 
@@ -102,14 +134,16 @@ struct PfTile<Q6_K> {
         const uint32_t k = (2 * ((k0 % 256) / 64) + hs) & 3u;
         const float d = f16_to_f32(dd);
         const float s_lo = (float)(int)(int8_t)(sc & 0xFFu), s_hi = (float)(int)(int8_t)(sc >> 8);
+        float y[32];
 #pragma unroll
         for (int l = 0; l < 32; l++) {
             const uint32_t qlb = byte32(l0, l1, l);
             const uint32_t nib = k < 2 ? (qlb & 15u) : (qlb >> 4);
             const uint32_t hb = (byte32(h0, h1, l) >> (2 * k)) & 3u;
             const int q = (int)(nib | (hb << 4)) - 32;
-            h[l] = (_Float16)(d * (l < 16 ? s_lo : s_hi) * (float)q);
+            y[l] = d * (l < 16 ? s_lo : s_hi) * (float)q;
         }
+        f16_run(y, h);
     }
 };
 
@@ -128,8 +162,10 @@ struct PfTile<Q8_K> {
     IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
 #pragma clang fp contract(off)
         const float d = __uint_as_float(db);
+        float y[32];
 #pragma unroll
-        for (int l = 0; l < 32; l++) h[l] = (_Float16)(d * (float)(int)(int8_t)byte32(q0, q1, l));
+        for (int l = 0; l < 32; l++) y[l] = d * (float)(int)(int8_t)byte32(q0, q1, l);
+        f16_run(y, h);
     }
 };
 
@@ -164,8 +200,10 @@ struct PfTile<F32> {
         for (int k = 0; k < 8; k++) v[k] = ld16(b + 16 * k);
     }
     IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
+        float y[32];
 #pragma unroll
-        for (int l = 0; l < 32; l++) h[l] = (_Float16)__uint_as_float(pick4(v[l >> 2], (uint32_t)(l & 3)));
+        for (int l = 0; l < 32; l++) y[l] = __uint_as_float(pick4(v[l >> 2], (uint32_t)(l & 3)));
+        f16_run(y, h);
     }
 };
 
@@ -185,8 +223,10 @@ struct PfTile<Q8_0> {
     IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
 #pragma clang fp contract(off)
         const float d = f16_to_f32(dd);
+        float y[32];
 #pragma unroll
-        for (int l = 0; l < 32; l++) h[l] = (_Float16)((float)(int)(int8_t)byte32(q0, q1, l) * d);
+        for (int l = 0; l < 32; l++) y[l] = (float)(int)(int8_t)byte32(q0, q1, l) * d;
+        f16_run(y, h);
     }
 };
 
@@ -203,16 +243,16 @@ struct PfTile32 {
     IFR_DEV void deq(uint32_t, uint32_t, _Float16 *h) const {
 #pragma clang fp contract(off)
         const float d = blk.d(), m = Blk32<FMT>::AFF ? blk.m() : 0.0f;
+        float y[32];
 #pragma unroll
         for (int l = 0; l < 32; l++) {
             const uint32_t b = byte32(blk.qs, blk.qs, l & 15);
             uint32_t q = l < 16 ? (b & 15u) : (b >> 4);
             if constexpr (Blk32<FMT>::FIVE) q |= ((blk.qh >> l) & 1u) << 4;
-            float y;
-            if constexpr (Blk32<FMT>::AFF) y = (float)q * d + m;
-            else y = (float)((int)q - (int)Blk32<FMT>::H) * d;
-            h[l] = (_Float16)y;
+            if constexpr (Blk32<FMT>::AFF) y[l] = (float)q * d + m;
+            else y[l] = (float)((int)q - (int)Blk32<FMT>::H) * d;
         }
+        f16_run(y, h);
     }
 };
 template <>

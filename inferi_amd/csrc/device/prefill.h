@@ -116,7 +116,7 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
                 const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
                 if (m < a.M) {
                     const float g = acc[i][0][e], u = acc[i][1][e];
-                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = (_Float16)(u * (g / (1.0f + expf(-g))));
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * (g / (1.0f + expf(-g))));
                 }
             }
     } else {
@@ -236,7 +236,7 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
     if (j >= F) return;
     const float *gu = (const float *)a.gu;
     const float g = gu[(size_t)m * 2 * F + j], u = gu[(size_t)m * 2 * F + F + j];
-    ((_Float16 *)a.h)[(size_t)m * F + j] = (_Float16)(u * (g / (1.0f + expf(-g))));
+    ((_Float16 *)a.h)[(size_t)m * F + j] = f16_of(u * (g / (1.0f + expf(-g))));
 }
 
 // ------------------------------------------------------------ attention --
