@@ -64,8 +64,11 @@ IFR_DEV uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const ld
 // loads to the kernel's own waits; the caller waits with vmcnt before the
 // LDS is read.
 // The address is a wave-uniform base plus this lane's 32-bit byte offset.
+// M0 is reserved by the compiler (it sets M0 itself before each of its own
+// uses and ignores a clobber entry for it); the compiler-generated code of
+// these kernels does not read M0.
 IFR_DEV void lds_dma16(const void *base, uint32_t off, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "m0");
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds));
 }
 
 // 16-byte global load issued as assembly (not counted by the compiler's

@@ -260,10 +260,7 @@ IFR_DEV void pf_silu_body(const PfArgs &a) {
 //                     the other, ...), so P^T needs no shuffle;
 // and out = O / l is written as f16 for the O GEMM.  The last query tiles,
 // which see the most keys, are dispatched first.
-#ifndef PFA_KEYS
-#define PFA_KEYS 64
-#endif
-constexpr int PFA_WAVES = 4, PFA_ROWS = 32 * PFA_WAVES, PFA_KT = PFA_KEYS; // keys per tile: 32 or 64
+constexpr int PFA_WAVES = 4, PFA_ROWS = 32 * PFA_WAVES, PFA_KT = 64; // keys per tile
 constexpr int PFA_KB = PFA_KT / 32;                                      // 32-key blocks per tile
 // A row's softmax reference maximum moves only when a tile's maximum passes
 // it by more than this (base-2 units): the weights 2^(s - m) then stay below
@@ -274,16 +271,24 @@ constexpr int PFA_KB = PFA_KT / 32;                                      // 32-k
 // moved.
 constexpr float PFA_LAZY = 8.0f;
 
+// x with its bits 2 and 3 exchanged
+IFR_DEV uint32_t swap23(uint32_t x) {
+    const uint32_t t = ((x >> 2) ^ (x >> 3)) & 1u;
+    return x ^ (t << 2) ^ (t << 3);
+}
+
 template <int HSP, bool F16>
 __device__ void pf_attn_body(const PfArgs &a) {
     constexpr int KC = HSP / 16;          // k-chunks of the scores (head dims)
     constexpr int DT = HSP / 32;          // O^T tiles along the head dims
     constexpr int KP = HSP + 8;           // K tile row pitch (halves)
-    // V^T row pitch (halves): 2 x an odd number of dwords, so the 32 lanes of
-    // an 8-byte operand read (rows li, dwords kb/2 + {0,1}) hit 64 distinct banks
-    constexpr int VP = PFA_KT + 4;
+    // V^T row pitch (halves): 16-byte rows for the one-read operands, and 36
+    // dwords, so the 16 rows li of a 16-byte read pass start on 16 distinct
+    // 4-bank groups
+    constexpr int VP = PFA_KT + 8;
     constexpr int CPK = HSP / 8;          // 8-dim chunks per key row
-    constexpr int NLD = PFA_KT * CPK / 256; // chunks of K (and of V) each thread stages per tile
+    constexpr int R = PFA_KT * CPK / 256; // keys each thread stages per tile (chunk dc of each)
+    static_assert(R == 2 || R == 4, "head sizes padded to 64 or 128");
     __shared__ __attribute__((aligned(16))) _Float16 ks[2][PFA_KT][KP];
     __shared__ __attribute__((aligned(16))) _Float16 vts[2][HSP][VP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -298,22 +303,32 @@ __device__ void pf_attn_body(const PfArgs &a) {
     const uint32_t qlast = a.p0 + q0 + nq - 1;  // largest query position of the tile
     const uint32_t ntk = qlast / PFA_KT + 1;    // key tiles
 
-    // this thread's staging chunks: key kk = tid % KT, dims 8 * dc .. +8 for
-    // dc = tid / KT + (256 / KT) i.  The loads are unconditional (a load
-    // behind a branch is drained at the branch's join, which would make the
-    // next tile's loads wait before this tile's products): a key past the
-    // tile's last query reads that query's row instead, a finite cache row
-    // whose weight the causal mask makes exactly 0, and a chunk past the
-    // head size reads the last chunk, which meets Q's zero padding in the
-    // scores and feeds only output dims that are never written.
-    const uint32_t kk = (uint32_t)tid % PFA_KT;
-    uint4 kraw[NLD][F16 ? 1 : 2], vraw[NLD][F16 ? 1 : 2];
+    // This thread stages keys R gk .. R gk + R - 1 of the tile, dims
+    // 8 dc .. +8 of each: dc = lane % 4 + 4 x (wave % (CPK / 4)), gk = lane / 4
+    // + 16 x (wave / (CPK / 4)); one load instruction reads 64 contiguous bytes
+    // (four chunks) of 16 key rows.  K goes to LDS as it is (ks[key][dim]);
+    // V transposed (vts[dim][key']) with key' = key with its bits 2 and 3
+    // swapped: the 8 keys that lane half hl of an O^T operand needs (4 hl ..
+    // 4 hl + 3 and 8 + 4 hl .. of a 16-key chunk, the score accumulator's
+    // order) then sit in one 16-byte run at 8 hl, and this thread's R keys
+    // stay adjacent, one 4- or 8-byte store per dim.  The loads are
+    // unconditional (a load behind a branch is drained at the branch's join,
+    // which would make the next tile's loads wait before this tile's
+    // products): a key past the tile's last query reads that query's row
+    // instead, a finite cache row whose weight the causal mask makes exactly
+    // 0, and a chunk past the head size reads the last chunk, which meets Q's
+    // zero padding in the scores and feeds only output dims that are never
+    // written.
+    const uint32_t dc = ((uint32_t)lane & 3u) + 4u * ((uint32_t)wave % (CPK / 4));
+    const uint32_t gk = ((uint32_t)lane >> 2) + 16u * ((uint32_t)wave / (CPK / 4));
+    const uint32_t vcol = swap23(R * gk); // V^T column of this thread's first key
+    uint4 kraw[R][F16 ? 1 : 2], vraw[R][F16 ? 1 : 2];
     auto gload = [&](uint32_t t) {
-        const uint32_t kp = t * PFA_KT + kk;
+        const size_t col = (size_t)kvh * hs + min(dc, hs / 8 - 1) * 8;
 #pragma unroll
-        for (int i = 0; i < NLD; i++) {
-            const uint32_t dc = (uint32_t)tid / PFA_KT + (256 / PFA_KT) * (uint32_t)i;
-            const size_t off = (size_t)min(kp, qlast) * a.kv_dim + (size_t)kvh * hs + min(dc, hs / 8 - 1) * 8;
+        for (int i = 0; i < R; i++) {
+            const uint32_t kp = t * PFA_KT + R * gk + (uint32_t)i;
+            const size_t off = (size_t)min(kp, qlast) * a.kv_dim + col;
 #pragma unroll
             for (int h = 0; h < (F16 ? 1 : 2); h++) {
                 if (F16) {
@@ -326,29 +341,41 @@ __device__ void pf_attn_body(const PfArgs &a) {
             }
         }
     };
+    // 16-bit element e of a staged 8-element chunk, as f16 bits
+    auto half_of = [&](const uint4 (&raw)[F16 ? 1 : 2], int e) -> uint32_t {
+        if constexpr (F16) {
+            const uint32_t w = e < 2 ? raw[0].x : e < 4 ? raw[0].y : e < 6 ? raw[0].z : raw[0].w;
+            return (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+        } else {
+            const uint4 &q = raw[e >> 2];
+            const uint32_t w = (e & 3) == 0 ? q.x : (e & 3) == 1 ? q.y : (e & 3) == 2 ? q.z : q.w;
+            return (uint32_t)__builtin_bit_cast(uint16_t, f16_of(__uint_as_float(w)));
+        }
+    };
     auto lstore = [&](uint32_t b) {
 #pragma unroll
-        for (int i = 0; i < NLD; i++) {
-            const uint32_t dc = (uint32_t)tid / PFA_KT + (256 / PFA_KT) * (uint32_t)i;
-            _Float16 kh[8], vh[8];
-            if constexpr (F16) {
-                __builtin_memcpy(kh, &kraw[i][0], 16);
-                __builtin_memcpy(vh, &vraw[i][0], 16);
-            } else {
-                float kf[8], vf[8];
-                __builtin_memcpy(kf, &kraw[i][0], 32);
-                __builtin_memcpy(vf, &vraw[i][0], 32);
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    kh[e] = (_Float16)kf[e];
-                    vh[e] = (_Float16)vf[e];
-                }
-            }
+        for (int i = 0; i < R; i++) {
             uint4 u;
-            __builtin_memcpy(&u, kh, 16);
-            *(uint4 *)&ks[b][kk][8 * dc] = u;
+            if constexpr (F16) {
+                u = kraw[i][0];
+            } else {
+                u.x = half_of(kraw[i], 0) | half_of(kraw[i], 1) << 16;
+                u.y = half_of(kraw[i], 2) | half_of(kraw[i], 3) << 16;
+                u.z = half_of(kraw[i], 4) | half_of(kraw[i], 5) << 16;
+                u.w = half_of(kraw[i], 6) | half_of(kraw[i], 7) << 16;
+            }
+            *(uint4 *)&ks[b][R * gk + (uint32_t)i][8 * dc] = u;
+        }
 #pragma unroll
-            for (int e = 0; e < 8; e++) vts[b][8 * dc + e][kk] = vh[e];
+        for (int e = 0; e < 8; e++) {
+            if constexpr (R == 4) {
+                uint2 v;
+                v.x = half_of(vraw[0], e) | half_of(vraw[1], e) << 16;
+                v.y = half_of(vraw[2], e) | half_of(vraw[3], e) << 16;
+                *(uint2 *)&vts[b][8 * dc + (uint32_t)e][vcol] = v;
+            } else {
+                *(uint32_t *)&vts[b][8 * dc + (uint32_t)e][vcol] = half_of(vraw[0], e) | half_of(vraw[1], e) << 16;
+            }
         }
     };
 
@@ -450,14 +477,10 @@ __device__ void pf_attn_body(const PfArgs &a) {
         for (int u = 0; u < PFA_KB; u++)
 #pragma unroll
             for (int cc = 0; cc < 2; cc++) {
-                const uint32_t kb = 32 * u + 16 * cc + 4 * hl;
+                const uint32_t kb = 32 * u + 16 * cc + 8 * hl; // (V^T columns, bits 2 and 3 swapped)
 #pragma unroll
                 for (int d = 0; d < DT; d++) {
-                    const _Float16 *vrow = &vts[b][32 * d + li][0];
-                    half8v av;
-                    const uint2 lo = *(const uint2 *)(vrow + kb), hi = *(const uint2 *)(vrow + kb + 8);
-                    __builtin_memcpy(&av, &lo, 8);
-                    __builtin_memcpy((char *)&av + 8, &hi, 8);
+                    const half8v av = *(const half8v *)&vts[b][32 * d + li][kb];
                     o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb[u][cc], o[d], 0, 0, 0);
                 }
             }
