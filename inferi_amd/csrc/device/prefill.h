@@ -321,7 +321,11 @@ __device__ void pf_attn_body(const PfArgs &a) {
     // written.
     const uint32_t dc = ((uint32_t)lane & 3u) + 4u * ((uint32_t)wave % (CPK / 4));
     const uint32_t gk = ((uint32_t)lane >> 2) + 16u * ((uint32_t)wave / (CPK / 4));
-    const uint32_t vcol = swap23(R * gk); // V^T column of this thread's first key
+    // V^T column of this thread's first key; rows with bit 4 set (dims
+    // 16-31 of each 32) hold their 32-key blocks' two 16-key halves
+    // exchanged, which puts the four rows 8 apart that one 16-lane pass of
+    // the stores writes on distinct banks (the reads apply the same exchange)
+    const uint32_t vcol = swap23(R * gk) ^ (16u * ((dc >> 1) & 1u));
     uint4 kraw[R][F16 ? 1 : 2], vraw[R][F16 ? 1 : 2];
     auto gload = [&](uint32_t t) {
         const size_t col = (size_t)kvh * hs + min(dc, hs / 8 - 1) * 8;
@@ -477,7 +481,8 @@ __device__ void pf_attn_body(const PfArgs &a) {
         for (int u = 0; u < PFA_KB; u++)
 #pragma unroll
             for (int cc = 0; cc < 2; cc++) {
-                const uint32_t kb = 32 * u + 16 * cc + 8 * hl; // (V^T columns, bits 2 and 3 swapped)
+                // V^T columns: key bits 2 and 3 swapped, halves exchanged on rows with bit 4 set
+                const uint32_t kb = (32 * u + 16 * cc + 8 * hl) ^ (16u * ((li >> 4) & 1u));
 #pragma unroll
                 for (int d = 0; d < DT; d++) {
                     const half8v av = *(const half8v *)&vts[b][32 * d + li][kb];
