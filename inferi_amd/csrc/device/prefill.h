@@ -153,20 +153,43 @@ IFR_DEV void pf_embed_body(const PfArgs &a) {
 }
 
 // xh[m] = f16((x[m] * (1/sqrt(mean(x[m]^2) + eps))) * gamma), rms_norm.rs:81-121
+// Rows of a multiple of 4 elements (every model here) go 16 bytes per lane;
+// other widths element by element.
 IFR_DEV void pf_rmsnorm_f16_body(const PfArgs &a) {
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, n = a.hidden;
     const float *x = (const float *)a.x + (size_t)m * n;
+    _Float16 *xh = (_Float16 *)a.xh + (size_t)m * a.ldh;
+    const bool vec = (n & 3u) == 0 && (a.ldh & 3u) == 0 && ((uintptr_t)a.gamma & 15u) == 0;
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+    if (vec) {
+        for (uint32_t i = 4 * threadIdx.x; i < n; i += 4 * blockDim.x) {
+            const float4 v = *(const float4 *)(x + i);
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+    }
     ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     float t = 0.0f;
     for (uint32_t w = 0; w < blockDim.x / 64; w++) t += red[w];
     const float rs = 1.0f / sqrtf(t / (float)n + a.eps);
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
-        ((_Float16 *)a.xh)[(size_t)m * a.ldh + i] = (_Float16)((x[i] * rs) * a.gamma[i]);
+    if (vec) {
+        for (uint32_t i = 4 * threadIdx.x; i < n; i += 4 * blockDim.x) {
+            const float4 v = *(const float4 *)(x + i), g = *(const float4 *)(a.gamma + i);
+            uint2 u;
+            u.x = pack_f16x2((v.x * rs) * g.x, (v.y * rs) * g.y);
+            u.y = pack_f16x2((v.z * rs) * g.z, (v.w * rs) * g.w);
+            *(uint2 *)(xh + i) = u;
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) xh[i] = f16_of((x[i] * rs) * a.gamma[i]);
+    }
 }
 
 // Token m (position p0 + m) of qkv [M][q_dim + 2 kv_dim]: RoPE on q (in
