@@ -185,6 +185,23 @@ def test_prefill_matches_sequential_decode_hs64(ctx, oracle_lib):
         w.close()
 
 
+@pytest.mark.parametrize("hs", [32, 64, 96])
+def test_prefill_f32_cache_small_heads(ctx, oracle_lib, hs):
+    """An f32 cache with head sizes staged on the 64-wide attention tile (two
+    keys per staging thread; 32: half its dims past the head) and on the
+    128-wide one with dims past the head (96), across 300 prompt tokens."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=8 * hs, ffn=512, n_heads=8, n_kv_heads=2, vocab=512, max_pos=330,
+                         rope_theta=10000.0, rms_eps=1e-5, kv_dtype=I.F32)
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=hs, std=0.05)
+    try:
+        prompt = np.random.default_rng(hs).integers(0, cfg.vocab, 301).tolist()
+        assert _prefill_vs_decode(ctx, cfg, w, prompt, 6) > 0
+    finally:
+        w.close()
+
+
 @pytest.mark.parametrize("chunk", [512, 0])
 def test_prefill_chunks_and_gqa4_hs128(ctx, oracle_lib, chunk):
     """Two prefill passes (512 + rest) or one (the default pass length),
