@@ -168,12 +168,15 @@ def time_sampler(ctx: I.LlmContext, n: int, iters: int = 50) -> float:
 def prefill_flops(cfg: I.Llama2Config, n: int) -> float:
     """Algorithmic FLOPs of a prompt of n tokens: 2 per weight per token for
     the layer matrices, plus causal attention (q.k and p.v: 2 x 2 x hs per
-    key per head, sum over t of t+1 keys)."""
+    key per head, sum over t of t+1 keys); of the last layer only the Q/K/V
+    product, since the prefill's product is the KV rows (its attention and
+    FFN outputs feed nothing)."""
     hs = cfg.hidden // cfg.n_heads
     kv = cfg.n_kv_heads * hs
-    mats = cfg.hidden * (cfg.hidden + 2 * kv) + cfg.hidden * cfg.hidden + 3 * cfg.hidden * cfg.ffn
+    qkv = cfg.hidden * (cfg.hidden + 2 * kv)
+    mats = qkv + cfg.hidden * cfg.hidden + 3 * cfg.hidden * cfg.ffn
     attn = 4.0 * hs * cfg.n_heads * (n * (n + 1) / 2)
-    return cfg.n_layers * (2.0 * n * mats + attn)
+    return (cfg.n_layers - 1) * (2.0 * n * mats + attn) + 2.0 * n * qkv
 
 
 STAGES = ("qkv", "attention", "attn_output", "ffn_gate_up", "ffn_down")

@@ -367,7 +367,8 @@ IFR_API ifr_status ifr_llama2_generate(ifr_ctx *ctx, ifr_llama2_state *s, const 
  * the matrix cores (ifr_gemm_quant) and causal attention over the cache;
  * their KV-cache rows are written and the position advances by n_tokens.
  * No logits are formed: the next decode step, at the prompt's last token,
- * produces them.  Waits for queued work (it reads the position).  The
+ * produces them (so the last layer's attention and FFN, whose outputs feed
+ * nothing else, are not run).  Waits for queued work (it reads the position).  The
  * attention and FFN matrices may be of any quantized GGUF type that
  * ifr_gemm_quant takes; both RoPE variants and QKV biases are handled. */
 IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *ctx, ifr_llama2_state *s, const ifr_llama2_weights *w,

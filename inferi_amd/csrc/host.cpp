@@ -1876,6 +1876,10 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
                 i = j;
             }
             if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
+            // the last layer's attention and FFN feed only its residual
+            // stream, which nothing reads (the pass's product is the KV rows;
+            // the next decode step starts from the embedding): not run
+            if (l + 1 == cfg.n_layers) break;
             if ((st = c->launch(attn_name, dim3(cfg.n_kv_heads, (M + attn_qt - 1) / attn_qt), dim3(256), 0, a))) return st;
             if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + 3, 1, s->pf_x, H, M, PF_EPI_ADD))) return st;
             a.gamma = (const float *)L.ffn_norm.data;
