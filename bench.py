@@ -304,6 +304,17 @@ def run_decode(args) -> None:
         pf["ms_tile128"] = round(ctx.event_elapsed(4, 5), 3)
         ctx.set_option("pf_tile", 0)
         log(f"bench: prefill on 128 x 128 GEMM tiles {pf['ms_tile128']:.2f} ms")
+        # and with the Q4_K products in the eight-wave form (no warp
+        # specialization; the same results bit for bit)
+        ctx.set_option("pf_ws", 0)
+        s.reset(prompt, 0)
+        ctx.sync()
+        ctx.event_record(4)
+        I.Llama2.prefill(ctx, s, w, n_pf)
+        ctx.event_record(5)
+        pf["ms_eight_wave"] = round(ctx.event_elapsed(4, 5), 3)
+        ctx.set_option("pf_ws", 1)
+        log(f"bench: prefill with the eight-wave Q4_K GEMM {pf['ms_eight_wave']:.2f} ms")
     I.Llama2.generate(ctx, s, w, args.warmup, use_graph=not args.no_graph)
     ctx.sync()
     pos0 = int(s.read("pos", np.uint32)[0])

@@ -104,8 +104,11 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * most 16384; 0 = 4096), read at a state's first prefill.  "pf_tile"
  * selects the prefill GEMM's tiles: 0 (the default) 256 x 256 tiles where a
  * product has at least 128 of them, else 128 x 128 tiles; 128 or 256 forces
- * one form.  Both forms sum each output element's products in the same
- * order, so the results do not depend on the tile or the pass length.
+ * one form.  "pf_ws" = 1 (the default) runs the Q4_K products on 256 x 256
+ * tiles in the warp-specialized form (eight MFMA waves and four waves that
+ * load and dequantize the tiles), 0 in the eight-wave form where every wave
+ * does both.  Every form sums each output element's products in the same
+ * order, so the results do not depend on the form or the pass length.
  * A captured decode step is captured again after any option change. */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 /* Reads an option (no reference counterpart): any key ifr_set_option takes. */

@@ -19,7 +19,9 @@
 // loads, issued a step ahead; W's GGUF bytes arrive in registers two steps
 // ahead and are dequantized into the other buffer while the matrix cores
 // work on the current one, so one barrier per step suffices.  (Four waves
-// of 128 x 128, one per SIMD, measured 10-20% slower.)
+// of 128 x 128, one per SIMD, measured 10-20% slower.)  Q4_K products take
+// a warp-specialized form of the same tile (pf_gemm_ws_body, below), where
+// four more waves do all the loading and dequantizing.
 //
 // Rows of the virtual n range come from up to three matrices of one GGUF
 // type stacked one after another (n < n1: w0, n < n2: w1, else w2), so Q, K
@@ -97,6 +99,38 @@ struct PgHalf {
         }
     }
 };
+// The block affine map of the step's two sub-blocks 2g, 2g + 1 (g = (k0 %
+// 256) / 64): y = d1 q + n1 (low nibbles), d2 q + n2 (high nibbles).
+struct Q4kAffine {
+    float d1, n1, d2, n2;
+};
+IFR_DEV Q4kAffine q4k_affine(const u32x4_a16 &hv, uint32_t k0) {
+#pragma clang fp contract(off)
+    uint32_t sc0, m0s, sc1, m1s;
+    scale_min_pair((k0 % 256) / 64, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
+    const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
+    return Q4kAffine{d * (float)sc0, -(dm * (float)m0s), d * (float)sc1, -(dm * (float)m1s)};
+}
+// The 16 qs bytes of part p (bytes [32 g + 16 p, +16) of the block's qs):
+// low nibbles -> chunks 2p, 2p + 1, high nibbles -> chunks 4 + 2p, 5 + 2p of
+// tile row r.
+IFR_DEV void q4k_store_part(const u32x4_a16 &qv, const Q4kAffine &f, uint32_t p, _Float16 *tile, uint32_t r) {
+    const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t l = q[i] & 0x0F0F0F0Fu, h = (q[i] >> 4) & 0x0F0F0F0Fu;
+        lo[2 * i] = pack_f16x2(fmaf(f.d1, ub<0>(l), f.n1), fmaf(f.d1, ub<1>(l), f.n1));
+        lo[2 * i + 1] = pack_f16x2(fmaf(f.d1, ub<2>(l), f.n1), fmaf(f.d1, ub<3>(l), f.n1));
+        hi[2 * i] = pack_f16x2(fmaf(f.d2, ub<0>(h), f.n2), fmaf(f.d2, ub<1>(h), f.n2));
+        hi[2 * i + 1] = pack_f16x2(fmaf(f.d2, ub<2>(h), f.n2), fmaf(f.d2, ub<3>(h), f.n2));
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        *(uint4 *)(tile + pg_swz(r, 2 * p + (uint32_t)c)) = make_uint4(lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]);
+        *(uint4 *)(tile + pg_swz(r, 4 + 2 * p + (uint32_t)c)) = make_uint4(hi[4 * c], hi[4 * c + 1], hi[4 * c + 2], hi[4 * c + 3]);
+    }
+}
 // Q4_K (quantization.rs:358-392): part p takes qs bytes [32 g + 16 p, +16)
 // of the step's group g = (k0 % 256) / 64: their low nibbles are elements
 // 16 p .. 16 p + 15 (sub-block 2g; chunks 2p, 2p + 1), their high nibbles
@@ -106,6 +140,35 @@ struct PgHalf {
 // the reference's multiply then subtract does.  The loads are issued as
 // assembly and waited for with wait<N> (N = loads issued after them that may
 // stay in flight).
+// The same values with one instruction less per weight: a 4-bit code q in
+// bits 0-3 (4-7) of a 16-bit half is the f16 subnormal q 2^-24 (q 2^-20),
+// exactly, so fma(d1 2^24, that, n1) is fma(d1, q, n1), the same single f32
+// rounding, with the code's conversion folded into the mixed-precision FMA
+// (v_fma_mix_f32 reads the half in place).  Masks take two codes per
+// instruction, one in each half; f16 subnormal inputs are kept (the default
+// f16 denormal mode).
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+IFR_DEV void q4k_store_part_mix(const u32x4_a16 &qv, const Q4kAffine &f, uint32_t p, _Float16 *tile, uint32_t r) {
+    const float dl = f.d1 * 0x1p24f, dh = f.d2 * 0x1p20f; // exact: powers of two
+    const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t u = q[i], v = q[i] >> 8;
+        // bytes 0, 2 (u) and 1, 3 (v): low nibbles at bits 0-3, high at 4-7
+        const f16x2v l02 = __builtin_bit_cast(f16x2v, u & 0x000F000Fu), l13 = __builtin_bit_cast(f16x2v, v & 0x000F000Fu);
+        const f16x2v h02 = __builtin_bit_cast(f16x2v, u & 0x00F000F0u), h13 = __builtin_bit_cast(f16x2v, v & 0x00F000F0u);
+        lo[2 * i] = pack_f16x2(fmaf(dl, (float)l02.x, f.n1), fmaf(dl, (float)l13.x, f.n1));
+        lo[2 * i + 1] = pack_f16x2(fmaf(dl, (float)l02.y, f.n1), fmaf(dl, (float)l13.y, f.n1));
+        hi[2 * i] = pack_f16x2(fmaf(dh, (float)h02.x, f.n2), fmaf(dh, (float)h13.x, f.n2));
+        hi[2 * i + 1] = pack_f16x2(fmaf(dh, (float)h02.y, f.n2), fmaf(dh, (float)h13.y, f.n2));
+    }
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        *(uint4 *)(tile + pg_swz(r, 2 * p + (uint32_t)c)) = make_uint4(lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]);
+        *(uint4 *)(tile + pg_swz(r, 4 + 2 * p + (uint32_t)c)) = make_uint4(hi[4 * c], hi[4 * c + 1], hi[4 * c + 2], hi[4 * c + 3]);
+    }
+}
 template <>
 struct PgHalf<Q4_K> {
     static constexpr bool MANUAL = true;
@@ -120,27 +183,28 @@ struct PgHalf<Q4_K> {
         asm volatile("s_waitcnt vmcnt(%2)" : "+v"(hv), "+v"(qv) : "n"(N));
     }
     IFR_DEV void store(uint32_t k0, uint32_t p, _Float16 *tile, uint32_t r) const {
-#pragma clang fp contract(off)
-        uint32_t sc0, m0s, sc1, m1s;
-        scale_min_pair((k0 % 256) / 64, hv.y, hv.z, hv.w, sc0, m0s, sc1, m1s);
-        const float d = f16_to_f32(hv.x & 0xFFFFu), dm = f16_to_f32(hv.x >> 16);
-        const float d1 = d * (float)sc0, n1 = -(dm * (float)m0s), d2 = d * (float)sc1, n2 = -(dm * (float)m1s);
-        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t l = q[i] & 0x0F0F0F0Fu, h = (q[i] >> 4) & 0x0F0F0F0Fu;
-            lo[2 * i] = pack_f16x2(fmaf(d1, ub<0>(l), n1), fmaf(d1, ub<1>(l), n1));
-            lo[2 * i + 1] = pack_f16x2(fmaf(d1, ub<2>(l), n1), fmaf(d1, ub<3>(l), n1));
-            hi[2 * i] = pack_f16x2(fmaf(d2, ub<0>(h), n2), fmaf(d2, ub<1>(h), n2));
-            hi[2 * i + 1] = pack_f16x2(fmaf(d2, ub<2>(h), n2), fmaf(d2, ub<3>(h), n2));
-        }
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            *(uint4 *)(tile + pg_swz(r, 2 * p + (uint32_t)c)) = make_uint4(lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]);
-            *(uint4 *)(tile + pg_swz(r, 4 + 2 * p + (uint32_t)c)) =
-                make_uint4(hi[4 * c], hi[4 * c + 1], hi[4 * c + 2], hi[4 * c + 3]);
-        }
+        q4k_store_part(qv, q4k_affine(hv, k0), p, tile, r);
+    }
+};
+// Q4_K staging of one whole tile row (both parts) per thread, for the
+// warp-specialized form: the block header once, then the 32 qs bytes.
+struct PgRowQ4K {
+    u32x4_a16 hv, q0, q1;
+    IFR_DEV void load(const uint8_t *wrow, uint32_t k0) {
+        const uint8_t *b = wrow + (size_t)(k0 / 256) * 144;
+        const uint8_t *q = b + 16 + 32 * ((k0 % 256) / 64);
+        ld16_asm(hv, b);
+        ld16_asm(q0, q);
+        ld16_asm(q1, q + 16);
+    }
+    template <int N>
+    IFR_DEV void wait() {
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(hv), "+v"(q0), "+v"(q1) : "n"(N));
+    }
+    IFR_DEV void store(uint32_t k0, _Float16 *tile, uint32_t r) const {
+        const Q4kAffine f = q4k_affine(hv, k0);
+        q4k_store_part_mix(q0, f, 0, tile, r);
+        q4k_store_part_mix(q1, f, 1, tile, r);
     }
 };
 
@@ -205,6 +269,76 @@ struct PgCtx {
     }
 };
 
+// The workgroup's output tile.  Tiles run in n-fastest order: consecutive
+// workgroups share an X tile.  Workgroup b runs on XCD b % 8; tile t = (b %
+// 8) * per + b / 8 gives each XCD a contiguous run of tiles (per = tiles / 8
+// when it divides).
+IFR_DEV void pg_tile(const PfGemmArgs &a, uint32_t &m0, uint32_t &n0) {
+    const uint32_t tn = a.tiles_n, tiles = tn * a.tiles_m;
+    const uint32_t b = blockIdx.x;
+    const uint32_t t = (tiles & 7u) == 0 ? (b & 7u) * (tiles >> 3) + (b >> 3) : b;
+    m0 = (t / tn) * PG_BM;
+    n0 = (t % tn) * PG_BN;
+}
+
+// GGUF row of tile row r (rows past N repeat the last row).
+template <int EPI>
+IFR_DEV const uint8_t *pg_wrow(const PfGemmArgs &a, uint32_t n0, uint32_t r) {
+    if constexpr (EPI == PG_SWIGLU) {
+        // wave column c = r / 64 holds FFN rows j in [n0 / 2 + 32 c, +32):
+        // tile rows 64 c + i are gate row j, 64 c + 32 + i up row j
+        const uint32_t j = min(n0 / 2 + 32 * (r >> 6) + (r & 31u), a.n1 - 1);
+        return ((r >> 5) & 1u ? a.w1 : a.w0) + (size_t)j * a.row_bytes;
+    } else {
+        const uint32_t n = min(n0 + r, a.N - 1);
+        const uint8_t *base = n < a.n1 ? a.w0 : n < a.n2 ? a.w1 : a.w2;
+        const uint32_t nr = n < a.n1 ? n : n < a.n2 ? n - a.n1 : n - a.n2;
+        return base + (size_t)nr * a.row_bytes;
+    }
+}
+
+// One wave's 128 x 64 share of the tile out of its accumulators.  D[row][col]
+// of block (i, j): col = lane % 32 (n), row = 8 (e / 4) + 4 (lane / 32) + e %
+// 4 (m).
+template <int EPI>
+IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[4][2], uint32_t lane, uint32_t wm, uint32_t wn,
+                         uint32_t m0, uint32_t n0) {
+    const uint32_t li = lane & 31u;
+    if constexpr (EPI == PG_SWIGLU) {
+        const uint32_t jn = n0 / 2 + wn / 2 + li;
+        if (jn >= a.n1) return;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                if (m < a.M) {
+                    const float gg = acc[i][0][e], u = acc[i][1][e];
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * (gg / (1.0f + expf(-gg))));
+                }
+            }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t n = n0 + wn + 32 * j + li;
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                    if (m < a.M) {
+                        float *yp = (float *)a.y + (size_t)m * a.ldy + n;
+                        if constexpr (EPI == PG_ADD)
+                            *yp += acc[i][j][e];
+                        else
+                            *yp = acc[i][j][e];
+                    }
+                }
+        }
+    }
+}
+
 template <int FMT, int EPI>
 __device__ void pf_gemm_body(const PfGemmArgs &a) {
     // four LDS objects, so the compiler sees that the direct loads into one
@@ -229,14 +363,8 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
     g.wn = 64 * (g.wave >> 1);
     g.nk = a.K / PG_BK;
     g.x = (const _Float16 *)a.x;
-
-    // tiles in n-fastest order: consecutive workgroups share an X tile.
-    // Workgroup b runs on XCD b % 8; tile t = (b % 8) * per + b / 8 gives
-    // each XCD a contiguous run of tiles (per = tiles / 8 when it divides).
-    const uint32_t tn = a.tiles_n, tiles = tn * a.tiles_m;
-    const uint32_t b = blockIdx.x;
-    const uint32_t t = (tiles & 7u) == 0 ? (b & 7u) * (tiles >> 3) + (b >> 3) : b;
-    const uint32_t m0 = (t / tn) * PG_BM, n0 = (t % tn) * PG_BN;
+    uint32_t m0, n0;
+    pg_tile(a, m0, n0);
 
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -245,17 +373,7 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
         g.xoff[j] = 2 * (min(m0 + row, a.M - 1) * a.ldx + 8 * c);
     }
     const uint32_t r = g.r;
-    if constexpr (EPI == PG_SWIGLU) {
-        // wave column c = r / 64 holds FFN rows j in [n0 / 2 + 32 c, +32):
-        // tile rows 64 c + i are gate row j, 64 c + 32 + i up row j
-        const uint32_t j = min(n0 / 2 + 32 * (r >> 6) + (r & 31u), a.n1 - 1);
-        g.wrow = ((r >> 5) & 1u ? a.w1 : a.w0) + (size_t)j * a.row_bytes;
-    } else {
-        const uint32_t n = min(n0 + r, a.N - 1);
-        const uint8_t *base = n < a.n1 ? a.w0 : n < a.n2 ? a.w1 : a.w2;
-        const uint32_t nr = n < a.n1 ? n : n < a.n2 ? n - a.n1 : n - a.n2;
-        g.wrow = base + (size_t)nr * a.row_bytes;
-    }
+    g.wrow = pg_wrow<EPI>(a, n0, r);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -284,43 +402,112 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
         asm volatile("s_waitcnt vmcnt(0)" : "+v"(g.st0.hv), "+v"(g.st0.qv), "+v"(g.st1.hv), "+v"(g.st1.qv)::"memory");
     else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    pg_epilogue<EPI>(a, g.acc, g.lane, g.wm, g.wn, m0, n0);
+}
 
-    // D[row][col] of block (i, j): col = lane % 32 (n), row = 8 (e / 4) +
-    // 4 (lane / 32) + e % 4 (m)
-    const uint32_t lane = g.lane, li = lane & 31u, wm = g.wm, wn = g.wn;
-    if constexpr (EPI == PG_SWIGLU) {
-        const uint32_t jn = n0 / 2 + wn / 2 + li;
-        if (jn >= a.n1) return;
+// Warp-specialized form of the Q4_K product (option pf_ws): the same tile,
+// LDS layout, products and epilogue, with the work split by role over 12
+// waves, three per SIMD.  Waves 0-7 only read operands from LDS and run the
+// MFMAs (each its 128 x 64 share, as above); waves 8-11 only stage: thread t
+// of them requests the X rows (direct loads, a step ahead) and tile row t's
+// GGUF bytes (header and 32 qs bytes, two steps ahead) and dequantizes the
+// whole row's 64 weights of the next step into the other buffer (one
+// thread per row: conflict-free row stores).  The dequantization runs in
+// waves of its own beside the MFMA waves' products instead of in their
+// instruction stream (4095-token 8B prefill 65.9 -> 62.1 ms).  One barrier
+// per step for all 12 waves, as in the eight-wave form; the results are the
+// same bit for bit (the same f16 operands, the same MFMA chains).
+constexpr int PGW_THREADS = 768;
+template <int EPI>
+__device__ void pf_gemm_ws_body(const PfGemmArgs &a) {
+    __shared__ __attribute__((aligned(1024))) _Float16 xs0[PG_BM * PG_BK], xs1[PG_BM * PG_BK];
+    __shared__ __attribute__((aligned(1024))) _Float16 ws0[PG_BN * PG_BK], ws1[PG_BN * PG_BK];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nk = a.K / PG_BK;
+    uint32_t m0, n0;
+    pg_tile(a, m0, n0);
+
+    if (wave < 8) {
+        // MFMA waves
+        const uint32_t wm = 128 * (wave & 1u), wn = 64 * (wave >> 1);
+        PgCtx<Q4_K> g;
+        g.lane = lane;
+        g.wm = wm;
+        g.wn = wn;
+        g.xs[0] = xs0;
+        g.xs[1] = xs1;
+        g.ws[0] = ws0;
+        g.ws[1] = ws1;
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                if (m < a.M) {
-                    const float gg = g.acc[i][0][e], u = g.acc[i][1][e];
-                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * (gg / (1.0f + expf(-gg))));
-                }
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) g.acc[i][j][e] = 0.0f;
+        asm volatile("s_barrier" ::: "memory");
+        for (uint32_t s = 0; s < nk; s += 2) {
+            g.template mfma_step<0>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (s + 1 < nk) {
+                g.template mfma_step<1>();
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             }
-    } else {
+        }
+        pg_epilogue<EPI>(a, g.acc, lane, wm, wn, m0, n0);
+        return;
+    }
+
+    // staging waves: thread t owns tile row t and, for the X tile, rows
+    // 64 v + 8 j + lane / 8 of its wave v's eight direct loads j
+    const uint32_t t = tid - 512u, v = wave - 8u;
+    const _Float16 *x = (const _Float16 *)a.x;
+    uint32_t xoff[8];
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const uint32_t n = n0 + wn + 32 * j + li;
-            if (n >= a.N) continue;
+    for (int j = 0; j < 8; j++) {
+        const uint32_t row = 64 * v + 8 * (uint32_t)j + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ pg_swz_of(row);
+        xoff[j] = 2 * (min(m0 + row, a.M - 1) * a.ldx + 8 * c);
+    }
+    const uint32_t xdst0 = lds_addr(xs0 + (64 * v) * PG_BK), xdst1 = lds_addr(xs1 + (64 * v) * PG_BK);
+    auto load_x = [&](uint32_t dst, uint32_t k) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                    if (m < a.M) {
-                        float *yp = (float *)a.y + (size_t)m * a.ldy + n;
-                        if constexpr (EPI == PG_ADD)
-                            *yp += g.acc[i][j][e];
-                        else
-                            *yp = g.acc[i][j][e];
-                    }
-                }
+        for (int j = 0; j < 8; j++) lds_dma16(x + k * PG_BK, xoff[j], __builtin_amdgcn_readfirstlane(dst + 1024 * j));
+    };
+    const uint8_t *wrow = pg_wrow<EPI>(a, n0, t);
+    PgRowQ4K st0, st1;
+    // prologue: X and weights of step 0 into buffer 0, weights of step 1 in
+    // flight (loads in flight at the first wait: the 3 of step 1)
+    load_x(xdst0, 0);
+    st0.load(wrow, 0);
+    st1.load(wrow, min(1u, nk - 1) * PG_BK);
+    st0.template wait<3>();
+    st0.store(0, ws0, t);
+    asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // step s: X of step s + 1 (8 loads) and the weights of step s + 2 (3)
+    // are requested, then the weights of step s + 1 are waited for (the 11
+    // just issued may stay in flight) and dequantized into the other buffer;
+    // at the end the X loads have landed (the 3 weight loads may stay in
+    // flight), then the barrier.  Steps past the end load step nk - 1 again
+    // into buffers nobody reads.
+    for (uint32_t s = 0; s < nk; s += 2) {
+        load_x(xdst1, min(s + 1, nk - 1));
+        st0.load(wrow, min(s + 2, nk - 1) * PG_BK);
+        st1.template wait<11>();
+        st1.store(min(s + 1, nk - 1) * PG_BK, ws1, t);
+        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (s + 1 < nk) {
+            load_x(xdst0, min(s + 2, nk - 1));
+            st1.load(wrow, min(s + 3, nk - 1) * PG_BK);
+            st0.template wait<11>();
+            st0.store(min(s + 2, nk - 1) * PG_BK, ws0, t);
+            asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
     }
+    // the clamped loads past the end: their destination registers stay
+    // allocated until they have landed
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(st0.hv), "+v"(st0.q0), "+v"(st0.q1), "+v"(st1.hv), "+v"(st1.q0),
+                 "+v"(st1.q1)::"memory");
 }
 
 } // namespace ifr

@@ -49,6 +49,7 @@ constexpr uint32_t MAX_PARTS = 1024;      // argmax partial keys per launch
 constexpr uint32_t PF_GEMM_TILE = 128;    // device/prefill.h: PF_BM = PF_BN
 constexpr uint32_t PF_BIG_TILE = 256;     // device/pf_gemm.h: PG_BM = PG_BN
 constexpr uint32_t PF_BIG_THREADS = 512;  // device/pf_gemm.h: PG_THREADS
+constexpr uint32_t PF_WS_THREADS = 768;   // device/pf_gemm.h: PGW_THREADS
 constexpr uint32_t PF_CHUNK = 4096;       // prompt tokens per prefill pass (at most)
 
 int qk_of(int32_t dt) {
@@ -142,6 +143,10 @@ struct ifr_ctx {
     // has enough of them, else 128 x 128), 128 or 256 to force one (option
     // pf_tile)
     uint32_t pf_tile = 0;
+    // Q4_K products on 256 x 256 tiles in the warp-specialized form (option
+    // pf_ws, default on; 0 = the eight-wave form; device/pf_gemm.h
+    // pf_gemm_ws_body)
+    int pf_ws = 1;
     // bumped by every option change: a captured decode step is captured
     // again when it differs
     uint64_t opt_gen = 0;
@@ -988,6 +993,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->pf_tile = (uint32_t)value;
         return IFR_OK;
     }
+    if (!strcmp(key, "pf_ws")) {
+        c->pf_ws = value ? 1 : 0;
+        return IFR_OK;
+    }
     if (!strcmp(key, "gemv_grp")) {
         c->gemv_grp = (int)value;
         return IFR_OK;
@@ -1009,6 +1018,7 @@ IFR_API ifr_status ifr_get_option(ifr_ctx *c, const char *key, int64_t *value) {
     else if (k == "gemv_exact") *value = c->gemv_exact;
     else if (k == "pf_chunk") *value = c->pf_chunk;
     else if (k == "pf_tile") *value = c->pf_tile;
+    else if (k == "pf_ws") *value = c->pf_ws;
     else if (k == "gemv_grp") *value = c->gemv_grp;
     else if (k == "gemv_waves") *value = c->gemv_waves;
     else return c->fail(IFR_EINVAL, "unknown option %s", key);
@@ -1724,6 +1734,9 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
     // the large form addresses X rows with 32-bit byte offsets
     const bool big_ok = (uint64_t)M * ldx * 2 < (1ull << 32);
     const bool big = big_ok && (c->pf_tile == 256 || (c->pf_tile == 0 && g.tiles_n * g.tiles_m >= PF_BIG_TILES_MIN));
+    if (big && c->pf_ws && m[0]->dtype == IFR_Q4_K)
+        return c->launch(std::string("pf_gemm_q4_k_ws_") + epi_name[epi], dim3(g.tiles_n * g.tiles_m),
+                         dim3(PF_WS_THREADS), 0, g);
     if (big)
         return c->launch(std::string("pf_gemm_") + gemv_fmt_name(m[0]->dtype) + "_" + epi_name[epi],
                          dim3(g.tiles_n * g.tiles_m), dim3(PF_BIG_THREADS), 0, g);

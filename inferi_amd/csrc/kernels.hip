@@ -178,6 +178,16 @@ PF_GEMM_KERNELS(q5_0, Q5_0)
 PF_GEMM_KERNELS(q5_1, Q5_1)
 PF_GEMM_KERNELS(f16, F16)
 PF_GEMM_KERNELS(f32, F32)
+// the warp-specialized Q4_K product (option pf_ws): 12 waves, three per SIMD
+extern "C" __global__ void __launch_bounds__(PGW_THREADS) pf_gemm_q4_k_ws_store(PfGemmArgs a) {
+    pf_gemm_ws_body<PG_STORE>(a);
+}
+extern "C" __global__ void __launch_bounds__(PGW_THREADS) pf_gemm_q4_k_ws_add(PfGemmArgs a) {
+    pf_gemm_ws_body<PG_ADD>(a);
+}
+extern "C" __global__ void __launch_bounds__(PGW_THREADS) pf_gemm_q4_k_ws_swiglu(PfGemmArgs a) {
+    pf_gemm_ws_body<PG_SWIGLU>(a);
+}
 extern "C" __global__ void __launch_bounds__(256) pf_embed_k(PfArgs a) { pf_embed_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { pf_rmsnorm_f16_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }

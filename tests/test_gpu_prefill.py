@@ -35,19 +35,27 @@ def synthetic_q(ctx, rows, cols, seed, dtype):
     return w
 
 
-def _gemm_case(ctx, dtype, rows, cols, m, w, rng, tiles=(128, 256)):
+# (pf_tile, pf_ws): the 128 x 128 form, the 256 x 256 eight-wave form and
+# the 256 x 256 warp-specialized form (Q4_K only; other types ignore pf_ws)
+TILE_FORMS = ((128, 0), (256, 0), (256, 1))
+
+
+def _gemm_case(ctx, dtype, rows, cols, m, w, rng, forms=TILE_FORMS):
     """y = x . deq(W)^T in each tile form against the f64 product of the same
     f16-rounded operands (bound 2e-5 * sum |x w|), then the accumulating form;
     the tile forms agree bit for bit."""
     import inferi_amd as I
 
     outs = []
-    for tile in tiles:
+    ws0 = ctx.get_option("pf_ws")
+    for tile, ws in forms:
         ctx.set_option("pf_tile", tile)
+        ctx.set_option("pf_ws", ws)
         try:
             outs.append(_gemm_case1(ctx, dtype, rows, cols, m, w, np.random.default_rng(rows + cols + m)))
         finally:
             ctx.set_option("pf_tile", 0)
+            ctx.set_option("pf_ws", ws0)
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), "tile forms differ"
 
@@ -246,7 +254,7 @@ def test_prefill_pass_length_and_tile_give_same_results(ctx):
     """The prompt in passes of 64, 192 or all its 299 tokens at once, with the
     GEMMs in 128 x 128 or 256 x 256 tiles: the same KV cache rows, logits and
     tokens bit for bit, since each output row's GEMM sum (k in the same order
-    in both tile forms) and each query's attention are computed the same way
+    in every tile form) and each query's attention are computed the same way
     in any pass."""
     import inferi_amd as I
 
@@ -255,19 +263,22 @@ def test_prefill_pass_length_and_tile_give_same_results(ctx):
     w = I.Llama2Weights.synthetic(ctx, cfg, seed=43, std=0.05)
     prompt = np.random.default_rng(5).integers(0, cfg.vocab, 300).astype(np.uint32)
     out = {}
+    ws0 = ctx.get_option("pf_ws")
     try:
-        for tile in (128, 256):
+        for tile, ws in TILE_FORMS:
             ctx.set_option("pf_tile", tile)
+            ctx.set_option("pf_ws", ws)
             for chunk in (64, 192, 0):
                 ctx.set_option("pf_chunk", chunk)
-                out[tile, chunk] = _prefill_run(ctx, cfg, w, prompt, 299, 6)
+                out[tile, ws, chunk] = _prefill_run(ctx, cfg, w, prompt, 299, 6)
     finally:
         ctx.set_option("pf_chunk", 0)
         ctx.set_option("pf_tile", 0)
+        ctx.set_option("pf_ws", ws0)
         w.close()
-    ref = out[256, 0]
+    ref = out[256, 0, 0]
     for key, got in out.items():
-        _same(got, ref, f"tile {key[0]}, passes of {key[1] or 299}")
+        _same(got, ref, f"tile {key[0]}{' warp-specialized' if key[1] else ''}, passes of {key[2] or 299}")
 
 
 def test_prefill_uses_weights_rewritten_in_place(ctx):
