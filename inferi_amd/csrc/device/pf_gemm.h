@@ -318,23 +318,37 @@ IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[4][2], uint3
                 }
             }
     } else {
+        // Y (ADD: Y + acc) block by block.  A block's 16 residual loads go
+        // out together, from rows clamped below M (a clamped row is read, not
+        // written), so a lane waits once per block instead of once per
+        // element behind each element's bounds branch (the O and down
+        // products' epilogue, 67 MB read and written at the 8B shape).
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const uint32_t n = n0 + wn + 32 * j + li;
             if (n >= a.N) continue;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++) {
+                float old[16];
+                if constexpr (EPI == PG_ADD) {
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                        old[e] = ((const float *)a.y)[(size_t)min(m, a.M - 1) * a.ldy + n];
+                    }
+                }
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
                     if (m < a.M) {
                         float *yp = (float *)a.y + (size_t)m * a.ldy + n;
                         if constexpr (EPI == PG_ADD)
-                            *yp += acc[i][j][e];
+                            *yp = old[e] + acc[i][j][e];
                         else
                             *yp = acc[i][j][e];
                     }
                 }
+            }
         }
     }
 }

@@ -120,20 +120,36 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
                 }
             }
     } else {
+        // eight values at a time; their residual loads (ADD) go out together
+        // from rows clamped below M, so a lane waits once per eight values,
+        // not once per value behind its bounds branch (eight, not sixteen:
+        // the form keeps its three waves per SIMD)
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const uint32_t n = n0 + wn + 32 * j + li;
+                if (n >= a.N) continue;
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
-                    if (m < a.M && n < a.N) {
-                        float *yp = (float *)a.y + (size_t)m * a.ldy + n;
-                        if constexpr (EPI == PG_ADD)
-                            *yp += acc[i][j][e];
-                        else
-                            *yp = acc[i][j][e];
+                for (int h = 0; h < 16; h += 8) {
+                    float old[8];
+                    if constexpr (EPI == PG_ADD) {
+#pragma unroll
+                        for (int e = h; e < h + 8; e++) {
+                            const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+                            old[e - h] = ((const float *)a.y)[(size_t)min(m, a.M - 1) * a.ldy + n];
+                        }
+                    }
+#pragma unroll
+                    for (int e = h; e < h + 8; e++) {
+                        const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
+                        if (m < a.M) {
+                            float *yp = (float *)a.y + (size_t)m * a.ldy + n;
+                            if constexpr (EPI == PG_ADD)
+                                *yp = old[e - h] + acc[i][j][e];
+                            else
+                                *yp = acc[i][j][e];
+                        }
                     }
                 }
             }
