@@ -30,7 +30,10 @@
 // and up (w1) rows of the same 32 FFN indices, so each lane holds gate and up
 // of the same (m, j) and the epilogue writes h[m][j] = f16(u * silu(g))
 // straight into the down product's input (the reference's silu, silu.rs:
-// 24-53, on the two products).
+// 24-53, on the two products, with the hardware exp2 and reciprocal of the
+// decode step's epilogue, silu_fast: the library's expf and correctly
+// rounded division took about 25 VALU instructions per value, 64 values per
+// lane at the end of every tile while the matrix cores idle).
 #pragma once
 #include "pf_tiles.h"
 
@@ -314,7 +317,7 @@ IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[4][2], uint3
                 const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
                 if (m < a.M) {
                     const float gg = acc[i][0][e], u = acc[i][1][e];
-                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * (gg / (1.0f + expf(-gg))));
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * silu_fast(gg));
                 }
             }
     } else {

@@ -116,7 +116,7 @@ __device__ void gemm_f16_body(const PfGemmArgs &a) {
                 const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * ((uint32_t)lane >> 5) + (e % 4);
                 if (m < a.M) {
                     const float g = acc[i][0][e], u = acc[i][1][e];
-                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * (g / (1.0f + expf(-g))));
+                    ((_Float16 *)a.y)[(size_t)m * a.ldy + jn] = f16_of(u * silu_fast(g));
                 }
             }
     } else {
@@ -266,16 +266,17 @@ IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
     }
 }
 
-// h[m][j] = f16(u * (g / (1 + exp(-g)))), g = gu[m][j], u = gu[m][F + j]
-// (silu.rs:24-53), for layers whose gate and up matrices differ in type (the
-// others take the GEMM's SwiGLU epilogue, the same arithmetic)
+// h[m][j] = f16(u * silu(g)), g = gu[m][j], u = gu[m][F + j] (silu.rs:
+// 24-53), for layers whose gate and up matrices differ in type (the others
+// take the GEMM's SwiGLU epilogue, the same arithmetic: silu_fast, the
+// hardware exp2 and reciprocal, as the decode step's gate/up epilogue)
 IFR_DEV void pf_silu_body(const PfArgs &a) {
     const uint32_t m = blockIdx.y, F = a.ffn;
     const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= F) return;
     const float *gu = (const float *)a.gu;
     const float g = gu[(size_t)m * 2 * F + j], u = gu[(size_t)m * 2 * F + F + j];
-    ((_Float16 *)a.h)[(size_t)m * F + j] = f16_of(u * (g / (1.0f + expf(-g))));
+    ((_Float16 *)a.h)[(size_t)m * F + j] = f16_of(u * silu_fast(g));
 }
 
 // ------------------------------------------------------------ attention --
