@@ -901,14 +901,16 @@ IFR_DEV const uint8_t *gemv_row_ptr(const GemvArgs &a, uint32_t v) {
 // vector (inferi-shaders/src/rope.rs:51-92): theta = base^(-(idx mod hs)/hs)
 // read from the state's table (rope_theta_f32 of every pair), angle =
 // pos * theta.
-IFR_DEV void rope_pair(float &a, float &b, uint32_t idx, uint32_t hs, uint32_t pos, const float *theta_tab) {
-    const float theta = theta_tab[(idx % hs) >> 1];
+IFR_DEV void rope_pair_theta(float &a, float &b, float theta, uint32_t pos) {
     const float ang = (float)pos * theta;
     float sn, cs;
     sincosf(ang, &sn, &cs);
     const float x = a, y = b;
     a = cs * x - sn * y;
     b = sn * x + cs * y;
+}
+IFR_DEV void rope_pair(float &a, float &b, uint32_t idx, uint32_t hs, uint32_t pos, const float *theta_tab) {
+    rope_pair_theta(a, b, theta_tab[(idx % hs) >> 1], pos);
 }
 
 // QKV epilogue of virtual rows v, v+1 (v even, one pair of one head): the
