@@ -248,93 +248,55 @@ IFR_DEV void pf_rmsnorm_f16_body(const PfArgs &a) {
 IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
     const uint32_t m = blockIdx.x, pos = a.p0 + m, hs = a.head_size;
     float *row = (float *)a.qkv + (size_t)m * a.ld_qkv;
-    const uint32_t qd = a.q_dim, kd = a.kv_dim, np = (qd + kd) / 2;
+    const uint32_t qd = a.q_dim, kd = a.kv_dim;
     // each thread owns whole rotation pairs of q | k: pair i of a vector
     // rotates (e0, e1) = (2i, 2i+1), or NeoX (rope.rs:97-141): within head
     // h = 2i / hs, (h hs + j, h hs + j + hs/2) with j = i mod hs/2; the
-    // biases (Qwen2) are added first, as transformer.rs:434-445 orders it.
-    // PB pairs per thread at a time: their loads (the pair, its biases, its
-    // theta) go out together from indices clamped into the row, then the
-    // rotations and stores, so a thread waits once per PB pairs (a loop of
-    // one pair at a time waited for each pair's loads: the compiler cannot
-    // move a load past the previous pair's stores into the same row).
-    constexpr uint32_t PB = 8;
-    for (uint32_t i0 = threadIdx.x; i0 < np; i0 += PB * blockDim.x) {
-        float x0[PB], x1[PB], b0[PB], b1[PB], th[PB];
-        uint32_t e0[PB], e1[PB];
-#pragma unroll
-        for (uint32_t c = 0; c < PB; c++) {
-            const uint32_t i = min(i0 + c * blockDim.x, np - 1);
-            const bool is_q = 2 * i < qd;
-            const uint32_t pi = is_q ? i : i - qd / 2; // pair index within its vector
-            if (a.neox) {
-                const uint32_t h = (2 * pi) / hs, j = pi % (hs / 2);
-                e0[c] = h * hs + j;
-                e1[c] = e0[c] + hs / 2;
-            } else {
-                e0[c] = 2 * pi;
-                e1[c] = e0[c] + 1;
-            }
-            const uint32_t base = is_q ? 0 : qd;
-            x0[c] = row[base + e0[c]];
-            x1[c] = row[base + e1[c]];
-            // no bias: a valid dummy read, not used
-            const float *bias = is_q ? a.q_bias : a.k_bias;
-            const float *bp = bias ? bias : row;
-            b0[c] = bp[e0[c]];
-            b1[c] = bp[e1[c]];
-            // theta index j (the table holds base^(-2j/hs))
-            const uint32_t tj = a.neox ? 2 * (pi % (hs / 2)) : e0[c];
-            th[c] = a.rope_tab[(tj % hs) >> 1];
+    // biases (Qwen2) are added first, as transformer.rs:434-445 orders it
+    for (uint32_t i = threadIdx.x; i < (qd + kd) / 2; i += blockDim.x) {
+        const bool is_q = 2 * i < qd;
+        const uint32_t pi = is_q ? i : i - qd / 2; // pair index within its vector
+        uint32_t e0, e1;
+        if (a.neox) {
+            const uint32_t h = (2 * pi) / hs, j = pi % (hs / 2);
+            e0 = h * hs + j;
+            e1 = e0 + hs / 2;
+        } else {
+            e0 = 2 * pi;
+            e1 = e0 + 1;
         }
-#pragma unroll
-        for (uint32_t c = 0; c < PB; c++) {
-            const uint32_t i = i0 + c * blockDim.x;
-            if (i >= np) continue;
-            const bool is_q = 2 * i < qd;
-            const float *bias = is_q ? a.q_bias : a.k_bias;
-            float y0 = x0[c], y1 = x1[c];
-            if (bias) {
-                y0 = y0 + b0[c];
-                y1 = y1 + b1[c];
-            }
-            rope_pair_theta(y0, y1, th[c], pos);
-            if (is_q) {
-                row[e0[c]] = y0;
-                row[e1[c]] = y1;
+        const uint32_t base = is_q ? 0 : qd;
+        float x0 = row[base + e0], x1 = row[base + e1];
+        const float *bias = is_q ? a.q_bias : a.k_bias;
+        if (bias) {
+            x0 = x0 + bias[e0];
+            x1 = x1 + bias[e1];
+        }
+        // theta index j (the table holds base^(-2j/hs)); rope_pair takes 2j
+        const uint32_t tj = a.neox ? 2 * (pi % (hs / 2)) : e0;
+        rope_pair(x0, x1, tj, hs, pos, a.rope_tab);
+        if (is_q) {
+            row[e0] = x0;
+            row[e1] = x1;
+        } else {
+            const size_t off = (size_t)pos * kd;
+            if (a.kv_f16) {
+                ((uint16_t *)a.k_cache)[off + e0] = f32_to_f16(x0);
+                ((uint16_t *)a.k_cache)[off + e1] = f32_to_f16(x1);
             } else {
-                const size_t off = (size_t)pos * kd;
-                if (a.kv_f16) {
-                    ((uint16_t *)a.k_cache)[off + e0[c]] = f32_to_f16(y0);
-                    ((uint16_t *)a.k_cache)[off + e1[c]] = f32_to_f16(y1);
-                } else {
-                    ((float *)a.k_cache)[off + e0[c]] = y0;
-                    ((float *)a.k_cache)[off + e1[c]] = y1;
-                }
+                ((float *)a.k_cache)[off + e0] = x0;
+                ((float *)a.k_cache)[off + e1] = x1;
             }
         }
     }
-    for (uint32_t i0 = threadIdx.x; i0 < kd; i0 += PB * blockDim.x) {
-        float v[PB], vb[PB];
-        const float *bp = a.v_bias ? a.v_bias : row;
-#pragma unroll
-        for (uint32_t c = 0; c < PB; c++) {
-            const uint32_t i = min(i0 + c * blockDim.x, kd - 1);
-            v[c] = row[qd + kd + i];
-            vb[c] = bp[i];
-        }
-#pragma unroll
-        for (uint32_t c = 0; c < PB; c++) {
-            const uint32_t i = i0 + c * blockDim.x;
-            if (i >= kd) continue;
-            float x = v[c];
-            if (a.v_bias) x = x + vb[c];
-            const size_t off = (size_t)pos * kd + i;
-            if (a.kv_f16)
-                ((uint16_t *)a.v_cache)[off] = f32_to_f16(x);
-            else
-                ((float *)a.v_cache)[off] = x;
-        }
+    for (uint32_t i = threadIdx.x; i < kd; i += blockDim.x) {
+        float v = row[qd + kd + i];
+        if (a.v_bias) v = v + a.v_bias[i];
+        const size_t off = (size_t)pos * kd + i;
+        if (a.kv_f16)
+            ((uint16_t *)a.v_cache)[off] = f32_to_f16(v);
+        else
+            ((float *)a.v_cache)[off] = v;
     }
 }
 
