@@ -300,18 +300,18 @@ IFR_DEV const uint8_t *pg_wrow(const PfGemmArgs &a, uint32_t n0, uint32_t r) {
     }
 }
 
-// One wave's 128 x 64 share of the tile out of its accumulators.  D[row][col]
-// of block (i, j): col = lane % 32 (n), row = 8 (e / 4) + 4 (lane / 32) + e %
-// 4 (m).
-template <int EPI>
-IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[4][2], uint32_t lane, uint32_t wm, uint32_t wn,
+// One wave's (32 MI) x 64 share of the tile out of its accumulators.
+// D[row][col] of block (i, j): col = lane % 32 (n), row = 8 (e / 4) + 4 (lane
+// / 32) + e % 4 (m).
+template <int EPI, int MI = 4>
+IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[MI][2], uint32_t lane, uint32_t wm, uint32_t wn,
                          uint32_t m0, uint32_t n0) {
     const uint32_t li = lane & 31u;
     if constexpr (EPI == PG_SWIGLU) {
         const uint32_t jn = n0 / 2 + wn / 2 + li;
         if (jn >= a.n1) return;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < MI; i++)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const uint32_t m = m0 + wm + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
@@ -331,7 +331,7 @@ IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[4][2], uint3
             const uint32_t n = n0 + wn + 32 * j + li;
             if (n >= a.N) continue;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < MI; i++) {
                 float old[16];
                 if constexpr (EPI == PG_ADD) {
 #pragma unroll
@@ -422,6 +422,125 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
     pg_epilogue<EPI>(a, g.acc, g.lane, g.wm, g.wn, m0, n0);
 }
 
+// The warp-specialized form's tile: workgroups below tiles_full take whole
+// tiles as pg_tile maps them; the rest take the last tiles_n * tiles_m -
+// tiles_full tiles as 256 x 128 halves, two workgroups per tile, so that a
+// launch whose tiles leave its last round part-empty (the Q/K/V product at
+// the 8B shape: 384 tiles for 256 CUs) ends in a round of halves over every
+// CU.  Returns whether this workgroup takes a half.
+IFR_DEV bool pg_tile_ws(const PfGemmArgs &a, uint32_t &m0, uint32_t &n0) {
+    const uint32_t tn = a.tiles_n, tiles = tn * a.tiles_m, tf = a.tiles_full;
+    const uint32_t b = blockIdx.x;
+    if (b < tf) {
+        const uint32_t t = (tf & 7u) == 0 ? (b & 7u) * (tf >> 3) + (b >> 3) : b;
+        m0 = (t / tn) * PG_BM;
+        n0 = (t % tn) * PG_BN;
+        return false;
+    }
+    // halves: each XCD (b % 8 with tf a multiple of 8) a contiguous run
+    const uint32_t h = b - tf, H = 2 * (tiles - tf);
+    const uint32_t u = (H & 7u) == 0 && (tf & 7u) == 0 ? (h & 7u) * (H >> 3) + (h >> 3) : h;
+    const uint32_t t = tf + u / 2;
+    m0 = (t / tn) * PG_BM;
+    n0 = (t % tn) * PG_BN + (PG_BN / 2) * (u & 1u);
+    return true;
+}
+
+// A 256 x 128 half tile (pg_tile_ws): the MFMA waves own 64 x 64 shares (2 x
+// 2 blocks), wave w at m 64 (w % 4), n 64 (w / 4); the staging waves load the
+// same 256 X rows and dequantize the half's 128 weight rows, two threads per
+// row (PgHalf's split: part t % 2 of row t / 2).  Each output is the same
+// MFMA chain over K as in a whole tile, so the results are the same bit for
+// bit.
+template <int EPI>
+__device__ void pf_gemm_ws_half(const PfGemmArgs &a, _Float16 *xs0, _Float16 *xs1, _Float16 *ws0, _Float16 *ws1,
+                                uint32_t m0, uint32_t n0) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nk = a.K / PG_BK;
+    if (wave < 8) {
+        const uint32_t wm = 64 * (wave & 3u), wn = 64 * (wave >> 2);
+        const uint32_t li = lane & 31u, hi = lane >> 5;
+        float16v acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+        auto step = [&](const _Float16 *xb, const _Float16 *wb) {
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                half8v av[2], bv[2];
+                const uint32_t c = 2 * (uint32_t)kk + hi;
+#pragma unroll
+                for (int i = 0; i < 2; i++) av[i] = *(const half8v *)(xb + pg_swz(wm + 32 * i + li, c));
+#pragma unroll
+                for (int j = 0; j < 2; j++) bv[j] = *(const half8v *)(wb + pg_swz(wn + 32 * j + li, c));
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+            }
+        };
+        asm volatile("s_barrier" ::: "memory");
+        for (uint32_t s = 0; s < nk; s += 2) {
+            step(xs0, ws0);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (s + 1 < nk) {
+                step(xs1, ws1);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            }
+        }
+        pg_epilogue<EPI, 2>(a, acc, lane, wm, wn, m0, n0);
+        return;
+    }
+    const uint32_t t = tid - 512u, v = wave - 8u, r = t >> 1, p = t & 1u;
+    const _Float16 *x = (const _Float16 *)a.x;
+    uint32_t xoff[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t row = 64 * v + 8 * (uint32_t)j + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ pg_swz_of(row);
+        xoff[j] = 2 * (min(m0 + row, a.M - 1) * a.ldx + 8 * c);
+    }
+    const uint32_t xdst0 = lds_addr(xs0 + (64 * v) * PG_BK), xdst1 = lds_addr(xs1 + (64 * v) * PG_BK);
+    auto load_x = [&](uint32_t dst, uint32_t k) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) lds_dma16(x + k * PG_BK, xoff[j], __builtin_amdgcn_readfirstlane(dst + 1024 * j));
+    };
+    const uint8_t *wrow = pg_wrow<EPI>(a, n0, r);
+    PgHalf<Q4_K> st0, st1;
+    auto store = [&](const PgHalf<Q4_K> &st, uint32_t k0, _Float16 *tile) {
+        q4k_store_part_mix(st.qv, q4k_affine(st.hv, k0), p, tile, r);
+    };
+    // as the whole tile's staging with two weight loads per step: in
+    // flight at the weight waits the 10 loads issued after them, at the
+    // step's end the 2 weight loads of the step after next
+    load_x(xdst0, 0);
+    st0.load(wrow, 0, p);
+    st1.load(wrow, min(1u, nk - 1) * PG_BK, p);
+    st0.template wait<2>();
+    store(st0, 0, ws0);
+    asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    for (uint32_t s = 0; s < nk; s += 2) {
+        load_x(xdst1, min(s + 1, nk - 1));
+        st0.load(wrow, min(s + 2, nk - 1) * PG_BK, p);
+        st1.template wait<10>();
+        store(st1, min(s + 1, nk - 1) * PG_BK, ws1);
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (s + 1 < nk) {
+            load_x(xdst0, min(s + 2, nk - 1));
+            st1.load(wrow, min(s + 3, nk - 1) * PG_BK, p);
+            st0.template wait<10>();
+            store(st0, min(s + 2, nk - 1) * PG_BK, ws0);
+            asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(st0.hv), "+v"(st0.qv), "+v"(st1.hv), "+v"(st1.qv)::"memory");
+}
+
 // Warp-specialized form of the Q4_K product (option pf_ws): the same tile,
 // LDS layout, products and epilogue, with the work split by role over 12
 // waves, three per SIMD.  Waves 0-7 only read operands from LDS and run the
@@ -443,7 +562,10 @@ __device__ void pf_gemm_ws_body(const PfGemmArgs &a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t nk = a.K / PG_BK;
     uint32_t m0, n0;
-    pg_tile(a, m0, n0);
+    if (pg_tile_ws(a, m0, n0)) { // (uniform)
+        pf_gemm_ws_half<EPI>(a, xs0, xs1, ws0, ws1, m0, n0);
+        return;
+    }
 
     if (wave < 8) {
         // MFMA waves

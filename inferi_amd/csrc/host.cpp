@@ -50,6 +50,7 @@ constexpr uint32_t PF_GEMM_TILE = 128;    // device/prefill.h: PF_BM = PF_BN
 constexpr uint32_t PF_BIG_TILE = 256;     // device/pf_gemm.h: PG_BM = PG_BN
 constexpr uint32_t PF_BIG_THREADS = 512;  // device/pf_gemm.h: PG_THREADS
 constexpr uint32_t PF_WS_THREADS = 768;   // device/pf_gemm.h: PGW_THREADS
+constexpr uint32_t PF_WS_ROUND = 256;     // workgroups of one round (one per CU on MI355X)
 constexpr uint32_t PF_CHUNK = 4096;       // prompt tokens per prefill pass (at most)
 
 int qk_of(int32_t dt) {
@@ -1734,9 +1735,14 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
     // the large form addresses X rows with 32-bit byte offsets
     const bool big_ok = (uint64_t)M * ldx * 2 < (1ull << 32);
     const bool big = big_ok && (c->pf_tile == 256 || (c->pf_tile == 0 && g.tiles_n * g.tiles_m >= PF_BIG_TILES_MIN));
-    if (big && c->pf_ws && m[0]->dtype == IFR_Q4_K)
-        return c->launch(std::string("pf_gemm_q4_k_ws_") + epi_name[epi], dim3(g.tiles_n * g.tiles_m),
+    if (big && c->pf_ws && m[0]->dtype == IFR_Q4_K) {
+        // a last round of at most 128 tiles (half the CUs) runs as twice as
+        // many 256 x 128 halves, one round over every CU
+        const uint32_t tiles = g.tiles_n * g.tiles_m, tail = tiles % PF_WS_ROUND;
+        g.tiles_full = tail != 0 && tail <= PF_WS_ROUND / 2 ? tiles - tail : tiles;
+        return c->launch(std::string("pf_gemm_q4_k_ws_") + epi_name[epi], dim3(tiles + (tiles - g.tiles_full)),
                          dim3(PF_WS_THREADS), 0, g);
+    }
     if (big)
         return c->launch(std::string("pf_gemm_") + gemv_fmt_name(m[0]->dtype) + "_" + epi_name[epi],
                          dim3(g.tiles_n * g.tiles_m), dim3(PF_BIG_THREADS), 0, g);

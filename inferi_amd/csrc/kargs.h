@@ -239,6 +239,9 @@ struct PfGemmArgs {
     uint32_t M, N, K, ldx, ldy, row_bytes;
     uint32_t n1, n2;     // stacked matrix boundaries
     uint32_t tiles_n, tiles_m; // tile grid (pf_gemm: 256 x 256 tiles)
+    // warp-specialized form: tiles at or past tiles_full run as two 256 x
+    // 128 halves, one workgroup each (tiles_full = tiles_n * tiles_m: none)
+    uint32_t tiles_full;
 };
 
 // Prefill pointwise and attention kernels (one chunk of M prompt tokens at

@@ -84,8 +84,12 @@ def _gemm_case1(ctx, dtype, rows, cols, m, w, rng):
 
 
 @pytest.mark.parametrize("rows,cols,m", [(128, 256, 128), (300, 512, 70), (1000, 1024, 257), (4096, 4096, 128),
-                                         (64, 14336, 33), (4096, 4096, 512), (512, 14336, 300), (1024, 4096, 4095)])
+                                         (64, 14336, 33), (4096, 4096, 512), (512, 14336, 300), (1024, 4096, 4095),
+                                         (6144, 4096, 4095)])
 def test_gemm_quant_matches_f64(ctx, oracle_lib, rows, cols, m):
+    """Q4_K at shapes whose 256 x 256 tile counts cover the warp-specialized
+    form's cases: fewer than 128 tiles (every tile in two halves), and 384
+    tiles (the 8B Q/K/V shape: 256 whole tiles, then 128 in halves)."""
     import inferi_amd as I
 
     rng = np.random.default_rng(rows * 7 + cols + m)
