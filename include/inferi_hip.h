@@ -109,6 +109,10 @@ IFR_API ifr_status ifr_device_info(ifr_ctx *ctx, char *name, size_t name_len, in
  * load and dequantize the tiles), 0 in the eight-wave form where every wave
  * does both.  Every form sums each output element's products in the same
  * order, so the results do not depend on the form or the pass length.
+ * "pf_rope_fuse" = 1 (the default) lets the warp-specialized Q/K/V product
+ * add the biases, apply RoPE and store k and v to the cache in its epilogue
+ * (pairs (2i, 2i + 1) only), 0 leaves that to a kernel of its own; both
+ * give the same results bit for bit.
  * A captured decode step is captured again after any option change. */
 IFR_API ifr_status ifr_set_option(ifr_ctx *ctx, const char *key, int64_t value);
 /* Reads an option (no reference counterpart): any key ifr_set_option takes. */

@@ -909,6 +909,16 @@ IFR_DEV void rope_pair_theta(float &a, float &b, float theta, uint32_t pos) {
     a = cs * x - sn * y;
     b = sn * x + cs * y;
 }
+// The rotation of the prompt path, given the angle's cosine and sine (the
+// prefill's per-pass table), written out so that the separate RoPE kernel
+// and the GEMM epilogue that fuses it round alike: a' = cos a - sin b, b' =
+// sin a + cos b, each one fused multiply-add over a rounded product.
+IFR_DEV void rope_rotate(float &a, float &b, float cs, float sn) {
+#pragma clang fp contract(off)
+    const float x = a, y = b;
+    a = fmaf(cs, x, -(sn * y));
+    b = fmaf(sn, x, cs * y);
+}
 IFR_DEV void rope_pair(float &a, float &b, uint32_t idx, uint32_t hs, uint32_t pos, const float *theta_tab) {
     rope_pair_theta(a, b, theta_tab[(idx % hs) >> 1], pos);
 }

@@ -357,7 +357,7 @@ IFR_DEV void pg_epilogue(const PfGemmArgs &a, const float16v (&acc)[MI][2], uint
 }
 
 template <int FMT, int EPI>
-__device__ void pf_gemm_body(const PfGemmArgs &a) {
+__device__ __attribute__((always_inline)) void pf_gemm_body(const PfGemmArgs &a) {
     // four LDS objects, so the compiler sees that the direct loads into one
     // buffer do not alias the operand reads of the other
     __shared__ __attribute__((aligned(1024))) _Float16 xs0[PG_BM * PG_BK], xs1[PG_BM * PG_BK];
@@ -422,6 +422,110 @@ __device__ void pf_gemm_body(const PfGemmArgs &a) {
     pg_epilogue<EPI>(a, g.acc, g.lane, g.wm, g.wn, m0, n0);
 }
 
+// The store epilogue of the stacked Q | K | V product with the RoPE and
+// KV-cache store fused (a.rope, warp-specialized form, pairs (2i, 2i + 1)):
+// what the store epilogue and pf_rope_kv_k together do, bit for bit.  Column
+// n is element e of q (n < n1), k (n < n2) or v; its bias is added, then q
+// and k rotate with the pair partner, column n ^ 1, held by lane ^ 1 (the
+// accumulator's columns are the lanes, and q, k and v start at even
+// columns), with the (cos, sin) of the row's position and theta_(e mod hs)/2
+// from the pass's table; q goes to Y, k and v to the cache rows of positions
+// p0 + m.  Eight rows at a time: their table loads go out together from
+// rows clamped below M.
+template <int MI>
+IFR_DEV void pg_epilogue_rope(const PfGemmArgs &a, const float16v (&acc)[MI][2], uint32_t lane, uint32_t wm,
+                              uint32_t wn, uint32_t m0, uint32_t n0) {
+    constexpr int RB = 4; // rows per batch
+    const uint32_t li = lane & 31u, odd = lane & 1u, hh = a.head_size / 2, kd = a.n2 - a.n1;
+    // per column block j: the column, its vector (0 q, 1 k, 2 v), element,
+    // bias and table column
+    bool nok[2];
+    uint32_t n[2], seg[2], e[2], tj[2];
+    float bv[2];
+    bool hb[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        n[j] = n0 + wn + 32 * j + li;
+        nok[j] = n[j] < a.N; // the same for both lanes of a pair
+        const uint32_t nc = nok[j] ? n[j] : a.N - 1;
+        seg[j] = nc < a.n1 ? 0u : nc < a.n2 ? 1u : 2u;
+        e[j] = nc - (seg[j] == 0 ? 0u : seg[j] == 1 ? a.n1 : a.n2);
+        // the three bias (and, below, cache) pointers are taken in branches
+        // of their own: a select among them becomes a load from an indexed
+        // copy of the argument block in scratch memory
+        hb[j] = false;
+        bv[j] = 0.0f;
+        if (seg[j] == 0) {
+            if (a.q_bias) {
+                hb[j] = true;
+                bv[j] = a.q_bias[e[j]];
+            }
+        } else if (seg[j] == 1) {
+            if (a.k_bias) {
+                hb[j] = true;
+                bv[j] = a.k_bias[e[j]];
+            }
+        } else if (a.v_bias) {
+            hb[j] = true;
+            bv[j] = a.v_bias[e[j]];
+        }
+        tj[j] = ((e[j] & ~1u) % a.head_size) >> 1;
+    }
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int h = 0; h < 16; h += RB) {
+            uint32_t m[RB];
+            float cs[2][RB], sn[2][RB];
+#pragma unroll
+            for (int q = 0; q < RB; q++) {
+                const int ee = h + q;
+                m[q] = m0 + wm + 32 * i + 8 * (ee / 4) + 4 * (lane >> 5) + (ee % 4);
+                const uint32_t rowt = min(m[q], a.M - 1) * hh;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float2 t = *(const float2 *)((const char *)a.rope_cs + 8u * (rowt + tj[j]));
+                    cs[j][q] = t.x;
+                    sn[j][q] = t.y;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < RB; q++) {
+                    float v = acc[i][j][h + q];
+                    if (hb[j]) v = v + bv[j];
+                    // lane ^ 1's value: a DPP quad permutation [1, 0, 3, 2]
+                    // (every lane, before any branch)
+                    const float pv = __builtin_bit_cast(
+                        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+                    if (seg[j] < 2) {
+                        float x = odd ? pv : v, y = odd ? v : pv;
+                        rope_rotate(x, y, cs[j][q], sn[j][q]);
+                        v = odd ? y : x;
+                    }
+                    if (nok[j] && m[q] < a.M) {
+                        // 32-bit byte offsets from the uniform bases (the
+                        // host fuses only caches under 4 GB per layer)
+                        const uint32_t off = (a.p0 + m[q]) * kd + e[j];
+                        if (seg[j] == 0)
+                            *(float *)((char *)a.y + 4u * (m[q] * a.ldy + n[j])) = v;
+                        else if (seg[j] == 1 && a.kv_f16)
+                            *(uint16_t *)((char *)a.k_cache + 2u * off) = f32_to_f16(v);
+                        else if (seg[j] == 1)
+                            *(float *)((char *)a.k_cache + 4u * off) = v;
+                        else if (a.kv_f16)
+                            *(uint16_t *)((char *)a.v_cache + 2u * off) = f32_to_f16(v);
+                        else
+                            *(float *)((char *)a.v_cache + 4u * off) = v;
+                    }
+                }
+            // one batch's loads and addresses at a time (hoisted across
+            // batches they spill beside the accumulators)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+}
+
 // The warp-specialized form's tile: workgroups below tiles_full take whole
 // tiles as pg_tile maps them; the rest take the last tiles_n * tiles_m -
 // tiles_full tiles as 256 x 128 halves, two workgroups per tile, so that a
@@ -453,7 +557,7 @@ IFR_DEV bool pg_tile_ws(const PfGemmArgs &a, uint32_t &m0, uint32_t &n0) {
 // MFMA chain over K as in a whole tile, so the results are the same bit for
 // bit.
 template <int EPI>
-__device__ void pf_gemm_ws_half(const PfGemmArgs &a, _Float16 *xs0, _Float16 *xs1, _Float16 *ws0, _Float16 *ws1,
+__device__ __attribute__((always_inline)) void pf_gemm_ws_half(const PfGemmArgs &a, _Float16 *xs0, _Float16 *xs1, _Float16 *ws0, _Float16 *ws1,
                                 uint32_t m0, uint32_t n0) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -493,7 +597,10 @@ __device__ void pf_gemm_ws_half(const PfGemmArgs &a, _Float16 *xs0, _Float16 *xs
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             }
         }
-        pg_epilogue<EPI, 2>(a, acc, lane, wm, wn, m0, n0);
+        if (EPI == PG_STORE && a.rope)
+            pg_epilogue_rope<2>(a, acc, lane, wm, wn, m0, n0);
+        else
+            pg_epilogue<EPI, 2>(a, acc, lane, wm, wn, m0, n0);
         return;
     }
     const uint32_t t = tid - 512u, v = wave - 8u, r = t >> 1, p = t & 1u;
@@ -555,7 +662,7 @@ __device__ void pf_gemm_ws_half(const PfGemmArgs &a, _Float16 *xs0, _Float16 *xs
 // same bit for bit (the same f16 operands, the same MFMA chains).
 constexpr int PGW_THREADS = 768;
 template <int EPI>
-__device__ void pf_gemm_ws_body(const PfGemmArgs &a) {
+__device__ __attribute__((always_inline)) void pf_gemm_ws_body(const PfGemmArgs &a) {
     __shared__ __attribute__((aligned(1024))) _Float16 xs0[PG_BM * PG_BK], xs1[PG_BM * PG_BK];
     __shared__ __attribute__((aligned(1024))) _Float16 ws0[PG_BN * PG_BK], ws1[PG_BN * PG_BK];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -593,7 +700,10 @@ __device__ void pf_gemm_ws_body(const PfGemmArgs &a) {
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             }
         }
-        pg_epilogue<EPI>(a, g.acc, lane, wm, wn, m0, n0);
+        if (EPI == PG_STORE && a.rope)
+            pg_epilogue_rope<4>(a, g.acc, lane, wm, wn, m0, n0);
+        else
+            pg_epilogue<EPI>(a, g.acc, lane, wm, wn, m0, n0);
         return;
     }
 

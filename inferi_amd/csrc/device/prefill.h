@@ -272,9 +272,11 @@ IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
             x0 = x0 + bias[e0];
             x1 = x1 + bias[e1];
         }
-        // theta index j (the table holds base^(-2j/hs)); rope_pair takes 2j
-        const uint32_t tj = a.neox ? 2 * (pi % (hs / 2)) : e0;
-        rope_pair(x0, x1, tj, hs, pos, a.rope_tab);
+        // theta index j (the table holds base^(-2j/hs)): the pass's (cos,
+        // sin) of pos * theta_j
+        const uint32_t tj = a.neox ? pi % (hs / 2) : (e0 % hs) >> 1;
+        const float *cs = a.rope_cs + ((size_t)m * (hs / 2) + tj) * 2;
+        rope_rotate(x0, x1, cs[0], cs[1]);
         if (is_q) {
             row[e0] = x0;
             row[e1] = x1;
@@ -298,6 +300,20 @@ IFR_DEV void pf_rope_kv_body(const PfArgs &a) {
         else
             ((float *)a.v_cache)[off] = v;
     }
+}
+
+// The pass's RoPE angles: rope_cs[m][j] = (cos, sin) of (p0 + m) * theta_j
+// for j < head_size / 2 (sincosf, as the decode step's rope_pair), shared by
+// every head and layer of the pass (pf_rope_kv_k and the Q/K/V product's
+// fused epilogue read it).
+IFR_DEV void pf_rope_tab_body(const PfArgs &a) {
+    const uint32_t m = blockIdx.x, j = threadIdx.x, hh = a.head_size / 2;
+    if (j >= hh) return;
+    const float ang = (float)(a.p0 + m) * a.rope_tab[j];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    a.rope_cs[((size_t)m * hh + j) * 2] = cs;
+    a.rope_cs[((size_t)m * hh + j) * 2 + 1] = sn;
 }
 
 // h[m][j] = f16(u * silu(g)), g = gu[m][j], u = gu[m][F + j] (silu.rs:

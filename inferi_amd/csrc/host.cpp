@@ -148,6 +148,10 @@ struct ifr_ctx {
     // pf_ws, default on; 0 = the eight-wave form; device/pf_gemm.h
     // pf_gemm_ws_body)
     int pf_ws = 1;
+    // the Q/K/V product's epilogue applies RoPE and stores k, v to the cache
+    // (warp-specialized form, pairs (2i, 2i + 1)) instead of pf_rope_kv_k
+    // (option pf_rope_fuse, default on)
+    int pf_rope_fuse = 1;
     // bumped by every option change: a captured decode step is captured
     // again when it differs
     uint64_t opt_gen = 0;
@@ -478,6 +482,7 @@ struct ifr_llama2_state {
     // prefill scratch (allocated at the first prefill): a chunk of pf_chunk tokens
     uint32_t pf_chunk = 0, pf_ldh = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_gu = nullptr;
+    float *pf_rope_cs = nullptr; // [pf_chunk][head_size / 2][2]: the pass's RoPE (cos, sin)
     uint16_t *pf_xh = nullptr, *pf_h = nullptr;
     // sampler of the step end: temperature 0 takes the argmax
     float temperature = 0.0f, topp = 0.0f;
@@ -998,6 +1003,10 @@ IFR_API ifr_status ifr_set_option(ifr_ctx *c, const char *key, int64_t value) {
         c->pf_ws = value ? 1 : 0;
         return IFR_OK;
     }
+    if (!strcmp(key, "pf_rope_fuse")) {
+        c->pf_rope_fuse = value ? 1 : 0;
+        return IFR_OK;
+    }
     if (!strcmp(key, "gemv_grp")) {
         c->gemv_grp = (int)value;
         return IFR_OK;
@@ -1020,6 +1029,7 @@ IFR_API ifr_status ifr_get_option(ifr_ctx *c, const char *key, int64_t *value) {
     else if (k == "pf_chunk") *value = c->pf_chunk;
     else if (k == "pf_tile") *value = c->pf_tile;
     else if (k == "pf_ws") *value = c->pf_ws;
+    else if (k == "pf_rope_fuse") *value = c->pf_rope_fuse;
     else if (k == "gemv_grp") *value = c->gemv_grp;
     else if (k == "gemv_waves") *value = c->gemv_waves;
     else return c->fail(IFR_EINVAL, "unknown option %s", key);
@@ -1707,9 +1717,13 @@ constexpr uint32_t PF_BIG_TILES_MIN = 128;
 // One product of a pass: nm (1 to 3) matrices of one type stacked by rows
 // into Y[M][ldy] f32 (stored or added), or (SwiGLU) gate m[0] and up m[1]
 // into h[M][ldy] = f16(up * silu(gate)).  X rows (pitch ldx halves) must be
-// 16-byte aligned.
+// 16-byte aligned.  rope (may be null): the stacked Q | K | V store product
+// may fuse pf_rope_kv_k's work into its epilogue (warp-specialized form
+// only); *fused says whether it did.
 static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const Tens *const *m, int nm, void *y,
-                                 uint32_t ldy, uint32_t M, PfEpi epi) {
+                                 uint32_t ldy, uint32_t M, PfEpi epi, const PfArgs *rope = nullptr,
+                                 bool *fused = nullptr) {
+    if (fused) *fused = false;
     PfGemmArgs g{};
     g.x = xh;
     g.w0 = m[0]->data;
@@ -1740,6 +1754,19 @@ static ifr_status launch_pf_gemm(ifr_ctx *c, const void *xh, uint32_t ldx, const
         // many 256 x 128 halves, one round over every CU
         const uint32_t tiles = g.tiles_n * g.tiles_m, tail = tiles % PF_WS_ROUND;
         g.tiles_full = tail != 0 && tail <= PF_WS_ROUND / 2 ? tiles - tail : tiles;
+        if (rope && epi == PF_EPI_STORE && nm == 3) {
+            g.rope = 1;
+            g.rope_cs = rope->rope_cs;
+            g.q_bias = rope->q_bias;
+            g.k_bias = rope->k_bias;
+            g.v_bias = rope->v_bias;
+            g.k_cache = rope->k_cache;
+            g.v_cache = rope->v_cache;
+            g.head_size = rope->head_size;
+            g.p0 = rope->p0;
+            g.kv_f16 = rope->kv_f16;
+            if (fused) *fused = true;
+        }
         return c->launch(std::string("pf_gemm_q4_k_ws_") + epi_name[epi], dim3(tiles + (tiles - g.tiles_full)),
                          dim3(PF_WS_THREADS), 0, g);
     }
@@ -1809,6 +1836,7 @@ static ifr_status pf_ensure_scratch(ifr_llama2_state *s) {
     if ((st = A((size_t)C * H * 4, (void **)&s->pf_x))) return st;
     if ((st = A((size_t)C * s->pf_ldh * 2, (void **)&s->pf_xh))) return st;
     if ((st = A((size_t)C * (qd + 2 * s->kv_dim) * 4, (void **)&s->pf_qkv))) return st;
+    if ((st = A((size_t)C * s->head_size * 4, (void **)&s->pf_rope_cs))) return st;
     return A((size_t)C * F * 2, (void **)&s->pf_h);
 }
 
@@ -1872,7 +1900,13 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
         a.h = s->pf_h;
         a.neox = cfg.rope_variant == IFR_ROPE_NEOX;
         a.kv_mul = G;
+        a.rope_cs = s->pf_rope_cs;
         if ((st = c->launch("pf_embed_k", dim3(M), dim3(256), 0, a))) return st;
+        if ((st = c->launch("pf_rope_tab_k", dim3(M), dim3(64), 0, a))) return st;
+        // the Q/K/V product may take over pf_rope_kv_k: pairs (2i, 2i + 1),
+        // and the epilogue's 32-bit offsets cover the cache and qkv rows
+        const bool fuse_ok = c->pf_rope_fuse && !a.neox && s->layer_kv_bytes < (1ull << 32) &&
+                             (uint64_t)M * ldq * 4 < (1ull << 32);
         for (uint32_t l = 0; l < cfg.n_layers; l++) {
             const LayerW &L = w->layers[l];
             const Tens *mats[7];
@@ -1886,15 +1920,17 @@ IFR_API ifr_status ifr_llama2_prefill(ifr_ctx *c, ifr_llama2_state *s, const ifr
             if ((st = c->launch("pf_rmsnorm_f16_k", dim3(M), dim3(256), 0, a))) return st;
             // Q, K and V into adjacent columns of qkv: each run of matrices of
             // one type as one stacked product
+            bool fused = false;
             for (int i = 0, col = 0; i < 3;) {
                 int j = i + 1;
                 while (j < 3 && mats[j]->dtype == mats[i]->dtype) j++;
-                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + i, j - i, s->pf_qkv + col, ldq, M, PF_EPI_STORE)))
+                if ((st = launch_pf_gemm(c, s->pf_xh, ldh, mats + i, j - i, s->pf_qkv + col, ldq, M, PF_EPI_STORE,
+                                         fuse_ok ? &a : nullptr, &fused)))
                     return st;
                 for (int k = i; k < j; k++) col += (int)mats[k]->rows;
                 i = j;
             }
-            if ((st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
+            if (!fused && (st = c->launch("pf_rope_kv_k", dim3(M), dim3(256), 0, a))) return st;
             // the last layer's attention and FFN feed only its residual
             // stream, which nothing reads (the pass's product is the KV rows;
             // the next decode step starts from the embedding): not run

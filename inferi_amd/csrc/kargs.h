@@ -242,6 +242,15 @@ struct PfGemmArgs {
     // warp-specialized form: tiles at or past tiles_full run as two 256 x
     // 128 halves, one workgroup each (tiles_full = tiles_n * tiles_m: none)
     uint32_t tiles_full;
+    // warp-specialized store product of stacked Q | K | V with rope != 0:
+    // the epilogue adds the biases, rotates q and k (pairs (2i, 2i+1)) with
+    // the pass's (cos, sin) table and stores q to Y and k, v to the cache
+    // rows of positions p0 + m (the work of pf_rope_kv_k)
+    const float *rope_cs;          // [M][head_size / 2][2]
+    const float *q_bias, *k_bias, *v_bias;
+    void *k_cache, *v_cache;
+    uint32_t head_size, p0, rope;
+    int32_t kv_f16;
 };
 
 // Prefill pointwise and attention kernels (one chunk of M prompt tokens at
@@ -268,6 +277,7 @@ struct PfArgs {
     const float *q_bias, *k_bias, *v_bias; // QKV biases (may be null)
     int32_t neox;        // RoPE pairs (j, j + hs/2) instead of (2j, 2j+1)
     uint32_t kv_mul;     // attention: query heads per KV head
+    float *rope_cs;      // [M][head_size / 2][2]: cos, sin of (p0 + m) * theta_j
 };
 
 } // namespace ifr

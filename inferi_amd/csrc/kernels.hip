@@ -190,6 +190,7 @@ extern "C" __global__ void __launch_bounds__(PGW_THREADS) pf_gemm_q4_k_ws_swiglu
 }
 extern "C" __global__ void __launch_bounds__(256) pf_embed_k(PfArgs a) { pf_embed_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rmsnorm_f16_k(PfArgs a) { pf_rmsnorm_f16_body(a); }
+extern "C" __global__ void __launch_bounds__(64) pf_rope_tab_k(PfArgs a) { pf_rope_tab_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_rope_kv_k(PfArgs a) { pf_rope_kv_body(a); }
 extern "C" __global__ void __launch_bounds__(256) pf_silu_k(PfArgs a) { pf_silu_body(a); }
 

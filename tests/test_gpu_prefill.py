@@ -285,6 +285,33 @@ def test_prefill_pass_length_and_tile_give_same_results(ctx):
         _same(got, ref, f"tile {key[0]}{' warp-specialized' if key[1] else ''}, passes of {key[2] or 299}")
 
 
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("kv,bias", [("F16", False), ("F32", True)])
+def test_prefill_fused_rope_same_results(ctx, kv, bias):
+    """The Q/K/V product's epilogue with RoPE and the KV-cache store fused
+    (option pf_rope_fuse, warp-specialized form) against the plain store
+    epilogue followed by pf_rope_kv_k: the same KV cache rows, logits and
+    tokens bit for bit, at the 8B widths (Q/K/V 6144 columns: a 4095-token
+    pass has 256 whole tiles and 128 in halves), with f16 and f32 caches and
+    with QKV biases on the (2i, 2i + 1) pairs."""
+    import inferi_amd as I
+
+    cfg = I.Llama2Config(n_layers=2, hidden=4096, ffn=1024, n_heads=32, n_kv_heads=8, vocab=1000, max_pos=4104,
+                         rope_theta=500000.0, rms_eps=1e-5, kv_dtype=getattr(I, kv))
+    w = I.Llama2Weights.synthetic(ctx, cfg, seed=7, qkv_bias=bias)
+    prompt = np.random.default_rng(17).integers(0, cfg.vocab, 4096).astype(np.uint32)
+    fuse0 = ctx.get_option("pf_rope_fuse")
+    out = {}
+    try:
+        for fuse in (0, 1):
+            ctx.set_option("pf_rope_fuse", fuse)
+            out[fuse] = _prefill_run(ctx, cfg, w, prompt, 4095, 3)
+    finally:
+        ctx.set_option("pf_rope_fuse", fuse0)
+        w.close()
+    _same(out[1], out[0], "fused RoPE epilogue")
+
+
 def test_prefill_uses_weights_rewritten_in_place(ctx):
     """The prefill kernels read the bound GGUF blocks themselves: new bytes
     written into a bound tensor's buffer (no ifr_llama2_weights_set call) are
